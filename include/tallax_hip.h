@@ -1,0 +1,105 @@
+/*
+ * tallax_hip.h -- C ABI of the MI355X (gfx950) sort / select / sample library.
+ *
+ * Conventions (every entry point):
+ *   - All array arguments are DEVICE pointers to dense row-major buffers owned
+ *     by the caller; scalars are passed by value.
+ *   - Work is enqueued on `stream` only; nothing synchronizes the host and
+ *     nothing allocates device memory.  Entry points that need scratch take a
+ *     caller-provided `workspace` of at least `*_workspace_size(...)` bytes,
+ *     which must be zero-filled once before its first use: the kernels leave
+ *     it zero-filled again when they complete.  Calls that may run
+ *     concurrently need distinct workspaces.
+ *   - Return value: 0 on success, otherwise a TALLAX_* status code; the
+ *     message of the last failure on the calling thread is returned by
+ *     tallax_last_error().
+ *   - dtype codes: TALLAX_F32 = 0, TALLAX_BF16 = 1, TALLAX_I32 = 2.
+ *
+ * Each entry point replaces one jit-wrapped Pallas call of the reference
+ * (oliverdutton/tallax); the reference interface is cited above each
+ * declaration as file:line.
+ */
+#ifndef TALLAX_HIP_H_
+#define TALLAX_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* tallax_stream_t; /* == hipStream_t */
+
+enum {
+  TALLAX_OK = 0,
+  TALLAX_INVALID_ARGUMENT = 1,
+  TALLAX_UNSUPPORTED = 2,
+  TALLAX_HIP_ERROR = 3,
+  TALLAX_WORKSPACE_TOO_SMALL = 4,
+};
+
+enum { TALLAX_F32 = 0, TALLAX_BF16 = 1, TALLAX_I32 = 2 };
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* tallax_last_error(void);
+
+/* ABI revision of this header. */
+int tallax_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Exact top-k along the last axis.
+ * Replaces tax.top_k(logits, k)  -- tallax/_src/top_k.py:516-567
+ * (= top_dynamic_k(max_k=k, guarantee_convergence=True), top_k.py:372-514,
+ * kernel dynamic_top_k_refs top_k.py:203-370).
+ * x: [rows, cols] f32 or bf16.  Outputs: out_vals [rows, k] (same dtype,
+ * descending), out_idx [rows, k] int32; ties broken to the lowest index.
+ * 1 <= k <= 128 (the reference raises NotImplementedError above 128,
+ * top_k.py:438-439), k <= cols.  NaN, -inf and finfo(dtype).min are never
+ * preferred over other values; slots that can only be filled by them hold
+ * finfo(dtype).min, as the reference's bins do (top_k.py:241-243).
+ * ---------------------------------------------------------------------- */
+size_t tallax_topk_workspace_size(int64_t rows, int64_t cols, int64_t k, int dtype);
+int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k, void* out_vals,
+                int32_t* out_idx, void* workspace, size_t workspace_bytes, tallax_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused vLLM-style sampler: top-k (per-row k, clamped to 128) -> top-p ->
+ * temperature -> Gumbel-max, one token per row, in one kernel launch.
+ * Replaces sampling.sample(rng_key, logits, tpu_sampling_metadata)
+ *   -- tallax/_src/sampling.py:331-343, i.e. _top_k_with_sharding
+ *   (sampling.py:271-328, single device: top_dynamic_k(max_k=128,
+ *   num_bins=256, bins_topm_schedule=(5,9), guarantee_convergence=True,
+ *   replace_val)) followed by top_p_and_sample (sampling.py:210-269).
+ * logits [rows, vocab] f32/bf16; top_k [rows] int32; top_p, temperature
+ * [rows] f32; rng_key: 2 uint32 words of threefry key data (device);
+ * dim0_offset: global row offset of this shard for the noise counters
+ * (sampling.py:249-251); replace_val: the value written over filtered
+ * candidates (the reference passes -1e12).  out_tokens [rows] int32.
+ * vocab >= 128.
+ * ---------------------------------------------------------------------- */
+size_t tallax_sample_workspace_size(int64_t rows, int64_t vocab, int dtype);
+int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, int64_t vocab,
+                                  const int32_t* top_k, const float* top_p, const float* temperature,
+                                  const uint32_t* rng_key, int64_t dim0_offset, double replace_val,
+                                  int32_t* out_tokens, void* workspace, size_t workspace_bytes,
+                                  tallax_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Top-p filter + temperature + Gumbel-max sampling over already-selected,
+ * descending candidates.
+ * Replaces top_p_and_sample(topk_logits, topk_idx, rng_key, top_p,
+ * temperature, *, vocab_size, replace_val) -- tallax/_src/sampling.py:210-269
+ * (kernel top_p_and_sample_refs/arrays, sampling.py:65-153).
+ * topk_logits [rows, k] f32/bf16, topk_idx [rows, k] int32, k <= 128.
+ * ---------------------------------------------------------------------- */
+int tallax_top_p_and_sample(const void* topk_logits, int dtype, const int32_t* topk_idx, int64_t rows,
+                            int64_t k, const uint32_t* rng_key, const float* top_p,
+                            const float* temperature, int64_t vocab_size, double replace_val,
+                            int64_t dim0_offset, int32_t* out_tokens, tallax_stream_t stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* TALLAX_HIP_H_ */

@@ -1,0 +1,34 @@
+/*
+ * tallax_hip_testing.h -- test hooks of the MI355X tallax library.
+ *
+ * These entry points have NO counterpart in the reference: they expose the
+ * device-side primitives the sampler is built from (float32 exp/log and the
+ * Threefry-2x32 Gumbel noise) so that tests can compare them bit for bit with
+ * the CPU oracle.  Conventions are those of tallax_hip.h.
+ */
+#ifndef TALLAX_HIP_TESTING_H_
+#define TALLAX_HIP_TESTING_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "tallax_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* exp_out[i] = exp(x[i]), log_out[i] = log(x[i]) with the sampler's float32 routines. */
+int tallax_testing_expf_logf(const float* x, float* exp_out, float* log_out, int64_t n,
+                             tallax_stream_t stream);
+
+/* bits_out[i] = x0 ^ x1 of threefry2x32((k0, k1), (0, counters[i])) and
+ * gumbel_out[i] = -log(-log(max(tiny, unit(bits)*(1-tiny) + tiny))). */
+int tallax_testing_gumbel(uint32_t k0, uint32_t k1, const uint32_t* counters, float* gumbel_out,
+                          uint32_t* bits_out, int64_t n, tallax_stream_t stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* TALLAX_HIP_TESTING_H_ */

@@ -1,0 +1,376 @@
+"""CPU oracle for the tallax sort / select / sample path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module, and only as the checker (or the timed CPU baseline).  The product
+(`tallax_amd`) never imports it and has no CPU fallback.
+
+Every function restates the reference (oliverdutton/tallax, read-only at
+/root/reference) in numpy and cites the file:line it follows.  Float work is
+done in numpy float32 with one IEEE operation per step, in the same order as
+the HIP kernels, so GPU results are compared bit for bit.
+
+Where the reference leaves a choice open (its tie order inside bitonic
+networks, the summation order of XLA reductions, XLA's exp/log), the oracle
+fixes the choice made by this build and says so; those parts are pinned by
+closed forms and invariants in tests/, not by the reference:
+  * top-k ties: lowest index first (the contract of BASELINE.json);
+  * the softmax denominator in top_p_mask: a stride-halving tree over 128
+    zero-padded slots; the per-tile sum inside cumsum: the pairwise tree
+    that the tile's own Hillis-Steele scan produces;
+  * exp/log: exp_f32/log_f32 below (<= 1 ulp, pinned against float64 numpy).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+F32 = np.float32
+U32 = np.uint32
+NUM_SUBLANES, NUM_LANES = 8, 128   # tallax/_src/utils.py:12-13
+
+F32_MIN = F32(np.finfo(np.float32).min)
+BF16_MIN = np.uint32(0xFF7F0000).view(np.float32)   # finfo(bfloat16).min widened to f32
+TINY = np.finfo(np.float32).tiny
+
+
+def _f(u: int) -> np.float32:
+    return np.array(u, dtype=np.uint32).view(np.float32)[()]
+
+
+# ---------------------------------------------------------------------------
+# bf16 helpers (numpy has no bfloat16: bf16 arrays are carried as uint16 bits)
+# ---------------------------------------------------------------------------
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even float32 -> bfloat16 bits (NaN kept quiet)."""
+    b = np.asarray(x, dtype=np.float32).view(np.uint32)
+    nan = (b & 0x7FFFFFFF) > 0x7F800000
+    r = (b + U32(0x7FFF) + ((b >> 16) & 1)) >> 16
+    r = np.where(nan, (b | 0x00400000) >> 16, r)
+    return r.astype(np.uint16)
+
+
+def round_to_dtype(x, dtype: str) -> np.ndarray:
+    x = np.asarray(x, dtype=np.float32)
+    return bf16_bits_to_f32(f32_to_bf16_bits(x)) if dtype == "bf16" else x
+
+
+def dtype_min(dtype: str) -> np.float32:
+    return BF16_MIN if dtype == "bf16" else F32_MIN
+
+
+# ---------------------------------------------------------------------------
+# Keys (tallax/_src/utils.py:139-200) and the top-k composite order
+# ---------------------------------------------------------------------------
+def float_to_sortable_int(x: np.ndarray) -> np.ndarray:
+    """standardize + float_to_sortable_int (utils.py:139-147,186-195):
+    NaN -> bits 0x7FFFFFFE, -0 -> +0, negative floats -> i ^ 0x7FFFFFFF."""
+    x = np.asarray(x, dtype=np.float32)
+    i = x.view(np.int32).copy()
+    i[np.isnan(x)] = 0x7FFFFFFE
+    i[x == 0] = 0
+    return np.where(i < 0, i ^ np.int32(0x7FFFFFFF), i).astype(np.int32)
+
+
+def sortable_int_to_float(i: np.ndarray) -> np.ndarray:
+    """utils.py:198-200."""
+    i = np.asarray(i, dtype=np.int32)
+    return np.where(i < 0, i ^ np.int32(0x7FFFFFFF), i).astype(np.int32).view(np.float32)
+
+
+def select_key(x: np.ndarray) -> np.ndarray:
+    """Unsigned key ordering values as the reference's strict-`>` top-k does
+    (top_k.py:64): monotone in value, -0 == +0, NaN below -inf."""
+    b = np.asarray(x, dtype=np.float32).view(np.uint32)
+    a = b & U32(0x7FFFFFFF)
+    k = np.where(b & U32(0x80000000), ~b, b | U32(0x80000000))
+    k = np.where(a == 0, U32(0x80000000), k)
+    k = np.where(a > U32(0x7F800000), U32(1), k)
+    return k.astype(np.uint32)
+
+
+def topk_composite(x: np.ndarray) -> np.ndarray:
+    """u64 per element: select key << 32 | ~index; larger = earlier in the
+    (value descending, index ascending) order."""
+    k = select_key(x).astype(np.uint64)
+    idx = np.arange(x.shape[-1], dtype=np.uint64)
+    return (k << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - idx)
+
+
+def top_k(x: np.ndarray, k: int, dtype: str = "f32"):
+    """Exact top-k along the last axis: the intended semantics of tax.top_k
+    (top_k.py:516-567) under BASELINE's tie rule, i.e. the first k of
+    xla_equivalent_sort(descending=True, is_stable=True) (sort.py:932-970).
+    Elements the binned reference can never admit (<= finfo.min or NaN,
+    top_k.py:64,241-243) are reported as finfo(dtype).min.
+    x: float32 values (bf16 inputs as their exact f32 values)."""
+    x = np.asarray(x, dtype=np.float32)
+    comp = topk_composite(x)
+    part = np.argpartition(comp, comp.shape[-1] - k, axis=-1)[..., -k:]
+    order = np.argsort(np.take_along_axis(comp, part, -1), axis=-1)[..., ::-1]
+    idx = np.take_along_axis(part, order, -1).astype(np.int32)
+    vals = np.take_along_axis(x, idx, -1).copy()
+    eligible = select_key(vals) > select_key(np.full((), dtype_min(dtype), np.float32))
+    vals[~eligible] = dtype_min(dtype)
+    return vals, idx
+
+
+# ---------------------------------------------------------------------------
+# exp / log (float32, one IEEE op per step; mirrors tallax_amd/csrc/tx_math.h)
+# ---------------------------------------------------------------------------
+_LOG2E, _LN2_HI, _LN2_LO = _f(0x3FB8AA3B), _f(0x3F317000), _f(0x3805FDF4)
+_EXP_C = [_f(0x39500D01), _f(0x3AB60B61), _f(0x3C088889), _f(0x3D2AAAAB), _f(0x3E2AAAAB), F32(0.5)]
+_LOG_C = [_f(0x3E1D89D9), _f(0x3E3A2E8C), _f(0x3E638E39), _f(0x3E924925), _f(0x3ECCCCCD), _f(0x3F2AAAAB)]
+_SQRT2 = _f(0x3FB504F3)
+
+
+def _pow2(n: np.ndarray) -> np.ndarray:
+    return ((np.clip(n, -126, 127).astype(np.int32) + 127) << 23).astype(np.int32).view(np.float32)
+
+
+def exp_f32(x) -> np.ndarray:
+    """Cody-Waite reduction, exp(r) = 1 + (r + r^2 q(r)) (see tx_math.h)."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(all="ignore"):
+        xc = np.minimum(np.maximum(x, F32(-120.0)), F32(100.0))
+        n = np.rint(xc * _LOG2E)
+        r = (xc - n * _LN2_HI) - n * _LN2_LO
+        q = np.full_like(r, _EXP_C[0])
+        for c in _EXP_C[1:6]:
+            q = q * r + c
+        p = F32(1.0) + ((r * r) * q + r)
+        ni = np.where(np.isnan(n), 0, n).astype(np.int32)
+        normal = (ni >= -126) & (ni <= 127)
+        n1 = np.where(ni < 0, -((-ni) // 2), ni // 2).astype(np.int32)
+        n2 = ni - n1
+        res = np.where(normal, p * _pow2(ni), (p * _pow2(n1)) * _pow2(n2))
+        res = np.where(np.isnan(x), x, res)
+    return res.astype(np.float32)
+
+
+def log_f32(x) -> np.ndarray:
+    """log via atanh series around 1 (see tx_math.h)."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(all="ignore"):
+        b = x.view(np.uint32)
+        sub = b < U32(0x00800000)
+        xs = np.where(sub, x * F32(8388608.0), x)
+        bs = xs.view(np.uint32)
+        e = np.where(sub, -23, 0).astype(np.int32) + (bs >> 23).astype(np.int32) - 127
+        m = ((bs & U32(0x007FFFFF)) | U32(0x3F800000)).view(np.float32)
+        big = m > _SQRT2
+        m = np.where(big, m * F32(0.5), m)
+        e = e + big.astype(np.int32)
+        f = m - F32(1.0)
+        s = f / (F32(2.0) + f)
+        z = s * s
+        R = np.full_like(z, _LOG_C[0])
+        for c in _LOG_C[1:]:
+            R = R * z + c
+        R = R * z
+        hfsq = (F32(0.5) * f) * f
+        dk = e.astype(np.float32)
+        res = dk * _LN2_HI - ((hfsq - (s * (hfsq + R) + dk * _LN2_LO)) - f)
+        res = np.where(x == 0, F32(-np.inf), res)
+        res = np.where(x == np.inf, F32(np.inf), res)
+        res = np.where((x < 0) | np.isnan(x), F32(np.nan), res)
+    return res.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Threefry-2x32-20 and the sparse uniform (tallax/_src/sparse_random.py)
+# ---------------------------------------------------------------------------
+_ROT = (13, 15, 26, 6, 17, 29, 16, 24)
+
+
+def threefry2x32(k0, k1, c0, c1):
+    """Threefry-2x32, 20 rounds (Salmon et al., SC'11), elementwise over the
+    counter arrays; JAX's threefry2x32_p (sparse_random.py:3,54)."""
+    k0, k1 = U32(k0), U32(k1)
+    c0 = np.asarray(c0, dtype=np.uint32)
+    c1 = np.asarray(c1, dtype=np.uint32)
+    ks = (k0, k1, U32(k0 ^ k1 ^ U32(0x1BD11BDA)))
+    with np.errstate(over="ignore"):
+        x0 = c0 + ks[0]
+        x1 = c1 + ks[1]
+        for blk in range(5):
+            for i in range(4):
+                r = _ROT[(blk & 1) * 4 + i]
+                x0 = x0 + x1
+                x1 = (x1 << U32(r)) | (x1 >> U32(32 - r))
+                x1 = x1 ^ x0
+            x0 = x0 + ks[(blk + 1) % 3]
+            x1 = x1 + ks[(blk + 2) % 3] + U32(blk + 1)
+    return x0.astype(np.uint32), x1.astype(np.uint32)
+
+
+def bits_to_uniform(bits: np.ndarray) -> np.ndarray:
+    """_bits_to_uniform (sparse_random.py:7-41) for float32."""
+    bits = np.asarray(bits, dtype=np.uint32)
+    return ((bits >> U32(9)) | U32(0x3F800000)).view(np.float32) - F32(1.0)
+
+
+def sparse_random_uniform(key, indices, dim1_size, minval=0.0, maxval=1.0):
+    """sparse_random_uniform (sparse_random.py:43-64): counter (hi=0,
+    lo=row*dim1_size+col as uint32), bits = x0 ^ x1."""
+    i0 = np.asarray(indices[0]).astype(np.int64)
+    i1 = np.asarray(indices[1]).astype(np.int64)
+    lo = ((i0 * int(dim1_size) + i1) & 0xFFFFFFFF).astype(np.uint32)
+    o0, o1 = threefry2x32(key[0], key[1], np.zeros_like(lo), lo)
+    f = bits_to_uniform(o0 ^ o1)
+    mn, mx = F32(minval), F32(maxval)
+    return np.maximum(mn, f * (mx - mn) + mn)
+
+
+def gumbel(key, indices, dim1_size) -> np.ndarray:
+    """-log(-log(u)), u from sparse_random_uniform(minval=tiny, maxval=1)
+    (sparse_random.py:75-84)."""
+    u = sparse_random_uniform(key, indices, dim1_size, minval=TINY, maxval=1.0)
+    return -log_f32(-log_f32(u))
+
+
+# ---------------------------------------------------------------------------
+# max_arrays (bitonic_top_k.py:43-97): argmax tournament along axis 0
+# ---------------------------------------------------------------------------
+def max_arrays_axis0(operands):
+    """Literal restatement of max_arrays(operands, num_keys=1, axis=0):
+    pad dim0 to max(2^ceil(log2 n), 8) with dtype min, halve (left = first
+    half, right = second half, keep left only if left > right), then the three
+    in-tile xor stages (4, 2, 1).  Returns row 0 of every operand."""
+    ops = [np.asarray(o) for o in operands]
+    n = ops[0].shape[0]
+    P = max(2 ** math.ceil(math.log2(n)), NUM_SUBLANES) if n > 1 else NUM_SUBLANES
+    padded = []
+    for o in ops:
+        fill = np.finfo(o.dtype).min if np.issubdtype(o.dtype, np.floating) else np.iinfo(o.dtype).min
+        pad = np.full((P - n,) + o.shape[1:], fill, dtype=o.dtype)
+        padded.append(np.concatenate([o, pad], axis=0))
+    ops = padded
+    while ops[0].shape[0] > NUM_SUBLANES:
+        h = ops[0].shape[0] // 2
+        mask = ops[0][:h] > ops[0][h:]
+        ops = [np.where(mask, o[:h], o[h:]) for o in ops]
+    iota = np.arange(NUM_SUBLANES)
+    for stage in (2, 1, 0):
+        perm = iota ^ (1 << stage)
+        mask = ops[0] > ops[0][perm]
+        ops = [np.where(mask, o, o[perm]) for o in ops]
+    return [o[0] for o in ops]
+
+
+# ---------------------------------------------------------------------------
+# cumsum (tallax/_src/cumsum.py:16-63)
+# ---------------------------------------------------------------------------
+def _hs_scan(t: np.ndarray, axis: int) -> np.ndarray:
+    """Hillis-Steele inclusive scan inside one tile (cumsum.py:21-30)."""
+    n = t.shape[axis]
+    t = t.copy()
+    s = 1
+    while s < n:
+        shifted = np.zeros_like(t)
+        src = [slice(None)] * t.ndim
+        dst = [slice(None)] * t.ndim
+        src[axis] = slice(0, n - s)
+        dst[axis] = slice(s, n)
+        shifted[tuple(dst)] = t[tuple(src)]
+        t = t + shifted
+        s *= 2
+    return t
+
+
+def cumsum(arr: np.ndarray, axis: int, reverse: bool = False) -> np.ndarray:
+    """cumsum_arrays (cumsum.py:32-63): pad to (8,128) tiles with 0, scan each
+    tile (Hillis-Steele along `axis`), add the running total of earlier tiles
+    (accumulated sequentially, tile sum = the tile's pairwise-tree sum), and
+    for reverse flip tile order and in-tile order around the whole scan."""
+    arr = np.asarray(arr)
+    assert arr.ndim == 2 and axis in (0, 1)
+    dt = arr.dtype
+    rows, cols = arr.shape
+    tr, tc = NUM_SUBLANES, NUM_LANES
+    pr, pc = -(-rows // tr) * tr, -(-cols // tc) * tc
+    a = np.zeros((pr, pc), dtype=dt)
+    a[:rows, :cols] = arr
+    tile = tr if axis == 0 else tc
+    if reverse:
+        a = np.flip(a, axis=axis)
+    n = a.shape[axis] // tile
+    with np.errstate(over="ignore"):
+        tiles = np.split(a, n, axis=axis)
+        outs = [_hs_scan(t, axis) for t in tiles]
+        sums = [np.take(o, [tile - 1], axis=axis) for o in outs]   # pairwise-tree tile sums
+        run = sums[0]
+        for i in range(1, n):
+            outs[i] = outs[i] + run
+            run = run + sums[i]
+        out = np.concatenate(outs, axis=axis)
+    if reverse:
+        out = np.flip(out, axis=axis)
+    return np.ascontiguousarray(out[:rows, :cols]).astype(dt)
+
+
+# ---------------------------------------------------------------------------
+# top_p_mask / top_p_and_sample / sample (tallax/_src/sampling.py)
+# ---------------------------------------------------------------------------
+def _tree_sum_axis0_128(e: np.ndarray) -> np.ndarray:
+    """Sum over axis 0 (k <= 128 rows) as a stride-halving tree over 128
+    zero-padded slots: x[:64] + x[64:], then x[:32] + x[32:], ..."""
+    k = e.shape[0]
+    assert k <= 128
+    x = np.zeros((128,) + e.shape[1:], dtype=np.float32)
+    x[:k] = e
+    while x.shape[0] > 1:
+        h = x.shape[0] // 2
+        x = x[:h] + x[h:]
+    return x
+
+
+def top_p_mask(topk_logits: np.ndarray, p: np.ndarray, replace_val: float) -> np.ndarray:
+    """top_p_mask(axis=0) (sampling.py:25-62) on [k, B] descending candidates."""
+    L = np.asarray(topk_logits, dtype=np.float32)
+    k = L.shape[0]
+    with np.errstate(all="ignore"):
+        e = exp_f32(L - L[:1])
+        s = _tree_sum_axis0_128(e)
+        probs = e / s
+    c = cumsum(probs, axis=0)
+    t = (c < np.asarray(p, dtype=np.float32)[None, :]).sum(0)
+    # take_along_axis_arrays: out-of-range index (t == k) gathers 0 (gather.py:11-45)
+    thr = np.where(t < k, L[np.minimum(t, k - 1), np.arange(L.shape[1])], F32(0.0))
+    return np.where(L >= thr[None, :], L, F32(replace_val)).astype(np.float32)
+
+
+def top_p_and_sample(topk_logits, topk_idx, key, top_p, temperature, vocab_size,
+                     replace_val, dim0_offset: int = 0) -> np.ndarray:
+    """top_p_and_sample_arrays (sampling.py:65-115): [B, k] -> [B] tokens."""
+    L = np.asarray(topk_logits, dtype=np.float32).T
+    I = np.asarray(topk_idx, dtype=np.int32).T
+    B = L.shape[1]
+    top_p = np.broadcast_to(np.asarray(top_p, dtype=np.float32), (B,))
+    temperature = np.broadcast_to(np.asarray(temperature, dtype=np.float32), (B,))
+    masked = top_p_mask(L, top_p, replace_val)
+    with np.errstate(all="ignore"):
+        scaled = masked / temperature[None, :]
+        batch = np.broadcast_to(np.arange(B, dtype=np.int64)[None, :] + dim0_offset, L.shape)
+        g = gumbel(key, (batch, I), vocab_size)
+        score = scaled + g
+    _, tok = max_arrays_axis0([score, I])
+    greedy = I[0]
+    return np.where(temperature < F32(1e-5), greedy, tok).astype(np.int32)
+
+
+def sample(key, logits, top_k_per_row, top_p, temperature, dtype: str = "f32",
+           replace_val: float = -1e12, dim0_offset: int = 0) -> np.ndarray:
+    """sample() (sampling.py:331-343) on one device: exact top-128 (per-row k
+    mask with replace_val in the logits dtype, top_k.py:365-369), then
+    top_p_and_sample with replace_val."""
+    x = np.asarray(logits, dtype=np.float32)
+    vals, idx = top_k(x, NUM_LANES, dtype)
+    kr = np.asarray(top_k_per_row, dtype=np.int64)
+    rv = round_to_dtype(F32(replace_val), dtype)
+    vals = np.where(np.arange(NUM_LANES)[None, :] < kr[:, None], vals, rv)
+    return top_p_and_sample(vals, idx, key, top_p, temperature, x.shape[1], replace_val, dim0_offset)

@@ -1,0 +1,121 @@
+"""ctypes binding of the C-ABI library `libtallax_hip.so` (declared in include/tallax_hip.h).
+
+The product path always goes through this library.  If it is missing, the
+import raises -- there is no CPU fallback.  Device buffers are torch tensors
+(torch-ROCm is the allocator and stream provider only); every call is issued
+on torch's current HIP stream of the tensor's device.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import threading
+
+import torch
+
+_LIB_PATH = pathlib.Path(__file__).resolve().parent / "_build" / "libtallax_hip.so"
+
+F32, BF16, I32 = 0, 1, 2
+_DT = {torch.float32: F32, torch.bfloat16: BF16, torch.int32: I32}
+
+# status codes (include/tallax_hip.h)
+OK, INVALID_ARGUMENT, UNSUPPORTED, HIP_ERROR, WORKSPACE_TOO_SMALL = 0, 1, 2, 3, 4
+
+_c_i64, _c_i32, _c_int, _c_sz, _c_p, _c_d = (
+    ctypes.c_int64, ctypes.c_int32, ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_double)
+
+_SIGNATURES = {
+    "tallax_last_error": ([], ctypes.c_char_p),
+    "tallax_abi_version": ([], _c_int),
+    "tallax_topk_workspace_size": ([_c_i64, _c_i64, _c_i64, _c_int], _c_sz),
+    "tallax_topk": ([_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_sz, _c_p], _c_int),
+    "tallax_sample_workspace_size": ([_c_i64, _c_i64, _c_int], _c_sz),
+    "tallax_fused_topk_topp_sample": (
+        [_c_p, _c_int, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_d, _c_p, _c_p, _c_sz, _c_p], _c_int),
+    "tallax_top_p_and_sample": (
+        [_c_p, _c_int, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_d, _c_i64, _c_p, _c_p], _c_int),
+    # test hooks (include/tallax_hip_testing.h)
+    "tallax_testing_expf_logf": ([_c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
+    "tallax_testing_gumbel": ([ctypes.c_uint32, ctypes.c_uint32, _c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
+}
+
+
+class TallaxError(RuntimeError):
+    """Raised when the HIP library reports a failure."""
+
+
+def _load() -> ctypes.CDLL:
+    if not _LIB_PATH.exists():
+        raise ImportError(
+            f"tallax_amd HIP library not built: {_LIB_PATH} is missing. "
+            "Run `python -c 'import __graft_entry__ as g; g.build()'` (hipcc, gfx950).")
+    lib = ctypes.CDLL(str(_LIB_PATH))
+    for name, (args, res) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    return lib
+
+
+LIB = _load()
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def check(status: int, what: str) -> None:
+    if status == OK:
+        return
+    msg = LIB.tallax_last_error().decode(errors="replace")
+    if status == UNSUPPORTED:
+        raise NotImplementedError(f"{what}: {msg}")
+    if status in (INVALID_ARGUMENT, WORKSPACE_TOO_SMALL):
+        raise ValueError(f"{what}: {msg}")
+    raise TallaxError(f"{what}: {msg} (status {status})")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise NotImplementedError(f"dtype {t.dtype} is not supported (float32, bfloat16, int32)") from None
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# Workspace: one zero-initialised byte buffer per device, grown on demand.
+# The kernels leave their arrival counters at zero when they finish, so the
+# buffer never needs clearing between calls.  Calls that overlap on one
+# device (different streams) must pass their own workspace.
+# ---------------------------------------------------------------------------
+_ws_lock = threading.Lock()
+_ws: dict[int, torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    with _ws_lock:
+        buf = _ws.get(idx)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
+            _ws[idx] = buf
+        return buf
+
+
+def require_cuda(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise ValueError("tallax_amd operands must be torch tensors on a ROCm (cuda) device")
+    if os.environ.get("TALLAX_AMD_STRICT_DEVICE", "1") == "1":
+        devs = {t.device for t in ts}
+        if len(devs) > 1:
+            raise ValueError(f"operands on different devices: {devs}")

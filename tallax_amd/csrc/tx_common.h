@@ -1,0 +1,96 @@
+// Shared device helpers for the tallax MI355X (gfx950) kernels.
+//
+// Everything here is wave64 CDNA4 code: cross-lane traffic uses ds_bpermute /
+// ds_swizzle through the HIP shuffle intrinsics, and no kernel uses MFMA
+// (nothing on the sort / select / sample path is a dense contraction).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tx {
+
+constexpr int kWave = 64;
+
+enum DType : int { kF32 = 0, kBF16 = 1, kI32 = 2 };
+
+// ---------------------------------------------------------------------------
+// Selection keys.
+//
+// A "select key" orders numbers the way the reference's top-k does: values
+// are compared as floats with strict `>` (tallax/_src/top_k.py:64), so -0 and
+// +0 are equal and NaN never wins a comparison.  We map a float's bits to an
+// unsigned 32-bit key that is monotone in value, with +0 == -0, and NaN mapped
+// to 1 (below -inf).  Key 0 is reserved for "no element" (out-of-row slots).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t select_key(uint32_t b) {
+  const uint32_t a = b & 0x7FFFFFFFu;
+  uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  k = (a == 0u) ? 0x80000000u : k;
+  k = (a > 0x7F800000u) ? 1u : k;
+  return k;
+}
+
+// Inverse of select_key for keys of real numbers (keys >= 0x007FFFFF).
+__device__ __forceinline__ uint32_t key_to_bits(uint32_t k) {
+  return (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+}
+
+// Keys at or below this value belong to elements the reference's binned
+// top-k can never select: its bins start at finfo(dtype).min and only admit
+// strictly greater values (top_k.py:241-243, :64).  That excludes -inf, NaN
+// and finfo.min itself.  For f32 the key of -FLT_MAX is 0x00800000; bf16's
+// finfo.min (0xFF7F) widens to 0xFF7F0000 whose key is 0x0080FFFF.
+__device__ __forceinline__ uint32_t ineligible_key_max(int dt) {
+  return dt == kBF16 ? 0x0080FFFFu : 0x00800000u;
+}
+
+// Composite key: value descending, then index ascending, as one u64 so that
+// every element of a row has a distinct key and "larger composite" == "earlier
+// in the lowest-index-tie-break order".
+__device__ __forceinline__ uint64_t make_comp(uint32_t key, uint32_t idx) {
+  return ((uint64_t)key << 32) | (uint64_t)(~idx);
+}
+__device__ __forceinline__ uint32_t comp_key(uint64_t c) { return (uint32_t)(c >> 32); }
+__device__ __forceinline__ int32_t comp_idx(uint64_t c) { return (int32_t)(~(uint32_t)c); }
+
+// ---------------------------------------------------------------------------
+// Wave helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, kWave);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, kWave);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ float shfl_f(float v, int src) { return __shfl(v, src, kWave); }
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+  return v;
+}
+
+// Unaligned-safe 16-byte vector source for a row.  Rows need not start on a
+// 16-byte boundary: we read whole 16-byte blocks starting at the aligned-down
+// address and mask out the elements that fall outside the row.  A 16-byte
+// block that contains at least one byte of the row lies inside the same GPU
+// page as that byte, so these reads never touch an unmapped page.
+template <int ES>
+struct RowVec {
+  const uint4* base;  // aligned-down start
+  int mis;            // number of leading elements of the first block outside the row
+  __device__ __forceinline__ RowVec(const void* row_ptr) {
+    const uintptr_t a = (uintptr_t)row_ptr;
+    base = (const uint4*)(a - (a & 15u));
+    mis = (int)((a & 15u) / ES);
+  }
+};
+
+// Bit reversal of the low `bits` bits of x.
+__device__ __forceinline__ uint32_t bitrev(uint32_t x, int bits) {
+  return __brev(x) >> (32 - bits);
+}
+
+}  // namespace tx

@@ -1,0 +1,32 @@
+// Host-side helpers shared by the C-ABI entry points.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+namespace tx {
+
+enum Status : int {
+  kOk = 0,
+  kInvalidArgument = 1,   // shapes / sizes / pointers the op rejects
+  kUnsupported = 2,       // valid request this build does not implement
+  kHipError = 3,          // the HIP runtime reported an error at launch
+  kWorkspaceTooSmall = 4,
+};
+
+// Thread-local message read back by tallax_last_error().
+void set_error(const char* fmt, ...);
+
+inline int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: HIP launch failed: %s", what, hipGetErrorString(e));
+    return kHipError;
+  }
+  return kOk;
+}
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace tx

@@ -1,0 +1,123 @@
+"""Sampling API (mirror of tallax/_src/sampling.py and tallax/sampling.py).
+
+`sample` is the vLLM-facing hook (sampling.py:331-343): one fused HIP kernel
+does the per-row top-k (clamped to 128, as the reference's max_k=128), the
+top-p filter, temperature and Gumbel-max draw.  `top_p_and_sample`
+(sampling.py:210-269) runs the same tail on candidates the caller already
+selected.
+
+Operands are torch tensors on a ROCm device; the rng key is the two uint32
+words of a threefry key (what `jax.random.key_data(key)` holds), as a device
+tensor of dtype int32/uint32 or a host sequence of two ints.
+"""
+from __future__ import annotations
+
+from typing import Any, Sequence
+
+import torch
+
+from . import _lib
+
+_SAMPLING_EPS = 1e-5  # sampling.py:22
+
+
+def _key_tensor(rng_key: Any, device: torch.device) -> torch.Tensor:
+    if isinstance(rng_key, torch.Tensor):
+        k = rng_key.reshape(-1)
+        if k.numel() != 2:
+            raise ValueError(f"rng_key must hold 2 uint32 words, got {k.numel()}")
+        if k.dtype not in (torch.int32, torch.uint32):
+            raise ValueError(f"rng_key dtype {k.dtype} must be int32 or uint32 key data")
+        return k.to(device=device).view(torch.int32).contiguous()
+    words = [int(w) & 0xFFFFFFFF for w in rng_key]
+    if len(words) != 2:
+        raise ValueError("rng_key must hold 2 uint32 words")
+    words = [w - (1 << 32) if w >= (1 << 31) else w for w in words]
+    return torch.tensor(words, dtype=torch.int32, device=device)
+
+
+def _per_row(v: Any, rows: int, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    t = v if isinstance(v, torch.Tensor) else torch.tensor(v, dtype=dtype)
+    t = t.to(device=device, dtype=dtype)
+    if t.ndim == 0:
+        t = t.expand(rows)
+    if t.shape != (rows,):
+        raise ValueError(f"per-row parameter has shape {tuple(t.shape)}, expected ({rows},)")
+    return t.contiguous()
+
+
+def sample(rng_key: Any, logits: torch.Tensor, tpu_sampling_metadata: Any,
+           *, replace_val: float = -1e12, dim0_offset: int = 0,
+           workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused top-k -> top-p -> temperature -> Gumbel-max sampler.
+
+    Reference: sample(rng_key, logits, tpu_sampling_metadata) (sampling.py:331-343).
+    `tpu_sampling_metadata` exposes `.top_k` (int, per row), `.top_p` and
+    `.temperature` (float, per row).  The per-row k is clamped to 128 as in
+    the reference (max_k=NUM_LANES, sampling.py:283-290).  Returns int32 [rows].
+    """
+    _lib.require_cuda(logits)
+    if logits.ndim != 2:
+        raise ValueError("Only 2D inputs supported")
+    logits = logits.contiguous()
+    rows, vocab = logits.shape
+    dev = logits.device
+    top_k = _per_row(tpu_sampling_metadata.top_k, rows, torch.int32, dev)
+    top_p = _per_row(tpu_sampling_metadata.top_p, rows, torch.float32, dev)
+    temp = _per_row(tpu_sampling_metadata.temperature, rows, torch.float32, dev)
+    key = _key_tensor(rng_key, dev)
+    dt = _lib.dtype_code(logits)
+    if dt == _lib.I32:
+        raise NotImplementedError("sample() needs float logits")
+    out = torch.empty(rows, dtype=torch.int32, device=dev)
+    need = _lib.LIB.tallax_sample_workspace_size(rows, vocab, dt)
+    ws = workspace if workspace is not None else _lib.workspace(dev, need)
+    _lib.check(_lib.LIB.tallax_fused_topk_topp_sample(
+        logits.data_ptr(), dt, rows, vocab, top_k.data_ptr(), top_p.data_ptr(), temp.data_ptr(),
+        key.data_ptr(), int(dim0_offset), float(replace_val), out.data_ptr(),
+        ws.data_ptr() if need else None, ws.numel() if need else 0, _lib.stream_of(logits)),
+        "sample")
+    return out
+
+
+def top_p_and_sample(topk_logits: torch.Tensor, topk_idx: torch.Tensor, rng_key: Any,
+                     top_p: Any, temperature: Any, *, vocab_size: int, replace_val: float,
+                     interpret: bool = False, dim0_offset: int = 0) -> torch.Tensor:
+    """Top-p filter, temperature and Gumbel-max draw over descending candidates.
+
+    Reference: top_p_and_sample (sampling.py:210-269).  topk_logits [B, k]
+    (k <= 128) sorted descending, topk_idx [B, k] int32 vocabulary ids.
+    `interpret` is accepted for signature compatibility and ignored.
+    """
+    del interpret
+    _lib.require_cuda(topk_logits, topk_idx)
+    if topk_logits.ndim != 2 or topk_idx.shape != topk_logits.shape:
+        raise ValueError("topk_logits and topk_idx must be 2D with the same shape")
+    rows, k = topk_logits.shape
+    dev = topk_logits.device
+    logits = topk_logits.contiguous()
+    idx = topk_idx.to(torch.int32).contiguous()
+    tp = _per_row(top_p, rows, torch.float32, dev)
+    tt = _per_row(temperature, rows, torch.float32, dev)
+    key = _key_tensor(rng_key, dev)
+    dt = _lib.dtype_code(logits)
+    if dt == _lib.I32:
+        raise NotImplementedError("top_p_and_sample needs float logits")
+    out = torch.empty(rows, dtype=torch.int32, device=dev)
+    _lib.check(_lib.LIB.tallax_top_p_and_sample(
+        logits.data_ptr(), dt, idx.data_ptr(), rows, k, key.data_ptr(), tp.data_ptr(), tt.data_ptr(),
+        int(vocab_size), float(replace_val), int(dim0_offset), out.data_ptr(), _lib.stream_of(logits)),
+        "top_p_and_sample")
+    return out
+
+
+class SamplingMetadata:
+    """Minimal stand-in for vLLM's TPU sampling metadata (.top_k/.top_p/.temperature)."""
+
+    def __init__(self, top_k: Any, top_p: Any, temperature: Any):
+        self.top_k = top_k
+        self.top_p = top_p
+        self.temperature = temperature
+
+
+__all__: Sequence[str] = ["sample", "top_p_and_sample", "SamplingMetadata"]

@@ -1,0 +1,186 @@
+"""GPU parity: exact top-k, the fused sampler and top_p_and_sample through the
+C ABI, against the oracle on identical seeded inputs (bit-exact values,
+indices and token ids)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tallax_oracle as O
+from tests.gpu_util import bits, from_dev_vals, host_values, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+# --------------------------------------------------------------------------- primitives
+def test_exp_log_bitexact(gpu):
+    from tallax_amd import _lib
+    rng = np.random.default_rng(11)
+    x = np.concatenate([
+        rng.uniform(-110, 95, 200000), rng.uniform(-1, 1, 50000),
+        rng.integers(0, 0x7F800000, 100000).astype(np.uint32).view(np.float32).astype(np.float64),
+        [0.0, -0.0, 1.0, np.inf, -np.inf, np.nan, -1.0, 1e-45, 88.72, -103.97, 2.0**-126]]).astype(np.float32)
+    xd = torch.from_numpy(x).to(gpu)
+    e = torch.empty_like(xd); l = torch.empty_like(xd)
+    _lib.check(_lib.LIB.tallax_testing_expf_logf(xd.data_ptr(), e.data_ptr(), l.data_ptr(), x.size,
+                                                 _lib.stream_of(xd)), "expf_logf")
+    torch.cuda.synchronize()
+    ge, gl = e.cpu().numpy(), l.cpu().numpy()
+    oe, ol = O.exp_f32(x), O.log_f32(x)
+    nan_e = np.isnan(oe); nan_l = np.isnan(ol)
+    assert np.array_equal(np.isnan(ge), nan_e) and np.array_equal(np.isnan(gl), nan_l)
+    assert np.array_equal(bits(ge)[~nan_e], bits(oe)[~nan_e])
+    assert np.array_equal(bits(gl)[~nan_l], bits(ol)[~nan_l])
+
+
+def test_gumbel_bitexact(gpu):
+    from tallax_amd import _lib
+    rng = np.random.default_rng(12)
+    ctr = rng.integers(0, 2**32, 300000, dtype=np.uint64).astype(np.uint32)
+    cd = torch.from_numpy(ctr.view(np.int32)).to(gpu)
+    g = torch.empty(ctr.size, dtype=torch.float32, device=gpu)
+    b = torch.empty(ctr.size, dtype=torch.int32, device=gpu)
+    _lib.check(_lib.LIB.tallax_testing_gumbel(0x12345678, 0x9abcdef0, cd.data_ptr(), g.data_ptr(),
+                                              b.data_ptr(), ctr.size, _lib.stream_of(cd)), "gumbel")
+    torch.cuda.synchronize()
+    o0, o1 = O.threefry2x32(0x12345678, 0x9abcdef0, np.zeros_like(ctr), ctr)
+    assert np.array_equal(b.cpu().numpy().view(np.uint32), o0 ^ o1)
+    og = -O.log_f32(-O.log_f32(O.sparse_random_uniform((0x12345678, 0x9abcdef0), (np.zeros(ctr.size, np.int64), ctr.astype(np.int64)), 1, minval=O.TINY)))
+    # counter here is 0 * 1 + ctr
+    assert np.array_equal(bits(g.cpu().numpy()), bits(og))
+
+
+# --------------------------------------------------------------------------- top-k
+TOPK_CASES = [
+    # rows, cols, k, dtype, kind
+    (8, 32768, 64, "f32", "normal"),        # config 1
+    (13, 167, 5, "f32", "normal"),          # ragged, misaligned rows
+    (3, 1000, 100, "bf16", "normal"),
+    (16, 4097, 64, "f32", "ints"),          # heavy ties
+    (4, 128, 128, "f32", "normal"),         # k == cols
+    (5, 300, 128, "bf16", "ints"),
+    (2, 5000, 17, "f32", "const"),          # every value equal: exact bisection path
+    (6, 20000, 50, "f32", "special"),       # NaN / -inf / -0 / finfo.min
+    (7, 70001, 128, "bf16", "normal"),      # odd length bf16 (misaligned rows)
+    (32, 201088, 64, "bf16", "normal"),     # the reference's own top-k benchmark shape
+]
+
+
+def _make(rows, cols, kind, seed):
+    rng = np.random.default_rng(seed)
+    if kind == "normal":
+        return rng.standard_normal((rows, cols)).astype(np.float32)
+    if kind == "ints":
+        return rng.integers(-6, 7, (rows, cols)).astype(np.float32)
+    if kind == "const":
+        return np.full((rows, cols), 1.5, np.float32)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    u = rng.random((rows, cols))
+    x[u < 0.05] = np.nan
+    x[(u >= 0.05) & (u < 0.1)] = -np.inf
+    x[(u >= 0.1) & (u < 0.2)] = -0.0
+    x[(u >= 0.2) & (u < 0.22)] = np.finfo(np.float32).min
+    x[0, :] = np.nan   # a row with no eligible value at all
+    x[1, : cols // 2] = 0.0
+    return x
+
+
+@pytest.mark.parametrize("rows,cols,k,dtype,kind", TOPK_CASES)
+def test_topk_parity(gpu, rows, cols, k, dtype, kind):
+    from tallax_amd import tax
+    _log(f"top_k rows={rows} cols={cols} k={k} dtype={dtype} kind={kind}")
+    x = _make(rows, cols, kind, seed=rows * 7919 + cols)
+    xv = host_values(x, dtype)
+    vals, idx = tax.top_k(to_dev(x, dtype, gpu), k)
+    torch.cuda.synchronize()
+    ov, oi = O.top_k(xv, k, dtype)
+    gi = idx.cpu().numpy()
+    gv = from_dev_vals(vals)
+    assert np.array_equal(gi, oi)
+    assert np.array_equal(bits(gv), bits(ov))
+
+
+def test_topk_config3_spikes(gpu):
+    """Config 3: f32 [128, 151936], N(0, sigma=2) plus 32 spikes per row at
+    exactly 8.0 (32-way ties inside the top-50), k=50."""
+    from tallax_amd import tax
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((128, 151936)) * 2).astype(np.float32)
+    for r in range(128):
+        x[r, rng.choice(151936, 32, replace=False)] = 8.0
+    vals, idx = tax.top_k(to_dev(x, "f32", gpu), 50)
+    torch.cuda.synchronize()
+    ov, oi = O.top_k(x, 50)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(bits(vals.cpu().numpy()), bits(ov))
+
+
+def test_topk_repeated_calls_reuse_workspace(gpu):
+    from tallax_amd import tax
+    rng = np.random.default_rng(5)
+    for i, (rows, cols) in enumerate([(64, 50000), (8, 100000), (64, 50000)]):
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        v, ix = tax.top_k(to_dev(x, "f32", gpu), 128)
+        torch.cuda.synchronize()
+        assert np.array_equal(ix.cpu().numpy(), O.top_k(x, 128)[1]), i
+
+
+# --------------------------------------------------------------------------- sampler
+def _sampler_inputs(rows, vocab, seed, sigma=3.0):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, vocab)) * sigma).astype(np.float32)
+    temp = rng.uniform(0.5, 1.5, rows).astype(np.float32)
+    topk = rng.integers(1, 1025, rows).astype(np.int32)
+    topp = rng.uniform(0.7, 1.0, rows).astype(np.float32)
+    return x, temp, topk, topp
+
+
+@pytest.mark.parametrize("rows,vocab,dtype", [(256, 128256, "bf16"), (64, 32000, "f32"),
+                                              (16, 4096, "bf16"), (8, 131, "f32")])
+def test_fused_sampler_parity(gpu, rows, vocab, dtype):
+    from tallax_amd import sampling
+    _log(f"sample rows={rows} vocab={vocab} dtype={dtype}")
+    x, temp, topk, topp = _sampler_inputs(rows, vocab, seed=vocab + rows)
+    temp[::17] = 1e-6      # greedy rows
+    topk[1::13] = 1        # top-1 rows
+    topp[2::11] = 0.9999999
+    key = (0, 1234)
+    meta = sampling.SamplingMetadata(torch.from_numpy(topk), torch.from_numpy(topp), torch.from_numpy(temp))
+    tok = sampling.sample(key, to_dev(x, dtype, gpu), meta)
+    torch.cuda.synchronize()
+    want = O.sample(key, host_values(x, dtype), topk, topp, temp, dtype=dtype)
+    assert np.array_equal(tok.cpu().numpy(), want)
+
+
+def test_fused_sampler_dim0_offset_and_key(gpu):
+    from tallax_amd import sampling
+    x, temp, topk, topp = _sampler_inputs(32, 50000, seed=9)
+    meta = sampling.SamplingMetadata(torch.from_numpy(topk), torch.from_numpy(topp), torch.from_numpy(temp))
+    for key, off in [((0, 7), 0), ((0xDEADBEEF, 0x01234567), 96)]:
+        tok = sampling.sample(key, to_dev(x, "f32", gpu), meta, dim0_offset=off)
+        torch.cuda.synchronize()
+        want = O.sample(key, x, topk, topp, temp, dtype="f32", dim0_offset=off)
+        assert np.array_equal(tok.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("k,dtype", [(128, "f32"), (128, "bf16"), (64, "f32"), (50, "f32"), (8, "bf16"), (1, "f32")])
+def test_top_p_and_sample_parity(gpu, k, dtype):
+    from tallax_amd import sampling
+    rng = np.random.default_rng(100 + k)
+    B = 300
+    L = -np.sort(-(rng.standard_normal((B, k)) * 2).astype(np.float32), axis=1)
+    L = host_values(L, dtype)
+    L = -np.sort(-L, axis=1)
+    I = rng.integers(0, 50000, (B, k)).astype(np.int32)
+    tp = rng.uniform(0.5, 1.0, B).astype(np.float32)
+    tt = rng.uniform(0.3, 2.0, B).astype(np.float32)
+    key = (3, 4)
+    tok = sampling.top_p_and_sample(to_dev(L, dtype, gpu), torch.from_numpy(I).to(gpu), key,
+                                    torch.from_numpy(tp), torch.from_numpy(tt), vocab_size=50000,
+                                    replace_val=-1e12)
+    torch.cuda.synchronize()
+    want = O.top_p_and_sample(L, I, key, tp, tt, 50000, -1e12)
+    assert np.array_equal(tok.cpu().numpy(), want)

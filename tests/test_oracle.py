@@ -1,0 +1,271 @@
+"""Pins the CPU oracle (oracle/tallax_oracle.py) before it is trusted as the
+GPU checker: known-answer vectors, an independent implementation (rocRAND),
+float64 numpy, closed forms, brute force and statistics."""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import tallax_oracle as O
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+# --------------------------------------------------------------------------- threefry
+def test_threefry_known_answers():
+    with open(os.path.join(HERE, "golden", "threefry_kat.json")) as f:
+        kat = json.load(f)["vectors"]
+    for v in kat:
+        k0, k1 = (int(x, 16) for x in v["key"])
+        c0, c1 = (int(x, 16) for x in v["counter"])
+        o0, o1 = O.threefry2x32(k0, k1, c0, c1)
+        assert (int(o0), int(o1)) == tuple(int(x, 16) for x in v["out"])
+
+
+@pytest.mark.skipif(shutil.which("/opt/rocm/bin/hipcc") is None, reason="hipcc absent")
+def test_threefry_matches_rocrand(tmp_path):
+    exe = tmp_path / "tf"
+    subprocess.run(["/opt/rocm/bin/hipcc", "-O1", os.path.join(HERE, "golden", "rocrand_threefry_check.cpp"),
+                    "-o", str(exe)], check=True, capture_output=True)
+    rng = np.random.default_rng(7)
+    q = rng.integers(0, 2**32, size=(2000, 4), dtype=np.uint64).astype(np.uint32)
+    inp = "\n".join(" ".join(f"{int(v):08x}" for v in row) for row in q) + "\n"
+    out = subprocess.run([str(exe)], input=inp, capture_output=True, text=True, check=True).stdout.split()
+    ref = np.array([int(x, 16) for x in out], dtype=np.uint64).reshape(-1, 2).astype(np.uint32)
+    mine = np.stack([np.array([int(a) for a in O.threefry2x32(r[0], r[1], r[2], r[3])]) for r in q[:200]])
+    assert np.array_equal(mine, ref[:200])
+    # vectorised path over the remaining rows (one key per call)
+    for r, exp in zip(q[200:400], ref[200:400]):
+        o0, o1 = O.threefry2x32(r[0], r[1], np.array([r[2]]), np.array([r[3]]))
+        assert (int(o0[0]), int(o1[0])) == (int(exp[0]), int(exp[1]))
+
+
+def test_bits_to_uniform_closed_form():
+    b = np.array([0, 0x1FF, 0x200, 0xFFFFFFFF, 0x80000000], dtype=np.uint32)
+    u = O.bits_to_uniform(b)
+    assert u[0] == 0.0 and u[1] == 0.0
+    assert u[2] == np.float32(2.0**-23)
+    assert u[3] == np.float32(1 - 2.0**-23)
+    assert u[4] == np.float32(0.5)
+    # u = max(tiny, f + tiny): f == 0 -> tiny, otherwise f itself (tiny is far below f's ulp)
+    g = O.sparse_random_uniform((0, 1), (np.zeros(1000, np.int64), np.arange(1000)), 1000,
+                                minval=O.TINY, maxval=1.0)
+    f = O.bits_to_uniform(np.bitwise_xor(*O.threefry2x32(0, 1, np.zeros(1000, np.uint32),
+                                                        np.arange(1000, dtype=np.uint32))))
+    assert np.array_equal(g, np.where(f == 0, np.float32(O.TINY), f))
+
+
+def test_sparse_counter_layout():
+    # counter = row * dim1_size + col (sparse_random.py:49-50), hi word 0
+    key = (0, 42)
+    rows = np.array([0, 3, 7]); cols = np.array([5, 0, 255])
+    u = O.sparse_random_uniform(key, (rows, cols), 256)
+    o0, o1 = O.threefry2x32(0, 42, np.zeros(3, np.uint32), (rows * 256 + cols).astype(np.uint32))
+    assert np.array_equal(u, O.bits_to_uniform(o0 ^ o1))
+
+
+# --------------------------------------------------------------------------- exp / log
+def _ulp_err(got, want64):
+    want = want64.astype(np.float32)
+    ok = np.isfinite(want) & (want != 0)
+    sp = np.spacing(np.abs(want[ok])).astype(np.float64)
+    return np.abs(got[ok].astype(np.float64) - want64[ok]) / sp
+
+
+def test_exp_accuracy_and_specials():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.uniform(-103.9, 88.7, 400000), rng.uniform(-1, 1, 100000),
+                        rng.uniform(-30, 0, 100000)]).astype(np.float32)
+    e = O.exp_f32(x)
+    err = _ulp_err(e, np.exp(x.astype(np.float64)))
+    assert err.max() <= 1.0, err.max()
+    assert O.exp_f32(np.float32(0)) == 1.0
+    assert O.exp_f32(np.float32(-np.inf)) == 0.0
+    assert O.exp_f32(np.float32(np.inf)) == np.inf
+    assert O.exp_f32(np.float32(89.0)) == np.inf
+    assert O.exp_f32(np.float32(-104.0)) == 0.0
+    assert np.isnan(O.exp_f32(np.float32(np.nan)))
+    # subnormal results: within one subnormal step of the float64 value
+    xs = np.linspace(-103.0, -87.5, 5000).astype(np.float32)
+    es = O.exp_f32(xs).astype(np.float64)
+    assert np.max(np.abs(es - np.exp(xs.astype(np.float64)))) <= 2.0**-149
+
+
+def test_log_accuracy_and_specials():
+    rng = np.random.default_rng(2)
+    bits = rng.integers(1, 0x7F800000, 500000, dtype=np.uint64).astype(np.uint32)  # all positive finite
+    x = np.concatenate([bits.view(np.float32), rng.uniform(0.5, 2.0, 200000).astype(np.float32),
+                        rng.uniform(0, 1, 200000).astype(np.float32)])
+    x = x[x > 0]
+    l = O.log_f32(x)
+    err = _ulp_err(l, np.log(x.astype(np.float64)))
+    assert err.max() <= 1.0, err.max()
+    assert O.log_f32(np.float32(1.0)) == 0.0
+    assert O.log_f32(np.float32(0.0)) == -np.inf
+    assert O.log_f32(np.float32(np.inf)) == np.inf
+    assert np.isnan(O.log_f32(np.float32(-1.0)))
+    for k in range(-149, 128, 7):
+        v = np.float32(2.0**k)
+        assert O.log_f32(v) == np.float32(k * np.log(2.0))
+
+
+# --------------------------------------------------------------------------- max_arrays tie rule
+def _bitrev(p, bits):
+    return int(format(p, f"0{bits}b")[::-1], 2)
+
+
+@pytest.mark.parametrize("n", [8, 16, 50, 64, 128])
+def test_max_arrays_tie_rule_is_bit_reversed_position(n):
+    """The literal tournament of max_arrays (bitonic_top_k.py:43-97) keeps, among
+    tied maxima, the position with the largest bit-reversed index over
+    log2(padded n) bits; without ties it is the plain argmax.  The HIP sampler
+    implements the bit-reversal rule directly."""
+    rng = np.random.default_rng(n)
+    P = max(2 ** int(np.ceil(np.log2(n))), 8)
+    bits = int(np.log2(P))
+    scores = rng.integers(0, 4, size=(n, 3000)).astype(np.float32)
+    pos = np.broadcast_to(np.arange(n, dtype=np.int32)[:, None], scores.shape)
+    _, win = O.max_arrays_axis0([scores, pos])
+    for b in range(scores.shape[1]):
+        m = scores[:, b].max()
+        cands = [p for p in range(n) if scores[p, b] == m]
+        assert win[b] == max(cands, key=lambda p: _bitrev(p, bits))
+    uniq = rng.standard_normal((n, 500)).astype(np.float32)
+    _, win = O.max_arrays_axis0([uniq, np.broadcast_to(np.arange(n, dtype=np.int32)[:, None], uniq.shape)])
+    assert np.array_equal(win, uniq.argmax(0))
+
+
+# --------------------------------------------------------------------------- top-k
+def _brute_topk(row, k, dmin):
+    keyed = []
+    for i, v in enumerate(row):
+        if np.isnan(v):
+            rank_v = -np.inf; nan = True
+        else:
+            rank_v = float(v); nan = False
+        keyed.append((0 if nan else 1, 0.0 if v == 0 else rank_v, -i))
+    order = sorted(range(len(row)), key=lambda i: keyed[i], reverse=True)[:k]
+    vals = np.array([row[i] for i in order], dtype=np.float32)
+    elig = np.array([(not np.isnan(v)) and v > dmin for v in vals])
+    vals[~elig] = dmin
+    return vals, np.array(order, dtype=np.int32)
+
+
+def test_topk_oracle_brute_force_with_ties_nan_inf():
+    rng = np.random.default_rng(3)
+    for trial in range(60):
+        n = int(rng.integers(1, 40)); k = int(rng.integers(1, n + 1))
+        row = rng.integers(-3, 4, n).astype(np.float32)
+        special = rng.random(n)
+        row[special < 0.1] = np.nan
+        row[(special >= 0.1) & (special < 0.2)] = -np.inf
+        row[(special >= 0.2) & (special < 0.3)] = -0.0
+        row[(special >= 0.3) & (special < 0.35)] = np.float32(np.finfo(np.float32).min)
+        v, i = O.top_k(row[None], k)
+        bv, bi = _brute_topk(row, k, O.F32_MIN)
+        assert np.array_equal(i[0], bi), (row, k)
+        assert np.array_equal(v[0].view(np.uint32), bv.view(np.uint32))
+
+
+def test_topk_oracle_matches_stable_sort_closed_form():
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((16, 3000)) * 4).round().astype(np.float32)  # heavy ties
+    v, i = O.top_k(x, 100)
+    ref_i = np.argsort(-x, axis=1, kind="stable")[:, :100]
+    assert np.array_equal(i, ref_i)
+    assert np.array_equal(v, np.take_along_axis(x, ref_i, 1))
+
+
+# --------------------------------------------------------------------------- cumsum
+@pytest.mark.parametrize("shape", [(8, 128), (16, 256), (128, 8), (256, 16), (13, 167)])
+@pytest.mark.parametrize("axis", [0, 1])
+@pytest.mark.parametrize("reverse", [False, True])
+def test_cumsum_oracle(shape, axis, reverse):
+    """tests/cumsum_test.py of the reference: float within rtol 1e-3/atol 1e-6
+    of lax.cumsum, int exact.  Here against float64/int64 numpy."""
+    rng = np.random.default_rng(42)
+    xf = rng.standard_normal(shape).astype(np.float32)
+    xi = rng.integers(0, 100, shape).astype(np.int32)
+    def ref(a):
+        a = np.flip(a, axis) if reverse else a
+        r = np.cumsum(a.astype(np.float64 if a.dtype.kind == "f" else np.int64), axis=axis)
+        return np.flip(r, axis) if reverse else r
+    got = O.cumsum(xf, axis, reverse)
+    assert got.dtype == np.float32
+    np.testing.assert_allclose(got, ref(xf), rtol=1e-5, atol=1e-5)
+    assert np.array_equal(O.cumsum(xi, axis, reverse), ref(xi).astype(np.int32))
+
+
+def test_cumsum_tile_sum_is_pairwise_tree():
+    rng = np.random.default_rng(5)
+    t = rng.standard_normal((8, 128)).astype(np.float32)
+    hs = O._hs_scan(t, 1)
+    x = t.copy()
+    while x.shape[1] > 1:  # adjacent pairs, then pairs of pairs
+        x = x[:, 0::2] + x[:, 1::2]
+    assert np.array_equal(hs[:, -1], x[:, 0])
+
+
+# --------------------------------------------------------------------------- top-p and sampling
+def test_top_p_mask_invariants():
+    rng = np.random.default_rng(6)
+    L = -np.sort(-rng.standard_normal((64, 300)).astype(np.float32) * 2, axis=0)
+    p = rng.uniform(0.05, 0.99, 300).astype(np.float32)
+    m = O.top_p_mask(L, p, -1e12)
+    kept = m > -1e11
+    assert kept[0].all()                                   # the top candidate always survives
+    assert np.all(np.diff(kept.astype(int), axis=0) <= 0)  # kept set is a prefix
+    # float64 restatement: kept count = (#cumsum < p) + 1 (+ ties), away from rounding edges
+    pr = np.exp(L.astype(np.float64) - L[0]); pr /= pr.sum(0)
+    cum = np.cumsum(pr, 0)
+    t = (cum < p).sum(0)
+    thr = L[np.minimum(t, 63), np.arange(300)]
+    want = (L >= thr).sum(0)
+    close = np.abs(cum - p).min(0) < 1e-5
+    assert np.array_equal(kept.sum(0)[~close], want[~close])
+    # p tiny keeps exactly the ties of the maximum
+    m0 = O.top_p_mask(L, np.full(300, 1e-9, np.float32), -1e12)
+    assert np.array_equal((m0 > -1e11).sum(0), (L == L[0]).sum(0))
+
+
+def test_sampler_greedy_and_k1():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((32, 4096)).astype(np.float32) * 3
+    argmax = np.argsort(-x, axis=1, kind="stable")[:, 0]
+    t = O.sample((0, 1), x, np.full(32, 50), np.full(32, 0.9, np.float32), np.full(32, 1e-6, np.float32))
+    assert np.array_equal(t, argmax)
+    t = O.sample((0, 1), x, np.full(32, 1), np.full(32, 0.9, np.float32), np.full(32, 1.0, np.float32))
+    assert np.array_equal(t, argmax)
+
+
+def test_sampler_distribution_is_softmax_of_filtered_logits():
+    """Gumbel-max over the kept candidates draws token j with probability
+    softmax(logits/T)[j] (chi-square, 20000 independent rows)."""
+    B = 20000
+    logits = np.array([2.0, 1.5, 1.0, 0.5, 0.0, -0.5, -1.0, -3.0], dtype=np.float32)
+    L = np.broadcast_to(logits, (B, 8))
+    I = np.broadcast_to(np.arange(8, dtype=np.int32) * 3, (B, 8))
+    T = np.full(B, 0.7, np.float32)
+    p = np.full(B, 0.95, np.float32)
+    tok = O.top_p_and_sample(L, I, (0, 99), p, T, vocab_size=24, replace_val=-1e12)
+    pr = np.exp(logits.astype(np.float64) - 2); pr /= pr.sum()
+    cut = int((np.cumsum(pr) < 0.95).sum())
+    kept = logits >= logits[cut]
+    q = np.exp(np.where(kept, logits / 0.7, -np.inf) - 2 / 0.7); q /= q.sum()
+    counts = np.bincount(tok // 3, minlength=8)
+    assert counts[~kept].sum() == 0
+    exp_c = q[kept] * B
+    chi2 = ((counts[kept] - exp_c) ** 2 / exp_c).sum()
+    assert chi2 < 30.0, (counts, exp_c)  # dof <= 7, p ~ 1e-4
+
+
+def test_sampler_replace_and_quirk_threshold_zero():
+    # k-mask replaces positions >= k with replace_val in the logits dtype
+    assert O.round_to_dtype(np.float32(-1e12), "bf16").view(np.uint32) == 0xD3690000
+    # top-p with cumsum never reaching p: threshold gathers 0 (out-of-range take)
+    L = np.array([[3.0], [2.0], [1.0], [-1.0]], dtype=np.float32)
+    m = O.top_p_mask(L, np.array([1.5], np.float32), -1e12)
+    assert np.array_equal(m[:, 0], np.array([3.0, 2.0, 1.0, -1e12], np.float32))
