@@ -1,0 +1,119 @@
+// Sampler tail: top-p filter, temperature and Gumbel-max draw over one row's
+// descending candidates, executed by one wave64.
+#pragma once
+#include <float.h>
+#include <math.h>
+
+#include "tx_common.h"
+#include "tx_math.h"
+
+namespace tx {
+
+// ---------------------------------------------------------------------------
+// Sampler tail on one row's sorted candidates, executed by one wave.
+// v[h], id[h]: f32 value and token index at position p = h*64 + lane, for
+// positions p < K (K <= 128).  Restates top_p_and_sample_arrays
+// (sampling.py:65-115), top_p_mask (sampling.py:25-62), the (8,128)-tile
+// cumsum order (cumsum.py:21-53) and max_arrays' tie rule
+// (bitonic_top_k.py:43-97).
+// ---------------------------------------------------------------------------
+__device__ __noinline__ int32_t sample_tail(const float v_in[2], const int32_t id_in[2], int K, float top_p,
+                               float temp, uint32_t k0, uint32_t k1, uint32_t row_ctr,
+                               uint32_t vocab, float mask_val) {
+#pragma clang fp contract(off)
+  const int l = lane_id();
+  const bool in[2] = {l < K, l + kWave < K};
+  float v[2] = {v_in[0], v_in[1]};
+  int32_t id[2] = {id_in[0], id_in[1]};
+
+  // softmax numerators exp(l - l[0]) and their total, summed as a
+  // stride-halving tree over 128 zero-padded slots.
+  const float l0 = shfl_f(v[0], 0);
+  float e[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) e[h] = in[h] ? tx_expf(v[h] - l0) : 0.0f;
+  float s = e[0] + e[1];
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) s = s + __shfl_xor(s, d, kWave);
+
+  // inclusive cumsum of probs along the candidate axis: Hillis-Steele inside
+  // 8-slot tiles, then the running total of earlier tiles added sequentially.
+  float c[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) c[h] = e[h] / s;
+#pragma unroll
+  for (int sh = 1; sh < 8; sh <<= 1) {
+    const bool ok = (l & 7) >= sh;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float u = __shfl_up(c[h], sh, kWave);
+      c[h] = c[h] + (ok ? u : 0.0f);
+    }
+  }
+  const int tile0 = l >> 3;  // tile of register 0; register 1 is tile0 + 8
+  float carry0 = 0.0f, carry1 = 0.0f;
+  float run = __shfl(c[0], 7, kWave);
+#pragma unroll
+  for (int g = 1; g < 16; ++g) {
+    if (tile0 == g) carry0 = run;
+    if (tile0 + 8 == g) carry1 = run;
+    const float tsg = __shfl(g < 8 ? c[0] : c[1], (g & 7) * 8 + 7, kWave);
+    run = run + tsg;
+  }
+  if (tile0 != 0) c[0] = c[0] + carry0;
+  c[1] = c[1] + carry1;
+
+  // threshold index t = #(cumsum < p); threshold value l[t] (0 when t == K,
+  // the out-of-range gather of take_along_axis_arrays).
+  const int t = __popcll(__ballot(in[0] && c[0] < top_p)) + __popcll(__ballot(in[1] && c[1] < top_p));
+  const float vt = __shfl(t < kWave ? v[0] : v[1], t & (kWave - 1), kWave);
+  const float thr = t < K ? vt : 0.0f;
+
+  // mask, temperature, Gumbel noise, argmax
+  int P = 8;
+  while (P < K) P <<= 1;
+  int pbits = 0;
+  while ((1 << pbits) < P) ++pbits;
+  float best_s = 0.0f;
+  uint32_t best_b = 0;
+  int32_t best_i = 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int p = h * kWave + l;
+    float sc;
+    int32_t tok = id[h];
+    if (in[h]) {
+      const float masked = v[h] >= thr ? v[h] : mask_val;
+      const float scaled = masked / temp;
+      uint32_t o0, o1;
+      threefry2x32(k0, k1, 0u, row_ctr * vocab + (uint32_t)id[h], o0, o1);
+      sc = scaled + gumbel_from_bits(o0 ^ o1);
+    } else if (p < P) {
+      sc = -FLT_MAX;  // max_arrays pads with finfo.min and iinfo.min payloads
+      tok = INT32_MIN;
+    } else {
+      sc = -INFINITY;
+    }
+    const uint32_t br = p < P ? bitrev((uint32_t)p, pbits) : 0u;
+    if (h == 0 || sc > best_s || (sc == best_s && br > best_b)) {
+      best_s = sc;
+      best_b = br;
+      best_i = tok;
+    }
+  }
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) {
+    const float os = __shfl_xor(best_s, d, kWave);
+    const uint32_t ob = (uint32_t)__shfl_xor((int)best_b, d, kWave);
+    const int32_t oi = __shfl_xor(best_i, d, kWave);
+    if (os > best_s || (os == best_s && ob > best_b)) {
+      best_s = os;
+      best_b = ob;
+      best_i = oi;
+    }
+  }
+  const int32_t greedy = __shfl(id[0], 0, kWave);
+  return temp < 1e-5f ? greedy : best_i;
+}
+
+}  // namespace tx
