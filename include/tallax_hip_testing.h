@@ -27,6 +27,11 @@ int tallax_testing_expf_logf(const float* x, float* exp_out, float* log_out, int
 int tallax_testing_gumbel(uint32_t k0, uint32_t k1, const uint32_t* counters, float* gumbel_out,
                           uint32_t* bits_out, int64_t n, tallax_stream_t stream);
 
+/* out[64 * d + lane] = value of lane (lane ^ 2^d) for d = 0..5 and
+ * out[384 + lane] = value of lane (63 - lane), as seen through the wave64
+ * lane-exchange helpers of the kernels (DPP / v_permlane*_swap); out holds 448 words. */
+int tallax_testing_lane_ops(uint32_t* out, tallax_stream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -38,6 +38,7 @@ _SIGNATURES = {
     # test hooks (include/tallax_hip_testing.h)
     "tallax_testing_expf_logf": ([_c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
     "tallax_testing_gumbel": ([ctypes.c_uint32, ctypes.c_uint32, _c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
+    "tallax_testing_lane_ops": ([_c_p, _c_p], _c_int),
 }
 
 

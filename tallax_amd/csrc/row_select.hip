@@ -21,11 +21,13 @@
 //       over the 4 waves of their ceil(k/4)-th largest maximum, so at least k
 //       elements are >= L;
 //     - elements passing the current filter become candidates (u64 composite
-//       key << 32 | ~index) in an LDS buffer; once it holds more than 512 the
-//       buffer is cut to its exact top-k and the filter tightens to
+//       key << 32 | ~index), appended by wave-level stream compaction
+//       (ballot + mbcnt) to a per-wave LDS region of 256 slots;
+//     - after tile 0, and whenever a wave region holds more than 128, the
+//       candidates are cut to their exact top-k and the filter tightens to
 //       "key > key of the k-th" (later elements have larger indices, so an
 //       equal key can no longer win a tie);
-//     - a tile with more than 512 candidates (heavy ties) contributes its
+//     - a tile that would overflow a region (heavy ties) contributes its
 //       exact top-k instead, found by bisection on the composite key.
 //   Selection sorts 128-element runs with a wave64 bitonic network and merges
 //   runs with bitonic merge-and-discard (tx_wave_sort.h).
@@ -35,6 +37,7 @@
 //   device-scope fence (an L2 write-back on gfx950) is ever issued.
 #include <float.h>
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "tallax_hip.h"
@@ -48,14 +51,12 @@ namespace tx {
 
 constexpr int kNT = 256;                   // threads per workgroup: 4 wave64s
 constexpr int kWaves = kNT / kWave;
-constexpr int kCap = 1024;                 // LDS candidate slots
-constexpr int kTileCap = 512;              // candidates one tile may add directly
-constexpr int kRefresh = kCap - kTileCap;  // cut the buffer to top-k above this
+constexpr int kCap = 1024;                 // LDS candidate slots (4 wave regions)
 constexpr int kMaxK = 128;                 // the reference's limit (top_k.py:438-439)
 constexpr int kRun = 128;                  // list length handed between kernels
 constexpr int kMaxSeg = 16;
 constexpr int kTargetBlocks = 1024;        // ~4 workgroups per CU on 256 CUs
-constexpr int kVF32 = 8;                   // 16-byte vectors per thread per tile
+constexpr int kVF32 = 4;                   // 16-byte vectors per thread per tile
 constexpr int kVBF16 = 4;
 
 struct SelArgs {
@@ -78,6 +79,9 @@ struct SelArgs {
   float replace_in_dtype;  // replace_val rounded to the logits dtype
   float replace_f32;       // replace_val rounded to float32
   int32_t* out_tokens;
+  // selection policy
+  int refresh_at;
+  int early_cut;
 };
 
 template <int DT>
@@ -113,13 +117,90 @@ struct ElemT<kBF16> {
   static constexpr uint32_t kMinBits = 0xff7f0000u;  // finfo(bfloat16).min, widened
 };
 
+constexpr int kWaveCap = kCap / kWaves;    // candidate slots per wave
+// Tunables (read once from the environment by the host; defaults in Tuning):
+//   TALLAX_SEL_REFRESH       cut the candidates to top-k once a wave region holds
+//                            more than this many (default 3/4 of its 256 slots);
+//   TALLAX_SEL_EARLY_CUT     1: also cut right after the first tile;
+//   TALLAX_SEL_BLOCKS        workgroups aimed for per launch (default 1024).
+
+// ---------------------------------------------------------------------------
+// Per-dtype selection traits.
+//
+// Canonical keys order values the way select_key does (-0 == +0, NaN lowest).
+// Raw keys, used only by the streaming filter, skip the canonicalisation:
+// raw(x) = bits ^ (sign ? all-ones : sign-bit) is monotone in value except
+// that -0 sits one below +0 and positive NaNs sit above +inf; raw_thr()
+// turns a canonical threshold into a raw one that passes every element the
+// canonical one does (positive NaNs become harmless extra candidates).
+//
+// bf16: canonical keys are 16 bits and a segment has < 65536 elements, so a
+// candidate composite is one u32: key << 16 | (0xFFFF - segment-local index).
+// f32: composite = canonical key << 32 | ~row index (u64).
+// ---------------------------------------------------------------------------
+template <int DT>
+struct Sel;
+
+template <>
+struct Sel<kBF16> {
+  using Comp = uint32_t;
+  static constexpr int kV = kVBF16;
+  static constexpr int kMaxTilesPerSeg = 7;  // 7 * 256 * 4 * 8 = 57344 < 65536 elements
+  static constexpr uint32_t kRawPosInf = 0xFF80u;
+  __device__ static __forceinline__ uint32_t canon(uint32_t h) {  // h: bf16 bits
+    const uint32_t a = h & 0x7FFFu;
+    uint32_t k = (h & 0x8000u) ? (~h & 0xFFFFu) : (h | 0x8000u);
+    k = a == 0u ? 0x8000u : k;
+    k = a > 0x7F80u ? 0u : k;
+    return k;
+  }
+  __device__ static __forceinline__ Comp comp(uint32_t h, uint32_t lidx) {
+    return (canon(h) << 16) | (0xFFFFu - lidx);
+  }
+  __device__ static __forceinline__ uint32_t comp_key(Comp c) { return c >> 16; }
+  // canonical key of a raw filter key (positive-NaN raw keys are handled by the caller)
+  __device__ static __forceinline__ uint32_t raw_to_canon(uint32_t r) {
+    return r == 0x7FFFu ? 0x8000u : (r < 0x007Fu ? 0u : r);
+  }
+  __device__ static __forceinline__ uint32_t raw_thr(uint32_t thr) {  // thr >= 1
+    return thr == 0x8000u ? 0x7FFFu : thr;
+  }
+  __device__ static __forceinline__ uint64_t to_global(Comp c, int64_t seg_e0) {
+    if (c == 0u) return 0ull;
+    const uint32_t k16 = c >> 16;
+    const uint32_t key = k16 == 0u ? 1u : (k16 >= 0x8000u ? (k16 << 16) : ((k16 << 16) | 0xFFFFu));
+    return make_comp(key, (uint32_t)(seg_e0 + (int64_t)(0xFFFFu - (c & 0xFFFFu))));
+  }
+};
+
+template <>
+struct Sel<kF32> {
+  using Comp = uint64_t;
+  static constexpr int kV = kVF32;
+  static constexpr int kMaxTilesPerSeg = 1 << 20;
+  static constexpr uint32_t kRawPosInf = 0xFF800000u;
+  __device__ static __forceinline__ uint32_t canon(uint32_t b) { return select_key(b); }
+  __device__ static __forceinline__ Comp comp(uint32_t b, uint32_t gidx) { return make_comp(select_key(b), gidx); }
+  __device__ static __forceinline__ uint32_t comp_key(Comp c) { return (uint32_t)(c >> 32); }
+  __device__ static __forceinline__ uint32_t raw_to_canon(uint32_t r) {
+    return r == 0x7FFFFFFFu ? 0x80000000u : (r < 0x007FFFFFu ? 1u : r);
+  }
+  __device__ static __forceinline__ uint32_t raw_thr(uint32_t thr) {
+    return thr <= 1u ? 0u : (thr == 0x80000000u ? 0x7FFFFFFFu : thr);
+  }
+  __device__ static __forceinline__ uint64_t to_global(Comp c, int64_t) { return c; }
+};
+
+template <typename C>
 struct SegShared {
-  uint64_t cand[kCap];
-  uint64_t scratch[kWaves * kRun];
-  uint64_t list[kRun];
+  C cand[kCap];  // wave w owns cand[w * kWaveCap, (w + 1) * kWaveCap)
+  C scratch[kWaves * kRun];
+  C list[kRun];
+  uint64_t list64[kRun];
   uint32_t wl[kWaves];
   int red[kWaves];
-  int cnt;
+  int wc[2][kWaves];  // per-wave candidate counts, double-buffered by tile parity
+  int nan_seen;
 };
 
 __device__ __forceinline__ int block_sum(int v, int* red) {
@@ -133,41 +214,94 @@ __device__ __forceinline__ int block_sum(int v, int* red) {
   return t;
 }
 
-// sh.list <- the 128 largest of sh.cand[0, C), descending, zero padded.
-__device__ void block_select(SegShared& sh, int C) {
+// sh.list <- the 128 largest candidates of all wave regions (counts cnt[w]),
+// descending, zero padded.  Each wave sorts its own region in runs of 128,
+// then the four partial lists are merged as a two-level tree.
+template <typename C>
+__device__ void block_select(SegShared<C>& sh, const int cnt[kWaves]) {
   const int w = threadIdx.x / kWave, l = lane_id();
-  uint64_t acc[2] = {0, 0};
-  bool any = false;
-  for (int r = w; r * kRun < C; r += kWaves) {
-    uint64_t c[2];
+  int cw = cnt[0];
+#pragma unroll
+  for (int q = 1; q < kWaves; ++q) cw = w == q ? cnt[q] : cw;
+  const C* reg = sh.cand + w * kWaveCap;
+  C acc[2] = {0, 0};
+  for (int r = 0; r * kRun < cw; ++r) {
+    C c[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int i = r * kRun + h * kWave + l;
-      c[h] = i < C ? sh.cand[i] : 0ull;
+      c[h] = i < cw ? reg[i] : (C)0;
     }
     wave_sort128_desc(c);
-    if (!any) {
+    if (r == 0) {
       acc[0] = c[0];
       acc[1] = c[1];
-      any = true;
     } else {
       wave_merge128_desc(acc, c);
     }
   }
-  sh.scratch[w * kRun + l] = acc[0];
-  sh.scratch[w * kRun + kWave + l] = acc[1];
+  if (w & 1) {
+    sh.scratch[w * kRun + l] = acc[0];
+    sh.scratch[w * kRun + kWave + l] = acc[1];
+  }
+  __syncthreads();
+  if (!(w & 1) && (w == 0 ? cnt[1] : cnt[3]) > 0) {
+    const C b[2] = {sh.scratch[(w + 1) * kRun + l], sh.scratch[(w + 1) * kRun + kWave + l]};
+    wave_merge128_desc(acc, b);
+  }
+  if (w == 2) {
+    sh.scratch[w * kRun + l] = acc[0];
+    sh.scratch[w * kRun + kWave + l] = acc[1];
+  }
   __syncthreads();
   if (w == 0) {
-    const int runs = (C + kRun - 1) / kRun;
-    const int nw = runs < kWaves ? runs : kWaves;
-    for (int q = 1; q < nw; ++q) {
-      const uint64_t b[2] = {sh.scratch[q * kRun + l], sh.scratch[q * kRun + kWave + l]};
+    if (cnt[2] + cnt[3] > 0) {
+      const C b[2] = {sh.scratch[2 * kRun + l], sh.scratch[2 * kRun + kWave + l]};
       wave_merge128_desc(acc, b);
     }
     sh.list[l] = acc[0];
     sh.list[kWave + l] = acc[1];
   }
   __syncthreads();
+}
+
+// Wave-level stream compaction: lanes with `pred` append `comp` to their
+// wave's region at wcnt + (rank among active lanes).  `wcnt` is wave-uniform;
+// entries beyond the region are counted but not stored.
+template <typename C>
+__device__ __forceinline__ void wave_append(bool pred, C comp, C* reg, int& wcnt) {
+  const uint64_t m = __ballot(pred);
+  if (m) {
+    if (pred) {
+      const int off = wcnt + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      if (off < kWaveCap) reg[off] = comp;
+    }
+    wcnt += (int)__popcll(m);
+  }
+}
+
+typedef short short2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
+
+// Raw keys of the two bf16 values of a dword, packed (v_pk_ashrrev_i16 + xor/or).
+__device__ __forceinline__ uint32_t raw_key2_bf16(uint32_t w) {
+  const short2_t m = __builtin_bit_cast(short2_t, w) >> (short2_t){15, 15};
+  return w ^ (__builtin_bit_cast(uint32_t, m) | 0x80008000u);
+}
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(ushort2_t, a),
+                                                                __builtin_bit_cast(ushort2_t, b)));
+}
+__device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat(__builtin_bit_cast(ushort2_t, a),
+                                                                    __builtin_bit_cast(ushort2_t, b)));
+}
+__device__ __forceinline__ uint32_t raw_key_f32(uint32_t b) {
+  return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+}
+__device__ __forceinline__ uint32_t dword_of(const uint4& v, int d) {
+  return d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
 }
 
 // Outputs of one row from its sorted top-128 list (in LDS).
@@ -209,12 +343,16 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
 // ---------------------------------------------------------------------------
 // Kernel A: one workgroup per (segment, row).
 // ---------------------------------------------------------------------------
-template <int DT, int V, bool SAMPLE>
-__global__ __launch_bounds__(kNT) void seg_select_kernel(SelArgs a) {
+template <int DT, bool SAMPLE>
+__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4, 8)))
+void seg_select_kernel(SelArgs a) {
   using T = ElemT<DT>;
-  constexpr int VEC = T::VEC, ES = T::ES, E = V * VEC;
+  using S = Sel<DT>;
+  using C = typename S::Comp;
+  constexpr bool kBF = DT == kBF16;
+  constexpr int VEC = T::VEC, ES = T::ES, V = S::kV;
   constexpr int64_t kTileVec = (int64_t)kNT * V;
-  __shared__ SegShared sh;
+  __shared__ SegShared<C> sh;
   const int tid = threadIdx.x;
   const int w = tid / kWave, l = lane_id();
   const int seg = blockIdx.x;
@@ -227,7 +365,12 @@ __global__ __launch_bounds__(kNT) void seg_select_kernel(SelArgs a) {
   const int64_t s0 = (int64_t)seg * a.vps;
   const int64_t s1 = s0 + a.vps < nv ? s0 + a.vps : nv;
   const int ntiles = s1 > s0 ? (int)((s1 - s0 + kTileVec - 1) / kTileVec) : 0;
-  if (tid == 0) sh.cnt = 0;
+  const int64_t seg_e0 = s0 * VEC - rv.mis;  // element index of the segment's first slot
+  C* reg = sh.cand + w * kWaveCap;
+  if (tid == 0) sh.nan_seen = 0;
+
+  // id stored in a composite: segment-local index (bf16) or row index (f32)
+  auto elem_id = [&](int64_t e) -> uint32_t { return kBF ? (uint32_t)(e - seg_e0) : (uint32_t)e; };
 
   uint4 cur[V], nxt[V];
 #pragma unroll
@@ -236,8 +379,10 @@ __global__ __launch_bounds__(kNT) void seg_select_kernel(SelArgs a) {
     cur[j] = v < s1 ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u);
   }
 
-  uint32_t thr = 1;  // candidates: key >= thr
-  int base = 0;      // candidates held before the current tile
+  uint32_t thr = 0;  // canonical: candidates are live elements with key >= thr
+  bool nan_mode = false;
+  int wcnt = 0;      // this wave's candidates (wave-uniform)
+  int cnt[kWaves] = {0, 0, 0, 0};
   for (int t = 0; t < ntiles; ++t) {
     const int64_t tb = s0 + (int64_t)t * kTileVec;
     if (t + 1 < ntiles) {
@@ -247,123 +392,210 @@ __global__ __launch_bounds__(kNT) void seg_select_kernel(SelArgs a) {
         nxt[j] = v < s1 ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u);
       }
     }
-    uint32_t key[E];
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
-      const int64_t v = tb + (int64_t)j * kNT + tid;
-      const int64_t e0 = v * VEC - rv.mis;
-      const bool live = v < s1;
-      const bool full = live && e0 >= 0 && e0 + VEC <= a.cols;
-#pragma unroll
-      for (int q = 0; q < VEC; ++q) {
-        const bool ok = full || (live && e0 + q >= 0 && e0 + q < a.cols);
-        key[j * VEC + q] = ok ? select_key(T::bits(cur[j], q)) : 0u;
-      }
-    }
-    auto elem_idx = [&](int j, int q) -> uint32_t {
-      return (uint32_t)((tb + (int64_t)j * kNT + tid) * VEC + q - rv.mis);
+    const int64_t e_base = (tb + tid) * VEC - rv.mis;  // element index of (j = 0, q = 0)
+    const bool interior = tb * VEC - rv.mis >= 0 && (tb + kTileVec) * VEC - rv.mis <= a.cols &&
+                          tb + kTileVec <= s1;
+    // canonical composite of slot (j, q) and whether it is a live element >= thr
+    auto slow_comp = [&](int j, int q, uint32_t th, bool& pass) -> C {
+      const int64_t e = e_base + (int64_t)j * kNT * VEC + q;
+      const bool ok = tb + (int64_t)j * kNT + tid < s1 && e >= 0 && e < a.cols;
+      const uint32_t bits = kBF ? (T::bits(cur[j], q) >> 16) : T::bits(cur[j], q);
+      pass = ok && S::canon(bits) >= th;
+      return S::comp(bits, elem_id(e));
     };
 
     if (t == 0) {
+      // lower bound L: at least k live elements of this tile have key >= L
       uint32_t tmax = 0;
+      bool nan_here = false;
+      if (interior) {
+        uint32_t r = 0;
+        if (kBF) {
+          uint32_t m2 = 0;
 #pragma unroll
-      for (int i = 0; i < E; ++i) tmax = key[i] > tmax ? key[i] : tmax;
+          for (int j = 0; j < V; ++j)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) m2 = pk_max_u16(m2, raw_key2_bf16(dword_of(cur[j], d)));
+          r = (m2 & 0xFFFFu) > (m2 >> 16) ? (m2 & 0xFFFFu) : (m2 >> 16);
+        } else {
+#pragma unroll
+          for (int j = 0; j < V; ++j)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const uint32_t rk = raw_key_f32(dword_of(cur[j], d));
+              r = rk > r ? rk : r;
+            }
+        }
+        nan_here = r > S::kRawPosInf;
+        tmax = S::raw_to_canon(r);
+      }
+      if (!interior || nan_here) {
+        tmax = 0;
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) {
+            bool pass;
+            const C cm = slow_comp(j, q, 0u, pass);
+            const uint32_t kk = S::comp_key(cm);
+            tmax = pass && kk > tmax ? kk : tmax;
+          }
+      }
+      if (nan_here) sh.nan_seen = 1;
       const uint32_t srt = wave_sort64_u32_desc(tmax);
-      const int jw = (k + kWaves - 1) / kWaves;
-      const uint32_t wl = (uint32_t)__shfl((int)srt, jw - 1, kWave);
+      const uint32_t wl = readlane_u32(srt, (k + kWaves - 1) / kWaves - 1);
       if (l == 0) sh.wl[w] = wl;
       __syncthreads();
       uint32_t L = sh.wl[0];
 #pragma unroll
       for (int i = 1; i < kWaves; ++i) L = sh.wl[i] < L ? sh.wl[i] : L;
-      thr = L > 1u ? L : 1u;
+      thr = kBF ? L : (L > 1u ? L : 1u);
+      nan_mode = sh.nan_seen != 0;
     }
 
-    // ---- append this tile's candidates ------------------------------------
-    int c = 0;
-#pragma unroll
-    for (int i = 0; i < E; ++i) c += key[i] >= thr;
-    int pos = c > 0 ? atomicAdd(&sh.cnt, c) : 0;
-    if (c > 0 && pos + c <= kCap) {
+    // ---- append this tile's candidates (wave-local compaction) -------------
+    const int wcnt0 = wcnt;
+    const bool fast = interior && !nan_mode && (!kBF || thr >= 1u);
+    if (fast) {
+      const uint32_t rt = S::raw_thr(thr);
 #pragma unroll
       for (int j = 0; j < V; ++j) {
+        uint32_t rk[4];
+        bool flag;
+        uint32_t rtm1 = 0;
+        if (kBF) {
+          rtm1 = (rt - 1u) * 0x10001u;
 #pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-          const uint32_t kk = key[j * VEC + q];
-          if (kk >= thr) sh.cand[pos++] = make_comp(kk, elem_idx(j, q));
+          for (int d = 0; d < 4; ++d) rk[d] = raw_key2_bf16(dword_of(cur[j], d));
+          const uint32_t mx = pk_max_u16(pk_max_u16(rk[0], rk[1]), pk_max_u16(rk[2], rk[3]));
+          flag = pk_sub_sat_u16(mx, rtm1) != 0u;
+        } else {
+#pragma unroll
+          for (int d = 0; d < 4; ++d) rk[d] = raw_key_f32(dword_of(cur[j], d));
+          const uint32_t m01 = rk[0] > rk[1] ? rk[0] : rk[1];
+          const uint32_t m23 = rk[2] > rk[3] ? rk[2] : rk[3];
+          flag = (m01 > m23 ? m01 : m23) >= rt;
+        }
+        if (__ballot(flag)) {
+          uint32_t mask = 0;
+          if (flag) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              if (kBF) {
+                const uint32_t sd = pk_sub_sat_u16(rk[d], rtm1);
+                mask |= ((sd & 0xFFFFu) != 0u ? 1u : 0u) << (2 * d);
+                mask |= ((sd >> 16) != 0u ? 1u : 0u) << (2 * d + 1);
+              } else {
+                mask |= (rk[d] >= rt ? 1u : 0u) << d;
+              }
+            }
+          }
+          for (;;) {
+            const bool have = mask != 0u;
+            if (!__ballot(have)) break;
+            C cm = 0;
+            if (have) {
+              const int e = __builtin_ctz(mask);
+              mask &= mask - 1u;
+              const int64_t eidx = e_base + (int64_t)j * kNT * VEC + e;
+              if (kBF) {
+                const uint32_t word = dword_of(cur[j], e >> 1);
+                cm = S::comp((e & 1) ? (word >> 16) : (word & 0xFFFFu), elem_id(eidx));
+              } else {
+                cm = S::comp(dword_of(cur[j], e), elem_id(eidx));
+              }
+            }
+            wave_append(have, cm, reg, wcnt);
+          }
         }
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j)
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          bool pass;
+          const C cm = slow_comp(j, q, thr, pass);
+          wave_append(pass, cm, reg, wcnt);
+        }
     }
+    if (l == 0) sh.wc[t & 1][w] = wcnt;
     __syncthreads();
-    int total = sh.cnt;
-    __syncthreads();
+    bool overflow = false;
+#pragma unroll
+    for (int q = 0; q < kWaves; ++q) {
+      cnt[q] = sh.wc[t & 1][q];
+      overflow |= cnt[q] > kWaveCap;
+    }
 
-    if (total - base > kTileCap) {
+    if (overflow) {
       // Heavy ties: keep only this tile's exact top-k among the passing
       // elements (composites are distinct, so exactly k pass the bisection).
-      uint64_t prefix = 0;
-      for (int bit = 63; bit >= 0; --bit) {
-        const uint64_t probe = prefix | (1ull << bit);
+      C prefix = 0;
+      for (int bit = (int)sizeof(C) * 8 - 1; bit >= 0; --bit) {
+        const C probe = prefix | ((C)1 << bit);
         int cc = 0;
 #pragma unroll
-        for (int j = 0; j < V; ++j) {
+        for (int j = 0; j < V; ++j)
 #pragma unroll
           for (int q = 0; q < VEC; ++q) {
-            const uint32_t kk = key[j * VEC + q];
-            cc += kk >= thr && make_comp(kk, elem_idx(j, q)) >= probe;
+            bool pass;
+            const C cm = slow_comp(j, q, thr, pass);
+            cc += pass && cm >= probe;
           }
-        }
         if (block_sum(cc, sh.red) >= k) prefix = probe;
       }
-      if (tid == 0) sh.cnt = base;
-      __syncthreads();
-      int cc = 0;
+      wcnt = wcnt0;
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
+      for (int j = 0; j < V; ++j)
 #pragma unroll
         for (int q = 0; q < VEC; ++q) {
-          const uint32_t kk = key[j * VEC + q];
-          cc += kk >= thr && make_comp(kk, elem_idx(j, q)) >= prefix;
+          bool pass;
+          const C cm = slow_comp(j, q, thr, pass);
+          wave_append(pass && cm >= prefix, cm, reg, wcnt);
         }
-      }
-      int p2 = cc > 0 ? atomicAdd(&sh.cnt, cc) : 0;
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-          const uint32_t kk = key[j * VEC + q];
-          if (kk >= thr) {
-            const uint64_t cm = make_comp(kk, elem_idx(j, q));
-            if (cm >= prefix) sh.cand[p2++] = cm;
-          }
-        }
-      }
+      if (l == 0) sh.wc[t & 1][w] = wcnt;
       __syncthreads();
-      total = sh.cnt;
-      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kWaves; ++q) cnt[q] = sh.wc[t & 1][q];
     }
 
-    if (total > kRefresh) {
-      // cut to the exact top-k so far; later elements need a strictly larger key
-      block_select(sh, total);
-      for (int i = tid; i < k; i += kNT) sh.cand[i] = sh.list[i];
-      if (tid == 0) sh.cnt = k;
-      const uint32_t kth = comp_key(sh.list[k - 1]);
-      __syncthreads();
-      total = k;
-      thr = kth + 1u;
+    int cmax = cnt[0], total = cnt[0];
+#pragma unroll
+    for (int q = 1; q < kWaves; ++q) {
+      cmax = cnt[q] > cmax ? cnt[q] : cmax;
+      total += cnt[q];
     }
-    base = total;
+    if (total >= k && ((a.early_cut && t == 0 && ntiles > 1) || cmax > a.refresh_at)) {
+      // cut to the exact top-k so far (spread over the wave regions); later
+      // elements need a strictly larger key than the k-th
+      block_select(sh, cnt);
+      const int share = (k + kWaves - 1) / kWaves;
+      for (int i = l; i < share; i += kWave) {
+        const int src = w * share + i;
+        if (src < k) reg[i] = sh.list[src];
+      }
+#pragma unroll
+      for (int q = 0; q < kWaves; ++q) {
+        const int lo = q * share, hi = (q + 1) * share < k ? (q + 1) * share : k;
+        cnt[q] = hi > lo ? hi - lo : 0;
+      }
+      wcnt = cnt[w == 0 ? 0 : w == 1 ? 1 : w == 2 ? 2 : 3];
+      thr = S::comp_key(sh.list[k - 1]) + 1u;
+      __syncthreads();
+    }
 #pragma unroll
     for (int j = 0; j < V; ++j) cur[j] = nxt[j];
   }
 
-  block_select(sh, base);
+  block_select(sh, cnt);
+  for (int i = tid; i < kRun; i += kNT) sh.list64[i] = S::to_global(sh.list[i], seg_e0);
+  __syncthreads();
   if (a.nseg == 1) {
-    finalize_row<DT, SAMPLE>(a, row, sh.list);
+    finalize_row<DT, SAMPLE>(a, row, sh.list64);
   } else {
     uint64_t* dst = a.ws_lists + ((size_t)row * a.nseg + seg) * kRun;
-    for (int i = tid; i < kRun; i += kNT) dst[i] = sh.list[i];
+    for (int i = tid; i < kRun; i += kNT) dst[i] = sh.list64[i];
   }
 }
 
@@ -420,23 +652,56 @@ struct Plan {
   int64_t vps;
 };
 
+struct Tuning {
+  int refresh_at = 192;
+  int early_cut = 0;
+  int target_blocks = kTargetBlocks;
+};
+
+static int env_int(const char* name, int dflt, int lo, int hi) {
+  const char* v = getenv(name);
+  if (!v || !*v) return dflt;
+  const long x = strtol(v, nullptr, 10);
+  return x < lo ? lo : (x > hi ? hi : (int)x);
+}
+
+static const Tuning& tuning() {
+  static const Tuning t = [] {
+    Tuning r;
+    r.refresh_at = env_int("TALLAX_SEL_REFRESH", r.refresh_at, 8, kWaveCap - 8);
+    r.early_cut = env_int("TALLAX_SEL_EARLY_CUT", r.early_cut, 0, 1);
+    r.target_blocks = env_int("TALLAX_SEL_BLOCKS", r.target_blocks, 1, 1 << 20);
+    return r;
+  }();
+  return t;
+}
+
 // Segments: enough workgroups for ~4 per CU, whole tiles per segment, at
-// most kMaxSeg segments per row.
-static void plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
+// most kMaxSeg segments per row; bf16 segments hold at most 7 tiles so that
+// segment-local indices fit the 16-bit field of the u32 composites.
+static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
   const int vec = dt == kF32 ? 4 : 8;
   const int V = dt == kF32 ? kVF32 : kVBF16;
+  const int64_t max_tiles = dt == kF32 ? ((int64_t)1 << 40) : 7;
   const int64_t tile = (int64_t)kNT * V;
   const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
   const int64_t tiles = (nv + tile - 1) / tile;
-  int64_t nseg = (kTargetBlocks + rows - 1) / rows;
+  int64_t nseg = (tuning().target_blocks + rows - 1) / rows;
   if (nseg > kMaxSeg) nseg = kMaxSeg;
   if (nseg > tiles) nseg = tiles;
+  const int64_t min_seg = (tiles + max_tiles - 1) / max_tiles;
+  if (nseg < min_seg) nseg = min_seg;
   if (nseg < 1) nseg = 1;
   int64_t vps = (nv + nseg - 1) / nseg;
   vps = (vps + tile - 1) / tile * tile;
   nseg = (nv + vps - 1) / vps;
+  if (nseg > kMaxSeg) {
+    set_error("row length %lld exceeds this build's limit for the dtype", (long long)cols);
+    return kUnsupported;
+  }
   p->nseg = (int)nseg;
   p->vps = vps;
+  return kOk;
 }
 
 static size_t ws_bytes_for(int64_t rows, const Plan& p) {
@@ -445,9 +710,10 @@ static size_t ws_bytes_for(int64_t rows, const Plan& p) {
 }
 
 template <int DT, bool SAMPLE>
-static int launch_select(const SelArgs& a, hipStream_t s, const char* what) {
-  constexpr int V = DT == kF32 ? kVF32 : kVBF16;
-  hipLaunchKernelGGL((seg_select_kernel<DT, V, SAMPLE>), dim3((unsigned)a.nseg, (unsigned)a.rows),
+static int launch_select(SelArgs a, hipStream_t s, const char* what) {
+  a.refresh_at = tuning().refresh_at;
+  a.early_cut = tuning().early_cut;
+  hipLaunchKernelGGL((seg_select_kernel<DT, SAMPLE>), dim3((unsigned)a.nseg, (unsigned)a.rows),
                      dim3(kNT), 0, s, a);
   int st = launch_status(what);
   if (st || a.nseg == 1) return st;
@@ -486,7 +752,7 @@ extern "C" {
 size_t tallax_topk_workspace_size(int64_t rows, int64_t cols, int64_t k, int dtype) {
   Plan p;
   if (k < 1 || k > kMaxK || (dtype != kF32 && dtype != kBF16) || rows < 0 || cols <= 0) return 0;
-  plan_rows(rows, cols, dtype, &p);
+  if (plan_rows(rows, cols, dtype, &p) != kOk) return 0;
   return ws_bytes_for(rows, p);
 }
 
@@ -499,7 +765,8 @@ int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k,
   if (!out_vals || !out_idx) { set_error("null output pointer"); return kInvalidArgument; }
   if (rows == 0) return kOk;
   Plan p;
-  plan_rows(rows, cols, dtype, &p);
+  st = plan_rows(rows, cols, dtype, &p);
+  if (st) return st;
   const size_t need = ws_bytes_for(rows, p);
   if (workspace_bytes < need || (need && !workspace)) {
     set_error("workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
@@ -529,7 +796,8 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
   if (!top_k || !top_p || !temperature || !rng_key || !out_tokens) { set_error("null pointer argument"); return kInvalidArgument; }
   if (rows == 0) return kOk;
   Plan p;
-  plan_rows(rows, vocab, dtype, &p);
+  st = plan_rows(rows, vocab, dtype, &p);
+  if (st) return st;
   const size_t need = ws_bytes_for(rows, p);
   if (workspace_bytes < need || (need && !workspace)) {
     set_error("workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);

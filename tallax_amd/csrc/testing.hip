@@ -27,9 +27,30 @@ __global__ void gumbel_probe_kernel(uint32_t k0, uint32_t k1, const uint32_t* ct
   }
 }
 
+// out[d * 64 + lane] = lane_xor(lane, 1 << d) for d = 0..5, out[6 * 64 + lane] = lane_rev(lane).
+__global__ void lane_ops_kernel(uint32_t* out) {
+  const uint32_t x = threadIdx.x;
+  out[0 * 64 + x] = lane_xor(x, 1);
+  out[1 * 64 + x] = lane_xor(x, 2);
+  out[2 * 64 + x] = lane_xor(x, 4);
+  out[3 * 64 + x] = lane_xor(x, 8);
+  out[4 * 64 + x] = lane_xor(x, 16);
+  out[5 * 64 + x] = lane_xor(x, 32);
+  out[6 * 64 + x] = lane_rev(x);
+}
+
 }  // namespace tx
 
 extern "C" {
+
+int tallax_testing_lane_ops(uint32_t* out, hipStream_t stream) {
+  if (!out) {
+    tx::set_error("bad arguments");
+    return tx::kInvalidArgument;
+  }
+  hipLaunchKernelGGL(tx::lane_ops_kernel, dim3(1), dim3(64), 0, stream, out);
+  return tx::launch_status("tallax_testing_lane_ops");
+}
 
 int tallax_testing_expf_logf(const float* x, float* exp_out, float* log_out, int64_t n,
                              hipStream_t stream) {

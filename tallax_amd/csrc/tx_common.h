@@ -1,8 +1,9 @@
 // Shared device helpers for the tallax MI355X (gfx950) kernels.
 //
-// Everything here is wave64 CDNA4 code: cross-lane traffic uses ds_bpermute /
-// ds_swizzle through the HIP shuffle intrinsics, and no kernel uses MFMA
-// (nothing on the sort / select / sample path is a dense contraction).
+// Everything here is wave64 CDNA4 code: cross-lane traffic uses VALU lane
+// exchanges (DPP and gfx950's v_permlane16/32_swap) rather than LDS-unit
+// shuffles, and no kernel uses MFMA (nothing on the sort / select / sample
+// path is a dense contraction).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -58,17 +59,77 @@ __device__ __forceinline__ int32_t comp_idx(uint64_t c) { return (int32_t)(~(uin
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// Value of lane (lane ^ d) for d in {1, 2, 4, 8, 16, 32}, with VALU lane
+// exchanges only (no LDS-unit round trip):
+//   d = 1, 2   DPP quad_perm [1,0,3,2] / [2,3,0,1];
+//   d = 4      DPP row_ror:12 (lane i reads i+4) or row_ror:4 (reads i-4),
+//              chosen by bit 2 of the lane;
+//   d = 8      DPP row_ror:8;
+//   d = 16, 32 v_permlane16_swap / v_permlane32_swap of the register with
+//              itself: result [0] holds the even rows (halves), [1] the odd
+//              ones, so the partner is [0] on odd and [1] on even lanes.
+// `d` must fold to a constant after unrolling.
+__device__ __forceinline__ uint32_t lane_xor(uint32_t x, int d) {
+  const int l = (int)(threadIdx.x & (kWave - 1));
+  switch (d) {
+    case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);
+    case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);
+    case 4: {
+      const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x12C, 0xF, 0xF, false);
+      const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x124, 0xF, 0xF, false);
+      return (l & 4) ? dn : up;
+    }
+    case 8: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);
+    case 16: {
+      const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+      return (l & 16) ? r[0] : r[1];
+    }
+    default: {
+      const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+      return (l & 32) ? r[0] : r[1];
+    }
+  }
+}
+
+__device__ __forceinline__ float lane_xor_f(float x, int d) {
+  return __uint_as_float(lane_xor(__float_as_uint(x), d));
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, m, kWave);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), m, kWave);
+  const uint32_t lo = lane_xor((uint32_t)v, m);
+  const uint32_t hi = lane_xor((uint32_t)(v >> 32), m);
   return ((uint64_t)hi << 32) | lo;
 }
 
-__device__ __forceinline__ float shfl_f(float v, int src) { return __shfl(v, src, kWave); }
+// Value of lane (lane - d) within a 16-lane row (DPP row_shr:d); lanes whose
+// source falls outside the row read 0.  d in {1, 2, 4}, constant after unrolling.
+__device__ __forceinline__ float row_shr_f(float x, int d) {
+  const int v = __float_as_int(x);
+  switch (d) {
+    case 1: return __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true));
+    case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true));
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true));
+  }
+}
+
+// Uniform broadcast of lane `src` (src must be wave-uniform).
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t x, int src) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, src);
+}
+__device__ __forceinline__ float readlane_f(float x, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), src));
+}
+
+// Value of lane (63 - lane): DPP row_mirror reverses each 16-lane row, then
+// rows are swapped pairwise (xor 16, then xor 32).
+__device__ __forceinline__ uint32_t lane_rev(uint32_t x) {
+  const uint32_t m = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xF, 0xF, false);
+  return lane_xor(lane_xor(m, 16), 32);
+}
 
 __device__ __forceinline__ int wave_sum_i(int v) {
 #pragma unroll
-  for (int d = kWave / 2; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+  for (int d = kWave / 2; d >= 1; d >>= 1) v += (int)lane_xor((uint32_t)v, d);
   return v;
 }
 

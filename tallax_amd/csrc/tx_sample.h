@@ -28,13 +28,13 @@ __device__ __noinline__ int32_t sample_tail(const float v_in[2], const int32_t i
 
   // softmax numerators exp(l - l[0]) and their total, summed as a
   // stride-halving tree over 128 zero-padded slots.
-  const float l0 = shfl_f(v[0], 0);
+  const float l0 = readlane_f(v[0], 0);
   float e[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) e[h] = in[h] ? tx_expf(v[h] - l0) : 0.0f;
   float s = e[0] + e[1];
 #pragma unroll
-  for (int d = kWave / 2; d >= 1; d >>= 1) s = s + __shfl_xor(s, d, kWave);
+  for (int d = kWave / 2; d >= 1; d >>= 1) s = s + lane_xor_f(s, d);
 
   // inclusive cumsum of probs along the candidate axis: Hillis-Steele inside
   // 8-slot tiles, then the running total of earlier tiles added sequentially.
@@ -46,18 +46,18 @@ __device__ __noinline__ int32_t sample_tail(const float v_in[2], const int32_t i
     const bool ok = (l & 7) >= sh;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const float u = __shfl_up(c[h], sh, kWave);
+      const float u = row_shr_f(c[h], sh);
       c[h] = c[h] + (ok ? u : 0.0f);
     }
   }
   const int tile0 = l >> 3;  // tile of register 0; register 1 is tile0 + 8
   float carry0 = 0.0f, carry1 = 0.0f;
-  float run = __shfl(c[0], 7, kWave);
+  float run = readlane_f(c[0], 7);
 #pragma unroll
   for (int g = 1; g < 16; ++g) {
     if (tile0 == g) carry0 = run;
     if (tile0 + 8 == g) carry1 = run;
-    const float tsg = __shfl(g < 8 ? c[0] : c[1], (g & 7) * 8 + 7, kWave);
+    const float tsg = readlane_f(g < 8 ? c[0] : c[1], (g & 7) * 8 + 7);
     run = run + tsg;
   }
   if (tile0 != 0) c[0] = c[0] + carry0;
@@ -66,7 +66,7 @@ __device__ __noinline__ int32_t sample_tail(const float v_in[2], const int32_t i
   // threshold index t = #(cumsum < p); threshold value l[t] (0 when t == K,
   // the out-of-range gather of take_along_axis_arrays).
   const int t = __popcll(__ballot(in[0] && c[0] < top_p)) + __popcll(__ballot(in[1] && c[1] < top_p));
-  const float vt = __shfl(t < kWave ? v[0] : v[1], t & (kWave - 1), kWave);
+  const float vt = readlane_f(t < kWave ? v[0] : v[1], t & (kWave - 1));
   const float thr = t < K ? vt : 0.0f;
 
   // mask, temperature, Gumbel noise, argmax
@@ -103,16 +103,16 @@ __device__ __noinline__ int32_t sample_tail(const float v_in[2], const int32_t i
   }
 #pragma unroll
   for (int d = kWave / 2; d >= 1; d >>= 1) {
-    const float os = __shfl_xor(best_s, d, kWave);
-    const uint32_t ob = (uint32_t)__shfl_xor((int)best_b, d, kWave);
-    const int32_t oi = __shfl_xor(best_i, d, kWave);
+    const float os = lane_xor_f(best_s, d);
+    const uint32_t ob = lane_xor(best_b, d);
+    const int32_t oi = (int32_t)lane_xor((uint32_t)best_i, d);
     if (os > best_s || (os == best_s && ob > best_b)) {
       best_s = os;
       best_b = ob;
       best_i = oi;
     }
   }
-  const int32_t greedy = __shfl(id[0], 0, kWave);
+  const int32_t greedy = (int32_t)readlane_u32((uint32_t)id[0], 0);
   return temp < 1e-5f ? greedy : best_i;
 }
 

@@ -16,6 +16,19 @@ def _log(msg):
 
 
 # --------------------------------------------------------------------------- primitives
+def test_lane_exchange_semantics(gpu):
+    """DPP / v_permlane*_swap lane exchanges used by every wave network."""
+    from tallax_amd import _lib
+    out = torch.zeros(7 * 64, dtype=torch.int32, device=gpu)
+    _lib.check(_lib.LIB.tallax_testing_lane_ops(out.data_ptr(), _lib.stream_of(out)), "lane_ops")
+    torch.cuda.synchronize()
+    o = out.cpu().numpy().reshape(7, 64)
+    lanes = np.arange(64)
+    for d in range(6):
+        assert np.array_equal(o[d], lanes ^ (1 << d)), d
+    assert np.array_equal(o[6], 63 - lanes)
+
+
 def test_exp_log_bitexact(gpu):
     from tallax_amd import _lib
     rng = np.random.default_rng(11)
