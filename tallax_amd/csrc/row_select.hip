@@ -54,10 +54,8 @@ constexpr int kWaves = kNT / kWave;
 constexpr int kCap = 1024;                 // LDS candidate slots (4 wave regions)
 constexpr int kMaxK = 128;                 // the reference's limit (top_k.py:438-439)
 constexpr int kRun = 128;                  // list length handed between kernels
-constexpr int kMaxSeg = 16;
+constexpr int kMaxSeg = 32;
 constexpr int kTargetBlocks = 1024;        // ~4 workgroups per CU on 256 CUs
-constexpr int kVF32 = 4;                   // 16-byte vectors per thread per tile
-constexpr int kVBF16 = 4;
 
 struct SelArgs {
   const void* x;
@@ -79,9 +77,6 @@ struct SelArgs {
   float replace_in_dtype;  // replace_val rounded to the logits dtype
   float replace_f32;       // replace_val rounded to float32
   int32_t* out_tokens;
-  // selection policy
-  int refresh_at;
-  int early_cut;
 };
 
 template <int DT>
@@ -118,11 +113,9 @@ struct ElemT<kBF16> {
 };
 
 constexpr int kWaveCap = kCap / kWaves;    // candidate slots per wave
-// Tunables (read once from the environment by the host; defaults in Tuning):
-//   TALLAX_SEL_REFRESH       cut the candidates to top-k once a wave region holds
-//                            more than this many (default 3/4 of its 256 slots);
-//   TALLAX_SEL_EARLY_CUT     1: also cut right after the first tile;
-//   TALLAX_SEL_BLOCKS        workgroups aimed for per launch (default 1024).
+constexpr int kStage = 6;                  // flagged 16-byte vectors staged per thread
+// Tunable (read once from the environment by the host):
+//   TALLAX_SEL_BLOCKS   workgroups aimed for per launch (default 1024).
 
 // ---------------------------------------------------------------------------
 // Per-dtype selection traits.
@@ -144,8 +137,6 @@ struct Sel;
 template <>
 struct Sel<kBF16> {
   using Comp = uint32_t;
-  static constexpr int kV = kVBF16;
-  static constexpr int kMaxTilesPerSeg = 7;  // 7 * 256 * 4 * 8 = 57344 < 65536 elements
   static constexpr uint32_t kRawPosInf = 0xFF80u;
   __device__ static __forceinline__ uint32_t canon(uint32_t h) {  // h: bf16 bits
     const uint32_t a = h & 0x7FFFu;
@@ -176,8 +167,6 @@ struct Sel<kBF16> {
 template <>
 struct Sel<kF32> {
   using Comp = uint64_t;
-  static constexpr int kV = kVF32;
-  static constexpr int kMaxTilesPerSeg = 1 << 20;
   static constexpr uint32_t kRawPosInf = 0xFF800000u;
   __device__ static __forceinline__ uint32_t canon(uint32_t b) { return select_key(b); }
   __device__ static __forceinline__ Comp comp(uint32_t b, uint32_t gidx) { return make_comp(select_key(b), gidx); }
@@ -214,15 +203,13 @@ __device__ __forceinline__ int block_sum(int v, int* red) {
   return t;
 }
 
-// sh.list <- the 128 largest candidates of all wave regions (counts cnt[w]),
+// sh.list <- the 128 largest candidates of all wave regions (counts cnt[w] in LDS),
 // descending, zero padded.  Each wave sorts its own region in runs of 128,
 // then the four partial lists are merged as a two-level tree.
 template <typename C>
-__device__ void block_select(SegShared<C>& sh, const int cnt[kWaves]) {
+__device__ __forceinline__ void block_select(SegShared<C>& sh, const int* cnt) {
   const int w = threadIdx.x / kWave, l = lane_id();
-  int cw = cnt[0];
-#pragma unroll
-  for (int q = 1; q < kWaves; ++q) cw = w == q ? cnt[q] : cw;
+  const int cw = cnt[w];
   const C* reg = sh.cand + w * kWaveCap;
   C acc[2] = {0, 0};
   for (int r = 0; r * kRun < cw; ++r) {
@@ -301,7 +288,19 @@ __device__ __forceinline__ uint32_t raw_key_f32(uint32_t b) {
   return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
 }
 __device__ __forceinline__ uint32_t dword_of(const uint4& v, int d) {
-  return d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
+  const uint32_t lo = (d & 1) ? v.y : v.x;
+  const uint32_t hi = (d & 1) ? v.w : v.z;
+  return (d & 2) ? hi : lo;
+}
+// Element q of a 16-byte vector as the value the select keys expect
+// (bf16: its 16 bits, f32: its 32 bits); q may be a run-time value.
+template <int DT>
+__device__ __forceinline__ uint32_t elem_bits(const uint4& v, int q) {
+  if (DT == kBF16) {
+    const uint32_t w = dword_of(v, q >> 1);
+    return (q & 1) ? (w >> 16) : (w & 0xFFFFu);
+  }
+  return dword_of(v, q);
 }
 
 // Outputs of one row from its sorted top-128 list (in LDS).
@@ -341,18 +340,21 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
 }
 
 // ---------------------------------------------------------------------------
-// Kernel A: one workgroup per (segment, row).
+// Kernel A: one workgroup per (segment, row).  The segment (MAXV 16-byte
+// vectors per thread) is loaded into registers with every load issued up
+// front, filtered once against the thread-maxima lower bound, and reduced to
+// its sorted top-128 by one block selection.
 // ---------------------------------------------------------------------------
-template <int DT, bool SAMPLE>
-__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(4, 8)))
+template <int DT, int MAXV, bool SAMPLE>
+__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(3, 8)))
 void seg_select_kernel(SelArgs a) {
   using T = ElemT<DT>;
   using S = Sel<DT>;
   using C = typename S::Comp;
   constexpr bool kBF = DT == kBF16;
-  constexpr int VEC = T::VEC, ES = T::ES, V = S::kV;
-  constexpr int64_t kTileVec = (int64_t)kNT * V;
+  constexpr int VEC = T::VEC, ES = T::ES;
   __shared__ SegShared<C> sh;
+  __shared__ uint4 stage[kStage * kNT];  // flagged vectors, slot-major
   const int tid = threadIdx.x;
   const int w = tid / kWave, l = lane_id();
   const int seg = blockIdx.x;
@@ -364,228 +366,239 @@ void seg_select_kernel(SelArgs a) {
   const int64_t nv = (a.cols + rv.mis + VEC - 1) / VEC;
   const int64_t s0 = (int64_t)seg * a.vps;
   const int64_t s1 = s0 + a.vps < nv ? s0 + a.vps : nv;
-  const int ntiles = s1 > s0 ? (int)((s1 - s0 + kTileVec - 1) / kTileVec) : 0;
   const int64_t seg_e0 = s0 * VEC - rv.mis;  // element index of the segment's first slot
   C* reg = sh.cand + w * kWaveCap;
   if (tid == 0) sh.nan_seen = 0;
 
-  // id stored in a composite: segment-local index (bf16) or row index (f32)
-  auto elem_id = [&](int64_t e) -> uint32_t { return kBF ? (uint32_t)(e - seg_e0) : (uint32_t)e; };
-
-  uint4 cur[V], nxt[V];
+  uint4 raw[MAXV];
 #pragma unroll
-  for (int j = 0; j < V; ++j) {
+  for (int j = 0; j < MAXV; ++j) {
     const int64_t v = s0 + (int64_t)j * kNT + tid;
-    cur[j] = v < s1 ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u);
+    raw[j] = v < s1 ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u);
   }
+  // Segment-local slot index of (j, q): lbase + j * kNT * VEC + q.  Live slots
+  // (inside the row and the segment) are those in [live_lo, live_hi).
+  const int lbase = tid * VEC;
+  const int64_t seg_elems = (s1 - s0) * VEC;
+  const int live_lo = seg_e0 < 0 ? (int)(-seg_e0) : 0;
+  const int live_hi = (int)(a.cols - seg_e0 < seg_elems ? a.cols - seg_e0 : seg_elems);
+  const uint32_t gbase = (uint32_t)seg_e0;  // row index = gbase + local index (mod 2^32)
+  // id stored in a composite: segment-local index (bf16) or row index (f32)
+  auto elem_id = [&](int lidx) -> uint32_t { return kBF ? (uint32_t)lidx : gbase + (uint32_t)lidx; };
+  // canonical composite of slot (j, q) (vector j passed in vv) and whether it
+  // is a live element >= th
+  auto slow_comp_v = [&](const uint4 vv, int j, int q, uint32_t th, bool& pass) -> C {
+    const int li = lbase + j * kNT * VEC + q;
+    const uint32_t bits = elem_bits<DT>(vv, q);
+    pass = li >= live_lo && li < live_hi && S::canon(bits) >= th;
+    return S::comp(bits, elem_id(li));
+  };
 
-  uint32_t thr = 0;  // canonical: candidates are live elements with key >= thr
-  bool nan_mode = false;
-  int wcnt = 0;      // this wave's candidates (wave-uniform)
-  int cnt[kWaves] = {0, 0, 0, 0};
-  for (int t = 0; t < ntiles; ++t) {
-    const int64_t tb = s0 + (int64_t)t * kTileVec;
-    if (t + 1 < ntiles) {
+  // Vector j of this thread covers local slots [lbase + j*kNT*VEC, + VEC):
+  // "full" if all of them are live elements, "dead" if none is.
+  auto vec_full = [&](int j) -> bool {
+    const int li0 = lbase + j * kNT * VEC;
+    return li0 >= live_lo && li0 + VEC <= live_hi;
+  };
+  auto vec_dead = [&](int j) -> bool {
+    const int li0 = lbase + j * kNT * VEC;
+    return li0 >= live_hi || li0 + VEC <= live_lo;
+  };
+  // raw filter max of a vector (raw keys, see Sel): packed for bf16
+  auto vec_raw_max = [&](const uint4 vv) -> uint32_t {
+    if (kBF) {
+      uint32_t mx = raw_key2_bf16(vv.x);
+      mx = pk_max_u16(mx, raw_key2_bf16(vv.y));
+      mx = pk_max_u16(mx, raw_key2_bf16(vv.z));
+      mx = pk_max_u16(mx, raw_key2_bf16(vv.w));
+      return mx;  // two 16-bit maxima
+    }
+    uint32_t mx = raw_key_f32(vv.x);
+    uint32_t r = raw_key_f32(vv.y);
+    mx = r > mx ? r : mx;
+    r = raw_key_f32(vv.z);
+    mx = r > mx ? r : mx;
+    r = raw_key_f32(vv.w);
+    return r > mx ? r : mx;
+  };
+
+  // ---- lower bound L: at least k live elements are >= L --------------------
+  uint32_t tmax = 0;
+  bool nan_here = false;
+  {
+    uint32_t r2 = 0;     // raw max over full vectors (bf16: packed pair)
+    uint32_t cpart = 0;  // canonical max over live elements of partial vectors
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        const int64_t v = tb + kTileVec + (int64_t)j * kNT + tid;
-        nxt[j] = v < s1 ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u);
+    for (int j = 0; j < MAXV; ++j) {
+      if (vec_full(j)) {
+        const uint32_t m = vec_raw_max(raw[j]);
+        r2 = kBF ? pk_max_u16(r2, m) : (m > r2 ? m : r2);
+      } else if (!vec_dead(j)) {
+#pragma unroll 1
+        for (int q = 0; q < VEC; ++q) {
+          bool pass;
+          const C cm = slow_comp_v(raw[j], j, q, 0u, pass);
+          const uint32_t kk = S::comp_key(cm);
+          cpart = pass && kk > cpart ? kk : cpart;
+        }
       }
     }
-    const int64_t e_base = (tb + tid) * VEC - rv.mis;  // element index of (j = 0, q = 0)
-    const bool interior = tb * VEC - rv.mis >= 0 && (tb + kTileVec) * VEC - rv.mis <= a.cols &&
-                          tb + kTileVec <= s1;
-    // canonical composite of slot (j, q) and whether it is a live element >= thr
-    auto slow_comp = [&](int j, int q, uint32_t th, bool& pass) -> C {
-      const int64_t e = e_base + (int64_t)j * kNT * VEC + q;
-      const bool ok = tb + (int64_t)j * kNT + tid < s1 && e >= 0 && e < a.cols;
-      const uint32_t bits = kBF ? (T::bits(cur[j], q) >> 16) : T::bits(cur[j], q);
-      pass = ok && S::canon(bits) >= th;
-      return S::comp(bits, elem_id(e));
+    const uint32_t r = kBF ? ((r2 & 0xFFFFu) > (r2 >> 16) ? (r2 & 0xFFFFu) : (r2 >> 16)) : r2;
+    nan_here = r > S::kRawPosInf;
+    tmax = S::raw_to_canon(r);
+    tmax = cpart > tmax ? cpart : tmax;
+    if (nan_here) {  // positive NaN raw keys would fake a high maximum: recompute canonically
+      tmax = 0;
+#pragma unroll
+      for (int j = 0; j < MAXV; ++j)
+#pragma unroll 1
+        for (int q = 0; q < VEC; ++q) {
+          bool pass;
+          const C cm = slow_comp_v(raw[j], j, q, 0u, pass);
+          const uint32_t kk = S::comp_key(cm);
+          tmax = pass && kk > tmax ? kk : tmax;
+        }
+    }
+  }
+  if (nan_here) sh.nan_seen = 1;
+  const uint32_t srt = wave_sort64_u32_desc(tmax);
+  const uint32_t wl = readlane_u32(srt, (k + kWaves - 1) / kWaves - 1);
+  if (l == 0) sh.wl[w] = wl;
+  __syncthreads();
+  uint32_t L = sh.wl[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) L = sh.wl[i] < L ? sh.wl[i] : L;
+  const uint32_t thr = kBF ? L : (L > 1u ? L : 1u);  // candidates: live elements with key >= thr
+  const bool nan_mode = sh.nan_seen != 0;
+
+  // ---- candidates (wave-local compaction) ------------------------------------
+  int wcnt = 0;
+  const bool fast = !nan_mode && (!kBF || thr >= 1u);
+  if (fast) {
+    const uint32_t rt = S::raw_thr(thr);
+    const uint32_t rtm1 = kBF ? (rt - 1u) * 0x10001u : 0u;
+    auto raw_flag = [&](uint32_t m) -> bool { return kBF ? pk_sub_sat_u16(m, rtm1) != 0u : m >= rt; };
+    // element mask of vector j (held in vv): bit q set if element q is live and passes
+    auto vec_mask = [&](const uint4 vv, int li0) -> uint32_t {
+      uint32_t m = 0;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        if (kBF) {
+          const uint32_t sd = pk_sub_sat_u16(raw_key2_bf16(dword_of(vv, d)), rtm1);
+          m |= ((sd & 0xFFFFu) != 0u ? 1u : 0u) << (2 * d);
+          m |= ((sd >> 16) != 0u ? 1u : 0u) << (2 * d + 1);
+        } else {
+          m |= (raw_key_f32(dword_of(vv, d)) >= rt ? 1u : 0u) << d;
+        }
+      }
+      if (li0 < live_lo || li0 + VEC > live_hi) {  // partial vector
+        uint32_t live = 0;
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) live |= (li0 + q >= live_lo && li0 + q < live_hi ? 1u : 0u) << q;
+        m &= live;
+      }
+      return m;
     };
-
-    if (t == 0) {
-      // lower bound L: at least k live elements of this tile have key >= L
-      uint32_t tmax = 0;
-      bool nan_here = false;
-      if (interior) {
-        uint32_t r = 0;
-        if (kBF) {
-          uint32_t m2 = 0;
-#pragma unroll
-          for (int j = 0; j < V; ++j)
-#pragma unroll
-            for (int d = 0; d < 4; ++d) m2 = pk_max_u16(m2, raw_key2_bf16(dword_of(cur[j], d)));
-          r = (m2 & 0xFFFFu) > (m2 >> 16) ? (m2 & 0xFFFFu) : (m2 >> 16);
-        } else {
-#pragma unroll
-          for (int j = 0; j < V; ++j)
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              const uint32_t rk = raw_key_f32(dword_of(cur[j], d));
-              r = rk > r ? rk : r;
-            }
+    auto extract = [&](const uint4 vv, int li0, uint32_t mask) {
+      for (;;) {
+        const bool hc = mask != 0u;
+        if (!__ballot(hc)) break;
+        C cm = 0;
+        if (hc) {
+          const int e = __builtin_ctz(mask);
+          mask &= mask - 1u;
+          cm = S::comp(elem_bits<DT>(vv, e), elem_id(li0 + e));
         }
-        nan_here = r > S::kRawPosInf;
-        tmax = S::raw_to_canon(r);
+        wave_append(hc, cm, reg, wcnt);
       }
-      if (!interior || nan_here) {
-        tmax = 0;
+    };
+    // pass 1: stage every flagged vector (one that may hold a candidate) in LDS
+    int nst = 0;         // vectors this lane flagged
+    uint32_t slots = 0;  // slot numbers j of the staged ones, 4 bits each
 #pragma unroll
-        for (int j = 0; j < V; ++j)
-#pragma unroll
-          for (int q = 0; q < VEC; ++q) {
-            bool pass;
-            const C cm = slow_comp(j, q, 0u, pass);
-            const uint32_t kk = S::comp_key(cm);
-            tmax = pass && kk > tmax ? kk : tmax;
+    for (int j = 0; j < MAXV; ++j) {
+      const bool flag = !vec_dead(j) && raw_flag(vec_raw_max(raw[j]));
+      if (__ballot(flag)) {
+        if (flag) {
+          if (nst < kStage) {
+            stage[nst * kNT + tid] = raw[j];
+            slots |= (uint32_t)j << (4 * nst);
           }
+          ++nst;
+        }
       }
-      if (nan_here) sh.nan_seen = 1;
-      const uint32_t srt = wave_sort64_u32_desc(tmax);
-      const uint32_t wl = readlane_u32(srt, (k + kWaves - 1) / kWaves - 1);
-      if (l == 0) sh.wl[w] = wl;
-      __syncthreads();
-      uint32_t L = sh.wl[0];
-#pragma unroll
-      for (int i = 1; i < kWaves; ++i) L = sh.wl[i] < L ? sh.wl[i] : L;
-      thr = kBF ? L : (L > 1u ? L : 1u);
-      nan_mode = sh.nan_seen != 0;
     }
-
-    // ---- append this tile's candidates (wave-local compaction) -------------
-    const int wcnt0 = wcnt;
-    const bool fast = interior && !nan_mode && (!kBF || thr >= 1u);
-    if (fast) {
-      const uint32_t rt = S::raw_thr(thr);
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        uint32_t rk[4];
-        bool flag;
-        uint32_t rtm1 = 0;
-        if (kBF) {
-          rtm1 = (rt - 1u) * 0x10001u;
-#pragma unroll
-          for (int d = 0; d < 4; ++d) rk[d] = raw_key2_bf16(dword_of(cur[j], d));
-          const uint32_t mx = pk_max_u16(pk_max_u16(rk[0], rk[1]), pk_max_u16(rk[2], rk[3]));
-          flag = pk_sub_sat_u16(mx, rtm1) != 0u;
-        } else {
-#pragma unroll
-          for (int d = 0; d < 4; ++d) rk[d] = raw_key_f32(dword_of(cur[j], d));
-          const uint32_t m01 = rk[0] > rk[1] ? rk[0] : rk[1];
-          const uint32_t m23 = rk[2] > rk[3] ? rk[2] : rk[3];
-          flag = (m01 > m23 ? m01 : m23) >= rt;
-        }
-        if (__ballot(flag)) {
-          uint32_t mask = 0;
-          if (flag) {
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              if (kBF) {
-                const uint32_t sd = pk_sub_sat_u16(rk[d], rtm1);
-                mask |= ((sd & 0xFFFFu) != 0u ? 1u : 0u) << (2 * d);
-                mask |= ((sd >> 16) != 0u ? 1u : 0u) << (2 * d + 1);
-              } else {
-                mask |= (rk[d] >= rt ? 1u : 0u) << d;
-              }
-            }
-          }
-          for (;;) {
-            const bool have = mask != 0u;
-            if (!__ballot(have)) break;
-            C cm = 0;
-            if (have) {
-              const int e = __builtin_ctz(mask);
-              mask &= mask - 1u;
-              const int64_t eidx = e_base + (int64_t)j * kNT * VEC + e;
-              if (kBF) {
-                const uint32_t word = dword_of(cur[j], e >> 1);
-                cm = S::comp((e & 1) ? (word >> 16) : (word & 0xFFFFu), elem_id(eidx));
-              } else {
-                cm = S::comp(dword_of(cur[j], e), elem_id(eidx));
-              }
-            }
-            wave_append(have, cm, reg, wcnt);
-          }
-        }
+    // pass 2: extract the candidates of the staged vectors
+    for (int i = 0; i < kStage; ++i) {
+      const bool have = i < nst;
+      if (!__ballot(have)) break;
+      uint32_t mask = 0;
+      uint4 vv = make_uint4(0u, 0u, 0u, 0u);
+      int li0 = 0;
+      if (have) {
+        vv = stage[i * kNT + tid];
+        li0 = lbase + (int)((slots >> (4 * i)) & 15u) * kNT * VEC;
+        mask = vec_mask(vv, li0);
       }
-    } else {
+      extract(vv, li0, mask);
+    }
+    // lanes that flagged more vectors than they could stage take the rest in place
+    const bool over = nst > kStage;
+    if (__ballot(over)) {
+      const int last = (int)((slots >> (4 * (kStage - 1))) & 15u);
 #pragma unroll
-      for (int j = 0; j < V; ++j)
+      for (int j = 0; j < MAXV; ++j) {
+        const int li0 = lbase + j * kNT * VEC;
+        const bool take = over && j > last && !vec_dead(j) && raw_flag(vec_raw_max(raw[j]));
+        if (__ballot(take)) extract(raw[j], li0, take ? vec_mask(raw[j], li0) : 0u);
+      }
+    }
+  } else {
 #pragma unroll
+    for (int j = 0; j < MAXV; ++j)
+#pragma unroll 1
+      for (int q = 0; q < VEC; ++q) {
+        bool pass;
+        const C cm = slow_comp_v(raw[j], j, q, thr, pass);
+        wave_append(pass, cm, reg, wcnt);
+      }
+  }
+  if (l == 0) sh.wc[0][w] = wcnt;
+  __syncthreads();
+  bool overflow = false;
+#pragma unroll
+  for (int q = 0; q < kWaves; ++q) overflow |= sh.wc[0][q] > kWaveCap;
+  const int* cnt = sh.wc[0];  // sh.wc[1] if the exact path runs
+
+  if (overflow) {
+    // Heavy ties: keep only the exact top-k among the passing elements
+    // (composites are distinct, so exactly k pass the bisection).
+    C prefix = 0;
+    for (int bit = (int)sizeof(C) * 8 - 1; bit >= 0; --bit) {
+      const C probe = prefix | ((C)1 << bit);
+      int cc = 0;
+#pragma unroll
+      for (int j = 0; j < MAXV; ++j)
+#pragma unroll 1
         for (int q = 0; q < VEC; ++q) {
           bool pass;
-          const C cm = slow_comp(j, q, thr, pass);
-          wave_append(pass, cm, reg, wcnt);
+          const C cm = slow_comp_v(raw[j], j, q, thr, pass);
+          cc += pass && cm >= probe;
         }
+      if (block_sum(cc, sh.red) >= k) prefix = probe;
     }
-    if (l == 0) sh.wc[t & 1][w] = wcnt;
+    wcnt = 0;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j)
+#pragma unroll 1
+      for (int q = 0; q < VEC; ++q) {
+        bool pass;
+        const C cm = slow_comp_v(raw[j], j, q, thr, pass);
+        wave_append(pass && cm >= prefix, cm, reg, wcnt);
+      }
+    if (l == 0) sh.wc[1][w] = wcnt;
     __syncthreads();
-    bool overflow = false;
-#pragma unroll
-    for (int q = 0; q < kWaves; ++q) {
-      cnt[q] = sh.wc[t & 1][q];
-      overflow |= cnt[q] > kWaveCap;
-    }
-
-    if (overflow) {
-      // Heavy ties: keep only this tile's exact top-k among the passing
-      // elements (composites are distinct, so exactly k pass the bisection).
-      C prefix = 0;
-      for (int bit = (int)sizeof(C) * 8 - 1; bit >= 0; --bit) {
-        const C probe = prefix | ((C)1 << bit);
-        int cc = 0;
-#pragma unroll
-        for (int j = 0; j < V; ++j)
-#pragma unroll
-          for (int q = 0; q < VEC; ++q) {
-            bool pass;
-            const C cm = slow_comp(j, q, thr, pass);
-            cc += pass && cm >= probe;
-          }
-        if (block_sum(cc, sh.red) >= k) prefix = probe;
-      }
-      wcnt = wcnt0;
-#pragma unroll
-      for (int j = 0; j < V; ++j)
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-          bool pass;
-          const C cm = slow_comp(j, q, thr, pass);
-          wave_append(pass && cm >= prefix, cm, reg, wcnt);
-        }
-      if (l == 0) sh.wc[t & 1][w] = wcnt;
-      __syncthreads();
-#pragma unroll
-      for (int q = 0; q < kWaves; ++q) cnt[q] = sh.wc[t & 1][q];
-    }
-
-    int cmax = cnt[0], total = cnt[0];
-#pragma unroll
-    for (int q = 1; q < kWaves; ++q) {
-      cmax = cnt[q] > cmax ? cnt[q] : cmax;
-      total += cnt[q];
-    }
-    if (total >= k && ((a.early_cut && t == 0 && ntiles > 1) || cmax > a.refresh_at)) {
-      // cut to the exact top-k so far (spread over the wave regions); later
-      // elements need a strictly larger key than the k-th
-      block_select(sh, cnt);
-      const int share = (k + kWaves - 1) / kWaves;
-      for (int i = l; i < share; i += kWave) {
-        const int src = w * share + i;
-        if (src < k) reg[i] = sh.list[src];
-      }
-#pragma unroll
-      for (int q = 0; q < kWaves; ++q) {
-        const int lo = q * share, hi = (q + 1) * share < k ? (q + 1) * share : k;
-        cnt[q] = hi > lo ? hi - lo : 0;
-      }
-      wcnt = cnt[w == 0 ? 0 : w == 1 ? 1 : w == 2 ? 2 : 3];
-      thr = S::comp_key(sh.list[k - 1]) + 1u;
-      __syncthreads();
-    }
-#pragma unroll
-    for (int j = 0; j < V; ++j) cur[j] = nxt[j];
+    cnt = sh.wc[1];
   }
 
   block_select(sh, cnt);
@@ -648,13 +661,12 @@ __global__ __launch_bounds__(kWave) void top_p_sample_kernel(const void* logits,
 // Host side.
 // ---------------------------------------------------------------------------
 struct Plan {
+  int maxv;
   int nseg;
   int64_t vps;
 };
 
 struct Tuning {
-  int refresh_at = 192;
-  int early_cut = 0;
   int target_blocks = kTargetBlocks;
 };
 
@@ -668,39 +680,40 @@ static int env_int(const char* name, int dflt, int lo, int hi) {
 static const Tuning& tuning() {
   static const Tuning t = [] {
     Tuning r;
-    r.refresh_at = env_int("TALLAX_SEL_REFRESH", r.refresh_at, 8, kWaveCap - 8);
-    r.early_cut = env_int("TALLAX_SEL_EARLY_CUT", r.early_cut, 0, 1);
     r.target_blocks = env_int("TALLAX_SEL_BLOCKS", r.target_blocks, 1, 1 << 20);
     return r;
   }();
   return t;
 }
 
-// Segments: enough workgroups for ~4 per CU, whole tiles per segment, at
-// most kMaxSeg segments per row; bf16 segments hold at most 7 tiles so that
-// segment-local indices fit the 16-bit field of the u32 composites.
+// Segments: MAXV vectors per thread, MAXV in {4, 8, 16}: the largest that
+// still gives ~4 workgroups per CU over the launch (the smallest otherwise).
+// bf16 segments hold < 65536 elements so segment-local indices fit the
+// 16-bit field of the u32 composites (16 * 256 * 8 = 32768).
 static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
   const int vec = dt == kF32 ? 4 : 8;
-  const int V = dt == kF32 ? kVF32 : kVBF16;
-  const int64_t max_tiles = dt == kF32 ? ((int64_t)1 << 40) : 7;
-  const int64_t tile = (int64_t)kNT * V;
   const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
-  const int64_t tiles = (nv + tile - 1) / tile;
-  int64_t nseg = (tuning().target_blocks + rows - 1) / rows;
-  if (nseg > kMaxSeg) nseg = kMaxSeg;
-  if (nseg > tiles) nseg = tiles;
-  const int64_t min_seg = (tiles + max_tiles - 1) / max_tiles;
-  if (nseg < min_seg) nseg = min_seg;
-  if (nseg < 1) nseg = 1;
-  int64_t vps = (nv + nseg - 1) / nseg;
-  vps = (vps + tile - 1) / tile * tile;
-  nseg = (nv + vps - 1) / vps;
+  static const int kOpts[3] = {16, 8, 4};
+  int maxv = 4;
+  for (int o = 0; o < 3; ++o) {
+    const int64_t per = (int64_t)kNT * kOpts[o];
+    const int64_t nseg = (nv + per - 1) / per;
+    if (rows * nseg >= tuning().target_blocks && nseg <= kMaxSeg) { maxv = kOpts[o]; break; }
+  }
+  int64_t per = (int64_t)kNT * maxv;
+  int64_t nseg = (nv + per - 1) / per;
+  while (nseg > kMaxSeg && maxv < 16) {
+    maxv *= 2;
+    per = (int64_t)kNT * maxv;
+    nseg = (nv + per - 1) / per;
+  }
   if (nseg > kMaxSeg) {
-    set_error("row length %lld exceeds this build's limit for the dtype", (long long)cols);
+    set_error("row length %lld exceeds this build's limit of %d segments", (long long)cols, kMaxSeg);
     return kUnsupported;
   }
+  p->maxv = maxv;
   p->nseg = (int)nseg;
-  p->vps = vps;
+  p->vps = per;
   return kOk;
 }
 
@@ -709,12 +722,17 @@ static size_t ws_bytes_for(int64_t rows, const Plan& p) {
   return (size_t)rows * p.nseg * kRun * sizeof(uint64_t);
 }
 
-template <int DT, bool SAMPLE>
-static int launch_select(SelArgs a, hipStream_t s, const char* what) {
-  a.refresh_at = tuning().refresh_at;
-  a.early_cut = tuning().early_cut;
-  hipLaunchKernelGGL((seg_select_kernel<DT, SAMPLE>), dim3((unsigned)a.nseg, (unsigned)a.rows),
+template <int DT, int MAXV, bool SAMPLE>
+static void launch_a(const SelArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((seg_select_kernel<DT, MAXV, SAMPLE>), dim3((unsigned)a.nseg, (unsigned)a.rows),
                      dim3(kNT), 0, s, a);
+}
+
+template <int DT, bool SAMPLE>
+static int launch_select(const SelArgs& a, int maxv, hipStream_t s, const char* what) {
+  if (maxv == 16) launch_a<DT, 16, SAMPLE>(a, s);
+  else if (maxv == 8) launch_a<DT, 8, SAMPLE>(a, s);
+  else launch_a<DT, 4, SAMPLE>(a, s);
   int st = launch_status(what);
   if (st || a.nseg == 1) return st;
   hipLaunchKernelGGL((seg_merge_kernel<DT, SAMPLE>), dim3((unsigned)a.rows), dim3(kWave), 0, s, a);
@@ -777,8 +795,8 @@ int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k,
   a.nseg = p.nseg; a.vps = p.vps;
   a.out_vals = out_vals; a.out_idx = out_idx;
   a.ws_lists = (uint64_t*)workspace;
-  return dtype == kF32 ? launch_select<kF32, false>(a, stream, "tallax_topk")
-                       : launch_select<kBF16, false>(a, stream, "tallax_topk");
+  return dtype == kF32 ? launch_select<kF32, false>(a, p.maxv, stream, "tallax_topk")
+                       : launch_select<kBF16, false>(a, p.maxv, stream, "tallax_topk");
 }
 
 size_t tallax_sample_workspace_size(int64_t rows, int64_t vocab, int dtype) {
@@ -813,8 +831,8 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
   a.replace_f32 = rf;
   a.replace_in_dtype = dtype == kBF16 ? round_to_bf16(rf) : rf;
   a.out_tokens = out_tokens;
-  return dtype == kF32 ? launch_select<kF32, true>(a, stream, "tallax_fused_topk_topp_sample")
-                       : launch_select<kBF16, true>(a, stream, "tallax_fused_topk_topp_sample");
+  return dtype == kF32 ? launch_select<kF32, true>(a, p.maxv, stream, "tallax_fused_topk_topp_sample")
+                       : launch_select<kBF16, true>(a, p.maxv, stream, "tallax_fused_topk_topp_sample");
 }
 
 int tallax_top_p_and_sample(const void* topk_logits, int dtype, const int32_t* topk_idx, int64_t rows,

@@ -79,11 +79,29 @@ TOPK_CASES = [
     (6, 20000, 50, "f32", "special"),       # NaN / -inf / -0 / finfo.min
     (7, 70001, 128, "bf16", "normal"),      # odd length bf16 (misaligned rows)
     (32, 201088, 64, "bf16", "normal"),     # the reference's own top-k benchmark shape
+    (4, 131072, 128, "bf16", "sorted_asc"), # structured inputs: weak thread-maxima bound
+    (4, 131072, 50, "f32", "sorted_desc"),
+    (8, 65536, 100, "bf16", "strided_hot"), # one thread owns a candidate in every vector
+    (8, 65536, 100, "f32", "strided_hot"),
+    (16, 128256, 128, "bf16", "normal"),    # vocabulary row of config 4
 ]
 
 
 def _make(rows, cols, kind, seed):
     rng = np.random.default_rng(seed)
+    if kind == "sorted_asc":
+        return np.sort(rng.standard_normal((rows, cols)).astype(np.float32), axis=1)
+    if kind == "sorted_desc":
+        return -np.sort(rng.standard_normal((rows, cols)).astype(np.float32), axis=1)
+    if kind == "strided_hot":
+        # elements (j * 256 + 5) * vec for j = 0..63 are large: with 256 threads
+        # per workgroup and vec elements per 16-byte vector they all fall to one thread
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        for vec in (4, 8):
+            idx = (np.arange(64) * 256 + 5) * vec
+            idx = idx[idx < cols]
+            x[:, idx] = 20.0 + np.arange(idx.size, dtype=np.float32) / 8
+        return x
     if kind == "normal":
         return rng.standard_normal((rows, cols)).astype(np.float32)
     if kind == "ints":
