@@ -49,9 +49,8 @@
 
 namespace tx {
 
-constexpr int kNT = 256;                   // threads per workgroup: 4 wave64s
-constexpr int kWaves = kNT / kWave;
-constexpr int kCap = 1024;                 // LDS candidate slots (4 wave regions)
+constexpr int kNT = 256;                   // threads per segment workgroup: 4 wave64s
+constexpr int kNTRow = 1024;               // threads per whole-row workgroup: 16 wave64s
 constexpr int kMaxK = 128;                 // the reference's limit (top_k.py:438-439)
 constexpr int kRun = 128;                  // list length handed between kernels
 constexpr int kMaxSeg = 32;
@@ -112,7 +111,12 @@ struct ElemT<kBF16> {
   static constexpr uint32_t kMinBits = 0xff7f0000u;  // finfo(bfloat16).min, widened
 };
 
-constexpr int kWaveCap = kCap / kWaves;    // candidate slots per wave
+// candidate slots per wave: 256 in 4-wave workgroups, 128 in 16-wave ones
+template <int NT>
+struct Geo {
+  static constexpr int NW = NT / kWave;
+  static constexpr int WCAP = NT == kNT ? 256 : 128;
+};
 constexpr int kStage = 6;                  // flagged 16-byte vectors staged per thread
 // Tunable (read once from the environment by the host):
 //   TALLAX_SEL_BLOCKS   workgroups aimed for per launch (default 1024).
@@ -131,11 +135,11 @@ constexpr int kStage = 6;                  // flagged 16-byte vectors staged per
 // candidate composite is one u32: key << 16 | (0xFFFF - segment-local index).
 // f32: composite = canonical key << 32 | ~row index (u64).
 // ---------------------------------------------------------------------------
-template <int DT>
+template <int DT, bool WIDE>
 struct Sel;
 
 template <>
-struct Sel<kBF16> {
+struct Sel<kBF16, false> {
   using Comp = uint32_t;
   static constexpr uint32_t kRawPosInf = 0xFF80u;
   __device__ static __forceinline__ uint32_t canon(uint32_t h) {  // h: bf16 bits
@@ -164,8 +168,29 @@ struct Sel<kBF16> {
   }
 };
 
+// bf16 in workgroups of more than 65535 elements: same canonical 16-bit keys,
+// composite = key << 32 | ~row index (u64).
 template <>
-struct Sel<kF32> {
+struct Sel<kBF16, true> {
+  using Comp = uint64_t;
+  static constexpr uint32_t kRawPosInf = 0xFF80u;
+  __device__ static __forceinline__ uint32_t canon(uint32_t h) { return Sel<kBF16, false>::canon(h); }
+  __device__ static __forceinline__ Comp comp(uint32_t h, uint32_t gidx) {
+    return ((uint64_t)canon(h) << 32) | (uint64_t)(~gidx);
+  }
+  __device__ static __forceinline__ uint32_t comp_key(Comp c) { return (uint32_t)(c >> 32); }
+  __device__ static __forceinline__ uint32_t raw_to_canon(uint32_t r) { return Sel<kBF16, false>::raw_to_canon(r); }
+  __device__ static __forceinline__ uint32_t raw_thr(uint32_t thr) { return Sel<kBF16, false>::raw_thr(thr); }
+  __device__ static __forceinline__ uint64_t to_global(Comp c, int64_t) {
+    if (c == 0ull) return 0ull;
+    const uint32_t k16 = (uint32_t)(c >> 32);
+    const uint32_t key = k16 == 0u ? 1u : (k16 >= 0x8000u ? (k16 << 16) : ((k16 << 16) | 0xFFFFu));
+    return make_comp(key, ~(uint32_t)c);
+  }
+};
+
+template <bool WIDE>
+struct Sel<kF32, WIDE> {
   using Comp = uint64_t;
   static constexpr uint32_t kRawPosInf = 0xFF800000u;
   __device__ static __forceinline__ uint32_t canon(uint32_t b) { return select_key(b); }
@@ -180,18 +205,20 @@ struct Sel<kF32> {
   __device__ static __forceinline__ uint64_t to_global(Comp c, int64_t) { return c; }
 };
 
-template <typename C>
+template <typename C, int NT>
 struct SegShared {
-  C cand[kCap];  // wave w owns cand[w * kWaveCap, (w + 1) * kWaveCap)
-  C scratch[kWaves * kRun];
+  static constexpr int NW = Geo<NT>::NW, WCAP = Geo<NT>::WCAP;
+  C cand[NW * WCAP];  // wave w owns cand[w * WCAP, (w + 1) * WCAP)
+  C scratch[NW * kRun];
   C list[kRun];
   uint64_t list64[kRun];
-  uint32_t wl[kWaves];
-  int red[kWaves];
-  int wc[2][kWaves];  // per-wave candidate counts, double-buffered by tile parity
+  uint32_t wl[NW];
+  int red[NW];
+  int wc[2][NW];  // per-wave candidate counts: [0] filter pass, [1] exact path
   int nan_seen;
 };
 
+template <int NW>
 __device__ __forceinline__ int block_sum(int v, int* red) {
   v = wave_sum_i(v);
   __syncthreads();
@@ -199,18 +226,57 @@ __device__ __forceinline__ int block_sum(int v, int* red) {
   __syncthreads();
   int t = 0;
 #pragma unroll
-  for (int i = 0; i < kWaves; ++i) t += red[i];
+  for (int i = 0; i < NW; ++i) t += red[i];
   return t;
 }
 
 // sh.list <- the 128 largest candidates of all wave regions (counts cnt[w] in LDS),
-// descending, zero padded.  Each wave sorts its own region in runs of 128,
-// then the four partial lists are merged as a two-level tree.
-template <typename C>
-__device__ __forceinline__ void block_select(SegShared<C>& sh, const int* cnt) {
+// descending, zero padded.  Small sets use rank selection; larger ones are
+// sorted per wave in runs of 128 and the per-wave lists merged as a binary
+// tree (log2(waves) levels).
+// Rank selection for small candidate sets (C <= kRankMax): candidates are
+// compacted into sh.scratch, then the thread holding candidate x counts the
+// candidates larger than x (broadcast LDS reads, all distinct) and writes x
+// to sh.list[rank] when rank < 128.
+constexpr int kRankMax = 512;
+
+template <typename C, int NT>
+__device__ __forceinline__ void rank_select(SegShared<C, NT>& sh, const int* cnt, int total) {
+  constexpr int NW = Geo<NT>::NW, WCAP = Geo<NT>::WCAP;
+  const int tid = threadIdx.x, w = tid / kWave, l = lane_id();
+  int off = 0;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) off += q < w ? cnt[q] : 0;
+  const int cw = cnt[w];
+  for (int i = l; i < cw; i += kWave) sh.scratch[off + i] = sh.cand[w * WCAP + i];
+  for (int i = tid; i < kRun; i += NT) sh.list[i] = 0;
+  __syncthreads();
+  for (int p = tid; p < total; p += NT) {
+    const C x = sh.scratch[p];
+    int r = 0;
+    int i = 0;
+    for (; i + 4 <= total; i += 4) {
+      r += (sh.scratch[i] > x) + (sh.scratch[i + 1] > x) + (sh.scratch[i + 2] > x) + (sh.scratch[i + 3] > x);
+    }
+    for (; i < total; ++i) r += sh.scratch[i] > x;
+    if (r < kRun) sh.list[r] = x;
+  }
+  __syncthreads();
+}
+
+template <typename C, int NT>
+__device__ __forceinline__ void block_select(SegShared<C, NT>& sh, const int* cnt) {
+  constexpr int NW = Geo<NT>::NW, WCAP = Geo<NT>::WCAP;
+  int total = 0;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) total += cnt[q];
+  if (total <= kRankMax) {
+    rank_select(sh, cnt, total);
+    return;
+  }
   const int w = threadIdx.x / kWave, l = lane_id();
   const int cw = cnt[w];
-  const C* reg = sh.cand + w * kWaveCap;
+  const C* reg = sh.cand + w * WCAP;
   C acc[2] = {0, 0};
   for (int r = 0; r * kRun < cw; ++r) {
     C c[2];
@@ -227,25 +293,19 @@ __device__ __forceinline__ void block_select(SegShared<C>& sh, const int* cnt) {
       wave_merge128_desc(acc, c);
     }
   }
-  if (w & 1) {
-    sh.scratch[w * kRun + l] = acc[0];
-    sh.scratch[w * kRun + kWave + l] = acc[1];
-  }
-  __syncthreads();
-  if (!(w & 1) && (w == 0 ? cnt[1] : cnt[3]) > 0) {
-    const C b[2] = {sh.scratch[(w + 1) * kRun + l], sh.scratch[(w + 1) * kRun + kWave + l]};
-    wave_merge128_desc(acc, b);
-  }
-  if (w == 2) {
-    sh.scratch[w * kRun + l] = acc[0];
-    sh.scratch[w * kRun + kWave + l] = acc[1];
-  }
-  __syncthreads();
-  if (w == 0) {
-    if (cnt[2] + cnt[3] > 0) {
-      const C b[2] = {sh.scratch[2 * kRun + l], sh.scratch[2 * kRun + kWave + l]};
+#pragma unroll
+  for (int st = 1; st < NW; st <<= 1) {
+    if ((w & (2 * st - 1)) == st) {
+      sh.scratch[w * kRun + l] = acc[0];
+      sh.scratch[w * kRun + kWave + l] = acc[1];
+    }
+    __syncthreads();
+    if ((w & (2 * st - 1)) == 0) {
+      const C b[2] = {sh.scratch[(w + st) * kRun + l], sh.scratch[(w + st) * kRun + kWave + l]};
       wave_merge128_desc(acc, b);
     }
+  }
+  if (w == 0) {
     sh.list[l] = acc[0];
     sh.list[kWave + l] = acc[1];
   }
@@ -255,14 +315,14 @@ __device__ __forceinline__ void block_select(SegShared<C>& sh, const int* cnt) {
 // Wave-level stream compaction: lanes with `pred` append `comp` to their
 // wave's region at wcnt + (rank among active lanes).  `wcnt` is wave-uniform;
 // entries beyond the region are counted but not stored.
-template <typename C>
+template <int WCAP, typename C>
 __device__ __forceinline__ void wave_append(bool pred, C comp, C* reg, int& wcnt) {
   const uint64_t m = __ballot(pred);
   if (m) {
     if (pred) {
       const int off = wcnt + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-      if (off < kWaveCap) reg[off] = comp;
+      if (off < WCAP) reg[off] = comp;
     }
     wcnt += (int)__popcll(m);
   }
@@ -345,16 +405,18 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
 // front, filtered once against the thread-maxima lower bound, and reduced to
 // its sorted top-128 by one block selection.
 // ---------------------------------------------------------------------------
-template <int DT, int MAXV, bool SAMPLE>
-__global__ __launch_bounds__(kNT) __attribute__((amdgpu_waves_per_eu(3, 8)))
+template <int DT, int MAXV, int NT, bool SAMPLE>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8)))
 void seg_select_kernel(SelArgs a) {
   using T = ElemT<DT>;
-  using S = Sel<DT>;
+  constexpr bool kWide = NT * MAXV * T::VEC > 65535;  // block-local bf16 indices need > 16 bits
+  using S = Sel<DT, kWide>;
   using C = typename S::Comp;
   constexpr bool kBF = DT == kBF16;
   constexpr int VEC = T::VEC, ES = T::ES;
-  __shared__ SegShared<C> sh;
-  __shared__ uint4 stage[kStage * kNT];  // flagged vectors, slot-major
+  constexpr int NW = Geo<NT>::NW, WCAP = Geo<NT>::WCAP;
+  __shared__ SegShared<C, NT> sh;
+  __shared__ uint4 stage[kStage * NT];  // flagged vectors, slot-major
   const int tid = threadIdx.x;
   const int w = tid / kWave, l = lane_id();
   const int seg = blockIdx.x;
@@ -367,41 +429,41 @@ void seg_select_kernel(SelArgs a) {
   const int64_t s0 = (int64_t)seg * a.vps;
   const int64_t s1 = s0 + a.vps < nv ? s0 + a.vps : nv;
   const int64_t seg_e0 = s0 * VEC - rv.mis;  // element index of the segment's first slot
-  C* reg = sh.cand + w * kWaveCap;
+  C* reg = sh.cand + w * WCAP;
   if (tid == 0) sh.nan_seen = 0;
 
   uint4 raw[MAXV];
 #pragma unroll
   for (int j = 0; j < MAXV; ++j) {
-    const int64_t v = s0 + (int64_t)j * kNT + tid;
+    const int64_t v = s0 + (int64_t)j * NT + tid;
     raw[j] = v < s1 ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u);
   }
-  // Segment-local slot index of (j, q): lbase + j * kNT * VEC + q.  Live slots
+  // Segment-local slot index of (j, q): lbase + j * NT * VEC + q.  Live slots
   // (inside the row and the segment) are those in [live_lo, live_hi).
   const int lbase = tid * VEC;
   const int64_t seg_elems = (s1 - s0) * VEC;
   const int live_lo = seg_e0 < 0 ? (int)(-seg_e0) : 0;
   const int live_hi = (int)(a.cols - seg_e0 < seg_elems ? a.cols - seg_e0 : seg_elems);
   const uint32_t gbase = (uint32_t)seg_e0;  // row index = gbase + local index (mod 2^32)
-  // id stored in a composite: segment-local index (bf16) or row index (f32)
-  auto elem_id = [&](int lidx) -> uint32_t { return kBF ? (uint32_t)lidx : gbase + (uint32_t)lidx; };
+  // id stored in a composite: block-local index (narrow bf16) or row index
+  auto elem_id = [&](int lidx) -> uint32_t { return (kBF && !kWide) ? (uint32_t)lidx : gbase + (uint32_t)lidx; };
   // canonical composite of slot (j, q) (vector j passed in vv) and whether it
   // is a live element >= th
   auto slow_comp_v = [&](const uint4 vv, int j, int q, uint32_t th, bool& pass) -> C {
-    const int li = lbase + j * kNT * VEC + q;
+    const int li = lbase + j * NT * VEC + q;
     const uint32_t bits = elem_bits<DT>(vv, q);
     pass = li >= live_lo && li < live_hi && S::canon(bits) >= th;
     return S::comp(bits, elem_id(li));
   };
 
-  // Vector j of this thread covers local slots [lbase + j*kNT*VEC, + VEC):
+  // Vector j of this thread covers local slots [lbase + j*NT*VEC, + VEC):
   // "full" if all of them are live elements, "dead" if none is.
   auto vec_full = [&](int j) -> bool {
-    const int li0 = lbase + j * kNT * VEC;
+    const int li0 = lbase + j * NT * VEC;
     return li0 >= live_lo && li0 + VEC <= live_hi;
   };
   auto vec_dead = [&](int j) -> bool {
-    const int li0 = lbase + j * kNT * VEC;
+    const int li0 = lbase + j * NT * VEC;
     return li0 >= live_hi || li0 + VEC <= live_lo;
   };
   // raw filter max of a vector (raw keys, see Sel): packed for bf16
@@ -425,13 +487,19 @@ void seg_select_kernel(SelArgs a) {
   // ---- lower bound L: at least k live elements are >= L --------------------
   uint32_t tmax = 0;
   bool nan_here = false;
+  // raw max of each vector (bf16: packed pair), kept for the filter pass when
+  // registers allow (MAXV <= 8), recomputed otherwise
+  constexpr bool kKeep = MAXV <= 8;
+  uint32_t vmax[kKeep ? MAXV : 1];
+  auto vmax_of = [&](int j) -> uint32_t { return kKeep ? vmax[kKeep ? j : 0] : vec_raw_max(raw[j]); };
   {
     uint32_t r2 = 0;     // raw max over full vectors (bf16: packed pair)
     uint32_t cpart = 0;  // canonical max over live elements of partial vectors
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
+      const uint32_t m = vec_raw_max(raw[j]);
+      if (kKeep) vmax[kKeep ? j : 0] = m;
       if (vec_full(j)) {
-        const uint32_t m = vec_raw_max(raw[j]);
         r2 = kBF ? pk_max_u16(r2, m) : (m > r2 ? m : r2);
       } else if (!vec_dead(j)) {
 #pragma unroll 1
@@ -462,12 +530,12 @@ void seg_select_kernel(SelArgs a) {
   }
   if (nan_here) sh.nan_seen = 1;
   const uint32_t srt = wave_sort64_u32_desc(tmax);
-  const uint32_t wl = readlane_u32(srt, (k + kWaves - 1) / kWaves - 1);
+  const uint32_t wl = readlane_u32(srt, (k + NW - 1) / NW - 1);  // this wave's quota of maxima
   if (l == 0) sh.wl[w] = wl;
   __syncthreads();
   uint32_t L = sh.wl[0];
 #pragma unroll
-  for (int i = 1; i < kWaves; ++i) L = sh.wl[i] < L ? sh.wl[i] : L;
+  for (int i = 1; i < NW; ++i) L = sh.wl[i] < L ? sh.wl[i] : L;
   const uint32_t thr = kBF ? L : (L > 1u ? L : 1u);  // candidates: live elements with key >= thr
   const bool nan_mode = sh.nan_seen != 0;
 
@@ -509,7 +577,7 @@ void seg_select_kernel(SelArgs a) {
           mask &= mask - 1u;
           cm = S::comp(elem_bits<DT>(vv, e), elem_id(li0 + e));
         }
-        wave_append(hc, cm, reg, wcnt);
+        wave_append<WCAP>(hc, cm, reg, wcnt);
       }
     };
     // pass 1: stage every flagged vector (one that may hold a candidate) in LDS
@@ -517,11 +585,11 @@ void seg_select_kernel(SelArgs a) {
     uint32_t slots = 0;  // slot numbers j of the staged ones, 4 bits each
 #pragma unroll
     for (int j = 0; j < MAXV; ++j) {
-      const bool flag = !vec_dead(j) && raw_flag(vec_raw_max(raw[j]));
+      const bool flag = !vec_dead(j) && raw_flag(vmax_of(j));
       if (__ballot(flag)) {
         if (flag) {
           if (nst < kStage) {
-            stage[nst * kNT + tid] = raw[j];
+            stage[nst * NT + tid] = raw[j];
             slots |= (uint32_t)j << (4 * nst);
           }
           ++nst;
@@ -536,8 +604,8 @@ void seg_select_kernel(SelArgs a) {
       uint4 vv = make_uint4(0u, 0u, 0u, 0u);
       int li0 = 0;
       if (have) {
-        vv = stage[i * kNT + tid];
-        li0 = lbase + (int)((slots >> (4 * i)) & 15u) * kNT * VEC;
+        vv = stage[i * NT + tid];
+        li0 = lbase + (int)((slots >> (4 * i)) & 15u) * NT * VEC;
         mask = vec_mask(vv, li0);
       }
       extract(vv, li0, mask);
@@ -548,8 +616,8 @@ void seg_select_kernel(SelArgs a) {
       const int last = (int)((slots >> (4 * (kStage - 1))) & 15u);
 #pragma unroll
       for (int j = 0; j < MAXV; ++j) {
-        const int li0 = lbase + j * kNT * VEC;
-        const bool take = over && j > last && !vec_dead(j) && raw_flag(vec_raw_max(raw[j]));
+        const int li0 = lbase + j * NT * VEC;
+        const bool take = over && j > last && !vec_dead(j) && raw_flag(vmax_of(j));
         if (__ballot(take)) extract(raw[j], li0, take ? vec_mask(raw[j], li0) : 0u);
       }
     }
@@ -560,14 +628,14 @@ void seg_select_kernel(SelArgs a) {
       for (int q = 0; q < VEC; ++q) {
         bool pass;
         const C cm = slow_comp_v(raw[j], j, q, thr, pass);
-        wave_append(pass, cm, reg, wcnt);
+        wave_append<WCAP>(pass, cm, reg, wcnt);
       }
   }
   if (l == 0) sh.wc[0][w] = wcnt;
   __syncthreads();
   bool overflow = false;
 #pragma unroll
-  for (int q = 0; q < kWaves; ++q) overflow |= sh.wc[0][q] > kWaveCap;
+  for (int q = 0; q < NW; ++q) overflow |= sh.wc[0][q] > WCAP;
   const int* cnt = sh.wc[0];  // sh.wc[1] if the exact path runs
 
   if (overflow) {
@@ -585,7 +653,7 @@ void seg_select_kernel(SelArgs a) {
           const C cm = slow_comp_v(raw[j], j, q, thr, pass);
           cc += pass && cm >= probe;
         }
-      if (block_sum(cc, sh.red) >= k) prefix = probe;
+      if (block_sum<NW>(cc, sh.red) >= k) prefix = probe;
     }
     wcnt = 0;
 #pragma unroll
@@ -594,7 +662,7 @@ void seg_select_kernel(SelArgs a) {
       for (int q = 0; q < VEC; ++q) {
         bool pass;
         const C cm = slow_comp_v(raw[j], j, q, thr, pass);
-        wave_append(pass && cm >= prefix, cm, reg, wcnt);
+        wave_append<WCAP>(pass && cm >= prefix, cm, reg, wcnt);
       }
     if (l == 0) sh.wc[1][w] = wcnt;
     __syncthreads();
@@ -602,13 +670,13 @@ void seg_select_kernel(SelArgs a) {
   }
 
   block_select(sh, cnt);
-  for (int i = tid; i < kRun; i += kNT) sh.list64[i] = S::to_global(sh.list[i], seg_e0);
+  for (int i = tid; i < kRun; i += NT) sh.list64[i] = S::to_global(sh.list[i], seg_e0);
   __syncthreads();
   if (a.nseg == 1) {
     finalize_row<DT, SAMPLE>(a, row, sh.list64);
   } else {
     uint64_t* dst = a.ws_lists + ((size_t)row * a.nseg + seg) * kRun;
-    for (int i = tid; i < kRun; i += kNT) dst[i] = sh.list64[i];
+    for (int i = tid; i < kRun; i += NT) dst[i] = sh.list64[i];
   }
 }
 
@@ -661,6 +729,7 @@ __global__ __launch_bounds__(kWave) void top_p_sample_kernel(const void* logits,
 // Host side.
 // ---------------------------------------------------------------------------
 struct Plan {
+  int nt;  // threads per workgroup: kNT (segments) or kNTRow (whole rows)
   int maxv;
   int nseg;
   int64_t vps;
@@ -686,14 +755,24 @@ static const Tuning& tuning() {
   return t;
 }
 
-// Segments: MAXV vectors per thread, MAXV in {4, 8, 16}: the largest that
-// still gives ~4 workgroups per CU over the launch (the smallest otherwise).
-// bf16 segments hold < 65536 elements so segment-local indices fit the
-// 16-bit field of the u32 composites (16 * 256 * 8 = 32768).
+// Work split.  A row of nv 16-byte vectors is handled either
+//   * whole by one 1024-thread workgroup (up to 16 vectors per thread) when
+//     that gives enough workgroups (>= 128 rows): no merge kernel at all; or
+//   * in segments of 256 x MAXV vectors, MAXV in {4, 8, 16}: the largest that
+//     still gives ~4 workgroups per CU over the launch, then a per-row merge.
 static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
   const int vec = dt == kF32 ? 4 : 8;
   const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
   static const int kOpts[3] = {16, 8, 4};
+  if (rows >= 128 && nv <= (int64_t)kNTRow * 16) {
+    int maxv = 16;
+    while (maxv > 4 && (int64_t)kNTRow * (maxv / 2) >= nv) maxv /= 2;
+    p->nt = kNTRow;
+    p->maxv = maxv;
+    p->nseg = 1;
+    p->vps = (int64_t)kNTRow * maxv;
+    return kOk;
+  }
   int maxv = 4;
   for (int o = 0; o < 3; ++o) {
     const int64_t per = (int64_t)kNT * kOpts[o];
@@ -711,6 +790,7 @@ static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
     set_error("row length %lld exceeds this build's limit of %d segments", (long long)cols, kMaxSeg);
     return kUnsupported;
   }
+  p->nt = kNT;
   p->maxv = maxv;
   p->nseg = (int)nseg;
   p->vps = per;
@@ -722,17 +802,23 @@ static size_t ws_bytes_for(int64_t rows, const Plan& p) {
   return (size_t)rows * p.nseg * kRun * sizeof(uint64_t);
 }
 
-template <int DT, int MAXV, bool SAMPLE>
+template <int DT, int MAXV, int NT, bool SAMPLE>
 static void launch_a(const SelArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((seg_select_kernel<DT, MAXV, SAMPLE>), dim3((unsigned)a.nseg, (unsigned)a.rows),
-                     dim3(kNT), 0, s, a);
+  hipLaunchKernelGGL((seg_select_kernel<DT, MAXV, NT, SAMPLE>), dim3((unsigned)a.nseg, (unsigned)a.rows),
+                     dim3(NT), 0, s, a);
 }
 
 template <int DT, bool SAMPLE>
-static int launch_select(const SelArgs& a, int maxv, hipStream_t s, const char* what) {
-  if (maxv == 16) launch_a<DT, 16, SAMPLE>(a, s);
-  else if (maxv == 8) launch_a<DT, 8, SAMPLE>(a, s);
-  else launch_a<DT, 4, SAMPLE>(a, s);
+static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const char* what) {
+  if (p.nt == kNTRow) {
+    if (p.maxv == 16) launch_a<DT, 16, kNTRow, SAMPLE>(a, s);
+    else if (p.maxv == 8) launch_a<DT, 8, kNTRow, SAMPLE>(a, s);
+    else launch_a<DT, 4, kNTRow, SAMPLE>(a, s);
+  } else {
+    if (p.maxv == 16) launch_a<DT, 16, kNT, SAMPLE>(a, s);
+    else if (p.maxv == 8) launch_a<DT, 8, kNT, SAMPLE>(a, s);
+    else launch_a<DT, 4, kNT, SAMPLE>(a, s);
+  }
   int st = launch_status(what);
   if (st || a.nseg == 1) return st;
   hipLaunchKernelGGL((seg_merge_kernel<DT, SAMPLE>), dim3((unsigned)a.rows), dim3(kWave), 0, s, a);
@@ -795,8 +881,8 @@ int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k,
   a.nseg = p.nseg; a.vps = p.vps;
   a.out_vals = out_vals; a.out_idx = out_idx;
   a.ws_lists = (uint64_t*)workspace;
-  return dtype == kF32 ? launch_select<kF32, false>(a, p.maxv, stream, "tallax_topk")
-                       : launch_select<kBF16, false>(a, p.maxv, stream, "tallax_topk");
+  return dtype == kF32 ? launch_select<kF32, false>(a, p, stream, "tallax_topk")
+                       : launch_select<kBF16, false>(a, p, stream, "tallax_topk");
 }
 
 size_t tallax_sample_workspace_size(int64_t rows, int64_t vocab, int dtype) {
@@ -831,8 +917,8 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
   a.replace_f32 = rf;
   a.replace_in_dtype = dtype == kBF16 ? round_to_bf16(rf) : rf;
   a.out_tokens = out_tokens;
-  return dtype == kF32 ? launch_select<kF32, true>(a, p.maxv, stream, "tallax_fused_topk_topp_sample")
-                       : launch_select<kBF16, true>(a, p.maxv, stream, "tallax_fused_topk_topp_sample");
+  return dtype == kF32 ? launch_select<kF32, true>(a, p, stream, "tallax_fused_topk_topp_sample")
+                       : launch_select<kBF16, true>(a, p, stream, "tallax_fused_topk_topp_sample");
 }
 
 int tallax_top_p_and_sample(const void* topk_logits, int dtype, const int32_t* topk_idx, int64_t rows,

@@ -36,4 +36,6 @@ def test_error_path_without_gpu():
     assert b"null" in _lib.LIB.tallax_last_error()
     st = _lib.LIB.tallax_topk(1, 0, 4, 100, 200, 1, 1, None, 0, None)
     assert st == _lib.UNSUPPORTED  # k > 128, like the reference's NotImplementedError
-    assert _lib.LIB.tallax_topk_workspace_size(256, 128256, 128, 1) > 0
+    # whole rows per workgroup need no workspace; segmented rows do
+    assert _lib.LIB.tallax_topk_workspace_size(256, 128256, 128, 1) == 0
+    assert _lib.LIB.tallax_topk_workspace_size(8, 200000, 64, 0) > 0
