@@ -14,7 +14,8 @@ torch.cuda.synchronize(); the kernel's own average duration is measured with
 HIP events recorded on the stream the kernel is launched on.  One JSON line
 is printed.
 
---config topk_c3 / topk_c1 time exact top-k (configs 3 and 1) instead.
+--config topk_c3 / topk_c1 time exact top-k (configs 3 and 1) instead;
+--config copy times torch's device copy of 256 MiB (the counter calibration).
 """
 from __future__ import annotations
 
@@ -30,12 +31,50 @@ sys.path.insert(0, ROOT)
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak, GB/s
 
 
+COPY_BYTES = 256 << 20  # calibration copy: 256 MiB read + 256 MiB written per launch
+
+
+def _copy_rate(torch, dev, stream, steps, warmup):
+    """Read+write GB/s of torch's device copy over COPY_BYTES (the calibration
+    kernel for the FETCH_SIZE / WRITE_SIZE counters and a measured peak)."""
+    n = COPY_BYTES // 4
+    bufs = [torch.empty(n, dtype=torch.float32, device=dev) for _ in range(3)]
+    for b in bufs:
+        b.fill_(1.0)
+    for s in range(warmup):
+        bufs[(s + 1) % 3].copy_(bufs[s % 3])
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for s in range(steps):
+        bufs[(s + 1) % 3].copy_(bufs[s % 3])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    return 2 * COPY_BYTES / (us * 1e-6) / 1e9, us
+
+
+def _measured_traffic(config):
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    (scaled by the copy calibration), as recorded in profiles/*.md lines
+    `traffic_bytes_per_launch[<config>] = <bytes>`; None if absent."""
+    import glob
+    import re
+    pat = re.compile(r"traffic_bytes_per_launch\[" + re.escape(config) + r"\]\s*=\s*([0-9]+)")
+    for f in sorted(glob.glob(os.path.join(ROOT, "profiles", "*.md"))):
+        m = pat.search(open(f).read())
+        if m:
+            return int(m.group(1))
+    return None
+
+
 def _parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="sampler", choices=["sampler", "topk_c3", "topk_c1"])
+    ap.add_argument("--config", default="sampler", choices=["sampler", "topk_c3", "topk_c1", "copy"])
     ap.add_argument("--nbuf", type=int, default=6)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -63,6 +102,15 @@ def main() -> int:
     gen = torch.Generator(device=dev)
     gen.manual_seed(4)
 
+    if args.config == "copy":
+        gbs, us = _copy_rate(torch, dev, stream, args.steps, args.warmup)
+        print(json.dumps({"metric": "device copy GB/s (read + write), calibration", "value": gbs,
+                          "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": us / 1e3, "higher_is_better": True, "scaling": "weak",
+                          "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+                          "config": {"workload": f"torch copy_ of {COPY_BYTES} bytes (f32)"}}), flush=True)
+        return 0
+
     if args.config == "sampler":
         rows, cols, dt_name, sigma = 256, 128256, "bf16", 3.0
         tdt = torch.bfloat16
@@ -82,7 +130,7 @@ def main() -> int:
         workload = ("fused top-k/top-p/temperature/Gumbel sampler (sampling.sample): bf16 logits "
                     "[256,128256] ~ N(0,3), top_k U{1..1024} (clamped to 128), top_p U[0.7,1), "
                     "T U[0.5,1.5), threefry key (0,1234)")
-        kernel_name = "row_select_kernel<1, 8, 128, true>"
+        kernel_name = _lib.select_plan(rows, cols, _lib.BF16)["kernel"].replace("SAMPLE", "true")
         bufs = [(torch.randn((rows, cols), generator=gen, device=dev) * sigma).to(tdt) for _ in range(args.nbuf)]
 
         def launch(x):
@@ -93,12 +141,11 @@ def main() -> int:
         if args.config == "topk_c3":
             rows, cols, k = 128, 151936, 50
             workload = ("exact top-k (tax.top_k) k=50: f32 [128,151936] ~ N(0, sigma=2) + 32 spikes/row at 8.0")
-            kernel_name = "row_select_kernel<0, 8, 64, false>"
         else:
             rows, cols, k = 8, 32768, 64
             workload = "exact top-k (tax.top_k) k=64: f32 [8,32768] ~ N(0,1)"
-            kernel_name = "row_select_kernel<0, 2, 64, false>"
         dt_name, tdt = "f32", torch.float32
+        kernel_name = _lib.select_plan(rows, cols, _lib.F32)["kernel"].replace("SAMPLE", "false")
         need = _lib.LIB.tallax_topk_workspace_size(rows, cols, k, _lib.F32)
         ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
         vals = torch.empty((rows, k), dtype=tdt, device=dev)
@@ -166,7 +213,10 @@ def main() -> int:
         ends[s].record(stream)
     torch.cuda.synchronize()
     durs_us = sorted(a.elapsed_time(b) * 1e3 for a, b in zip(starts, ends))
-    kern_us = sum(durs_us) / len(durs_us)
+    # Average launch duration: HIP events on the launch stream around the K
+    # back-to-back launches of the timed region (per-launch event pairs add
+    # their own packets to every launch, so they are reported separately).
+    kern_us = gpu_ms * 1e3 / args.steps
     achieved = alg_bytes / (kern_us * 1e-6) / 1e9
 
     # ---- CPU baseline: the numpy oracle on a bounded sample of the same workload
@@ -191,6 +241,7 @@ def main() -> int:
                          f"workload through the numpy oracle (oracle/tallax_oracle.py), single thread, "
                          f"{t_cpu:.1f} s"}
 
+    copy_gbs, _ = _copy_rate(torch, dev, stream, 10, 3)
     rows_per_s = rows * args.steps / total_s
     rec = {
         "metric": "rows/s + achieved HBM GB/s (% peak): fused top-k/top-p @256x128256 bf16"
@@ -208,9 +259,10 @@ def main() -> int:
         "data": f"synthetic (torch.randn on device, seed 4; {args.nbuf} rotating input buffers)",
         "config": {"workload": workload, "rows": rows, "cols": cols, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": _measured_traffic(args.config),
+                     "measured_copy_GBs": copy_gbs, "frac_of_copy": achieved / copy_gbs,
                      "kernel": kernel_name, "kernel_avg_us": kern_us,
-                     "kernel_median_us": durs_us[len(durs_us) // 2],
+                     "event_pair_median_us": durs_us[len(durs_us) // 2],
                      "algorithmic_bytes_per_launch": alg_bytes},
         "cpu_baseline": cpu,
         "parity_vs_oracle": parity,

@@ -32,6 +32,12 @@ int tallax_testing_gumbel(uint32_t k0, uint32_t k1, const uint32_t* counters, fl
  * lane-exchange helpers of the kernels (DPP / v_permlane*_swap); out holds 448 words. */
 int tallax_testing_lane_ops(uint32_t* out, tallax_stream_t stream);
 
+/* Work split the selection entry points (tallax_topk, tallax_fused_topk_topp_sample)
+ * choose for a [rows, cols] input of `dtype`: out[0] threads per workgroup,
+ * out[1] 16-byte vectors per thread, out[2] workgroups (segments) per row,
+ * out[3] vectors per segment.  Host only: no device work. */
+int tallax_testing_select_plan(int64_t rows, int64_t cols, int dtype, int32_t* out);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

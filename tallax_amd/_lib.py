@@ -39,6 +39,7 @@ _SIGNATURES = {
     "tallax_testing_expf_logf": ([_c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
     "tallax_testing_gumbel": ([ctypes.c_uint32, ctypes.c_uint32, _c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
     "tallax_testing_lane_ops": ([_c_p, _c_p], _c_int),
+    "tallax_testing_select_plan": ([_c_i64, _c_i64, _c_int, _c_p], _c_int),
 }
 
 
@@ -120,3 +121,14 @@ def require_cuda(*ts: torch.Tensor) -> None:
         devs = {t.device for t in ts}
         if len(devs) > 1:
             raise ValueError(f"operands on different devices: {devs}")
+
+
+def select_plan(rows: int, cols: int, dtype: int) -> dict:
+    """Work split of the selection kernels for a [rows, cols] input (host only)."""
+    out = (ctypes.c_int32 * 4)()
+    check(LIB.tallax_testing_select_plan(rows, cols, dtype, out), "select_plan")
+    nt, maxv, nseg, vps = list(out)
+    dt = {F32: 0, BF16: 1}[dtype]
+    return {"threads": nt, "vectors_per_thread": maxv, "segments": nseg, "vectors_per_segment": vps,
+            "kernel": f"seg_select_kernel<{dt}, {maxv}, {nt}, SAMPLE>"
+                      + (" + seg_merge_kernel" if nseg > 1 else "")}

@@ -921,6 +921,21 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
                        : launch_select<kBF16, true>(a, p, stream, "tallax_fused_topk_topp_sample");
 }
 
+int tallax_testing_select_plan(int64_t rows, int64_t cols, int dtype, int32_t* out) {
+  if (!out || (dtype != kF32 && dtype != kBF16) || rows < 0 || cols <= 0) {
+    set_error("bad arguments");
+    return kInvalidArgument;
+  }
+  Plan p;
+  const int st = plan_rows(rows, cols, dtype, &p);
+  if (st) return st;
+  out[0] = p.nt;
+  out[1] = p.maxv;
+  out[2] = p.nseg;
+  out[3] = (int32_t)p.vps;
+  return kOk;
+}
+
 int tallax_top_p_and_sample(const void* topk_logits, int dtype, const int32_t* topk_idx, int64_t rows,
                             int64_t k, const uint32_t* rng_key, const float* top_p,
                             const float* temperature, int64_t vocab_size, double replace_val,
