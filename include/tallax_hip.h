@@ -6,10 +6,10 @@
  *     by the caller; scalars are passed by value.
  *   - Work is enqueued on `stream` only; nothing synchronizes the host and
  *     nothing allocates device memory.  Entry points that need scratch take a
- *     caller-provided `workspace` of at least `*_workspace_size(...)` bytes,
- *     which must be zero-filled once before its first use: the kernels leave
- *     it zero-filled again when they complete.  Calls that may run
- *     concurrently need distinct workspaces.
+ *     caller-provided `workspace` of at least `*_workspace_size(...)` bytes
+ *     (0 when the work split needs none; no initial contents are required:
+ *     every byte read is written earlier in the same call).  Calls that may
+ *     run concurrently need distinct workspaces.
  *   - Return value: 0 on success, otherwise a TALLAX_* status code; the
  *     message of the last failure on the calling thread is returned by
  *     tallax_last_error().
