@@ -212,10 +212,11 @@ struct SegShared {
   C scratch[NW * kRun];
   C list[kRun];
   uint64_t list64[kRun];
+  float samp_e[kRun];  // sampler: softmax numerators of the top-128
+  float samp_g[kRun];  // sampler: their Gumbel noise
   uint32_t wl[NW];
   int red[NW];
-  int wc[2][NW];  // per-wave candidate counts: [0] filter pass, [1] exact path
-  int nan_seen;
+  int wc[NW];  // per-wave candidate counts
 };
 
 template <int NW>
@@ -231,36 +232,52 @@ __device__ __forceinline__ int block_sum(int v, int* red) {
 }
 
 // sh.list <- the 128 largest candidates of all wave regions (counts cnt[w] in LDS),
-// descending, zero padded.  Small sets use rank selection; larger ones are
-// sorted per wave in runs of 128 and the per-wave lists merged as a binary
-// tree (log2(waves) levels).
-// Rank selection for small candidate sets (C <= kRankMax): candidates are
-// compacted into sh.scratch, then the thread holding candidate x counts the
-// candidates larger than x (broadcast LDS reads, all distinct) and writes x
-// to sh.list[rank] when rank < 128.
-constexpr int kRankMax = 512;
-
+// descending, zero padded.  Sets of at most 64 per wave use chunk_select;
+// larger ones are sorted per wave region in runs of 128 and the per-wave
+// lists merged as a binary tree (log2(waves) levels).
+// Chunked selection for candidate sets of at most 64 per wave: the
+// candidates are compacted into sh.scratch, wave w sorts chunk w (64, one per
+// lane), and the sorted chunks are merged pairwise: 64 + 64 -> 128 by a
+// bitonic merge, then 128-runs by merge-and-discard, until one run is left.
 template <typename C, int NT>
-__device__ __forceinline__ void rank_select(SegShared<C, NT>& sh, const int* cnt, int total) {
+__device__ __forceinline__ void chunk_select(SegShared<C, NT>& sh, const int* cnt, int total) {
   constexpr int NW = Geo<NT>::NW, WCAP = Geo<NT>::WCAP;
   const int tid = threadIdx.x, w = tid / kWave, l = lane_id();
   int off = 0;
 #pragma unroll
-  for (int q = 0; q < NW; ++q) off += q < w ? cnt[q] : 0;
-  const int cw = cnt[w];
+  for (int q = 0; q < NW; ++q) off += q < w ? (cnt[q] < WCAP ? cnt[q] : WCAP) : 0;
+  const int cw = cnt[w] < WCAP ? cnt[w] : WCAP;
   for (int i = l; i < cw; i += kWave) sh.scratch[off + i] = sh.cand[w * WCAP + i];
-  for (int i = tid; i < kRun; i += NT) sh.list[i] = 0;
   __syncthreads();
-  for (int p = tid; p < total; p += NT) {
-    const C x = sh.scratch[p];
-    int r = 0;
-    int i = 0;
-    for (; i + 4 <= total; i += 4) {
-      r += (sh.scratch[i] > x) + (sh.scratch[i + 1] > x) + (sh.scratch[i + 2] > x) + (sh.scratch[i + 3] > x);
-    }
-    for (; i < total; ++i) r += sh.scratch[i] > x;
-    if (r < kRun) sh.list[r] = x;
+  const int nch = (total + kWave - 1) / kWave;  // 64-chunks, <= NW
+  if (w < nch) {
+    const int i = w * kWave + l;
+    const C v = wave_sort64_desc<C>(i < total ? sh.scratch[i] : (C)0);
+    sh.scratch[i] = v;
   }
+  __syncthreads();
+  // level 0: chunks 2r, 2r+1 -> 128-run r (stored in place at scratch + 128 r)
+  const int nrun = (nch + 1) / 2;
+  if (w < nrun) {
+    C c[2];
+    c[0] = sh.scratch[2 * w * kWave + l];
+    c[1] = 2 * w + 1 < nch ? sh.scratch[(2 * w + 1) * kWave + (kWave - 1 - l)] : (C)0;  // reversed: bitonic
+    wave_bitonic_merge128_desc(c);
+    sh.scratch[w * kRun + l] = c[0];
+    sh.scratch[w * kRun + kWave + l] = c[1];
+  }
+  __syncthreads();
+  for (int st = 1; st < nrun; st <<= 1) {
+    if ((w & (2 * st - 1)) == 0 && w + st < nrun) {
+      C acc[2] = {sh.scratch[w * kRun + l], sh.scratch[w * kRun + kWave + l]};
+      const C b[2] = {sh.scratch[(w + st) * kRun + l], sh.scratch[(w + st) * kRun + kWave + l]};
+      wave_merge128_desc(acc, b);
+      sh.scratch[w * kRun + l] = acc[0];
+      sh.scratch[w * kRun + kWave + l] = acc[1];
+    }
+    __syncthreads();
+  }
+  for (int i = tid; i < kRun; i += NT) sh.list[i] = nrun > 0 ? sh.scratch[i] : (C)0;
   __syncthreads();
 }
 
@@ -269,13 +286,13 @@ __device__ __forceinline__ void block_select(SegShared<C, NT>& sh, const int* cn
   constexpr int NW = Geo<NT>::NW, WCAP = Geo<NT>::WCAP;
   int total = 0;
 #pragma unroll
-  for (int q = 0; q < NW; ++q) total += cnt[q];
-  if (total <= kRankMax) {
-    rank_select(sh, cnt, total);
+  for (int q = 0; q < NW; ++q) total += cnt[q] < WCAP ? cnt[q] : WCAP;
+  if (total <= NW * kWave) {
+    chunk_select(sh, cnt, total);
     return;
   }
   const int w = threadIdx.x / kWave, l = lane_id();
-  const int cw = cnt[w];
+  const int cw = cnt[w] < WCAP ? cnt[w] : WCAP;
   const C* reg = sh.cand + w * WCAP;
   C acc[2] = {0, 0};
   for (int r = 0; r * kRun < cw; ++r) {
@@ -347,7 +364,7 @@ __device__ __forceinline__ uint32_t pk_sub_sat_u16(uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint32_t raw_key_f32(uint32_t b) {
   return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
 }
-__device__ __forceinline__ uint32_t dword_of(const uint4& v, int d) {
+__device__ __forceinline__ uint32_t dword_of(const uint4 v, int d) {
   const uint32_t lo = (d & 1) ? v.y : v.x;
   const uint32_t hi = (d & 1) ? v.w : v.z;
   return (d & 2) ? hi : lo;
@@ -355,7 +372,7 @@ __device__ __forceinline__ uint32_t dword_of(const uint4& v, int d) {
 // Element q of a 16-byte vector as the value the select keys expect
 // (bf16: its 16 bits, f32: its 32 bits); q may be a run-time value.
 template <int DT>
-__device__ __forceinline__ uint32_t elem_bits(const uint4& v, int q) {
+__device__ __forceinline__ uint32_t elem_bits(const uint4 v, int q) {
   if (DT == kBF16) {
     const uint32_t w = dword_of(v, q >> 1);
     return (q & 1) ? (w >> 16) : (w & 0xFFFFu);
@@ -363,9 +380,10 @@ __device__ __forceinline__ uint32_t elem_bits(const uint4& v, int q) {
   return dword_of(v, q);
 }
 
-// Outputs of one row from its sorted top-128 list (in LDS).
+// Outputs of one row from its sorted top-128 list (in LDS).  Called by every
+// thread of the workgroup; se / sg are 128-float LDS buffers (sampler only).
 template <int DT, bool SAMPLE>
-__device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list) {
+__device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list, float* se, float* sg) {
   using T = ElemT<DT>;
   const uint32_t inel = ineligible_key_max(DT);
   const char* rowp = (const char*)a.x + (size_t)(row * a.cols) * T::ES;
@@ -378,32 +396,95 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
       T::store(a.out_vals, row * a.k + i, b);
       a.out_idx[row * a.k + i] = idx;
     }
-  } else if (threadIdx.x < kWave) {
+    return;
+  }
+  // value at position p of the top-128, positions >= top_k[row] replaced
+  const int kr = a.top_k[row];
+  auto value_at = [&](int p) -> float {
+    const uint32_t kk = comp_key(list[p]);
+    const float val = __uint_as_float(kk > inel ? key_to_bits(kk) : T::kMinBits);
+    return p < kr ? val : a.replace_in_dtype;
+  };
+  const uint32_t row_ctr = (uint32_t)(row + a.dim0_offset);
+  const uint32_t k0 = a.rng_key[0], k1 = a.rng_key[1];
+  const float v0 = value_at(0);
+  // numerators and noise of all 128 candidates, one per thread
+  for (int p = threadIdx.x; p < kMaxK; p += blockDim.x) {
+    se[p] = candidate_exp(value_at(p), v0);
+    sg[p] = candidate_noise(k0, k1, row_ctr, (uint32_t)a.cols, comp_idx(list[p]));
+  }
+  __syncthreads();
+  if (threadIdx.x < kWave) {
     const int l = lane_id();
-    const int kr = a.top_k[row];
-    float v[2];
+    float v[2], e[2], g[2];
     int32_t id[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int p = h * kWave + l;
-      const uint64_t c = list[p];
-      const uint32_t kk = comp_key(c);
-      id[h] = comp_idx(c);
-      const float val = __uint_as_float(kk > inel ? key_to_bits(kk) : T::kMinBits);
-      v[h] = p < kr ? val : a.replace_in_dtype;
+      v[h] = value_at(p);
+      id[h] = comp_idx(list[p]);
+      e[h] = se[p];
+      g[h] = sg[p];
     }
-    const uint32_t row_ctr = (uint32_t)(row + a.dim0_offset);
-    const int32_t tok = sample_tail(v, id, kMaxK, a.top_p[row], a.temperature[row], a.rng_key[0],
-                                    a.rng_key[1], row_ctr, (uint32_t)a.cols, a.replace_f32);
+    const int32_t tok = sample_tail(v[0], v[1], id[0], id[1], e[0], e[1], g[0], g[1], kMaxK, a.top_p[row],
+                                    a.temperature[row], a.replace_f32);
     if (l == 0) a.out_tokens[row] = tok;
   }
 }
 
 // ---------------------------------------------------------------------------
+// Views of the raw bits used to bound vector maxima cheaply:
+//   signed view   f32 bits as int32, bf16 halves as int16: monotone over
+//                 non-negative values (positive NaNs sit above +inf), every
+//                 negative value is below +0.  One integer max per element
+//                 pair, so it serves rows whose threshold is positive.
+//   ordered view  bits ^ (sign ? 0x7F..F : 0): monotone over all values
+//                 (-0 one below +0, positive NaNs above +inf, negative NaNs
+//                 below -inf); canonical key = ordered + 2^(bits-1), except
+//                 -0 (ordered -1) whose key is that of +0.
+// Slots outside the row or the segment hold all-ones (a negative NaN): -1 in
+// the signed view and the minimum of the ordered view.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pk_max_i16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(short2_t, a),
+                                                                __builtin_bit_cast(short2_t, b)));
+}
+__device__ __forceinline__ int32_t imax32(int32_t a, int32_t b) { return a > b ? a : b; }
+// larger of the two signed halves, sign-extended
+__device__ __forceinline__ int32_t hmax_i16(uint32_t m) {
+  return imax32((int32_t)(int16_t)(m & 0xFFFFu), (int32_t)(int16_t)(m >> 16));
+}
+__device__ __forceinline__ uint32_t ord2_bf16(uint32_t w) {
+  const short2_t m = __builtin_bit_cast(short2_t, w) >> (short2_t){15, 15};
+  return w ^ (__builtin_bit_cast(uint32_t, m) & 0x7FFF7FFFu);
+}
+__device__ __forceinline__ uint32_t ord_f32(uint32_t b) {
+  return b ^ ((uint32_t)((int32_t)b >> 31) & 0x7FFFFFFFu);
+}
+// signed-view maximum of a 16-byte vector (sign-extended)
+template <int DT>
+__device__ __forceinline__ int32_t vec_smax(const uint4 v) {
+  if (DT == kBF16) return hmax_i16(pk_max_i16(pk_max_i16(v.x, v.y), pk_max_i16(v.z, v.w)));
+  return imax32(imax32((int32_t)v.x, (int32_t)v.y), imax32((int32_t)v.z, (int32_t)v.w));
+}
+// ordered-view maximum of a 16-byte vector
+template <int DT>
+__device__ __forceinline__ int32_t vec_omax(const uint4 v) {
+  if (DT == kBF16)
+    return hmax_i16(pk_max_i16(pk_max_i16(ord2_bf16(v.x), ord2_bf16(v.y)),
+                               pk_max_i16(ord2_bf16(v.z), ord2_bf16(v.w))));
+  return imax32(imax32((int32_t)ord_f32(v.x), (int32_t)ord_f32(v.y)),
+                imax32((int32_t)ord_f32(v.z), (int32_t)ord_f32(v.w)));
+}
+
+// ---------------------------------------------------------------------------
 // Kernel A: one workgroup per (segment, row).  The segment (MAXV 16-byte
 // vectors per thread) is loaded into registers with every load issued up
-// front, filtered once against the thread-maxima lower bound, and reduced to
-// its sorted top-128 by one block selection.
+// front; a per-thread maximum bounds the k-th key from below (L); vectors
+// that may hold an element >= L are staged in LDS and their passing elements
+// appended to per-wave candidate regions; one block selection gives the
+// sorted top-128.  Candidate regions that overflow (heavy ties) switch to an
+// exact bisection on the composite key over the same staged rounds.
 // ---------------------------------------------------------------------------
 template <int DT, int MAXV, int NT, bool SAMPLE>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8)))
@@ -415,8 +496,11 @@ void seg_select_kernel(SelArgs a) {
   constexpr bool kBF = DT == kBF16;
   constexpr int VEC = T::VEC, ES = T::ES;
   constexpr int NW = Geo<NT>::NW, WCAP = Geo<NT>::WCAP;
+  constexpr uint32_t kZeroKey = kBF ? 0x8000u : 0x80000000u;  // canonical key of +-0
+  constexpr int32_t kPosInf = kBF ? 0x7F80 : 0x7F800000;      // +inf bits (signed / ordered view)
+  constexpr int32_t kOrdNegInf = kBF ? -32641 : (int32_t)0x807FFFFFu;  // ordered view of -inf
   __shared__ SegShared<C, NT> sh;
-  __shared__ uint4 stage[kStage * NT];  // flagged vectors, slot-major
+  __shared__ uint4 stage[kStage * NT];  // staged vectors, slot-major
   const int tid = threadIdx.x;
   const int w = tid / kWave, l = lane_id();
   const int seg = blockIdx.x;
@@ -430,13 +514,12 @@ void seg_select_kernel(SelArgs a) {
   const int64_t s1 = s0 + a.vps < nv ? s0 + a.vps : nv;
   const int64_t seg_e0 = s0 * VEC - rv.mis;  // element index of the segment's first slot
   C* reg = sh.cand + w * WCAP;
-  if (tid == 0) sh.nan_seen = 0;
 
   uint4 raw[MAXV];
 #pragma unroll
   for (int j = 0; j < MAXV; ++j) {
     const int64_t v = s0 + (int64_t)j * NT + tid;
-    raw[j] = v < s1 ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u);
+    raw[j] = v < s1 ? rv.base[v] : make_uint4(~0u, ~0u, ~0u, ~0u);
   }
   // Segment-local slot index of (j, q): lbase + j * NT * VEC + q.  Live slots
   // (inside the row and the segment) are those in [live_lo, live_hi).
@@ -445,19 +528,7 @@ void seg_select_kernel(SelArgs a) {
   const int live_lo = seg_e0 < 0 ? (int)(-seg_e0) : 0;
   const int live_hi = (int)(a.cols - seg_e0 < seg_elems ? a.cols - seg_e0 : seg_elems);
   const uint32_t gbase = (uint32_t)seg_e0;  // row index = gbase + local index (mod 2^32)
-  // id stored in a composite: block-local index (narrow bf16) or row index
   auto elem_id = [&](int lidx) -> uint32_t { return (kBF && !kWide) ? (uint32_t)lidx : gbase + (uint32_t)lidx; };
-  // canonical composite of slot (j, q) (vector j passed in vv) and whether it
-  // is a live element >= th
-  auto slow_comp_v = [&](const uint4 vv, int j, int q, uint32_t th, bool& pass) -> C {
-    const int li = lbase + j * NT * VEC + q;
-    const uint32_t bits = elem_bits<DT>(vv, q);
-    pass = li >= live_lo && li < live_hi && S::canon(bits) >= th;
-    return S::comp(bits, elem_id(li));
-  };
-
-  // Vector j of this thread covers local slots [lbase + j*NT*VEC, + VEC):
-  // "full" if all of them are live elements, "dead" if none is.
   auto vec_full = [&](int j) -> bool {
     const int li0 = lbase + j * NT * VEC;
     return li0 >= live_lo && li0 + VEC <= live_hi;
@@ -466,69 +537,62 @@ void seg_select_kernel(SelArgs a) {
     const int li0 = lbase + j * NT * VEC;
     return li0 >= live_hi || li0 + VEC <= live_lo;
   };
-  // raw filter max of a vector (raw keys, see Sel): packed for bf16
-  auto vec_raw_max = [&](const uint4 vv) -> uint32_t {
-    if (kBF) {
-      uint32_t mx = raw_key2_bf16(vv.x);
-      mx = pk_max_u16(mx, raw_key2_bf16(vv.y));
-      mx = pk_max_u16(mx, raw_key2_bf16(vv.z));
-      mx = pk_max_u16(mx, raw_key2_bf16(vv.w));
-      return mx;  // two 16-bit maxima
-    }
-    uint32_t mx = raw_key_f32(vv.x);
-    uint32_t r = raw_key_f32(vv.y);
-    mx = r > mx ? r : mx;
-    r = raw_key_f32(vv.z);
-    mx = r > mx ? r : mx;
-    r = raw_key_f32(vv.w);
-    return r > mx ? r : mx;
-  };
-
-  // ---- lower bound L: at least k live elements are >= L --------------------
-  uint32_t tmax = 0;
-  bool nan_here = false;
-  // raw max of each vector (bf16: packed pair), kept for the filter pass when
-  // registers allow (MAXV <= 8), recomputed otherwise
-  constexpr bool kKeep = MAXV <= 8;
-  uint32_t vmax[kKeep ? MAXV : 1];
-  auto vmax_of = [&](int j) -> uint32_t { return kKeep ? vmax[kKeep ? j : 0] : vec_raw_max(raw[j]); };
-  {
-    uint32_t r2 = 0;     // raw max over full vectors (bf16: packed pair)
-    uint32_t cpart = 0;  // canonical max over live elements of partial vectors
+  // live-slot mask of the vector at local slot li0 (bit q: slot li0 + q is live)
+  auto live_mask = [&](int li0) -> uint32_t {
+    uint32_t m = 0;
 #pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-      const uint32_t m = vec_raw_max(raw[j]);
-      if (kKeep) vmax[kKeep ? j : 0] = m;
-      if (vec_full(j)) {
-        r2 = kBF ? pk_max_u16(r2, m) : (m > r2 ? m : r2);
-      } else if (!vec_dead(j)) {
+    for (int q = 0; q < VEC; ++q) m |= (li0 + q >= live_lo && li0 + q < live_hi ? 1u : 0u) << q;
+    return m;
+  };
+  // dead slots of partial vectors (first / last of a row) become all-ones
+#pragma unroll
+  for (int j = 0; j < MAXV; ++j) {
+    if (!vec_full(j) && !vec_dead(j)) {
+      const uint32_t lm = live_mask(lbase + j * NT * VEC);
+      uint32_t d[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (kBF) {
+          d[i] |= ((lm >> (2 * i)) & 1u) ? 0u : 0x0000FFFFu;
+          d[i] |= ((lm >> (2 * i + 1)) & 1u) ? 0u : 0xFFFF0000u;
+        } else {
+          d[i] |= ((lm >> i) & 1u) ? 0u : ~0u;
+        }
+      }
+      raw[j] = make_uint4(d[0], d[1], d[2], d[3]);
+    }
+  }
+
+  // ---- thread maximum as a canonical key ---------------------------------------
+  int32_t smax = kBF ? -32768 : (int32_t)0x80000000u;
+#pragma unroll
+  for (int j = 0; j < MAXV; ++j) smax = imax32(smax, vec_smax<DT>(raw[j]));
+  uint32_t tmax;
+  if (smax >= 0 && smax <= kPosInf) {
+    tmax = (uint32_t)smax | kZeroKey;
+  } else {  // no non-negative element, or a positive NaN: use the ordered view
+    int32_t omax = kBF ? -32768 : (int32_t)0x80000000u;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) omax = imax32(omax, vec_omax<DT>(raw[j]));
+    if (omax < kOrdNegInf) {
+      tmax = 0;  // only NaNs / dead slots: 0 is a valid (low) bound
+    } else if (omax <= kPosInf) {
+      tmax = omax == -1 ? kZeroKey : (uint32_t)omax + kZeroKey;
+    } else {  // positive NaN: canonical maximum slot by slot
+      tmax = 0;
+#pragma unroll
+      for (int j = 0; j < MAXV; ++j) {
+        const int li0 = lbase + j * NT * VEC;
 #pragma unroll 1
         for (int q = 0; q < VEC; ++q) {
-          bool pass;
-          const C cm = slow_comp_v(raw[j], j, q, 0u, pass);
-          const uint32_t kk = S::comp_key(cm);
-          cpart = pass && kk > cpart ? kk : cpart;
+          const uint32_t kk = S::canon(elem_bits<DT>(raw[j], q));
+          tmax = (li0 + q >= live_lo && li0 + q < live_hi && kk > tmax) ? kk : tmax;
         }
       }
     }
-    const uint32_t r = kBF ? ((r2 & 0xFFFFu) > (r2 >> 16) ? (r2 & 0xFFFFu) : (r2 >> 16)) : r2;
-    nan_here = r > S::kRawPosInf;
-    tmax = S::raw_to_canon(r);
-    tmax = cpart > tmax ? cpart : tmax;
-    if (nan_here) {  // positive NaN raw keys would fake a high maximum: recompute canonically
-      tmax = 0;
-#pragma unroll
-      for (int j = 0; j < MAXV; ++j)
-#pragma unroll 1
-        for (int q = 0; q < VEC; ++q) {
-          bool pass;
-          const C cm = slow_comp_v(raw[j], j, q, 0u, pass);
-          const uint32_t kk = S::comp_key(cm);
-          tmax = pass && kk > tmax ? kk : tmax;
-        }
-    }
   }
-  if (nan_here) sh.nan_seen = 1;
+
+  // ---- lower bound L: at least k live elements are >= L --------------------
   const uint32_t srt = wave_sort64_u32_desc(tmax);
   const uint32_t wl = readlane_u32(srt, (k + NW - 1) / NW - 1);  // this wave's quota of maxima
   if (l == 0) sh.wl[w] = wl;
@@ -536,144 +600,158 @@ void seg_select_kernel(SelArgs a) {
   uint32_t L = sh.wl[0];
 #pragma unroll
   for (int i = 1; i < NW; ++i) L = sh.wl[i] < L ? sh.wl[i] : L;
-  const uint32_t thr = kBF ? L : (L > 1u ? L : 1u);  // candidates: live elements with key >= thr
-  const bool nan_mode = sh.nan_seen != 0;
+  const uint32_t thr = kBF ? L : (L > 1u ? L : 1u);  // candidates: live elements with canonical key >= thr
 
-  // ---- candidates (wave-local compaction) ------------------------------------
-  int wcnt = 0;
-  const bool fast = !nan_mode && (!kBF || thr >= 1u);
-  if (fast) {
-    const uint32_t rt = S::raw_thr(thr);
-    const uint32_t rtm1 = kBF ? (rt - 1u) * 0x10001u : 0u;
-    auto raw_flag = [&](uint32_t m) -> bool { return kBF ? pk_sub_sat_u16(m, rtm1) != 0u : m >= rt; };
-    // element mask of vector j (held in vv): bit q set if element q is live and passes
-    auto vec_mask = [&](const uint4 vv, int li0) -> uint32_t {
-      uint32_t m = 0;
+  // ---- flags: vectors whose maximum may reach thr ------------------------------
+  const bool nan_level = kBF ? thr == 0u : thr <= 1u;  // thr admits NaNs: every live vector
+  const bool pos_thr = !nan_level && thr > kZeroKey;   // positive threshold: signed view
+  const int32_t st = (int32_t)(thr - kZeroKey);        // its bits, when positive
+  uint32_t fl = 0;
+  if (pos_thr) {
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) fl |= (vec_smax<DT>(raw[j]) >= st ? 1u : 0u) << j;
+  } else {
+    const int32_t ot = nan_level ? (int32_t)0x80000000u : (thr == kZeroKey ? -1 : (int32_t)(thr - kZeroKey));
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) fl |= (!vec_dead(j) && vec_omax<DT>(raw[j]) >= ot ? 1u : 0u) << j;
+  }
+  const int nfl = __popc(fl);
+
+  // ---- candidates -----------------------------------------------------------------
+  // Flagged vectors are staged in LDS kStage at a time ("rounds"); each staged
+  // element passes if it is live, its canonical key is >= thr and, with a
+  // probe, its composite is >= probe.  Passing elements are appended to the
+  // wave's region, or only counted (count_only).
+  auto pass_mask = [&](const uint4 vv, int li0, bool use_probe, C probe) -> uint32_t {
+    uint32_t m = 0;
+    if (pos_thr && !use_probe) {
+      // positive threshold: st <= bits <= +inf in the signed view (NaNs excluded);
+      // dead slots (all-ones, -1) fail
+      const uint32_t span = (uint32_t)(kPosInf - st);
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
+        const uint32_t x = dword_of(vv, d);
         if (kBF) {
-          const uint32_t sd = pk_sub_sat_u16(raw_key2_bf16(dword_of(vv, d)), rtm1);
-          m |= ((sd & 0xFFFFu) != 0u ? 1u : 0u) << (2 * d);
-          m |= ((sd >> 16) != 0u ? 1u : 0u) << (2 * d + 1);
+          m |= ((uint32_t)((int32_t)(int16_t)(x & 0xFFFFu) - st) <= span ? 1u : 0u) << (2 * d);
+          m |= ((uint32_t)(((int32_t)x >> 16) - st) <= span ? 1u : 0u) << (2 * d + 1);
         } else {
-          m |= (raw_key_f32(dword_of(vv, d)) >= rt ? 1u : 0u) << d;
+          m |= ((uint32_t)((int32_t)x - st) <= span ? 1u : 0u) << d;
         }
-      }
-      if (li0 < live_lo || li0 + VEC > live_hi) {  // partial vector
-        uint32_t live = 0;
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) live |= (li0 + q >= live_lo && li0 + q < live_hi ? 1u : 0u) << q;
-        m &= live;
       }
       return m;
-    };
-    auto extract = [&](const uint4 vv, int li0, uint32_t mask) {
-      for (;;) {
-        const bool hc = mask != 0u;
-        if (!__ballot(hc)) break;
-        C cm = 0;
-        if (hc) {
-          const int e = __builtin_ctz(mask);
-          mask &= mask - 1u;
-          cm = S::comp(elem_bits<DT>(vv, e), elem_id(li0 + e));
-        }
-        wave_append<WCAP>(hc, cm, reg, wcnt);
-      }
-    };
-    // pass 1: stage every flagged vector (one that may hold a candidate) in LDS
-    int nst = 0;         // vectors this lane flagged
-    uint32_t slots = 0;  // slot numbers j of the staged ones, 4 bits each
+    }
 #pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
-      const bool flag = !vec_dead(j) && raw_flag(vmax_of(j));
-      if (__ballot(flag)) {
-        if (flag) {
-          if (nst < kStage) {
-            stage[nst * NT + tid] = raw[j];
-            slots |= (uint32_t)j << (4 * nst);
-          }
-          ++nst;
-        }
-      }
+    for (int q = 0; q < VEC; ++q) {
+      const uint32_t bits = elem_bits<DT>(vv, q);
+      bool p = S::canon(bits) >= thr;
+      if (use_probe) p = p && S::comp(bits, elem_id(li0 + q)) >= probe;
+      m |= (p ? 1u : 0u) << q;
     }
-    // pass 2: extract the candidates of the staged vectors
-    for (int i = 0; i < kStage; ++i) {
-      const bool have = i < nst;
-      if (!__ballot(have)) break;
-      uint32_t mask = 0;
-      uint4 vv = make_uint4(0u, 0u, 0u, 0u);
-      int li0 = 0;
-      if (have) {
-        vv = stage[i * NT + tid];
-        li0 = lbase + (int)((slots >> (4 * i)) & 15u) * NT * VEC;
-        mask = vec_mask(vv, li0);
-      }
-      extract(vv, li0, mask);
-    }
-    // lanes that flagged more vectors than they could stage take the rest in place
-    const bool over = nst > kStage;
-    if (__ballot(over)) {
-      const int last = (int)((slots >> (4 * (kStage - 1))) & 15u);
+    if (li0 < live_lo || li0 + VEC > live_hi) m &= live_mask(li0);
+    return m;
+  };
+  auto rounds = [&](bool count_only, bool use_probe, C probe, int& wcnt) -> int {
+    int cnt = 0;
+#pragma unroll 1
+    for (int first = 0;; first += kStage) {
+      uint32_t slots = 0;
+      int o = 0;
 #pragma unroll
       for (int j = 0; j < MAXV; ++j) {
-        const int li0 = lbase + j * NT * VEC;
-        const bool take = over && j > last && !vec_dead(j) && raw_flag(vmax_of(j));
-        if (__ballot(take)) extract(raw[j], li0, take ? vec_mask(raw[j], li0) : 0u);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < MAXV; ++j)
-#pragma unroll 1
-      for (int q = 0; q < VEC; ++q) {
-        bool pass;
-        const C cm = slow_comp_v(raw[j], j, q, thr, pass);
-        wave_append<WCAP>(pass, cm, reg, wcnt);
-      }
-  }
-  if (l == 0) sh.wc[0][w] = wcnt;
-  __syncthreads();
-  bool overflow = false;
-#pragma unroll
-  for (int q = 0; q < NW; ++q) overflow |= sh.wc[0][q] > WCAP;
-  const int* cnt = sh.wc[0];  // sh.wc[1] if the exact path runs
-
-  if (overflow) {
-    // Heavy ties: keep only the exact top-k among the passing elements
-    // (composites are distinct, so exactly k pass the bisection).
-    C prefix = 0;
-    for (int bit = (int)sizeof(C) * 8 - 1; bit >= 0; --bit) {
-      const C probe = prefix | ((C)1 << bit);
-      int cc = 0;
-#pragma unroll
-      for (int j = 0; j < MAXV; ++j)
-#pragma unroll 1
-        for (int q = 0; q < VEC; ++q) {
-          bool pass;
-          const C cm = slow_comp_v(raw[j], j, q, thr, pass);
-          cc += pass && cm >= probe;
+        if ((fl >> j) & 1u) {
+          const int sl = o - first;
+          if (sl >= 0 && sl < kStage) {
+            stage[sl * NT + tid] = raw[j];
+            slots |= (uint32_t)j << (4 * sl);
+          }
+          ++o;
         }
-      if (block_sum<NW>(cc, sh.red) >= k) prefix = probe;
-    }
-    wcnt = 0;
-#pragma unroll
-    for (int j = 0; j < MAXV; ++j)
-#pragma unroll 1
-      for (int q = 0; q < VEC; ++q) {
-        bool pass;
-        const C cm = slow_comp_v(raw[j], j, q, thr, pass);
-        wave_append<WCAP>(pass && cm >= prefix, cm, reg, wcnt);
       }
-    if (l == 0) sh.wc[1][w] = wcnt;
-    __syncthreads();
-    cnt = sh.wc[1];
+      const int nst = nfl - first;
+#pragma unroll 1
+      for (int i = 0; i < kStage; ++i) {
+        const bool have = i < nst;
+        if (!__ballot(have)) break;
+        uint32_t mask = 0;
+        uint4 vv = make_uint4(0u, 0u, 0u, 0u);
+        int li0 = 0;
+        if (have) {
+          vv = stage[i * NT + tid];
+          li0 = lbase + (int)((slots >> (4 * i)) & 15u) * NT * VEC;
+          mask = pass_mask(vv, li0, use_probe, probe);
+        }
+        if (count_only) {
+          cnt += __popc(mask);
+        } else {
+          for (;;) {
+            const bool hc = mask != 0u;
+            if (!__ballot(hc)) break;
+            C cm = 0;
+            if (hc) {
+              const int e = __builtin_ctz(mask);
+              mask &= mask - 1u;
+              // the element, read back from its staged copy
+              const uint32_t bits = kBF ? (uint32_t)((const uint16_t*)&stage[i * NT + tid])[e]
+                                        : ((const uint32_t*)&stage[i * NT + tid])[e];
+              cm = S::comp(bits, elem_id(li0 + e));
+            }
+            wave_append<WCAP>(hc, cm, reg, wcnt);
+          }
+        }
+      }
+      if (!__ballot(nfl > first + kStage)) break;
+    }
+    return cnt;
+  };
+
+  // Filter pass; if a region overflows, bisect for the k-th composite among
+  // the passing elements (composites are distinct, so exactly k are >= it)
+  // and collect those.  Control flow is block-uniform.
+  constexpr int kIdxTop = sizeof(C) == 4 ? 15 : 31;  // top bit of the index field
+  constexpr int kKeyTop = sizeof(C) == 4 ? 31 : (kBF ? 47 : 63);
+  // index bits that vary: ~idx has ones above them for every idx < 2^ib
+  int ib = kIdxTop + 1;
+  if (sizeof(C) == 8) {
+    const uint64_t span = (uint64_t)(kBF && !kWide ? live_hi : (uint32_t)(gbase + (uint32_t)live_hi));
+    ib = span <= 1 ? 1 : 64 - __clzll(span - 1);
+    ib = ib > 32 ? 32 : ib;
+  }
+  int phase = 0;  // 0 filter, 1 bisection count, 2 final append
+  int bit = kKeyTop;
+  C prefix = 0;
+#pragma unroll 1
+  for (;;) {
+    const C probe = phase == 1 ? (C)(prefix | ((C)1 << bit)) : prefix;
+    int wcnt = 0;
+    const int cnt = rounds(phase == 1, phase != 0, probe, wcnt);
+    if (phase != 1) {
+      if (l == 0) sh.wc[w] = wcnt;
+      __syncthreads();
+      bool overflow = false;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) overflow |= sh.wc[q] > WCAP;
+      if (!overflow || phase == 2) break;  // phase 2 admits exactly k <= WCAP
+      __syncthreads();
+      phase = 1;
+      bit = kKeyTop;
+      prefix = 0;
+    } else {
+      if (block_sum<NW>(cnt, sh.red) >= k) prefix = probe;
+      if (bit == kIdxTop + 1) {  // key resolved: fixed high index bits, then the varying ones
+        if (ib <= kIdxTop) prefix |= (C)((((uint64_t)1 << (kIdxTop + 1)) - 1) & ~(((uint64_t)1 << ib) - 1));
+        bit = ib - 1;
+      } else {
+        --bit;
+      }
+      if (bit < 0) phase = 2;
+    }
   }
 
-  block_select(sh, cnt);
+  block_select(sh, (const int*)sh.wc);
   for (int i = tid; i < kRun; i += NT) sh.list64[i] = S::to_global(sh.list[i], seg_e0);
   __syncthreads();
   if (a.nseg == 1) {
-    finalize_row<DT, SAMPLE>(a, row, sh.list64);
+    finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_e, sh.samp_g);
   } else {
     uint64_t* dst = a.ws_lists + ((size_t)row * a.nseg + seg) * kRun;
     for (int i = tid; i < kRun; i += NT) dst[i] = sh.list64[i];
@@ -686,6 +764,7 @@ void seg_select_kernel(SelArgs a) {
 template <int DT, bool SAMPLE>
 __global__ __launch_bounds__(kWave) void seg_merge_kernel(SelArgs a) {
   __shared__ uint64_t list[kRun];
+  __shared__ float se[kRun], sg[kRun];
   const int64_t row = blockIdx.x;
   const int l = lane_id();
   const uint64_t* src = a.ws_lists + (size_t)row * a.nseg * kRun;
@@ -697,7 +776,7 @@ __global__ __launch_bounds__(kWave) void seg_merge_kernel(SelArgs a) {
   list[l] = acc[0];
   list[kWave + l] = acc[1];
   __syncthreads();
-  finalize_row<DT, SAMPLE>(a, row, list);
+  finalize_row<DT, SAMPLE>(a, row, list, se, sg);
 }
 
 // Standalone top_p_and_sample (sampling.py:210-269) on already-sorted
@@ -712,16 +791,20 @@ __global__ __launch_bounds__(kWave) void top_p_sample_kernel(const void* logits,
   const int64_t row = blockIdx.x;
   const int l = lane_id();
   const char* rowp = (const char*)logits + (size_t)row * K * T::ES;
-  float v[2];
+  float v[2], e[2], g[2];
   int32_t id[2];
+  const float v0 = __uint_as_float(T::load_bits(rowp, 0));
+  const uint32_t row_ctr = (uint32_t)(row + dim0_offset);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int p = h * kWave + l;
     v[h] = p < K ? __uint_as_float(T::load_bits(rowp, p)) : 0.0f;
     id[h] = p < K ? idx[row * K + p] : 0;
+    e[h] = p < K ? candidate_exp(v[h], v0) : 0.0f;
+    g[h] = p < K ? candidate_noise(rng_key[0], rng_key[1], row_ctr, vocab, id[h]) : 0.0f;
   }
-  const int32_t tok = sample_tail(v, id, K, top_p[row], temperature[row], rng_key[0], rng_key[1],
-                                  (uint32_t)(row + dim0_offset), vocab, replace_f32);
+  const int32_t tok = sample_tail(v[0], v[1], id[0], id[1], e[0], e[1], g[0], g[1], K, top_p[row],
+                                  temperature[row], replace_f32);
   if (l == 0) out[row] = tok;
 }
 

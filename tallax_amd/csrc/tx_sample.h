@@ -9,29 +9,47 @@
 
 namespace tx {
 
+// Gumbel noise of candidate token `id` in row `row_ctr`: threefry2x32 on the
+// counter (0, row * vocab + id) (sparse_random.py:49-57,75-84).
+__device__ __forceinline__ float candidate_noise(uint32_t k0, uint32_t k1, uint32_t row_ctr, uint32_t vocab,
+                                                 int32_t id) {
+  uint32_t o0, o1;
+  threefry2x32(k0, k1, 0u, row_ctr * vocab + (uint32_t)id, o0, o1);
+  return gumbel_from_bits(o0 ^ o1);
+}
+
+// Softmax numerator exp(v - v0) of a candidate (top_p_mask, sampling.py:45).
+__device__ __forceinline__ float candidate_exp(float v, float v0) {
+#pragma clang fp contract(off)
+  return tx_expf(v - v0);
+}
+
 // ---------------------------------------------------------------------------
 // Sampler tail on one row's sorted candidates, executed by one wave.
-// v[h], id[h]: f32 value and token index at position p = h*64 + lane, for
-// positions p < K (K <= 128).  Restates top_p_and_sample_arrays
+// For position p = h*64 + lane < K (K <= 128): v[h] the f32 value, id[h] the
+// token, e[h] = exp(v - v[0]) and g[h] its Gumbel noise (both computed by the
+// caller, possibly by other waves).  Restates top_p_and_sample_arrays
 // (sampling.py:65-115), top_p_mask (sampling.py:25-62), the (8,128)-tile
 // cumsum order (cumsum.py:21-53) and max_arrays' tie rule
 // (bitonic_top_k.py:43-97).
 // ---------------------------------------------------------------------------
-__device__ __noinline__ int32_t sample_tail(const float v_in[2], const int32_t id_in[2], int K, float top_p,
-                               float temp, uint32_t k0, uint32_t k1, uint32_t row_ctr,
-                               uint32_t vocab, float mask_val) {
+// (Arguments are scalars, position h = 0 / 1, so the call passes registers.)
+__device__ __noinline__ int32_t sample_tail(float v_0, float v_1, int32_t id_0, int32_t id_1, float e_0,
+                                            float e_1, float g_0, float g_1, int K, float top_p, float temp,
+                                            float mask_val) {
 #pragma clang fp contract(off)
   const int l = lane_id();
   const bool in[2] = {l < K, l + kWave < K};
-  float v[2] = {v_in[0], v_in[1]};
-  int32_t id[2] = {id_in[0], id_in[1]};
+  const float v[2] = {v_0, v_1};
+  const int32_t id[2] = {id_0, id_1};
+  const float e_in[2] = {e_0, e_1};
+  const float g_in[2] = {g_0, g_1};
 
-  // softmax numerators exp(l - l[0]) and their total, summed as a
-  // stride-halving tree over 128 zero-padded slots.
-  const float l0 = readlane_f(v[0], 0);
+  // total of the softmax numerators, summed as a stride-halving tree over
+  // 128 zero-padded slots.
   float e[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) e[h] = in[h] ? tx_expf(v[h] - l0) : 0.0f;
+  for (int h = 0; h < 2; ++h) e[h] = in[h] ? e_in[h] : 0.0f;
   float s = e[0] + e[1];
 #pragma unroll
   for (int d = kWave / 2; d >= 1; d >>= 1) s = s + lane_xor_f(s, d);
@@ -85,9 +103,7 @@ __device__ __noinline__ int32_t sample_tail(const float v_in[2], const int32_t i
     if (in[h]) {
       const float masked = v[h] >= thr ? v[h] : mask_val;
       const float scaled = masked / temp;
-      uint32_t o0, o1;
-      threefry2x32(k0, k1, 0u, row_ctr * vocab + (uint32_t)id[h], o0, o1);
-      sc = scaled + gumbel_from_bits(o0 ^ o1);
+      sc = scaled + g_in[h];
     } else if (p < P) {
       sc = -FLT_MAX;  // max_arrays pads with finfo.min and iinfo.min payloads
       tok = INT32_MIN;

@@ -41,6 +41,22 @@ __device__ __forceinline__ C cx(C v, C o, bool keep_max) {
   return ((v > o) == keep_max) ? v : o;
 }
 
+// Sort 64 composites (one per lane) in descending order.
+template <typename C>
+__device__ __forceinline__ C wave_sort64_desc(C v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride >= 1; stride >>= 1) {
+      const bool desc = (l & size) == 0;
+      const bool lower = (l & stride) == 0;
+      v = cx(v, lane_xor_c(v, stride), lower == desc);
+    }
+  }
+  return v;
+}
+
 // Sort a run of 128 composites (u32 or u64) in descending order.
 template <typename C>
 __device__ __forceinline__ void wave_sort128_desc(C c[2]) {
