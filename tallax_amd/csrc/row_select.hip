@@ -50,7 +50,7 @@
 namespace tx {
 
 constexpr int kNT = 256;                   // threads per segment workgroup: 4 wave64s
-constexpr int kNTRow = 1024;               // threads per whole-row workgroup: 16 wave64s
+constexpr int kNTRow = 512;                // threads per whole-row workgroup: 8 wave64s, 2 per SIMD
 constexpr int kMaxK = 128;                 // the reference's limit (top_k.py:438-439)
 constexpr int kRun = 128;                  // list length handed between kernels
 constexpr int kMaxSeg = 32;
@@ -111,11 +111,11 @@ struct ElemT<kBF16> {
   static constexpr uint32_t kMinBits = 0xff7f0000u;  // finfo(bfloat16).min, widened
 };
 
-// candidate slots per wave: 256 in 4-wave workgroups, 128 in 16-wave ones
+// waves per workgroup and candidate slots per wave
 template <int NT>
 struct Geo {
   static constexpr int NW = NT / kWave;
-  static constexpr int WCAP = NT == kNT ? 256 : 128;
+  static constexpr int WCAP = 256;
 };
 constexpr int kStage = 6;                  // flagged 16-byte vectors staged per thread
 // Tunable (read once from the environment by the host):
@@ -212,8 +212,7 @@ struct SegShared {
   C scratch[NW * kRun];
   C list[kRun];
   uint64_t list64[kRun];
-  float samp_e[kRun];  // sampler: softmax numerators of the top-128
-  float samp_g[kRun];  // sampler: their Gumbel noise
+  float samp_g[kRun];  // sampler: Gumbel noise of the top-128
   uint32_t wl[NW];
   int red[NW];
   int wc[NW];  // per-wave candidate counts
@@ -381,9 +380,9 @@ __device__ __forceinline__ uint32_t elem_bits(const uint4 v, int q) {
 }
 
 // Outputs of one row from its sorted top-128 list (in LDS).  Called by every
-// thread of the workgroup; se / sg are 128-float LDS buffers (sampler only).
+// thread of the workgroup; sg is a 128-float LDS buffer (sampler only).
 template <int DT, bool SAMPLE>
-__device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list, float* se, float* sg) {
+__device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list, float* sg) {
   using T = ElemT<DT>;
   const uint32_t inel = ineligible_key_max(DT);
   const char* rowp = (const char*)a.x + (size_t)(row * a.cols) * T::ES;
@@ -407,27 +406,36 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
   };
   const uint32_t row_ctr = (uint32_t)(row + a.dim0_offset);
   const uint32_t k0 = a.rng_key[0], k1 = a.rng_key[1];
-  const float v0 = value_at(0);
-  // numerators and noise of all 128 candidates, one per thread
-  for (int p = threadIdx.x; p < kMaxK; p += blockDim.x) {
-    se[p] = candidate_exp(value_at(p), v0);
+  const int tid = threadIdx.x, l = lane_id();
+  // Waves 1-2 compute the Gumbel noise of the 128 candidates while wave 0
+  // finds the top-p threshold (a 64-thread block does both in wave 0).
+  const bool split = blockDim.x >= 3 * kWave;
+  if (split && tid >= kWave && tid < kWave + kMaxK) {
+    const int p = tid - kWave;
     sg[p] = candidate_noise(k0, k1, row_ctr, (uint32_t)a.cols, comp_idx(list[p]));
   }
-  __syncthreads();
-  if (threadIdx.x < kWave) {
-    const int l = lane_id();
-    float v[2], e[2], g[2];
-    int32_t id[2];
+  float v[2], e[2], g[2];
+  int32_t id[2];
+  float thr = 0.0f;
+  if (tid < kWave) {
+    const float v0 = value_at(0);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int p = h * kWave + l;
       v[h] = value_at(p);
       id[h] = comp_idx(list[p]);
-      e[h] = se[p];
-      g[h] = sg[p];
+      e[h] = candidate_exp(v[h], v0);
+      if (!split) g[h] = candidate_noise(k0, k1, row_ctr, (uint32_t)a.cols, id[h]);
     }
-    const int32_t tok = sample_tail(v[0], v[1], id[0], id[1], e[0], e[1], g[0], g[1], kMaxK, a.top_p[row],
-                                    a.temperature[row], a.replace_f32);
+    thr = top_p_threshold(v, e, kMaxK, a.top_p[row]);
+  }
+  if (split) __syncthreads();
+  if (tid < kWave) {
+    if (split) {
+      g[0] = sg[l];
+      g[1] = sg[kWave + l];
+    }
+    const int32_t tok = gumbel_argmax(v, id, g, kMaxK, thr, a.temperature[row], a.replace_f32);
     if (l == 0) a.out_tokens[row] = tok;
   }
 }
@@ -487,7 +495,7 @@ __device__ __forceinline__ int32_t vec_omax(const uint4 v) {
 // exact bisection on the composite key over the same staged rounds.
 // ---------------------------------------------------------------------------
 template <int DT, int MAXV, int NT, bool SAMPLE>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4, 8)))
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT == kNTRow ? 2 : 4, 8)))
 void seg_select_kernel(SelArgs a) {
   using T = ElemT<DT>;
   constexpr bool kWide = NT * MAXV * T::VEC > 65535;  // block-local bf16 indices need > 16 bits
@@ -662,7 +670,7 @@ void seg_select_kernel(SelArgs a) {
           const int sl = o - first;
           if (sl >= 0 && sl < kStage) {
             stage[sl * NT + tid] = raw[j];
-            slots |= (uint32_t)j << (4 * sl);
+            slots |= (uint32_t)j << (5 * sl);
           }
           ++o;
         }
@@ -677,7 +685,7 @@ void seg_select_kernel(SelArgs a) {
         int li0 = 0;
         if (have) {
           vv = stage[i * NT + tid];
-          li0 = lbase + (int)((slots >> (4 * i)) & 15u) * NT * VEC;
+          li0 = lbase + (int)((slots >> (5 * i)) & 31u) * NT * VEC;
           mask = pass_mask(vv, li0, use_probe, probe);
         }
         if (count_only) {
@@ -751,7 +759,7 @@ void seg_select_kernel(SelArgs a) {
   for (int i = tid; i < kRun; i += NT) sh.list64[i] = S::to_global(sh.list[i], seg_e0);
   __syncthreads();
   if (a.nseg == 1) {
-    finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_e, sh.samp_g);
+    finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_g);
   } else {
     uint64_t* dst = a.ws_lists + ((size_t)row * a.nseg + seg) * kRun;
     for (int i = tid; i < kRun; i += NT) dst[i] = sh.list64[i];
@@ -764,7 +772,7 @@ void seg_select_kernel(SelArgs a) {
 template <int DT, bool SAMPLE>
 __global__ __launch_bounds__(kWave) void seg_merge_kernel(SelArgs a) {
   __shared__ uint64_t list[kRun];
-  __shared__ float se[kRun], sg[kRun];
+  __shared__ float sg[kRun];
   const int64_t row = blockIdx.x;
   const int l = lane_id();
   const uint64_t* src = a.ws_lists + (size_t)row * a.nseg * kRun;
@@ -776,7 +784,7 @@ __global__ __launch_bounds__(kWave) void seg_merge_kernel(SelArgs a) {
   list[l] = acc[0];
   list[kWave + l] = acc[1];
   __syncthreads();
-  finalize_row<DT, SAMPLE>(a, row, list, se, sg);
+  finalize_row<DT, SAMPLE>(a, row, list, sg);
 }
 
 // Standalone top_p_and_sample (sampling.py:210-269) on already-sorted
@@ -803,8 +811,8 @@ __global__ __launch_bounds__(kWave) void top_p_sample_kernel(const void* logits,
     e[h] = p < K ? candidate_exp(v[h], v0) : 0.0f;
     g[h] = p < K ? candidate_noise(rng_key[0], rng_key[1], row_ctr, vocab, id[h]) : 0.0f;
   }
-  const int32_t tok = sample_tail(v[0], v[1], id[0], id[1], e[0], e[1], g[0], g[1], K, top_p[row],
-                                  temperature[row], replace_f32);
+  const float thr = top_p_threshold(v, e, K, top_p[row]);
+  const int32_t tok = gumbel_argmax(v, id, g, K, thr, temperature[row], replace_f32);
   if (l == 0) out[row] = tok;
 }
 
@@ -839,7 +847,7 @@ static const Tuning& tuning() {
 }
 
 // Work split.  A row of nv 16-byte vectors is handled either
-//   * whole by one 1024-thread workgroup (up to 16 vectors per thread) when
+//   * whole by one 512-thread workgroup (up to 32 vectors per thread) when
 //     that gives enough workgroups (>= 128 rows): no merge kernel at all; or
 //   * in segments of 256 x MAXV vectors, MAXV in {4, 8, 16}: the largest that
 //     still gives ~4 workgroups per CU over the launch, then a per-row merge.
@@ -847,9 +855,9 @@ static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
   const int vec = dt == kF32 ? 4 : 8;
   const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
   static const int kOpts[3] = {16, 8, 4};
-  if (rows >= 128 && nv <= (int64_t)kNTRow * 16) {
-    int maxv = 16;
-    while (maxv > 4 && (int64_t)kNTRow * (maxv / 2) >= nv) maxv /= 2;
+  if (rows >= 128 && nv <= (int64_t)kNTRow * 32) {
+    int maxv = 32;
+    while (maxv > 8 && (int64_t)kNTRow * (maxv / 2) >= nv) maxv /= 2;
     p->nt = kNTRow;
     p->maxv = maxv;
     p->nseg = 1;
@@ -894,9 +902,9 @@ static void launch_a(const SelArgs& a, hipStream_t s) {
 template <int DT, bool SAMPLE>
 static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const char* what) {
   if (p.nt == kNTRow) {
-    if (p.maxv == 16) launch_a<DT, 16, kNTRow, SAMPLE>(a, s);
-    else if (p.maxv == 8) launch_a<DT, 8, kNTRow, SAMPLE>(a, s);
-    else launch_a<DT, 4, kNTRow, SAMPLE>(a, s);
+    if (p.maxv == 32) launch_a<DT, 32, kNTRow, SAMPLE>(a, s);
+    else if (p.maxv == 16) launch_a<DT, 16, kNTRow, SAMPLE>(a, s);
+    else launch_a<DT, 8, kNTRow, SAMPLE>(a, s);
   } else {
     if (p.maxv == 16) launch_a<DT, 16, kNT, SAMPLE>(a, s);
     else if (p.maxv == 8) launch_a<DT, 8, kNT, SAMPLE>(a, s);

@@ -25,37 +25,30 @@ __device__ __forceinline__ float candidate_exp(float v, float v0) {
 }
 
 // ---------------------------------------------------------------------------
-// Sampler tail on one row's sorted candidates, executed by one wave.
-// For position p = h*64 + lane < K (K <= 128): v[h] the f32 value, id[h] the
-// token, e[h] = exp(v - v[0]) and g[h] its Gumbel noise (both computed by the
-// caller, possibly by other waves).  Restates top_p_and_sample_arrays
-// (sampling.py:65-115), top_p_mask (sampling.py:25-62), the (8,128)-tile
-// cumsum order (cumsum.py:21-53) and max_arrays' tie rule
+// Sampler tail on one row's sorted candidates, executed by one wave, in two
+// parts so that the Gumbel noise can be computed by other waves meanwhile.
+// Position p = h*64 + lane < K (K <= 128) holds value v[h], token id[h],
+// numerator e[h] = exp(v - v[0]) and noise g[h].  Restates
+// top_p_and_sample_arrays (sampling.py:65-115), top_p_mask (sampling.py:25-62),
+// the (8,128)-tile cumsum order (cumsum.py:21-53) and max_arrays' tie rule
 // (bitonic_top_k.py:43-97).
 // ---------------------------------------------------------------------------
-// (Arguments are scalars, position h = 0 / 1, so the call passes registers.)
-__device__ __noinline__ int32_t sample_tail(float v_0, float v_1, int32_t id_0, int32_t id_1, float e_0,
-                                            float e_1, float g_0, float g_1, int K, float top_p, float temp,
-                                            float mask_val) {
+
+// Top-p threshold: probs = e / sum(e) (sum as a stride-halving tree over 128
+// zero-padded slots), inclusive cumsum (Hillis-Steele inside 8-slot tiles,
+// then the running total of earlier tiles added sequentially),
+// t = #(cumsum < p), threshold v[t], or 0 when t == K (the out-of-range
+// gather of take_along_axis_arrays).
+__device__ __forceinline__ float top_p_threshold(const float v[2], const float e_in[2], int K, float top_p) {
 #pragma clang fp contract(off)
   const int l = lane_id();
   const bool in[2] = {l < K, l + kWave < K};
-  const float v[2] = {v_0, v_1};
-  const int32_t id[2] = {id_0, id_1};
-  const float e_in[2] = {e_0, e_1};
-  const float g_in[2] = {g_0, g_1};
-
-  // total of the softmax numerators, summed as a stride-halving tree over
-  // 128 zero-padded slots.
   float e[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) e[h] = in[h] ? e_in[h] : 0.0f;
   float s = e[0] + e[1];
 #pragma unroll
   for (int d = kWave / 2; d >= 1; d >>= 1) s = s + lane_xor_f(s, d);
-
-  // inclusive cumsum of probs along the candidate axis: Hillis-Steele inside
-  // 8-slot tiles, then the running total of earlier tiles added sequentially.
   float c[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) c[h] = e[h] / s;
@@ -80,14 +73,19 @@ __device__ __noinline__ int32_t sample_tail(float v_0, float v_1, int32_t id_0, 
   }
   if (tile0 != 0) c[0] = c[0] + carry0;
   c[1] = c[1] + carry1;
-
-  // threshold index t = #(cumsum < p); threshold value l[t] (0 when t == K,
-  // the out-of-range gather of take_along_axis_arrays).
   const int t = __popcll(__ballot(in[0] && c[0] < top_p)) + __popcll(__ballot(in[1] && c[1] < top_p));
   const float vt = readlane_f(t < kWave ? v[0] : v[1], t & (kWave - 1));
-  const float thr = t < K ? vt : 0.0f;
+  return t < K ? vt : 0.0f;
+}
 
-  // mask, temperature, Gumbel noise, argmax
+// Keep v >= thr (others become mask_val), divide by the temperature, add the
+// noise and return the token of the maximum score; ties go to the largest
+// bit-reversed position over log2(P) bits, P = max(8, pow2ceil(K)), with
+// finfo.min / INT32_MIN padding as max_arrays pads.  T < 1e-5: greedy id[0].
+__device__ __forceinline__ int32_t gumbel_argmax(const float v[2], const int32_t id[2], const float g[2], int K,
+                                                 float thr, float temp, float mask_val) {
+#pragma clang fp contract(off)
+  const int l = lane_id();
   int P = 8;
   while (P < K) P <<= 1;
   int pbits = 0;
@@ -100,12 +98,12 @@ __device__ __noinline__ int32_t sample_tail(float v_0, float v_1, int32_t id_0, 
     const int p = h * kWave + l;
     float sc;
     int32_t tok = id[h];
-    if (in[h]) {
+    if (p < K) {
       const float masked = v[h] >= thr ? v[h] : mask_val;
       const float scaled = masked / temp;
-      sc = scaled + g_in[h];
+      sc = scaled + g[h];
     } else if (p < P) {
-      sc = -FLT_MAX;  // max_arrays pads with finfo.min and iinfo.min payloads
+      sc = -FLT_MAX;
       tok = INT32_MIN;
     } else {
       sc = -INFINITY;
