@@ -98,6 +98,30 @@ int tallax_top_p_and_sample(const void* topk_logits, int dtype, const int32_t* t
                             const float* temperature, int64_t vocab_size, double replace_val,
                             int64_t dim0_offset, int32_t* out_tokens, tallax_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Gather along an axis: out = values[indices] along `axis` (0 or 1), 0 where
+ * the index is negative or >= the values' extent (no negative wrap).
+ * Replaces tumpy.take_along_axis(arr, indices, axis)
+ *   -- tallax/tumpy.py:99-112, tallax/_src/gather.py:59-83
+ *   (kernel take_along_axis_arrays, gather.py:11-45).
+ * values [vrows, vcols] f32/bf16/int32; indices [irows, icols] int32;
+ * out [irows, icols] in the values' dtype.  axis 1 needs vrows == irows,
+ * axis 0 needs vcols == icols.
+ * ---------------------------------------------------------------------- */
+int tallax_take_along_axis(const void* values, int dtype, int64_t vrows, int64_t vcols, const int32_t* indices,
+                           int64_t irows, int64_t icols, int axis, void* out, tallax_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Inclusive cumulative sum along `axis` (0 or 1), optionally reversed, in the
+ * reference's summation order: Hillis-Steele inside (8, 128) tiles, then the
+ * running total of earlier tiles added sequentially.
+ * Replaces tax.cumsum(arr, axis, reverse) -- tallax/_src/cumsum.py:75-101
+ *   (kernel cumsum_arrays, cumsum.py:32-63).
+ * x, out [rows, cols] f32 or int32 (int32 adds wrap).
+ * ---------------------------------------------------------------------- */
+int tallax_cumsum(const void* x, int dtype, int64_t rows, int64_t cols, int axis, int reverse, void* out,
+                  tallax_stream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -314,6 +314,25 @@ def cumsum(arr: np.ndarray, axis: int, reverse: bool = False) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# take_along_axis (tallax/_src/gather.py:11-83)
+# ---------------------------------------------------------------------------
+def take_along_axis(values: np.ndarray, indices: np.ndarray, axis: int) -> np.ndarray:
+    """take_along_axis_arrays (gather.py:11-45): out = values[idx] along
+    `axis` where 0 <= idx < extent, else 0 (the accumulators start at zero
+    and only in-range tiles overwrite them; no negative wrap)."""
+    values = np.asarray(values)
+    idx = np.asarray(indices).astype(np.int64)
+    assert values.ndim == 2 and idx.ndim == 2 and axis in (0, 1)
+    ext = values.shape[axis]
+    ok = (idx >= 0) & (idx < ext)
+    safe = np.where(ok, idx, 0)
+    if ext == 0:
+        return np.zeros(idx.shape, dtype=values.dtype)
+    got = np.take_along_axis(values, safe, axis=axis)
+    return np.where(ok, got, np.zeros((), dtype=values.dtype)).astype(values.dtype)
+
+
+# ---------------------------------------------------------------------------
 # top_p_mask / top_p_and_sample / sample (tallax/_src/sampling.py)
 # ---------------------------------------------------------------------------
 def _tree_sum_axis0_128(e: np.ndarray) -> np.ndarray:

@@ -26,6 +26,7 @@ LIB_PATH = OUT_DIR / LIB_NAME
 SOURCES = [
     "capi.hip",
     "row_select.hip",
+    "scan_gather.hip",
     "testing.hip",
 ]
 

@@ -52,4 +52,37 @@ def top_k(logits: torch.Tensor, k: int, block_token: int = 8, num_bins: int = NU
     return vals, idx
 
 
-__all__ = ["top_k"]
+def _axis2(axis: int) -> int:
+    axis = int(axis)
+    if axis < 0:
+        axis += 2
+    if axis not in (0, 1):
+        raise ValueError(f"axis {axis} out of range for a 2D operand")
+    return axis
+
+
+def cumsum(arr: torch.Tensor, axis: int, reverse: bool = False, interpret: bool = False) -> torch.Tensor:
+    """Inclusive cumulative sum along `axis` (0 or 1) in the reference's order.
+
+    Reference: cumsum (tallax/_src/cumsum.py:75-101): Hillis-Steele scans
+    inside (8, 128) tiles plus a sequential carry of tile totals; dtype is
+    preserved (float32 and int32 here; cast bfloat16 to float32 first, as the
+    reference's docstring advises).  Negative axes are normalised (the
+    reference's `1 - axis` batch axis only works for 0 and 1).
+    """
+    del interpret
+    _lib.require_cuda(arr)
+    _canonical_2d(arr)
+    axis = _axis2(axis)
+    x = arr.contiguous()
+    dt = _lib.dtype_code(x)
+    if dt == _lib.BF16:
+        raise NotImplementedError("cumsum on bfloat16: cast to float32 first")
+    out = torch.empty_like(x)
+    rows, cols = x.shape
+    _lib.check(_lib.LIB.tallax_cumsum(x.data_ptr(), dt, rows, cols, axis, int(bool(reverse)), out.data_ptr(),
+                                      _lib.stream_of(x)), "cumsum")
+    return out
+
+
+__all__ = ["top_k", "cumsum"]

@@ -269,3 +269,23 @@ def test_sampler_replace_and_quirk_threshold_zero():
     L = np.array([[3.0], [2.0], [1.0], [-1.0]], dtype=np.float32)
     m = O.top_p_mask(L, np.array([1.5], np.float32), -1e12)
     assert np.array_equal(m[:, 0], np.array([3.0, 2.0, 1.0, -1e12], np.float32))
+
+
+# --------------------------------------------------------------------------- take_along_axis
+def test_take_along_axis_oracle_closed_form():
+    """gather.py:11-45: in-range indices gather exactly as numpy does; negative
+    and out-of-range ones give 0 (no wrap), on both axes."""
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal((6, 50)).astype(np.float32)
+    idx = rng.integers(0, 50, (6, 70)).astype(np.int32)
+    assert np.array_equal(O.take_along_axis(v, idx, 1), np.take_along_axis(v, idx, 1))
+    idx2 = idx.copy()
+    idx2[:, ::3] = -1
+    idx2[:, 1::5] = 50
+    got = O.take_along_axis(v, idx2, 1)
+    bad = (idx2 < 0) | (idx2 >= 50)
+    assert np.all(got[bad] == 0) and np.array_equal(got[~bad], np.take_along_axis(v, idx2 % 50, 1)[~bad])
+    vt = v.T.copy()
+    assert np.array_equal(O.take_along_axis(vt, idx.T.copy(), 0), np.take_along_axis(vt, idx.T, 0))
+    iv = rng.integers(-100, 100, (4, 9)).astype(np.int32)
+    assert O.take_along_axis(iv, np.full((4, 2), 9, np.int32), 1).dtype == np.int32
