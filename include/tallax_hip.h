@@ -122,6 +122,28 @@ int tallax_take_along_axis(const void* values, int dtype, int64_t vrows, int64_t
 int tallax_cumsum(const void* x, int dtype, int64_t rows, int64_t cols, int axis, int reverse, void* out,
                   tallax_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Row-wise sort by one key: the kernel under tax.sort / tumpy.sort /
+ * tumpy.argsort.  Replaces the sort pallas_calls of
+ *   tax.sort(operand, num_keys, is_stable, return_argsort, descending)
+ *   -- tallax/_src/sort.py:768-929 (engine sort.py:414-571; key transforms
+ *   utils.py:139-227); tumpy.sort/argsort -- tallax/tumpy.py:6-97.
+ * Orders each row of `key` [rows, cols] (f32/bf16/int32; floats standardised:
+ * NaN above +inf, -0 == +0) ascending, or descending, with ties by ascending
+ * index (descending index when ties_descending).  With perm_in, sorts
+ * key[row, perm_in[row, j]] with ties by position j and composes, so that
+ * repeated calls give a stable multi-key (LSD) sort.  Outputs: perm_out
+ * [rows, cols] int32 = source column of each sorted position; optional
+ * key_out = the sorted keys decoded (f32 keys: f32; int32: int32; bf16: bf16
+ * with NaN 0x7FFF, or f32 with NaN 0x7FFFFFFE, chosen by key_out_dtype);
+ * optional aux / aux_out: a second key gathered by perm_out and decoded the
+ * same way.  cols <= 16384.
+ * ---------------------------------------------------------------------- */
+int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols, int descending,
+                     int ties_descending, const int32_t* perm_in, int32_t* perm_out, void* key_out,
+                     int key_out_dtype, const void* aux, int aux_dtype, void* aux_out, int aux_out_dtype,
+                     tallax_stream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

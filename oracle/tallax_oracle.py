@@ -314,6 +314,56 @@ def cumsum(arr: np.ndarray, axis: int, reverse: bool = False) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# sort (tallax/_src/sort.py:768-929, xla_equivalent_sort sort.py:932-970)
+# ---------------------------------------------------------------------------
+def sort(operands, num_keys: int, is_stable: bool = False, return_argsort: bool = False,
+         descending: bool = False, dtypes=None):
+    """tax.sort semantics on 2D numpy operands (float32 values, int32, or
+    bfloat16 given as float32 values with dtypes[i] == "bf16").
+
+    Order: lexicographic on the keys (floats standardised and compared as
+    sortable ints, utils.py:139-195), then by original index: ascending in both
+    directions when stable (sort.py:804-813,925-926; xla_equivalent_sort
+    inserts -iota for descending), and for the packed bf16 + index path with a
+    non-stable descending sort by descending index (the packed key is unique,
+    utils.py:205-216).  Non-stable ties elsewhere follow the network and are
+    not pinned by the reference; the ascending-index order is one valid
+    outcome.  Returns (outputs tuple, path) with path "packed" or "unpacked";
+    sorted float keys are decoded from the sortable ints (-0 -> +0, NaN ->
+    0x7FFFFFFE, or bfloat16 0x7FFF on the packed path); bfloat16 keys come back
+    as float32 on the unpacked path (utils.py:144-145 promotes them)."""
+    ops = [np.asarray(o) for o in operands]
+    dtypes = list(dtypes) if dtypes is not None else [("i32" if o.dtype == np.int32 else "f32") for o in ops]
+    rows, cols = ops[0].shape
+    if cols & (cols - 1) and any(d == "i32" for d in dtypes):
+        is_stable = True                                        # sort.py:798-802
+    use_indices = return_argsort or is_stable
+    packed = dtypes[0] == "bf16" and len(ops) + int(use_indices) == 2 and use_indices and cols <= 65536
+    ties_desc = packed and descending and not is_stable
+    keys = []
+    for i in range(num_keys):
+        k = ops[i].astype(np.int32) if dtypes[i] == "i32" else float_to_sortable_int(ops[i].astype(np.float32))
+        k = k.astype(np.int64)
+        keys.append(-k if descending else k)
+    idx = np.broadcast_to(np.arange(cols, dtype=np.int64), (rows, cols))
+    tie = -idx if ties_desc else idx
+    perm = np.empty((rows, cols), dtype=np.int64)
+    for r in range(rows):
+        perm[r] = np.lexsort([tie[r]] + [k[r] for k in reversed(keys)])
+    outs = []
+    for i, o in enumerate(ops):
+        g = np.take_along_axis(o, perm, axis=1)
+        if i < num_keys and dtypes[i] != "i32":
+            g = sortable_int_to_float(float_to_sortable_int(g.astype(np.float32)))
+            if packed:
+                g = (g.view(np.uint32) & U32(0xFFFF0000)).view(np.float32)   # bf16 result, NaN 0x7FFF
+        outs.append(g)
+    if return_argsort:
+        outs.append(perm.astype(np.int32))
+    return tuple(outs), ("packed" if packed else "unpacked")
+
+
+# ---------------------------------------------------------------------------
 # take_along_axis (tallax/_src/gather.py:11-83)
 # ---------------------------------------------------------------------------
 def take_along_axis(values: np.ndarray, indices: np.ndarray, axis: int) -> np.ndarray:

@@ -37,6 +37,8 @@ _SIGNATURES = {
         [_c_p, _c_int, _c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_d, _c_i64, _c_p, _c_p], _c_int),
     "tallax_take_along_axis": ([_c_p, _c_int, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p], _c_int),
     "tallax_cumsum": ([_c_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _c_p, _c_p], _c_int),
+    "tallax_sort_rows": ([_c_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _c_p, _c_p, _c_p, _c_int, _c_p, _c_int,
+                          _c_p, _c_int, _c_p], _c_int),
     # test hooks (include/tallax_hip_testing.h)
     "tallax_testing_expf_logf": ([_c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
     "tallax_testing_gumbel": ([ctypes.c_uint32, ctypes.c_uint32, _c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),

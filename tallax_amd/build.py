@@ -27,6 +27,7 @@ SOURCES = [
     "capi.hip",
     "row_select.hip",
     "scan_gather.hip",
+    "sort_rows.hip",
     "testing.hip",
 ]
 

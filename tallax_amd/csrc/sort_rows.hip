@@ -1,0 +1,288 @@
+// Row-wise stable sort for gfx950: the kernel under tax.sort, tumpy.sort and
+// tumpy.argsort.
+//
+// Reference semantics (tallax/_src/sort.py:768-929, utils.py:139-227):
+//   * float keys are standardised (NaN -> the sortable int 0x7FFFFFFE, i.e.
+//     above +inf; -0 -> +0) and compared as sortable ints
+//     (i < 0 ? i ^ 0x7FFFFFFF : i); bfloat16 keys are widened to float32
+//     first; int32 keys compare as int32.  Sorted float keys come back
+//     decoded from the sortable ints (so -0 -> +0 and NaN -> 0x7FFFFFFE),
+//     as float32 for bfloat16 keys on the unpacked path and as bfloat16 on
+//     the packed bf16+index path (NaN -> 0x7FFF there).
+//   * a stable sort orders ties by ascending original index in both
+//     directions (sort.py:804-813, 925-926); the packed bf16 path with a
+//     non-stable descending argsort orders ties by descending index (the
+//     packed key makes the order unique, utils.py:205-216).
+//
+// One workgroup sorts one row: records (transformed key, tie value) are
+// padded to P = 2^m >= cols with the largest record and sorted ascending by a
+// bitonic network.  Each thread holds E consecutive records in registers;
+// strides < E are exchanged within the thread, strides < 64 E across lanes
+// with DPP / v_permlane*_swap, larger strides through LDS.
+#include <stdint.h>
+
+#include "tallax_hip.h"
+#include "tx_common.h"
+#include "tx_host.h"
+#include "tx_wave_sort.h"
+
+namespace tx {
+
+constexpr int kSortMaxCols = 16384;
+
+struct SortArgs {
+  const void* key;
+  int key_dtype;
+  int64_t cols;
+  int P;            // padded length, power of two
+  int descending;
+  int ties_desc;    // ties by descending original index
+  const int32_t* perm_in;  // optional: sort key[perm_in] with position ties, compose
+  int32_t* perm_out;
+  void* key_out;
+  int key_out_dtype;
+  const void* aux;  // optional second key, output gathered by the final permutation
+  int aux_dtype;
+  void* aux_out;
+  int aux_out_dtype;
+};
+
+// sortable order of a key as an unsigned 32-bit value (standardised floats)
+__device__ __forceinline__ uint32_t sort_order_bits(const void* p, int dtype, int64_t i) {
+  if (dtype == kI32) return (uint32_t)((const int32_t*)p)[i] ^ 0x80000000u;
+  uint32_t b = dtype == kBF16 ? ((uint32_t)((const uint16_t*)p)[i]) << 16 : ((const uint32_t*)p)[i];
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) b = 0x7FFFFFFEu;  // NaN: sortable_int_to_float(INT32_MAX - 1)
+  if ((b & 0x7FFFFFFFu) == 0u) b = 0u;                   // -0 -> +0
+  const int32_t s = (int32_t)b < 0 ? (int32_t)(b ^ 0x7FFFFFFFu) : (int32_t)b;
+  return (uint32_t)s ^ 0x80000000u;
+}
+// standardised value bits back from the sortable order
+__device__ __forceinline__ uint32_t order_to_value_bits(uint32_t u) {
+  const int32_t s = (int32_t)(u ^ 0x80000000u);
+  return s < 0 ? ((uint32_t)s ^ 0x7FFFFFFFu) : (uint32_t)s;
+}
+__device__ __forceinline__ void store_sorted(void* out, int out_dtype, int in_dtype, int64_t i, uint32_t u) {
+  if (in_dtype == kI32) {
+    ((int32_t*)out)[i] = (int32_t)(u ^ 0x80000000u);
+    return;
+  }
+  const uint32_t b = order_to_value_bits(u);
+  if (out_dtype == kBF16)
+    ((uint16_t*)out)[i] = (uint16_t)(b >> 16);
+  else
+    ((uint32_t*)out)[i] = b;
+}
+
+template <typename R>
+struct RecT;
+template <>
+struct RecT<uint64_t> {  // key << 32 | tie (tie < 2^31)
+  static constexpr int kTieBits = 32;
+  __device__ static uint64_t make(uint32_t key, uint32_t tie) { return ((uint64_t)key << 32) | tie; }
+  __device__ static uint32_t key(uint64_t r) { return (uint32_t)(r >> 32); }
+  __device__ static uint32_t tie(uint64_t r) { return (uint32_t)r; }
+};
+template <>
+struct RecT<uint32_t> {  // bf16 keys: (key >> 16) << 16 | tie (tie < 2^16)
+  static constexpr int kTieBits = 16;
+  __device__ static uint32_t make(uint32_t key, uint32_t tie) { return (key & 0xFFFF0000u) | tie; }
+  __device__ static uint32_t key(uint32_t r) { return r & 0xFFFF0000u; }
+  __device__ static uint32_t tie(uint32_t r) { return r & 0xFFFFu; }
+};
+
+template <typename R>
+__device__ __forceinline__ void cx_pair(R& a, R& b, bool asc) {
+  const bool sw = (a > b) == asc;
+  const R lo = sw ? b : a;
+  const R hi = sw ? a : b;
+  a = lo;
+  b = hi;
+}
+
+// one stage at a stride S < E: pairs inside the thread's registers
+template <typename R, int E, int S>
+__device__ __forceinline__ void intra_stage(R v[E], int size, int t) {
+  if (S >= E) return;
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    if ((r & S) == 0) {
+      const int i = t * E + r;
+      cx_pair(v[r], v[r | S], (i & size) == 0);
+    }
+  }
+}
+
+// one cross-lane stage at lane distance d (compile-time after the switch)
+template <typename R, int E>
+__device__ __forceinline__ void lane_stage(R v[E], int d, int size, int stride, int t) {
+  const int l = lane_id();
+  const bool lower = (l & d) == 0;
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int i = t * E + r;
+    const bool asc = (i & size) == 0;
+    R o;
+    switch (d) {
+      case 1: o = lane_xor_c(v[r], 1); break;
+      case 2: o = lane_xor_c(v[r], 2); break;
+      case 4: o = lane_xor_c(v[r], 4); break;
+      case 8: o = lane_xor_c(v[r], 8); break;
+      case 16: o = lane_xor_c(v[r], 16); break;
+      default: o = lane_xor_c(v[r], 32); break;
+    }
+    // lower lane keeps min when ascending
+    v[r] = cx(v[r], o, lower != asc);
+  }
+  (void)stride;
+}
+
+template <typename R, int E>
+__global__ __launch_bounds__(1024) void sort_rows_kernel(SortArgs a) {
+  using RT = RecT<R>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  R* lds = (R*)smem;
+  const int t = threadIdx.x;
+  const int NT = blockDim.x;
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * a.cols;
+  const uint32_t tie_mask = RT::kTieBits == 32 ? 0x7FFFFFFFu : 0xFFFFu;
+  R v[E];
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int i = t * E + r;
+    if (i < a.cols) {
+      const int64_t src = a.perm_in ? (int64_t)a.perm_in[base + i] : (int64_t)i;
+      uint32_t k = sort_order_bits(a.key, a.key_dtype, base + src);
+      if (a.descending) k = ~k;
+      const uint32_t tie = a.ties_desc ? (tie_mask - (uint32_t)i) : (uint32_t)i;
+      v[r] = RT::make(k, tie);
+    } else {
+      v[r] = ~(R)0;  // padding: after every real record
+    }
+  }
+  const int P = a.P;
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride >= 1; stride >>= 1) {
+      if (stride < E) {
+        switch (stride) {
+          case 1: intra_stage<R, E, 1>(v, size, t); break;
+          case 2: intra_stage<R, E, 2>(v, size, t); break;
+          case 4: intra_stage<R, E, 4>(v, size, t); break;
+          default: intra_stage<R, E, 8>(v, size, t); break;
+        }
+      } else if (stride < kWave * E) {
+        lane_stage<R, E>(v, stride / E, size, stride, t);
+      } else {
+        // through LDS: element i exchanges with i ^ stride
+#pragma unroll
+        for (int r = 0; r < E; ++r) lds[t * E + r] = v[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < E; ++r) {
+          const int i = t * E + r;
+          const R o = lds[i ^ stride];
+          const bool asc = (i & size) == 0;
+          const bool lower = (i & stride) == 0;
+          v[r] = cx(v[r], o, lower != asc);
+        }
+        __syncthreads();
+      }
+    }
+  }
+  // outputs
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int i = t * E + r;
+    if (i >= a.cols) continue;
+    const uint32_t tie = RT::tie(v[r]);
+    const int pos = a.ties_desc ? (int)(tie_mask - tie) : (int)tie;
+    const int32_t src = a.perm_in ? a.perm_in[base + pos] : pos;
+    a.perm_out[base + i] = src;
+    if (a.key_out) {
+      uint32_t k = RT::key(v[r]);
+      if (a.descending) k = ~k;
+      if (sizeof(R) == 4) {  // rebuild the full order bits of a bf16 key from its high half
+        k &= 0xFFFF0000u;
+        if (k < 0x80000000u) k |= 0xFFFFu;         // negative values: low half of the order is all ones
+        else if (k > 0xFF800000u) k = 0xFFFFFFFEu;  // the NaN sentinel 0x7FFFFFFE
+      }
+      store_sorted(a.key_out, a.key_out_dtype, a.key_dtype, base + i, k);
+    }
+    if (a.aux_out) {
+      const uint32_t u = sort_order_bits(a.aux, a.aux_dtype, base + src);
+      store_sorted(a.aux_out, a.aux_out_dtype, a.aux_dtype, base + i, u);
+    }
+  }
+}
+
+template <typename R, int E>
+static int launch_sort(const SortArgs& a, int64_t rows, hipStream_t s) {
+  const int nt = a.P / E;
+  const size_t lds = (size_t)a.P * sizeof(R);
+  if (lds > 64 * 1024) {
+    static const hipError_t attr = hipFuncSetAttribute((const void*)sort_rows_kernel<R, E>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       (int)(kSortMaxCols * sizeof(R)));
+    if (attr != hipSuccess) {
+      set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr));
+      return kHipError;
+    }
+  }
+  hipLaunchKernelGGL((sort_rows_kernel<R, E>), dim3((unsigned)rows), dim3(nt), lds, s, a);
+  return kOk;
+}
+
+}  // namespace tx
+
+using namespace tx;
+
+extern "C" {
+
+int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols, int descending,
+                     int ties_descending, const int32_t* perm_in, int32_t* perm_out, void* key_out,
+                     int key_out_dtype, const void* aux, int aux_dtype, void* aux_out, int aux_out_dtype,
+                     hipStream_t stream) {
+  if (!key || !perm_out) { set_error("null pointer argument"); return kInvalidArgument; }
+  for (int d : {key_dtype, aux ? aux_dtype : kF32}) {
+    if (d != kF32 && d != kBF16 && d != kI32) { set_error("dtype %d not supported", d); return kUnsupported; }
+  }
+  if ((aux == nullptr) != (aux_out == nullptr)) { set_error("aux and aux_out go together"); return kInvalidArgument; }
+  auto out_ok = [](int in, int out) {
+    return in == kBF16 ? (out == kBF16 || out == kF32) : out == in;
+  };
+  if (key_out && !out_ok(key_dtype, key_out_dtype)) { set_error("key_out dtype %d invalid for key dtype %d", key_out_dtype, key_dtype); return kInvalidArgument; }
+  if (aux_out && !out_ok(aux_dtype, aux_out_dtype)) { set_error("aux_out dtype %d invalid for aux dtype %d", aux_out_dtype, aux_dtype); return kInvalidArgument; }
+  if (rows < 0 || cols < 0) { set_error("negative extent"); return kInvalidArgument; }
+  if (rows == 0 || cols == 0) return kOk;
+  if (cols > kSortMaxCols) {
+    set_error("rows of %lld elements exceed this build's in-LDS sort limit of %d", (long long)cols, kSortMaxCols);
+    return kUnsupported;
+  }
+  if (rows > 2147483647) { set_error("too many rows"); return kUnsupported; }
+  SortArgs a = {};
+  a.key = key; a.key_dtype = key_dtype; a.cols = cols;
+  int P = 256;
+  while (P < cols) P <<= 1;
+  a.P = P;
+  a.descending = descending != 0;
+  a.ties_desc = ties_descending != 0;
+  a.perm_in = perm_in; a.perm_out = perm_out;
+  a.key_out = key_out; a.key_out_dtype = key_out_dtype;
+  a.aux = aux; a.aux_dtype = aux_dtype; a.aux_out = aux_out; a.aux_out_dtype = aux_out_dtype;
+  // bf16 keys on the packed path fit (16-bit key | 16-bit tie) in one u32
+  const bool narrow = key_dtype == kBF16 && !perm_in && cols <= 65536;
+  int st;
+  if (narrow) {
+    if (P <= 4096) st = launch_sort<uint32_t, 4>(a, rows, stream);
+    else if (P == 8192) st = launch_sort<uint32_t, 8>(a, rows, stream);
+    else st = launch_sort<uint32_t, 16>(a, rows, stream);
+  } else {
+    if (P <= 4096) st = launch_sort<uint64_t, 4>(a, rows, stream);
+    else if (P == 8192) st = launch_sort<uint64_t, 8>(a, rows, stream);
+    else st = launch_sort<uint64_t, 16>(a, rows, stream);
+  }
+  if (st) return st;
+  return launch_status("tallax_sort_rows");
+}
+
+}  // extern "C"

@@ -52,6 +52,99 @@ def top_k(logits: torch.Tensor, k: int, block_token: int = 8, num_bins: int = NU
     return vals, idx
 
 
+_SORT_DTYPES = (torch.float32, torch.bfloat16, torch.int32)
+
+
+def sort(operand, num_keys: int, is_stable: bool = False, return_argsort: bool = False,
+         descending: bool = False, num_vmem_substages=None, block_token=None, interpret: bool = False) -> tuple:
+    """Row-wise lexicographic sort of one or more 2D operands by the first
+    `num_keys` of them.
+
+    Reference: sort (tallax/_src/sort.py:768-929).  Mirrors its host logic:
+      * integer operands with a non-power-of-two row force a stable sort
+        (sort.py:798-802);
+      * stable / argsort insert the column index as a tie-breaking key;
+        descending + stable keeps ties in ascending index order
+        (sort.py:804-813, 925-926);
+      * a bfloat16 key sorted together with only the index (rows <= 65536)
+        takes the packed path and comes back as bfloat16 (NaN -> 0x7FFF,
+        sort.py:823-831, utils.py:205-227); otherwise float keys come back
+        standardised and decoded (-0 -> +0, NaN -> 0x7FFFFFFE), bfloat16 keys
+        as float32 (utils.py:139-147 promotes them);
+      * non-key operands are permuted unchanged; with return_argsort the
+        int32 indices are appended last.
+    Non-stable ties are ordered by ascending index (the reference leaves that
+    order to its network).  Keys: float32, bfloat16, int32; up to two keys;
+    rows of up to 16384 elements.  `num_vmem_substages`, `block_token` and
+    `interpret` are TPU tuning knobs, accepted and ignored.
+    """
+    del num_vmem_substages, block_token, interpret
+    operands = list(operand) if isinstance(operand, (list, tuple)) else [operand]
+    if not operands:
+        raise ValueError("sort needs at least one operand")
+    _lib.require_cuda(*operands)
+    shapes = {tuple(x.shape) for x in operands}
+    if len(shapes) != 1:
+        raise ValueError(f"Inputs must all have the same shape, but found shapes={[tuple(x.shape) for x in operands]}")
+    shape = shapes.pop()
+    if len(shape) != 2:
+        raise ValueError("Only 2D inputs supported")
+    num_keys = int(num_keys)
+    if not 1 <= num_keys <= len(operands):
+        raise ValueError(f"num_keys={num_keys} must be in [1, {len(operands)}]")
+    if num_keys > 2:
+        raise NotImplementedError("more than two sort keys")
+    for x in operands:
+        if x.dtype not in _SORT_DTYPES:
+            raise NotImplementedError(f"sort operand dtype {x.dtype}")
+    rows, cols = shape
+    if cols & (cols - 1) and any(not x.dtype.is_floating_point for x in operands):
+        is_stable = True
+    use_indices = return_argsort or is_stable
+    packed = (operands[0].dtype == torch.bfloat16 and len(operands) + int(use_indices) == 2 and use_indices
+              and cols <= 2 ** 16)
+    ties_desc = packed and descending and not is_stable
+    ops = [x.contiguous() for x in operands]
+    dev = ops[0].device
+    stream = _lib.stream_of(ops[0])
+
+    def key_out_dtype(x):
+        if x.dtype == torch.bfloat16:
+            return torch.bfloat16 if packed else torch.float32
+        return x.dtype
+
+    perm = torch.empty(shape, dtype=torch.int32, device=dev)
+    outs = [None] * len(ops)
+    k0 = ops[0]
+    out0 = torch.empty(shape, dtype=key_out_dtype(k0), device=dev)
+    if num_keys == 1:
+        _lib.check(_lib.LIB.tallax_sort_rows(
+            k0.data_ptr(), _lib.dtype_code(k0), rows, cols, int(bool(descending)), int(ties_desc), None,
+            perm.data_ptr(), out0.data_ptr(), _lib.dtype_code(out0), None, 0, None, 0, stream), "sort")
+    else:  # stable LSD passes: by key 1, then by key 0 with position ties
+        k1 = ops[1]
+        perm1 = torch.empty(shape, dtype=torch.int32, device=dev)
+        _lib.check(_lib.LIB.tallax_sort_rows(
+            k1.data_ptr(), _lib.dtype_code(k1), rows, cols, int(bool(descending)), 0, None, perm1.data_ptr(),
+            None, 0, None, 0, None, 0, stream), "sort")
+        out1 = torch.empty(shape, dtype=key_out_dtype(k1), device=dev)
+        _lib.check(_lib.LIB.tallax_sort_rows(
+            k0.data_ptr(), _lib.dtype_code(k0), rows, cols, int(bool(descending)), 0, perm1.data_ptr(),
+            perm.data_ptr(), out0.data_ptr(), _lib.dtype_code(out0), k1.data_ptr(), _lib.dtype_code(k1),
+            out1.data_ptr(), _lib.dtype_code(out1), stream), "sort")
+        outs[1] = out1
+    outs[0] = out0
+    for i in range(num_keys, len(ops)):
+        x = ops[i]
+        o = torch.empty(shape, dtype=x.dtype, device=dev)
+        _lib.check(_lib.LIB.tallax_take_along_axis(x.data_ptr(), _lib.dtype_code(x), rows, cols, perm.data_ptr(),
+                                                   rows, cols, 1, o.data_ptr(), stream), "sort payload")
+        outs[i] = o
+    if return_argsort:
+        outs.append(perm)
+    return tuple(outs)
+
+
 def _axis2(axis: int) -> int:
     axis = int(axis)
     if axis < 0:
@@ -85,4 +178,4 @@ def cumsum(arr: torch.Tensor, axis: int, reverse: bool = False, interpret: bool 
     return out
 
 
-__all__ = ["top_k", "cumsum"]
+__all__ = ["sort", "top_k", "cumsum"]

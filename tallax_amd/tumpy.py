@@ -10,6 +10,45 @@ import torch
 from . import _lib
 
 
+def _rows_view(a: torch.Tensor, axis):
+    if axis is None:
+        work = a.reshape(-1)
+        return work.reshape(1, -1), tuple(work.shape)
+    ndim = a.ndim
+    canonical = axis if axis >= 0 else axis + ndim
+    if canonical != ndim - 1:
+        raise ValueError("tumpy only supports sorting along the last axis.")
+    return a.reshape(-1, a.shape[-1]), tuple(a.shape)
+
+
+def sort(a: torch.Tensor, axis=-1, kind=None, order=None, stable: bool = True, descending: bool = False,
+         interpret: bool = False) -> torch.Tensor:
+    """Sorted copy along the last axis (or of the flattened array, axis=None).
+
+    Reference: tumpy.sort (tallax/tumpy.py:6-52) -> tax.sort(num_keys=1,
+    is_stable=stable, return_argsort=False).  `kind` and `order` are ignored.
+    """
+    del kind, order, interpret
+    from . import tax
+    a2, shape = _rows_view(a, axis)
+    (out,) = tax.sort(a2, num_keys=1, is_stable=stable, descending=descending, return_argsort=False)
+    return out.reshape(shape)
+
+
+def argsort(a: torch.Tensor, axis=-1, kind=None, order=None, stable: bool = True, descending: bool = False,
+            interpret: bool = False) -> torch.Tensor:
+    """int32 indices that sort `a` along the last axis (or flattened).
+
+    Reference: tumpy.argsort (tallax/tumpy.py:54-97) -> tax.sort(num_keys=1,
+    is_stable=stable, return_argsort=True).
+    """
+    del kind, order, interpret
+    from . import tax
+    a2, shape = _rows_view(a, axis)
+    _, idx = tax.sort(a2, num_keys=1, is_stable=stable, descending=descending, return_argsort=True)
+    return idx.reshape(shape)
+
+
 def take_along_axis(arr: torch.Tensor, indices: torch.Tensor, axis: int, interpret: bool = False) -> torch.Tensor:
     """out = arr[indices] along `axis` (0 or 1); 0 where an index is negative or
     out of range.
@@ -41,4 +80,4 @@ def take_along_axis(arr: torch.Tensor, indices: torch.Tensor, axis: int, interpr
     return out
 
 
-__all__ = ["take_along_axis"]
+__all__ = ["sort", "argsort", "take_along_axis"]

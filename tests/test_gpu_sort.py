@@ -1,0 +1,129 @@
+"""GPU parity: tax.sort / tumpy.sort / tumpy.argsort through the C ABI against
+the oracle's restatement of sort.py on identical seeded inputs (bit-exact
+keys, indices and payloads), including config 2 (bf16 keys [256, 4096]
+rounded to 1/16, stable argsort, then take_along_axis of an f32 array)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tallax_oracle as O
+from tests.gpu_util import bits, from_dev_vals, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+def _host(t: torch.Tensor) -> np.ndarray:
+    if t.dtype == torch.bfloat16:
+        return from_dev_vals(t)
+    return t.cpu().numpy()
+
+
+def _same(a: np.ndarray, b: np.ndarray) -> bool:
+    if a.dtype == np.int32 or b.dtype == np.int32:
+        return np.array_equal(a, b)
+    return np.array_equal(bits(a), bits(b))
+
+
+def _special_row(rng, cols):
+    x = rng.standard_normal(cols).astype(np.float32)
+    for v in (np.nan, -0.0, 0.0, np.inf, -np.inf, -np.nan):
+        x[rng.integers(0, cols, max(1, cols // 50))] = v
+    return x
+
+
+def test_config2_argsort_then_gather(gpu):
+    from tallax_amd import tumpy
+    _log("config 2: bf16 [256,4096] stable argsort + take_along_axis")
+    rng = np.random.default_rng(1)
+    keys = np.round(rng.standard_normal((256, 4096)) * 16) / 16
+    keys = keys.astype(np.float32)
+    vals = np.random.default_rng(2).standard_normal((256, 4096)).astype(np.float32)
+    kd = to_dev(keys, "bf16", gpu)
+    idx = tumpy.argsort(kd)
+    got = tumpy.take_along_axis(torch.from_numpy(vals).to(gpu), idx, 1)
+    torch.cuda.synchronize()
+    (sk, want_idx), path = O.sort([O.round_to_dtype(keys, "bf16")], 1, is_stable=True, return_argsort=True,
+                                  dtypes=["bf16"])
+    assert path == "packed"
+    assert np.array_equal(idx.cpu().numpy(), want_idx)
+    assert np.array_equal(bits(got.cpu().numpy()), bits(O.take_along_axis(vals, want_idx, 1)))
+    sorted_keys = tumpy.sort(kd)
+    assert sorted_keys.dtype == torch.bfloat16
+    assert _same(from_dev_vals(sorted_keys), sk)
+
+
+@pytest.mark.parametrize("cols", [1, 7, 255, 256, 1000, 4096, 5000, 16384])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "i32"])
+@pytest.mark.parametrize("descending", [False, True])
+@pytest.mark.parametrize("stable,argsort", [(True, True), (False, True), (True, False), (False, False)])
+def test_sort_one_key(gpu, cols, dtype, descending, stable, argsort):
+    from tallax_amd import tax
+    _log(f"sort {dtype} cols={cols} desc={descending} stable={stable} argsort={argsort}")
+    rng = np.random.default_rng(cols * 3 + descending)
+    rows = 5
+    if dtype == "i32":
+        x = rng.integers(-5, 5, (rows, cols)).astype(np.int32)
+        x[0] = rng.integers(-2**31, 2**31, cols, dtype=np.int64).astype(np.int32)
+        xd = torch.from_numpy(x).to(gpu)
+        host = x
+    else:
+        x = np.round(rng.standard_normal((rows, cols)) * 8).astype(np.float32) / 8
+        x[1] = _special_row(rng, cols)
+        xd = to_dev(x, dtype, gpu)
+        host = O.round_to_dtype(x, dtype)
+    got = tax.sort(xd, num_keys=1, is_stable=stable, return_argsort=argsort, descending=descending)
+    torch.cuda.synchronize()
+    want, path = O.sort([host], 1, is_stable=stable, return_argsort=argsort, descending=descending,
+                        dtypes=[dtype])
+    assert len(got) == len(want)
+    if dtype == "bf16":
+        assert got[0].dtype == (torch.bfloat16 if path == "packed" else torch.float32)
+    for g, w in zip(got, want):
+        assert _same(_host(g), w)
+
+
+@pytest.mark.parametrize("descending", [False, True])
+def test_sort_two_keys_with_payloads(gpu, descending):
+    from tallax_amd import tax
+    rng = np.random.default_rng(9)
+    rows, cols = 6, 3000
+    k0 = rng.integers(0, 4, (rows, cols)).astype(np.int32)
+    k1 = np.round(rng.standard_normal((rows, cols)) * 2).astype(np.float32) / 2
+    k1[0, ::13] = np.nan
+    pay_f = rng.standard_normal((rows, cols)).astype(np.float32)
+    pay_b = rng.standard_normal((rows, cols)).astype(np.float32)
+    ops = [torch.from_numpy(k0).to(gpu), torch.from_numpy(k1).to(gpu), torch.from_numpy(pay_f).to(gpu),
+           to_dev(pay_b, "bf16", gpu)]
+    got = tax.sort(ops, num_keys=2, return_argsort=True, descending=descending)
+    torch.cuda.synchronize()
+    want, _ = O.sort([k0, k1, pay_f, O.round_to_dtype(pay_b, "bf16")], 2, return_argsort=True,
+                     descending=descending, dtypes=["i32", "f32", "f32", "bf16"])
+    assert got[3].dtype == torch.bfloat16
+    for g, w in zip(got, want):
+        assert _same(_host(g), w)
+
+
+def test_tumpy_axes_and_errors(gpu):
+    from tallax_amd import tumpy
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((2, 3, 40)).astype(np.float32)
+    xd = torch.from_numpy(x).to(gpu)
+    s = tumpy.sort(xd)
+    assert tuple(s.shape) == (2, 3, 40)
+    assert np.array_equal(s.cpu().numpy(), np.sort(x, axis=-1))
+    a = tumpy.argsort(xd, axis=None)
+    assert tuple(a.shape) == (240,)
+    assert np.array_equal(a.cpu().numpy(), np.argsort(x.reshape(-1), kind="stable"))
+    d = tumpy.argsort(xd, descending=True)
+    assert np.array_equal(d.cpu().numpy(), np.argsort(-x, axis=-1, kind="stable"))
+    with pytest.raises(ValueError):
+        tumpy.sort(xd, axis=0)
+    from tallax_amd import tax
+    with pytest.raises(ValueError):
+        tax.sort([xd[0], xd[1, :2]], num_keys=1)
+    with pytest.raises(ValueError):
+        tax.sort(xd, num_keys=1)   # 3D

@@ -289,3 +289,65 @@ def test_take_along_axis_oracle_closed_form():
     assert np.array_equal(O.take_along_axis(vt, idx.T.copy(), 0), np.take_along_axis(vt, idx.T, 0))
     iv = rng.integers(-100, 100, (4, 9)).astype(np.int32)
     assert O.take_along_axis(iv, np.full((4, 2), 9, np.int32), 1).dtype == np.int32
+
+
+# --------------------------------------------------------------------------- sort
+def test_sort_oracle_matches_stable_argsort_and_torch():
+    """Stable ascending / descending orders equal np.argsort(kind="stable") on
+    the sortable keys and torch.sort(stable=True) on NaN-free data; descending
+    stable equals xla_equivalent_sort's (-iota key, then reverse) construction
+    (sort.py:955-969)."""
+    import torch
+    rng = np.random.default_rng(21)
+    x = np.round(rng.standard_normal((6, 300)) * 4).astype(np.float32) / 4     # many ties
+    (v, i), path = O.sort([x], 1, is_stable=True, return_argsort=True)
+    assert path == "unpacked"
+    assert np.array_equal(i, np.argsort(x, axis=1, kind="stable"))
+    tv, ti = torch.sort(torch.from_numpy(x), dim=1, stable=True)
+    assert np.array_equal(i, ti.numpy()) and np.array_equal(v, tv.numpy())
+    (vd, idd), _ = O.sort([x], 1, is_stable=True, return_argsort=True, descending=True)
+    # xla_equivalent_sort: lexsort ascending on (x, -iota), then reverse
+    cols = x.shape[1]
+    for r in range(x.shape[0]):
+        o = np.lexsort([-np.arange(cols), x[r]])[::-1]
+        assert np.array_equal(idd[r], o)
+    td, tdi = torch.sort(torch.from_numpy(x), dim=1, descending=True, stable=True)
+    assert np.array_equal(idd, tdi.numpy())
+
+
+def test_sort_oracle_key_decode_and_paths():
+    """S1: NaN sorts above +inf and decodes to 0x7FFFFFFE, -0 decodes to +0;
+    bf16 keys come back as float32 unpacked, bf16 (NaN 0x7FFF) packed."""
+    x = np.array([[1.0, np.nan, -0.0, np.inf, -np.inf, 0.0, -2.5, np.nan]], np.float32)
+    (v,), _ = O.sort([x], 1)
+    b = v.view(np.uint32)[0]
+    assert list(b[:3]) == [0xFF800000, 0xC0200000, 0]          # -inf, -2.5, +0 (was -0 or +0)
+    assert b[3] == 0 and b[5] == 0x7F800000 and b[6] == b[7] == 0x7FFFFFFE
+    xb = O.round_to_dtype(x, "bf16")
+    (vb, ib), path = O.sort([xb], 1, is_stable=True, return_argsort=True, dtypes=["bf16"])
+    assert path == "packed"
+    assert vb.view(np.uint32)[0, -1] == 0x7FFF0000 and vb.view(np.uint32)[0, 2] == 0
+    (vu,), path = O.sort([xb], 1, is_stable=False, dtypes=["bf16"])
+    assert path == "unpacked" and vu.view(np.uint32)[0, -1] == 0x7FFFFFFE
+
+
+def test_sort_oracle_packed_descending_nonstable_ties():
+    """The packed bf16+index key is unique, so a non-stable descending argsort
+    has ties in descending index order (utils.py:205-216); stable keeps them
+    ascending (sort.py:807-809)."""
+    x = np.array([[1.0, 2.0, 1.0, 2.0, 1.0]], np.float32)
+    (_, i_ns), _ = O.sort([x], 1, is_stable=False, return_argsort=True, descending=True, dtypes=["bf16"])
+    (_, i_st), _ = O.sort([x], 1, is_stable=True, return_argsort=True, descending=True, dtypes=["bf16"])
+    assert list(i_ns[0]) == [3, 1, 4, 2, 0]
+    assert list(i_st[0]) == [1, 3, 0, 2, 4]
+
+
+def test_sort_oracle_two_keys_and_forced_stable():
+    rng = np.random.default_rng(4)
+    k0 = rng.integers(0, 3, (3, 50)).astype(np.int32)       # non-power-of-two int keys: forced stable
+    k1 = rng.integers(0, 4, (3, 50)).astype(np.float32)
+    pay = rng.standard_normal((3, 50)).astype(np.float32)
+    (a, b, c), _ = O.sort([k0, k1, pay], 2)
+    for r in range(3):
+        o = np.lexsort([np.arange(50), k1[r], k0[r]])
+        assert np.array_equal(c[r], pay[r, o]) and np.array_equal(a[r], k0[r, o])
