@@ -120,6 +120,173 @@ def top_k(x: np.ndarray, k: int, dtype: str = "f32"):
 
 
 # ---------------------------------------------------------------------------
+# approximate top-k: top_dynamic_k (tallax/_src/top_k.py:13-106, 203-514)
+# and its schedule maths (tallax/top_k_convergence_theory.py:5-128)
+# ---------------------------------------------------------------------------
+def log2_ceil(x: int) -> int:
+    """utils.log2 (utils.py:21-23): ceil(log2(x))."""
+    return int(math.ceil(math.log2(x)))
+
+
+def _log_convolve(log_a, log_b, trunc_len):
+    ma, mb = np.max(log_a), np.max(log_b)
+    if ma == -np.inf or mb == -np.inf:
+        return np.full(min(len(log_a) + len(log_b) - 1, trunc_len), -np.inf)
+    conv = np.convolve(np.exp(log_a - ma), np.exp(log_b - mb))[:trunc_len]
+    with np.errstate(divide="ignore"):
+        return np.log(conv) + ma + mb
+
+
+def depth_probs(k: int, num_bins: int) -> np.ndarray:
+    """compute_depth_probs (top_k_convergence_theory.py:45-103): P(max bin
+    occupancy == m), m = 1..k, for k balls thrown uniformly into num_bins bins:
+    P(max <= m) = k! / num_bins^k * [x^k] (sum_{i<=m} x^i / i!)^num_bins,
+    the polynomial power taken by squaring in log space, truncated at x^k."""
+    from scipy.special import gammaln
+    log_fact_k = gammaln(k + 1)
+    log_denom = k * np.log(num_bins)
+    probs = np.zeros(k)
+    prev = 0.0
+    for m in range(1, k + 1):
+        coeffs = -gammaln(np.arange(min(m + 1, k + 1)) + 1.0)
+        cur, res, power = coeffs, np.array([0.0]), num_bins
+        while power > 0:
+            if power % 2 == 1:
+                res = _log_convolve(res, cur, k + 1)
+            if power > 1:
+                cur = _log_convolve(cur, cur, k + 1)
+            power //= 2
+        log_cdf = (res[k] if len(res) > k else -np.inf) + log_fact_k - log_denom
+        cdf = min(1.0, float(np.exp(log_cdf)) if log_cdf > -700 else 0.0)
+        probs[m - 1] = max(0.0, cdf - prev)
+        prev = cdf
+        if cdf >= 1.0 - 1e-14:
+            break
+    return probs
+
+
+def calculate_depth_thresholds(k, num_bins, block_size=8, target_yields=(0.66, 0.95, 0.9999)):
+    """top_k_convergence_theory.py:106-128: the smallest depths d (1-based)
+    with P(max occupancy <= d) ** block_size >= each target yield."""
+    cdf = depth_probs(k, num_bins).cumsum()
+    block = cdf ** block_size
+    depths = set()
+    for thr in target_yields:
+        for i, val in enumerate(block):
+            if val >= thr:
+                depths.add(i + 1)
+                break
+    return tuple(sorted(depths))
+
+
+def topm_schedule(max_k, num_bins, block_token, schedule=None):
+    """top_dynamic_k's schedule (top_k.py:472-478): the auto schedule is the
+    depth thresholds at yields (0.8, 0.98, 0.9999) plus one; deduplicated,
+    sorted, with a leading 0."""
+    if schedule is None:
+        schedule = tuple(t + 1 for t in calculate_depth_thresholds(max_k, num_bins, block_token,
+                                                                   target_yields=(0.8, 0.98, 0.9999)))
+    return (0,) + tuple(sorted(set(int(m) for m in schedule)))
+
+
+def binned_topm(x: np.ndarray, m: int, num_bins: int, dtype: str = "f32"):
+    """binned_top_k (top_k.py:13-106) run to depth m: bin b holds columns
+    j = b (mod num_bins); each bin keeps its m largest values; values <=
+    finfo.min or NaN are never admitted.  The values at each rank are exactly
+    those of the reference's strict-> sinking insert (pinned by a literal
+    simulation in tests/test_oracle.py); among tied values the reference's
+    kept indices depend on the insertion path, and this restatement keeps the
+    lowest indices (the BASELINE tie contract).  Returns (vals [R, m, num_bins] f32, idxs
+    [R, m, num_bins] int32), rank-major; unfilled slots hold (finfo.min, -1)."""
+    x = np.asarray(x, dtype=np.float32)
+    rows, cols = x.shape
+    lo = dtype_min(dtype)
+    nb = -(-cols // num_bins)
+    pad = np.full((rows, nb * num_bins), np.nan, np.float32)
+    pad[:, :cols] = x
+    vb = pad.reshape(rows, nb, num_bins)                        # [R, slice, bin]
+    jb = (np.arange(nb)[:, None] * num_bins + np.arange(num_bins)[None, :]).astype(np.int64)
+    admitted = vb > lo                                          # False for NaN, -inf, finfo.min, padding
+    key = np.where(admitted, vb, -np.inf).astype(np.float64)
+    # order inside each bin: value descending, index ascending
+    order = np.lexsort((np.broadcast_to(jb, vb.shape), -key), axis=1)[:, :m, :]
+    vals = np.take_along_axis(key, order, axis=1)
+    idxs = np.take_along_axis(np.broadcast_to(jb, vb.shape), order, axis=1)
+    ok = vals > -np.inf
+    out_v = np.full((rows, m, num_bins), lo, np.float32)
+    out_i = np.full((rows, m, num_bins), -1, np.int32)
+    take = min(m, nb)
+    out_v[:, :take][ok[:, :take]] = vals[:, :take][ok[:, :take]].astype(np.float32)
+    out_i[:, :take][ok[:, :take]] = idxs[:, :take][ok[:, :take]].astype(np.int32)
+    return out_v, out_i
+
+
+def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, replace_val=None,
+                  dtype: str = "f32"):
+    """top_dynamic_k with guarantee_convergence=False (top_k.py:203-514):
+    (vals [R, max_k], idxs [R, max_k] int32, valid bool, depths [R] int32,
+    cutoff_vals [R] f32).
+
+    For each schedule step m (after the leading 0), evaluated while some row
+    of the row's block of `block_token` rows has not converged:
+      pivot = max over bins of the m-th largest, num_larger = #(ranks < m-1
+      that are >= pivot); a row converges when num_larger >= k[row]; depth =
+      m - 1 at the first convergence (max_k if never); cutoff = the pivot of
+      the last step evaluated (top_k.py:283-320).
+    valid = (max depth over all rows < schedule[-1]) or schedule[-1] == max_k.
+    The output is the top-128 of the first depth_upper ranks of every bin,
+    depth_upper the power-of-two bucket of the global max depth
+    (top_k.py:333-364), ordered by value then lowest index (the reference's
+    network order inside ties is not pinned), then truncated to max_k;
+    positions >= k[row] get replace_val in the input dtype when given."""
+    x = np.asarray(x, dtype=np.float32)
+    rows, cols = x.shape
+    if rows % block_token:
+        raise ValueError("num_tokens must be divisible by block_token")
+    if max_k > NUM_LANES:
+        raise NotImplementedError
+    kk = np.broadcast_to(np.asarray(k, dtype=np.int64), (rows,))
+    sched = topm_schedule(max_k, num_bins, block_token, schedule)
+    max_m = sched[-1]
+    buf = max(max_m, 2 ** log2_ceil(max_m - 1)) if max_m > 1 else max_m
+    bv, bi = binned_topm(x, buf, num_bins, dtype)
+    depths = np.full(rows, max_k, np.int32)
+    cutoff = np.zeros(rows, np.float32)
+    for b0 in range(0, rows, block_token):
+        blk = slice(b0, b0 + block_token)
+        for m in sched[1:]:
+            pivot = bv[blk, m - 1, :].max(axis=1)
+            num_larger = (bv[blk, :m - 1, :] >= pivot[:, None, None]).sum(axis=(1, 2))
+            conv = num_larger >= kk[blk]
+            d = depths[blk]
+            depths[blk] = np.where(conv & (d == max_k), m - 1, d)
+            cutoff[blk] = pivot
+            if conv.all():
+                break
+    gmax = int(depths.max())
+    valid = bool(gmax < sched[-1] or sched[-1] == max_k)
+    gsched = sorted(set(2 ** log2_ceil(s - 1) if s > 1 else s for s in sched))
+    upper = gsched[-1]
+    for lo_d, up_d in zip(gsched, gsched[1:]):
+        if lo_d < gmax <= up_d:
+            upper = up_d
+            break
+    sv = bv[:, :upper, :].reshape(rows, -1)
+    si = bi[:, :upper, :].reshape(rows, -1)
+    filler = si < 0
+    kv = np.where(filler, -np.inf, sv.astype(np.float64))
+    ki = np.where(filler, np.iinfo(np.int64).max, si.astype(np.int64))
+    order = np.lexsort((ki, -kv), axis=1)[:, :NUM_LANES]
+    vals = np.take_along_axis(sv, order, 1)[:, :max_k].copy()
+    idxs = np.take_along_axis(si, order, 1)[:, :max_k].copy()
+    if replace_val is not None:
+        pos = np.arange(vals.shape[1])[None, :]
+        rv = round_to_dtype(np.float32(replace_val), dtype)
+        vals = np.where(pos < kk[:, None], vals, rv).astype(np.float32)
+    return vals, idxs, valid, depths, cutoff
+
+
+# ---------------------------------------------------------------------------
 # exp / log (float32, one IEEE op per step; mirrors tallax_amd/csrc/tx_math.h)
 # ---------------------------------------------------------------------------
 _LOG2E, _LN2_HI, _LN2_LO = _f(0x3FB8AA3B), _f(0x3F317000), _f(0x3805FDF4)

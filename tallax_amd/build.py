@@ -28,6 +28,7 @@ SOURCES = [
     "row_select.hip",
     "scan_gather.hip",
     "sort_rows.hip",
+    "binned.hip",
     "testing.hip",
 ]
 

@@ -65,6 +65,7 @@ struct SelArgs {
   // top-k outputs
   void* out_vals;
   int32_t* out_idx;
+  const int32_t* k_rows;  // optional: positions >= k_rows[row] get replace_in_dtype
   // segment lists: rows * nseg * kRun composites
   uint64_t* ws_lists;
   // sampler
@@ -391,7 +392,8 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
       const uint64_t c = list[i];
       const uint32_t kk = comp_key(c);
       const int32_t idx = comp_idx(c);
-      const uint32_t b = kk > inel ? T::load_bits(rowp, idx) : T::kMinBits;
+      uint32_t b = kk > inel ? T::load_bits(rowp, idx) : T::kMinBits;
+      if (a.k_rows && i >= a.k_rows[row]) b = __float_as_uint(a.replace_in_dtype);
       T::store(a.out_vals, row * a.k + i, b);
       a.out_idx[row * a.k + i] = idx;
     }
@@ -974,6 +976,35 @@ int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k,
   a.ws_lists = (uint64_t*)workspace;
   return dtype == kF32 ? launch_select<kF32, false>(a, p, stream, "tallax_topk")
                        : launch_select<kBF16, false>(a, p, stream, "tallax_topk");
+}
+
+int tallax_topk_replace(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k, const int32_t* k_rows,
+                        double replace_val, void* out_vals, int32_t* out_idx, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  int st = check_common(x, dtype, rows, cols);
+  if (st) return st;
+  if (k < 1 || k > kMaxK) { set_error("k=%lld outside [1, %d]", (long long)k, kMaxK); return k > kMaxK ? kUnsupported : kInvalidArgument; }
+  if (k > cols) { set_error("k=%lld exceeds row length %lld", (long long)k, (long long)cols); return kInvalidArgument; }
+  if (!out_vals || !out_idx || !k_rows) { set_error("null pointer argument"); return kInvalidArgument; }
+  if (rows == 0) return kOk;
+  Plan p;
+  st = plan_rows(rows, cols, dtype, &p);
+  if (st) return st;
+  const size_t need = ws_bytes_for(rows, p);
+  if (workspace_bytes < need || (need && !workspace)) {
+    set_error("workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
+    return kWorkspaceTooSmall;
+  }
+  SelArgs a = {};
+  a.x = x; a.rows = rows; a.cols = cols; a.k = (int)k;
+  a.nseg = p.nseg; a.vps = p.vps;
+  a.out_vals = out_vals; a.out_idx = out_idx;
+  a.k_rows = k_rows;
+  const float rf = (float)replace_val;
+  a.replace_in_dtype = dtype == kBF16 ? round_to_bf16(rf) : rf;
+  a.ws_lists = (uint64_t*)workspace;
+  return dtype == kF32 ? launch_select<kF32, false>(a, p, stream, "tallax_topk_replace")
+                       : launch_select<kBF16, false>(a, p, stream, "tallax_topk_replace");
 }
 
 size_t tallax_sample_workspace_size(int64_t rows, int64_t vocab, int dtype) {

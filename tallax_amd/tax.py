@@ -52,6 +52,84 @@ def top_k(logits: torch.Tensor, k: int, block_token: int = 8, num_bins: int = NU
     return vals, idx
 
 
+def _k_rows(k, rows: int, device) -> torch.Tensor:
+    t = k if isinstance(k, torch.Tensor) else torch.tensor(k, dtype=torch.int32)
+    t = t.to(device=device, dtype=torch.int32)
+    if t.ndim == 0:
+        t = t.expand(rows)
+    if tuple(t.shape) != (rows,):
+        raise ValueError(f"k has shape {tuple(t.shape)}, expected () or ({rows},)")
+    return t.contiguous()
+
+
+def top_dynamic_k(logits: torch.Tensor, k, max_k: int, block_token: int = 8, num_bins: int = NUM_LANES,
+                  bins_topm_unroll: int = 32, bins_topm_schedule=None, guarantee_convergence: bool = False,
+                  replace_val=None, interpret: bool = False):
+    """Per-row top-k (k <= max_k <= 128) by binned top-m supersets.
+
+    Reference: top_dynamic_k (tallax/_src/top_k.py:385-514).
+      * guarantee_convergence=False: the binned algorithm, returning
+        (vals [R, max_k], idxs [R, max_k] int32, valid (bool scalar tensor),
+        depths [R] int32, cutoff_vals [R] float32).  Bins are columns mod
+        num_bins; the schedule (auto from the convergence theory if None)
+        decides depths/cutoffs; the result is the top-128 of the first
+        depth_upper ranks of every bin, ordered by value then lowest index.
+      * guarantee_convergence=True: (vals, idxs), the exact top-max_k (the
+        converged answer, ties to the lowest index, as tax.top_k).
+    Positions >= k[row] hold replace_val (in the logits dtype) when given.
+    Raises ValueError if rows % block_token != 0 and NotImplementedError for
+    max_k > 128, like the reference.
+    """
+    del bins_topm_unroll, interpret
+    from . import schedule as sch
+    _lib.require_cuda(logits)
+    _canonical_2d(logits)
+    rows, cols = logits.shape
+    if rows % block_token != 0:
+        raise ValueError("num_tokens must be divisible by block_token")
+    max_k = int(max_k)
+    if max_k > NUM_LANES:
+        raise NotImplementedError(f"max_k={max_k} > {NUM_LANES}")
+    x = logits.contiguous()
+    dt = _lib.dtype_code(x)
+    if dt == _lib.I32:
+        raise NotImplementedError("top_dynamic_k on int32 logits is not supported")
+    kr = _k_rows(k, rows, x.device)
+    dev = x.device
+    stream = _lib.stream_of(x)
+    vals = torch.empty((rows, max_k), dtype=x.dtype, device=dev)
+    idx = torch.empty((rows, max_k), dtype=torch.int32, device=dev)
+    if guarantee_convergence:
+        if max_k > cols:
+            raise ValueError(f"max_k={max_k} exceeds row length {cols}")
+        need = _lib.LIB.tallax_topk_workspace_size(rows, cols, max_k, dt)
+        ws = _lib.workspace(dev, need)
+        if replace_val is None:
+            _lib.check(_lib.LIB.tallax_topk(x.data_ptr(), dt, rows, cols, max_k, vals.data_ptr(), idx.data_ptr(),
+                                            ws.data_ptr() if need else None, ws.numel() if need else 0, stream),
+                       "top_dynamic_k")
+        else:
+            _lib.check(_lib.LIB.tallax_topk_replace(x.data_ptr(), dt, rows, cols, max_k, kr.data_ptr(),
+                                                    float(replace_val), vals.data_ptr(), idx.data_ptr(),
+                                                    ws.data_ptr() if need else None, ws.numel() if need else 0,
+                                                    stream), "top_dynamic_k")
+        return vals, idx
+    steps = sch.topm_schedule(max_k, num_bins, block_token, bins_topm_schedule)
+    import ctypes
+    arr = (ctypes.c_int32 * len(steps))(*steps)
+    need = _lib.LIB.tallax_top_dynamic_k_workspace_size(rows, num_bins, arr, len(steps))
+    ws = _lib.workspace(dev, max(need, 1))
+    valid = torch.empty(1, dtype=torch.int32, device=dev)
+    depths = torch.empty(rows, dtype=torch.int32, device=dev)
+    cutoff = torch.empty(rows, dtype=torch.float32, device=dev)
+    _lib.check(_lib.LIB.tallax_top_dynamic_k(
+        x.data_ptr(), dt, rows, cols, kr.data_ptr(), max_k, block_token, num_bins, arr, len(steps),
+        int(replace_val is not None), float(replace_val) if replace_val is not None else 0.0, vals.data_ptr(),
+        idx.data_ptr(), valid.data_ptr(), depths.data_ptr(), cutoff.data_ptr(), ws.data_ptr(), ws.numel(),
+        stream), "top_dynamic_k")
+    return vals, idx, valid.reshape(()).bool(), depths, cutoff
+
+
 _SORT_DTYPES = (torch.float32, torch.bfloat16, torch.int32)
 
 
@@ -178,4 +256,4 @@ def cumsum(arr: torch.Tensor, axis: int, reverse: bool = False, interpret: bool 
     return out
 
 
-__all__ = ["sort", "top_k", "cumsum"]
+__all__ = ["sort", "top_k", "top_dynamic_k", "cumsum"]

@@ -1,0 +1,97 @@
+"""GPU parity: tax.top_dynamic_k (approximate, binned) and its exact
+guarantee_convergence=True form through the C ABI against the oracle on
+identical seeded inputs (bit-exact values, indices, valid, depths and
+cutoffs), with config 3's recall@50 of the approximate result against the
+exact one reported."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tallax_oracle as O
+from tests.gpu_util import bits, from_dev_vals, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+def _check(got, want):
+    gv, gi, gvalid, gd, gc = got
+    wv, wi, wvalid, wd, wc = want
+    assert bool(gvalid.item()) == wvalid
+    assert np.array_equal(gd.cpu().numpy(), wd)
+    assert np.array_equal(bits(gc.cpu().numpy()), bits(wc))
+    assert np.array_equal(gi.cpu().numpy(), wi)
+    assert np.array_equal(bits(from_dev_vals(gv)), bits(wv))
+
+
+def test_config3_approx_and_recall(gpu):
+    from tallax_amd import tax
+    _log("config 3 approximate: f32 [128,151936] + spikes, k=50")
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((128, 151936)) * 2).astype(np.float32)
+    for r in range(128):
+        x[r, rng.choice(151936, 32, replace=False)] = 8.0
+    xd = torch.from_numpy(x).to(gpu)
+    got = tax.top_dynamic_k(xd, 50, 50)
+    torch.cuda.synchronize()
+    want = O.top_dynamic_k(x, 50, 50)
+    _check(got, want)
+    ev, ei = O.top_k(x, 50)
+    gi = got[1].cpu().numpy()
+    recall = np.mean([len(set(gi[r]) & set(ei[r])) / 50 for r in range(128)])
+    _log(f"recall@50 of approximate vs exact: {recall:.4f}")
+    assert recall == 1.0 and bool(got[2].item())
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("rows,cols,max_k,num_bins,block_token,schedule", [
+    (16, 20000, 64, 128, 8, None),
+    (8, 5000, 128, 256, 8, None),
+    (12, 3000, 20, 64, 4, (3, 6)),
+    (8, 300, 32, 128, 8, (2, 4, 9)),     # short rows: fillers at depth
+    (16, 50000, 8, 512, 8, (2,)),        # unconverged rows: approximate, valid False
+])
+def test_top_dynamic_k_parity(gpu, dtype, rows, cols, max_k, num_bins, block_token, schedule):
+    from tallax_amd import tax
+    _log(f"top_dynamic_k {dtype} [{rows},{cols}] max_k={max_k} bins={num_bins} bt={block_token} sched={schedule}")
+    rng = np.random.default_rng(rows * cols + max_k)
+    x = np.round(rng.standard_normal((rows, cols)) * 16).astype(np.float32) / 16   # many ties
+    x[0, ::5] = np.nan
+    x[1, ::3] = -np.inf
+    x[2, 1::4] = O.dtype_min(dtype)
+    k = rng.integers(1, max_k + 1, rows).astype(np.int32)
+    xd = to_dev(x, dtype, gpu)
+    got = tax.top_dynamic_k(xd, torch.from_numpy(k).to(gpu), max_k, block_token=block_token, num_bins=num_bins,
+                            bins_topm_schedule=schedule, replace_val=-1e12)
+    torch.cuda.synchronize()
+    want = O.top_dynamic_k(O.round_to_dtype(x, dtype), k, max_k, block_token=block_token, num_bins=num_bins,
+                           schedule=schedule, replace_val=-1e12, dtype=dtype)
+    _check(got, want)
+
+
+def test_top_dynamic_k_guaranteed_is_exact(gpu):
+    from tallax_amd import tax
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((256, 128256)) * 3).astype(np.float32)
+    k = rng.integers(1, 1025, 256).clip(max=128).astype(np.int32)
+    xd = to_dev(x, "bf16", gpu)
+    vals, idx = tax.top_dynamic_k(xd, torch.from_numpy(k).to(gpu), 128, num_bins=256, bins_topm_schedule=(5, 9),
+                                  guarantee_convergence=True, replace_val=-1e12)
+    torch.cuda.synchronize()
+    hv = O.round_to_dtype(x, "bf16")
+    ev, ei = O.top_k(hv, 128, dtype="bf16")
+    ev = np.where(np.arange(128)[None, :] < k[:, None], ev, O.round_to_dtype(np.float32(-1e12), "bf16"))
+    assert np.array_equal(idx.cpu().numpy(), ei)
+    assert np.array_equal(bits(from_dev_vals(vals)), bits(ev))
+
+
+def test_top_dynamic_k_errors(gpu):
+    from tallax_amd import tax
+    x = torch.zeros((12, 100), device=gpu)
+    with pytest.raises(ValueError):
+        tax.top_dynamic_k(x, 4, 4, block_token=8)
+    with pytest.raises(NotImplementedError):
+        tax.top_dynamic_k(x[:8], 4, 129)

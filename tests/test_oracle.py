@@ -351,3 +351,73 @@ def test_sort_oracle_two_keys_and_forced_stable():
     for r in range(3):
         o = np.lexsort([np.arange(50), k1[r], k0[r]])
         assert np.array_equal(c[r], pay[r, o]) and np.array_equal(a[r], k0[r, o])
+
+
+# --------------------------------------------------------------------------- approximate top-k
+def test_depth_probs_closed_forms_and_monte_carlo():
+    """compute_depth_probs (top_k_convergence_theory.py:45-103): P(max bin
+    occupancy == m) for k balls in n bins.  Closed forms for tiny cases and a
+    Monte Carlo estimate for a realistic one; the product's restatement
+    (tallax_amd/schedule.py) agrees with the oracle's."""
+    from tallax_amd import schedule as S
+    assert np.allclose(O.depth_probs(1, 128), [1.0])
+    assert np.allclose(O.depth_probs(2, 2), [0.5, 0.5])
+    assert np.allclose(O.depth_probs(3, 3), [6 / 27, 18 / 27, 3 / 27])
+    rng = np.random.default_rng(0)
+    k, n, trials = 50, 128, 20000
+    occ = np.zeros((trials, n), np.int32)
+    balls = rng.integers(0, n, (trials, k))
+    np.add.at(occ, (np.repeat(np.arange(trials), k), balls.ravel()), 1)
+    mc = np.bincount(occ.max(1), minlength=k + 1)[1:] / trials
+    p = O.depth_probs(k, n)
+    assert np.abs(np.cumsum(mc) - np.cumsum(p)).max() < 0.015
+    for kk, nn in [(50, 128), (128, 256), (8, 16), (1, 128)]:
+        assert np.allclose(S.max_occupancy_pdf(kk, nn), O.depth_probs(kk, nn), rtol=1e-9, atol=1e-12)
+        assert S.topm_schedule(kk, nn, 8) == O.topm_schedule(kk, nn, 8)[1:]
+
+
+def test_binned_topm_brute_force():
+    """binned_top_k (top_k.py:13-106) simulated literally (strict-> sinking
+    insert in index order; NaN / -inf / finfo.min never admitted): the values at
+    every rank equal the oracle's per-bin top-m exactly.  The indices agree
+    wherever the value is untied; among tied values the reference's kept
+    indices depend on the insertion path (a displaced element cannot pass an
+    equal one), so the oracle's lowest-index choice is the documented
+    contract there."""
+    rng = np.random.default_rng(8)
+    x = np.round(rng.standard_normal((3, 70)) * 2).astype(np.float32) / 2
+    x[0, ::7] = np.nan
+    x[1, ::5] = -np.inf
+    x[2, ::3] = O.F32_MIN
+    x[:, 60:] = rng.standard_normal((3, 10)).astype(np.float32) * 7    # some untied values
+    v, i = O.binned_topm(x, 4, 8)
+    for r in range(3):
+        for b in range(8):
+            lv, li = [O.F32_MIN] * 4, [-1] * 4
+            for j in range(b, 70, 8):
+                bv, bi = x[r, j], j
+                for q in range(4):
+                    if bv > lv[q]:
+                        lv[q], bv = bv, lv[q]
+                        li[q], bi = bi, li[q]
+            assert np.array_equal(v[r, :, b], np.array(lv, np.float32))
+            col = x[r, b::8]
+            for q in range(4):
+                if li[q] >= 0 and np.sum(col == lv[q]) == 1:
+                    assert i[r, q, b] == li[q]
+
+
+def test_top_dynamic_k_converged_rows_are_exact():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((16, 20000)).astype(np.float32)
+    x[3, rng.choice(20000, 40, replace=False)] = 8.0        # ties inside the top-k
+    vals, idx, valid, depths, cutoff = O.top_dynamic_k(x, 50, 50)
+    ev, ei = O.top_k(x, 50)
+    assert valid and (depths < 50).all()
+    assert np.array_equal(vals, ev) and np.array_equal(idx, ei)
+    # cutoff is a pivot: a value present in the row, below every kept value
+    assert all(cutoff[r] in x[r] and cutoff[r] <= vals[r, -1] for r in range(16))
+    # an unconvergeable schedule: depth stays max_k, valid is False, result approximate
+    v2, i2, valid2, d2, _ = O.top_dynamic_k(x, 50, 50, schedule=(2,))
+    assert not valid2 and (d2 == 50).all()
+    assert np.all(np.diff(v2, axis=1) <= 0)
