@@ -176,6 +176,21 @@ int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols,
                      int key_out_dtype, const void* aux, int aux_dtype, void* aux_out, int aux_out_dtype,
                      tallax_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Prefill-scale softmax -> top-k -> cumsum -> top-p cutoff, fused (BASELINE
+ * config 5).  Replaces the composition the reference runs for it:
+ * jax.nn.softmax, tax.sort(probs, descending=True, return_argsort=True) cut
+ * to k (tallax/_src/sort.py:768-929), tax.cumsum(axis=1)
+ * (tallax/_src/cumsum.py:75-101) and sum(cumsum < p).
+ * logits [rows, cols] f32 -> out_probs [rows, k] f32 (descending softmax
+ * probabilities), out_idx [rows, k] int32 (the k largest logits, ties to the
+ * lowest index), out_cumsum [rows, k] f32 (tile order of tax.cumsum),
+ * out_cutoff [rows] int32 = #(cumsum < p).  1 <= k <= 2048, k <= cols.
+ * Rows holding NaN or +inf give NaN probabilities, indices 0..k-1, cutoff 0.
+ * ---------------------------------------------------------------------- */
+int tallax_softmax_topk_cumsum(const float* logits, int64_t rows, int64_t cols, int k, float p, float* out_probs,
+                               int32_t* out_idx, float* out_cumsum, int32_t* out_cutoff, tallax_stream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -531,6 +531,30 @@ def sort(operands, num_keys: int, is_stable: bool = False, return_argsort: bool 
 
 
 # ---------------------------------------------------------------------------
+# config 5: softmax -> top-k -> cumsum -> top-p cutoff
+# ---------------------------------------------------------------------------
+def softmax_topk_cumsum_f64(x: np.ndarray, k: int, p: float):
+    """The float64 truth for the composition jax.nn.softmax, tax.sort(probs,
+    descending=True, return_argsort=True)[:, :k], tax.cumsum(axis=1) and
+    #(cumsum < p): (idx [R, k] int32, probs64, cum64, cutoff64).  Positions are
+    the k largest logits, ties to the lowest index (probability is monotone in
+    the logit, so this is the descending probability order with equal
+    probabilities in a valid order)."""
+    x = np.asarray(x, dtype=np.float32)
+    comp = topk_composite(x)
+    part = np.argpartition(comp, comp.shape[-1] - k, axis=-1)[..., -k:]
+    order = np.argsort(np.take_along_axis(comp, part, -1), axis=-1)[..., ::-1]
+    idx = np.take_along_axis(part, order, -1).astype(np.int32)
+    x64 = x.astype(np.float64)
+    m = x64.max(axis=1, keepdims=True)
+    with np.errstate(invalid="ignore"):
+        e = np.exp(x64 - m)
+    probs = np.take_along_axis(e, idx, 1) / e.sum(axis=1, keepdims=True)
+    cum = np.cumsum(probs, axis=1)
+    return idx, probs, cum, (cum < p).sum(axis=1).astype(np.int32)
+
+
+# ---------------------------------------------------------------------------
 # take_along_axis (tallax/_src/gather.py:11-83)
 # ---------------------------------------------------------------------------
 def take_along_axis(values: np.ndarray, indices: np.ndarray, axis: int) -> np.ndarray:

@@ -3,6 +3,6 @@
 Public modules mirror the reference: `tax` (tallax/tax.py), `tumpy`
 (tallax/tumpy.py) and `sampling` (tallax/_src/sampling.py).
 """
-from . import sampling, tax, tumpy  # noqa: F401
+from . import prefill, sampling, tax, tumpy  # noqa: F401
 
-__all__ = ["tax", "tumpy", "sampling"]
+__all__ = ["tax", "tumpy", "sampling", "prefill"]

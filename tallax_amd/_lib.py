@@ -43,6 +43,8 @@ _SIGNATURES = {
     "tallax_top_dynamic_k_workspace_size": ([_c_i64, _c_int, _c_p, _c_int], _c_sz),
     "tallax_top_dynamic_k": ([_c_p, _c_int, _c_i64, _c_i64, _c_p, _c_int, _c_int, _c_int, _c_p, _c_int, _c_int,
                               _c_d, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p], _c_int),
+    "tallax_softmax_topk_cumsum": ([_c_p, _c_i64, _c_i64, _c_int, ctypes.c_float, _c_p, _c_p, _c_p, _c_p, _c_p],
+                                   _c_int),
     # test hooks (include/tallax_hip_testing.h)
     "tallax_testing_expf_logf": ([_c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
     "tallax_testing_gumbel": ([ctypes.c_uint32, ctypes.c_uint32, _c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),

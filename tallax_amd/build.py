@@ -29,6 +29,7 @@ SOURCES = [
     "scan_gather.hip",
     "sort_rows.hip",
     "binned.hip",
+    "softmax_topk.hip",
     "testing.hip",
 ]
 

@@ -1,0 +1,344 @@
+// Prefill-scale softmax -> top-k -> cumsum -> top-p cutoff, fused, for gfx950
+// (f32 [1024, 201088], k = 2048, p = 0.9).
+//
+// The reference composes it from jax.nn.softmax, tax.sort(probs,
+// descending=True, return_argsort=True) cut to k (sort.py:768-929), tax.cumsum
+// (cumsum.py:32-101) and a count of cumsum < p.  Here, per row:
+//   * probs = exp(x - max) / sum(exp(x - max)) (float32; the sum order is this
+//     kernel's, so probabilities and their cumsum are pinned to float64 by
+//     tolerance, not bit for bit);
+//   * the k selected positions are the k largest logits, ties to the lowest
+//     index.  Probability is a non-decreasing function of the logit, so this
+//     is a descending sort of the probabilities in which equal probabilities
+//     keep a valid (the reference's non-stable sort leaves their order open)
+//     order, and it is exact;
+//   * cumsum over the k sorted probabilities in the reference's tile order
+//     (128-position tiles, Hillis-Steele inside, sequential carry);
+//   * cutoff = #(cumsum < p).
+// A row holding NaN or +inf gives NaN probabilities (as jax.nn.softmax does),
+// indices 0..k-1 and cutoff 0.
+//
+// One 1024-thread workgroup per row, two streaming passes:
+//   pass 1: the row maximum and each thread's four largest select keys; the
+//           k-th largest of those 4096 keys, T0, has at least k elements >= it;
+//   pass 2: exp-sum, and every element with key >= T0 appended to LDS
+//           (expected ~k + 4 % for Gaussian rows);
+// then a workgroup bitonic sort of the candidates, the outputs, the tile
+// scan and the cutoff.  If the candidates overflow (heavy ties), the k-th
+// composite is found by bisection over the row instead.
+#include <float.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "tallax_hip.h"
+#include "tx_block_sort.h"
+#include "tx_common.h"
+#include "tx_host.h"
+#include "tx_scan.h"
+
+namespace tx {
+
+constexpr int kPfNT = 1024;
+constexpr int kPfNW = kPfNT / kWave;
+constexpr int kPfCap = 8192;   // candidate records in LDS
+constexpr int kPfMaxK = 4096;
+
+struct PfArgs {
+  const float* x;
+  int64_t rows, cols;
+  int k;
+  float p;
+  float* out_probs;
+  int32_t* out_idx;
+  float* out_cum;
+  int32_t* out_cutoff;
+};
+
+__device__ __forceinline__ float pf_exp(float x, float m) {
+#pragma clang fp contract(off)
+  return __builtin_amdgcn_exp2f((x - m) * 1.44269504088896341f);
+}
+
+template <int E>
+__device__ void pf_sort_desc(uint64_t* pool, int n) {
+  uint64_t v[E];
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int i = t * E + r;
+    v[r] = i < n ? pool[i] : 0ull;
+  }
+  __syncthreads();
+  block_bitonic_sort<uint64_t, E>(v, pool, kPfNT * E, true);
+#pragma unroll
+  for (int r = 0; r < E; ++r) pool[t * E + r] = v[r];
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
+  extern __shared__ __align__(16) uint64_t pool[];  // kPfCap records
+  __shared__ float redf[kPfNW];
+  __shared__ int redi[kPfNW];
+  __shared__ uint32_t s_t0;
+  __shared__ int s_cnt;
+  __shared__ float s_cum_carry[kPfMaxK / 128];
+  __shared__ float s_tile_sum[kPfMaxK / 128];
+  const int t = threadIdx.x, w = t / kWave, l = lane_id();
+  const int64_t row = blockIdx.x;
+  const float* xr = a.x + row * a.cols;
+  const RowVec<4> rv(xr);
+  const int64_t nv = (a.cols + rv.mis + 3) / 4;
+  const int k = a.k;
+
+  // ---- pass 1: maximum, NaN / +inf, per-thread top-4 select keys ----------
+  float m = -INFINITY;
+  bool bad = false;
+  uint32_t top[4] = {0u, 0u, 0u, 0u};
+  auto pass1_vec = [&](const uint4 q, int64_t v) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t e = v * 4 - rv.mis + i;
+      if (e < 0 || e >= a.cols) continue;
+      const float x = __uint_as_float(d[i]);
+      m = fmaxf(m, x);
+      bad = bad || (x != x) || x == INFINITY;
+      uint32_t key = select_key(d[i]);
+      if (key > top[3]) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool sw = key > top[r];
+          const uint32_t tv = top[r];
+          top[r] = sw ? key : tv;
+          key = sw ? tv : key;
+        }
+      }
+    }
+  };
+  {
+    int64_t v = t;
+    for (; v + 3 * kPfNT < nv; v += 4 * kPfNT) {
+      const uint4 q0 = rv.base[v], q1 = rv.base[v + kPfNT], q2 = rv.base[v + 2 * kPfNT], q3 = rv.base[v + 3 * kPfNT];
+      pass1_vec(q0, v);
+      pass1_vec(q1, v + kPfNT);
+      pass1_vec(q2, v + 2 * kPfNT);
+      pass1_vec(q3, v + 3 * kPfNT);
+    }
+    for (; v < nv; v += kPfNT) pass1_vec(rv.base[v], v);
+  }
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) m = fmaxf(m, lane_xor_f(m, d));
+  const bool wbad = __ballot(bad) != 0ull;
+  if (l == 0) {
+    redf[w] = m;
+    redi[w] = wbad ? 1 : 0;
+  }
+  // threshold: the k-th largest of the 4096 per-thread keys
+  uint32_t* keys = (uint32_t*)pool;
+  block_bitonic_sort<uint32_t, 4>(top, keys, kPfNT * 4, true);
+  if (t == (k - 1) / 4) s_t0 = top[(k - 1) % 4];
+  if (t == 0) s_cnt = 0;
+  __syncthreads();
+  m = redf[0];
+  bool row_bad = redi[0] != 0;
+  for (int i = 1; i < kPfNW; ++i) {
+    m = fmaxf(m, redf[i]);
+    row_bad = row_bad || redi[i] != 0;
+  }
+  const uint32_t t0 = s_t0 > 1u ? s_t0 : 1u;  // >= 1: dead slots (key 0) never pass
+
+  // ---- pass 2: exp-sum and candidates -----------------------------------------
+  float s = 0.0f;
+  auto pass2_vec = [&](const uint4 q, int64_t v) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    float vs = 0.0f;
+    uint32_t mask = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t e = v * 4 - rv.mis + i;
+      const bool live = e >= 0 && e < a.cols;
+      const float x = __uint_as_float(d[i]);
+      vs += live ? pf_exp(x, m) : 0.0f;
+      mask |= (live && select_key(d[i]) >= t0 ? 1u : 0u) << i;
+    }
+    s += vs;
+    const uint64_t any = __ballot(mask != 0u);
+    if (any) {
+      for (;;) {
+        const bool hc = mask != 0u;
+        const uint64_t bm = __ballot(hc);
+        if (!bm) break;
+        uint64_t c = 0;
+        if (hc) {
+          const int i = __builtin_ctz(mask);
+          mask &= mask - 1u;
+          c = make_comp(select_key(d[i]), (uint32_t)(v * 4 - rv.mis + i));
+        }
+        // one atomic per wave step, issued by the first active lane (lanes
+        // may have left the vector loop already)
+        const int lead = __builtin_ctzll(__ballot(true));
+        int base = 0;
+        if (l == lead) base = atomicAdd(&s_cnt, (int)__popcll(bm));
+        base = __builtin_amdgcn_readfirstlane(base);
+        if (hc) {
+          const int off = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
+          if (off < kPfCap) pool[off] = c;
+        }
+      }
+    }
+  };
+  __syncthreads();  // the key sort above used the pool
+  {
+    int64_t v = t;
+    for (; v + 3 * kPfNT < nv; v += 4 * kPfNT) {
+      const uint4 q0 = rv.base[v], q1 = rv.base[v + kPfNT], q2 = rv.base[v + 2 * kPfNT], q3 = rv.base[v + 3 * kPfNT];
+      pass2_vec(q0, v);
+      pass2_vec(q1, v + kPfNT);
+      pass2_vec(q2, v + 2 * kPfNT);
+      pass2_vec(q3, v + 3 * kPfNT);
+    }
+    for (; v < nv; v += kPfNT) pass2_vec(rv.base[v], v);
+  }
+  s = wave_sum_f(s);
+  __syncthreads();
+  if (l == 0) redf[w] = s;
+  __syncthreads();
+  s = 0.0f;
+  for (int i = 0; i < kPfNW; ++i) s += redf[i];
+  const int n = s_cnt;
+
+  // ---- the k largest composites, sorted ---------------------------------------
+  if (n <= kPfCap) {
+    if (n <= kPfNT) pf_sort_desc<1>(pool, n);
+    else if (n <= 2 * kPfNT) pf_sort_desc<2>(pool, n);
+    else if (n <= 4 * kPfNT) pf_sort_desc<4>(pool, n);
+    else pf_sort_desc<8>(pool, n);
+  } else {
+    // heavy ties: bisection for the k-th largest composite over the row
+    uint64_t prefix = 0;
+    for (int bit = 63; bit >= 0; --bit) {
+      const uint64_t probe = prefix | (1ull << bit);
+      int c = 0;
+      for (int64_t v = t; v < nv; v += kPfNT) {
+        const uint4 q = rv.base[v];
+        const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t e = v * 4 - rv.mis + i;
+          if (e >= 0 && e < a.cols) c += make_comp(select_key(d[i]), (uint32_t)e) >= probe;
+        }
+      }
+      c = wave_sum_i(c);
+      __syncthreads();
+      if (l == 0) redi[w] = c;
+      __syncthreads();
+      int tot = 0;
+      for (int i = 0; i < kPfNW; ++i) tot += redi[i];
+      if (tot >= k) prefix = probe;
+    }
+    if (t == 0) s_cnt = 0;
+    __syncthreads();
+    for (int64_t v = t; v < nv; v += kPfNT) {
+      const uint4 q = rv.base[v];
+      const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t e = v * 4 - rv.mis + i;
+        if (e >= 0 && e < a.cols) {
+          const uint64_t c = make_comp(select_key(d[i]), (uint32_t)e);
+          if (c >= prefix) pool[atomicAdd(&s_cnt, 1)] = c;  // exactly k <= kPfCap of them
+        }
+      }
+    }
+    __syncthreads();
+    pf_sort_desc<4>(pool, k);
+  }
+
+  // ---- probabilities, indices, cumsum, cutoff -----------------------------------
+  float* probs = (float*)(pool + kPfMaxK);  // k floats after the first k records
+  for (int p = t; p < k; p += kPfNT) {
+    const uint64_t c = pool[p];
+    int32_t idx = comp_idx(c);
+    float pr = pf_exp(__uint_as_float(key_to_bits(comp_key(c))), m) / s;
+    if (row_bad) {
+      idx = p;
+      pr = NAN;
+    }
+    probs[p] = pr;
+    a.out_probs[row * k + p] = pr;
+    a.out_idx[row * k + p] = idx;
+  }
+  __syncthreads();
+  const int ntiles = (k + 127) / 128;
+  float c[2] = {0.0f, 0.0f};
+  const bool has_tile = w < ntiles;
+  if (has_tile) {  // wave w scans tile w (k <= 16 tiles of 128 per pass)
+    for (int h = 0; h < 2; ++h) {
+      const int p = w * 128 + h * kWave + l;
+      c[h] = p < k ? probs[p] : 0.0f;
+    }
+    hs_scan128(c, l);
+    if (l == kWave - 1) s_tile_sum[w] = c[1];
+  }
+  __syncthreads();
+  if (t == 0) {
+    float acc = 0.0f;
+    for (int i = 0; i < ntiles; ++i) {
+      s_cum_carry[i] = acc;
+      acc = i == 0 ? s_tile_sum[0] : add_in_order(acc, s_tile_sum[i]);
+    }
+  }
+  __syncthreads();
+  int below = 0;
+  if (has_tile) {
+    const float cy = s_cum_carry[w];
+    for (int h = 0; h < 2; ++h) {
+      const int p = w * 128 + h * kWave + l;
+      const float v = w == 0 ? c[h] : add_in_order(c[h], cy);
+      if (p < k) {
+        a.out_cum[row * k + p] = v;
+        below += v < a.p ? 1 : 0;
+      }
+    }
+  }
+  below = wave_sum_i(below);
+  if (l == 0) redi[w] = below;
+  __syncthreads();
+  if (t == 0) {
+    int tot = 0;
+    for (int i = 0; i < kPfNW; ++i) tot += redi[i];
+    a.out_cutoff[row] = tot;
+  }
+}
+
+}  // namespace tx
+
+using namespace tx;
+
+extern "C" {
+
+int tallax_softmax_topk_cumsum(const float* logits, int64_t rows, int64_t cols, int k, float p, float* out_probs,
+                               int32_t* out_idx, float* out_cumsum, int32_t* out_cutoff, hipStream_t stream) {
+  if (!logits || !out_probs || !out_idx || !out_cumsum || !out_cutoff) { set_error("null pointer argument"); return kInvalidArgument; }
+  if (rows < 0 || cols <= 0) { set_error("bad shape [%lld, %lld]", (long long)rows, (long long)cols); return kInvalidArgument; }
+  if (k < 1 || k > kPfMaxK || k > 16 * 128) {
+    set_error("k=%d outside [1, 2048]", k);
+    return k > 2048 ? kUnsupported : kInvalidArgument;
+  }
+  if (k > cols) { set_error("k=%d exceeds row length %lld", k, (long long)cols); return kInvalidArgument; }
+  if (cols >= (int64_t)1 << 31) { set_error("cols must fit int32 indices"); return kInvalidArgument; }
+  if (rows == 0) return kOk;
+  if (rows > 2147483647) { set_error("too many rows"); return kUnsupported; }
+  PfArgs a = {};
+  a.x = logits; a.rows = rows; a.cols = cols; a.k = k; a.p = p;
+  a.out_probs = out_probs; a.out_idx = out_idx; a.out_cum = out_cumsum; a.out_cutoff = out_cutoff;
+  const size_t lds = (size_t)kPfCap * 8;
+  static const hipError_t attr = hipFuncSetAttribute((const void*)softmax_topk_kernel,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) { set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr)); return kHipError; }
+  hipLaunchKernelGGL(softmax_topk_kernel, dim3((unsigned)rows), dim3(kPfNT), lds, stream, a);
+  return launch_status("tallax_softmax_topk_cumsum");
+}
+
+}  // extern "C"

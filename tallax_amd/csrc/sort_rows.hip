@@ -24,6 +24,7 @@
 #include "tallax_hip.h"
 #include "tx_common.h"
 #include "tx_host.h"
+#include "tx_block_sort.h"
 #include "tx_wave_sort.h"
 
 namespace tx {
@@ -90,59 +91,12 @@ struct RecT<uint32_t> {  // bf16 keys: (key >> 16) << 16 | tie (tie < 2^16)
   __device__ static uint32_t tie(uint32_t r) { return r & 0xFFFFu; }
 };
 
-template <typename R>
-__device__ __forceinline__ void cx_pair(R& a, R& b, bool asc) {
-  const bool sw = (a > b) == asc;
-  const R lo = sw ? b : a;
-  const R hi = sw ? a : b;
-  a = lo;
-  b = hi;
-}
-
-// one stage at a stride S < E: pairs inside the thread's registers
-template <typename R, int E, int S>
-__device__ __forceinline__ void intra_stage(R v[E], int size, int t) {
-  if (S >= E) return;
-#pragma unroll
-  for (int r = 0; r < E; ++r) {
-    if ((r & S) == 0) {
-      const int i = t * E + r;
-      cx_pair(v[r], v[r | S], (i & size) == 0);
-    }
-  }
-}
-
-// one cross-lane stage at lane distance d (compile-time after the switch)
-template <typename R, int E>
-__device__ __forceinline__ void lane_stage(R v[E], int d, int size, int stride, int t) {
-  const int l = lane_id();
-  const bool lower = (l & d) == 0;
-#pragma unroll
-  for (int r = 0; r < E; ++r) {
-    const int i = t * E + r;
-    const bool asc = (i & size) == 0;
-    R o;
-    switch (d) {
-      case 1: o = lane_xor_c(v[r], 1); break;
-      case 2: o = lane_xor_c(v[r], 2); break;
-      case 4: o = lane_xor_c(v[r], 4); break;
-      case 8: o = lane_xor_c(v[r], 8); break;
-      case 16: o = lane_xor_c(v[r], 16); break;
-      default: o = lane_xor_c(v[r], 32); break;
-    }
-    // lower lane keeps min when ascending
-    v[r] = cx(v[r], o, lower != asc);
-  }
-  (void)stride;
-}
-
 template <typename R, int E>
 __global__ __launch_bounds__(1024) void sort_rows_kernel(SortArgs a) {
   using RT = RecT<R>;
   extern __shared__ __align__(16) unsigned char smem[];
   R* lds = (R*)smem;
   const int t = threadIdx.x;
-  const int NT = blockDim.x;
   const int64_t row = blockIdx.x;
   const int64_t base = row * a.cols;
   const uint32_t tie_mask = RT::kTieBits == 32 ? 0x7FFFFFFFu : 0xFFFFu;
@@ -160,35 +114,7 @@ __global__ __launch_bounds__(1024) void sort_rows_kernel(SortArgs a) {
       v[r] = ~(R)0;  // padding: after every real record
     }
   }
-  const int P = a.P;
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride >= 1; stride >>= 1) {
-      if (stride < E) {
-        switch (stride) {
-          case 1: intra_stage<R, E, 1>(v, size, t); break;
-          case 2: intra_stage<R, E, 2>(v, size, t); break;
-          case 4: intra_stage<R, E, 4>(v, size, t); break;
-          default: intra_stage<R, E, 8>(v, size, t); break;
-        }
-      } else if (stride < kWave * E) {
-        lane_stage<R, E>(v, stride / E, size, stride, t);
-      } else {
-        // through LDS: element i exchanges with i ^ stride
-#pragma unroll
-        for (int r = 0; r < E; ++r) lds[t * E + r] = v[r];
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < E; ++r) {
-          const int i = t * E + r;
-          const R o = lds[i ^ stride];
-          const bool asc = (i & size) == 0;
-          const bool lower = (i & stride) == 0;
-          v[r] = cx(v[r], o, lower != asc);
-        }
-        __syncthreads();
-      }
-    }
-  }
+  block_bitonic_sort<R, E>(v, lds, a.P, false);
   // outputs
 #pragma unroll
   for (int r = 0; r < E; ++r) {

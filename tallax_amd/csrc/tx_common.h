@@ -133,6 +133,12 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) v += lane_xor_f(v, d);
+  return v;
+}
+
 // Unaligned-safe 16-byte vector source for a row.  Rows need not start on a
 // 16-byte boundary: we read whole 16-byte blocks starting at the aligned-down
 // address and mask out the elements that fall outside the row.  A 16-byte

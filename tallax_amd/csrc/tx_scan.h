@@ -1,0 +1,51 @@
+// Scan helpers shared by cumsum and the fused softmax / top-k / cumsum
+// kernel: the reference's per-tile Hillis-Steele order (cumsum.py:21-30) on
+// 128-position tiles held two per lane (position p = h * 64 + lane).
+#pragma once
+#include "tx_common.h"
+
+namespace tx {
+
+template <typename T>
+__device__ __forceinline__ T shfl_up_or_zero(T v, int s, int l) {
+  // value of lane l - s (0 when l < s), via the LDS crossbar (no LDS memory)
+  const int src = l - s;
+  const int x = __builtin_amdgcn_ds_bpermute((src < 0 ? l : src) << 2, __builtin_bit_cast(int, v));
+  return src < 0 ? (T)0 : __builtin_bit_cast(T, x);
+}
+
+template <typename T>
+__device__ __forceinline__ T add_in_order(T a, T b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+template <>
+__device__ __forceinline__ int32_t add_in_order<int32_t>(int32_t a, int32_t b) {
+  return (int32_t)((uint32_t)a + (uint32_t)b);  // wrapping, as the reference's int32 adds
+}
+
+// Hillis-Steele inclusive scan of one 128-position tile (p = h * 64 + lane).
+template <typename T>
+__device__ __forceinline__ void hs_scan128(T c[2], int l) {
+#pragma unroll
+  for (int s = 1; s < 128; s <<= 1) {
+    T n[2];
+    if (s < kWave) {
+      const T lo0 = shfl_up_or_zero(c[0], s, l);
+      const T lo1 = shfl_up_or_zero(c[1], s, l);
+      // position 64 + l - s for l < s comes from register 0, lane 64 + l - s
+      const int src = l - s + kWave;
+      const T wrap = __builtin_bit_cast(
+          T, __builtin_amdgcn_ds_bpermute((l < s ? src : l) << 2, __builtin_bit_cast(int, c[0])));
+      n[0] = add_in_order(c[0], lo0);
+      n[1] = add_in_order(c[1], l < s ? wrap : lo1);
+    } else {  // s == 64: position p >= 64 adds position p - 64, the others add 0
+      n[0] = add_in_order(c[0], (T)0);
+      n[1] = add_in_order(c[1], c[0]);
+    }
+    c[0] = n[0];
+    c[1] = n[1];
+  }
+}
+
+}  // namespace tx

@@ -1,0 +1,80 @@
+"""GPU parity of the fused config-5 pipeline (softmax -> top-2048 -> cumsum ->
+cutoff at p = 0.9): indices bit-exact (the k largest logits, lowest index on
+ties); probabilities and cumsum within 1e-5 relative of float64; the cumsum
+bit-exact to tax.cumsum's tile order over the kernel's own probabilities;
+cutoff equal to the float64 one except where the float64 cumsum lies within
+1e-5 of p (reported)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tallax_oracle as O
+from tests.gpu_util import bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _log(msg):
+    print(msg, flush=True)
+
+
+def _run(x, k, p, gpu):
+    from tallax_amd import prefill
+    probs, idx, cum, cut = prefill.softmax_topk_cumsum(torch.from_numpy(x).to(gpu), k, p)
+    torch.cuda.synchronize()
+    return probs.cpu().numpy(), idx.cpu().numpy(), cum.cpu().numpy(), cut.cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,cols,k,sigma", [
+    (64, 201088, 2048, 2.0),     # config 5's row shape
+    (24, 50001, 1000, 1.0),      # ragged, odd length
+    (16, 3000, 2048, 4.0),       # candidates ~ all of the row
+    (8, 129, 100, 2.0),
+])
+def test_prefill_parity(gpu, rows, cols, k, sigma):
+    _log(f"softmax_topk_cumsum [{rows},{cols}] k={k} sigma={sigma}")
+    rng = np.random.default_rng(cols + k)
+    x = (rng.standard_normal((rows, cols)) * sigma).astype(np.float32)
+    x[0, 5:50] = x[0].max()                                   # ties at the top
+    gp, gi, gc, gcut = _run(x, k, 0.9, gpu)
+    idx, p64, c64, cut64 = O.softmax_topk_cumsum_f64(x, k, 0.9)
+    assert np.array_equal(gi, idx)
+    assert np.all(np.abs(gp - p64) <= 1e-5 * np.abs(p64) + 1e-30)
+    assert np.array_equal(bits(gc), bits(O.cumsum(gp, 1)))
+    assert np.all(np.abs(gc - c64) <= 1e-5 * np.abs(c64))
+    near = np.abs(c64 - 0.9).min(axis=1) < 1e-5
+    bad = (gcut != cut64) & ~near
+    _log(f"cutoff: {int((gcut != cut64).sum())} disagreements, {int(near.sum())} rows within 1e-5 of p")
+    assert not bad.any()
+
+
+def test_prefill_ties_fallback_and_nonfinite(gpu):
+    """Heavy ties overflow the candidate buffer and take the exact bisection
+    path; rows with NaN / +inf give NaN probabilities and indices 0..k-1."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((8, 40000)) * 2).astype(np.float32)
+    x[0] = 1.0                                                  # constant row
+    x[1] = np.round(x[1])                                       # few distinct values
+    x[2, 17] = np.nan
+    x[3, 99] = np.inf
+    x[4, :] = -np.inf
+    x[4, 1000:1100] = 3.0
+    gp, gi, gc, gcut = _run(x, 512, 0.9, gpu)
+    idx, p64, c64, cut64 = O.softmax_topk_cumsum_f64(x, 512, 0.9)
+    for r in (0, 1, 5, 6, 7):
+        assert np.array_equal(gi[r], idx[r])
+        assert np.allclose(gp[r], p64[r], rtol=1e-5, atol=0)
+    for r in (2, 3):
+        assert np.isnan(gp[r]).all() and np.array_equal(gi[r], np.arange(512)) and gcut[r] == 0
+    # -inf elsewhere: exactly the 100 finite logits share the mass
+    assert np.array_equal(gi[4][:100], np.arange(1000, 1100))
+    assert np.allclose(gp[4][:100], 0.01, rtol=1e-5) and np.all(gp[4][100:] == 0)
+
+
+def test_prefill_errors(gpu):
+    from tallax_amd import prefill
+    x = torch.zeros((4, 100), device=gpu)
+    with pytest.raises(ValueError):
+        prefill.softmax_topk_cumsum(x, 101)
+    with pytest.raises(NotImplementedError):
+        prefill.softmax_topk_cumsum(torch.zeros((4, 5000), device=gpu), 4096)
