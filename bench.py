@@ -1,21 +1,27 @@
 #!/usr/bin/env python3
 """Benchmark of the tallax MI355X hot path (one GPU).
 
-Default workload (BASELINE.json metric / config 4): the fused top-k/top-p
-sampler (`tallax_amd.sampling.sample`, one HIP kernel) on bf16 logits
-[256, 128256] ~ N(0, sigma=3), per-row temperature U[0.5,1.5), top_k
-uniform in [1, 1024], top_p U[0.7,1.0), threefry key data (0, 1234).
-A "step" samples one token for each of the 256 rows.
+Default workload (BASELINE.json metric, config 4): the fused top-k/top-p
+sampler (one HIP kernel, `tallax_fused_topk_topp_sample`) on bf16 logits
+[256, 128256] ~ N(0, sigma=3), per-row temperature U[0.5,1.5), top_k uniform
+in [1, 1024], top_p U[0.7,1.0), threefry key data (0, 1234).  A "step"
+samples one token for each of the 256 rows.
 
-Timing: inputs are resident in HBM before the timed region; the step rotates
-over `--nbuf` distinct logits buffers (6 x 65.7 MB > the 256 MB MALL) so
-every step streams its logits from HBM.  Whole-job time is bracketed by
-torch.cuda.synchronize(); the kernel's own average duration is measured with
-HIP events recorded on the stream the kernel is launched on.  One JSON line
+--config selects another BASELINE config (each a parity-checked entry point):
+  topk_c3        exact top-k k=50, f32 [128,151936] + 32 spikes/row at 8.0
+  topk_c3_approx approximate (binned) top_dynamic_k k=max_k=50, same input
+  topk_c1        exact top-k k=64, f32 [8,32768]
+  sort_c2        bf16 keys [256,4096] (multiples of 1/16) stable argsort, then
+                 take_along_axis of an f32 [256,4096] array
+  prefill_c5     f32 [1024,201088] softmax -> top-2048 -> cumsum -> cutoff p=0.9
+  copy           torch's device copy of 256 MiB (the counter calibration)
+
+Timing: inputs are resident in HBM before the timed region; steps rotate
+over distinct input buffers (more bytes than the 256 MB MALL) so every step
+streams its input from HBM.  K back-to-back steps are bracketed by
+torch.cuda.synchronize(); HIP events recorded on the launch stream around
+them give the average launch duration used for the roofline.  One JSON line
 is printed.
-
---config topk_c3 / topk_c1 time exact top-k (configs 3 and 1) instead;
---config copy times torch's device copy of 256 MiB (the counter calibration).
 """
 from __future__ import annotations
 
@@ -29,9 +35,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak, GB/s
-
-
 COPY_BYTES = 256 << 20  # calibration copy: 256 MiB read + 256 MiB written per launch
+CONFIGS = ["sampler", "topk_c3", "topk_c3_approx", "topk_c1", "sort_c2", "prefill_c5", "copy"]
 
 
 def _copy_rate(torch, dev, stream, steps, warmup):
@@ -74,12 +79,259 @@ def _parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="sampler", choices=["sampler", "topk_c3", "topk_c1", "copy"])
-    ap.add_argument("--nbuf", type=int, default=6)
+    ap.add_argument("--config", default="sampler", choices=CONFIGS)
+    ap.add_argument("--nbuf", type=int, default=None, help="input buffers to rotate (default per config)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     return ap.parse_args()
+
+
+class Workload:
+    """One benchmarked entry point: launch(i) runs step i on buffer i % nbuf."""
+    metric = ""
+    rows = 0
+    alg_bytes = 0
+    dtype = "f32"
+    workload = ""
+    kernel = ""
+    cpu_batch = 8
+    shape = (0, 0)
+
+
+def _sampler(torch, np, _lib, dev, s_handle, gen, nbuf):
+    w = Workload()
+    rows, cols = 256, 128256
+    rng = np.random.default_rng(5)
+    temp = rng.uniform(0.5, 1.5, rows).astype(np.float32)
+    topk = rng.integers(1, 1025, rows).astype(np.int32)
+    topp = rng.uniform(0.7, 1.0, rows).astype(np.float32)
+    d_temp, d_topk, d_topp = (torch.from_numpy(a).to(dev) for a in (temp, topk, topp))
+    key = (0, 1234)
+    d_key = torch.tensor(key, dtype=torch.int32, device=dev)
+    out = torch.empty(rows, dtype=torch.int32, device=dev)
+    need = _lib.LIB.tallax_sample_workspace_size(rows, cols, _lib.BF16)
+    ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
+    bufs = [(torch.randn((rows, cols), generator=gen, device=dev) * 3.0).to(torch.bfloat16)
+            for _ in range(nbuf or 6)]
+    w.metric = "rows/s + achieved HBM GB/s (% peak): fused top-k/top-p @256x128256 bf16"
+    w.rows, w.dtype, w.shape = rows, "bf16", (rows, cols)
+    w.alg_bytes = rows * cols * 2 + rows * 12 + 8 + rows * 4
+    w.workload = ("fused top-k/top-p/temperature/Gumbel sampler (sampling.sample): bf16 logits [256,128256] ~ "
+                  "N(0,3), top_k U{1..1024} (clamped to 128), top_p U[0.7,1), T U[0.5,1.5), threefry key (0,1234)")
+    w.kernel = _lib.select_plan(rows, cols, _lib.BF16)["kernel"].replace("SAMPLE", "true")
+    w.cpu_batch = 16
+
+    def launch(i):
+        x = bufs[i % len(bufs)]
+        _lib.check(_lib.LIB.tallax_fused_topk_topp_sample(
+            x.data_ptr(), _lib.BF16, rows, cols, d_topk.data_ptr(), d_topp.data_ptr(), d_temp.data_ptr(),
+            d_key.data_ptr(), 0, -1e12, out.data_ptr(), ws.data_ptr(), ws.numel(), s_handle), "sample")
+
+    def host0(O):
+        if not hasattr(w, "h0"):
+            w.h0 = O.bf16_bits_to_f32(bufs[0].view(torch.int16).cpu().numpy().view(np.uint16))
+        return w.h0
+
+    def parity(O):
+        h = host0(O)
+        launch(0)
+        torch.cuda.synchronize()
+        return bool(np.array_equal(out.cpu().numpy(), O.sample(key, h, topk, topp, temp, dtype="bf16")))
+
+    def cpu_step(O, r0, batch):
+        h = host0(O)
+        sl = slice(r0, r0 + batch)
+        O.sample(key, h[sl], topk[sl], topp[sl], temp[sl], dtype="bf16", dim0_offset=r0)
+        return h[sl].shape[0]
+
+    w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
+    return w
+
+
+def _spiky(torch, gen, dev, rows, cols):
+    x = torch.randn((rows, cols), generator=gen, device=dev) * 2.0
+    sp = torch.rand((rows, cols), generator=gen, device=dev).argsort(dim=1)[:, :32]
+    x.scatter_(1, sp, 8.0)
+    return x.contiguous()
+
+
+def _topk(torch, np, _lib, dev, s_handle, gen, nbuf, which):
+    w = Workload()
+    if which == "topk_c1":
+        rows, cols, k = 8, 32768, 64
+        w.workload = "exact top-k (tax.top_k) k=64: f32 [8,32768] ~ N(0,1)"
+        bufs = [torch.randn((rows, cols), generator=gen, device=dev) for _ in range(nbuf or 6)]
+    else:
+        rows, cols, k = 128, 151936, 50
+        bufs = [_spiky(torch, gen, dev, rows, cols) for _ in range(nbuf or 6)]
+        w.workload = ("exact top-k (tax.top_k) k=50: f32 [128,151936] ~ N(0, sigma=2) + 32 spikes/row at 8.0"
+                      if which == "topk_c3" else
+                      "approximate top-k (tax.top_dynamic_k, binned, auto schedule) k=max_k=50: f32 [128,151936] "
+                      "~ N(0, sigma=2) + 32 spikes/row at 8.0")
+    w.metric = f"rows/s + achieved HBM GB/s (% peak): {which}"
+    w.rows, w.shape = rows, (rows, cols)
+    w.alg_bytes = rows * cols * 4 + rows * k * 8
+    vals = torch.empty((rows, k), dtype=torch.float32, device=dev)
+    idx = torch.empty((rows, k), dtype=torch.int32, device=dev)
+    approx = which == "topk_c3_approx"
+    if approx:
+        import ctypes
+        from tallax_amd import schedule as S
+        steps = S.topm_schedule(k, 128, 8)
+        arr = (ctypes.c_int32 * len(steps))(*steps)
+        need = _lib.LIB.tallax_top_dynamic_k_workspace_size(rows, 128, arr, len(steps))
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
+        kr = torch.full((rows,), k, dtype=torch.int32, device=dev)
+        valid = torch.empty(1, dtype=torch.int32, device=dev)
+        depths = torch.empty(rows, dtype=torch.int32, device=dev)
+        cutoff = torch.empty(rows, dtype=torch.float32, device=dev)
+        w.kernel = "binned_lists_kernel<8> + binned_finish_kernel + binned_select_kernel"
+        w.alg_bytes += rows * 12 + 4
+
+        def launch(i):
+            x = bufs[i % len(bufs)]
+            _lib.check(_lib.LIB.tallax_top_dynamic_k(
+                x.data_ptr(), _lib.F32, rows, cols, kr.data_ptr(), k, 8, 128, arr, len(steps), 0, 0.0,
+                vals.data_ptr(), idx.data_ptr(), valid.data_ptr(), depths.data_ptr(), cutoff.data_ptr(),
+                ws.data_ptr(), ws.numel(), s_handle), "top_dynamic_k")
+    else:
+        need = _lib.LIB.tallax_topk_workspace_size(rows, cols, k, _lib.F32)
+        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
+        w.kernel = _lib.select_plan(rows, cols, _lib.F32)["kernel"].replace("SAMPLE", "false")
+
+        def launch(i):
+            x = bufs[i % len(bufs)]
+            _lib.check(_lib.LIB.tallax_topk(x.data_ptr(), _lib.F32, rows, cols, k, vals.data_ptr(),
+                                            idx.data_ptr(), ws.data_ptr(), ws.numel(), s_handle), "top_k")
+
+    def host0():
+        if not hasattr(w, "h0"):
+            w.h0 = bufs[0].cpu().numpy()
+        return w.h0
+
+    def parity(O):
+        h = host0()
+        launch(0)
+        torch.cuda.synchronize()
+        got = idx.cpu().numpy()
+        ev, ei = O.top_k(h, k)
+        if approx:
+            want = O.top_dynamic_k(h, k, k)
+            w.recall = float(np.mean([len(set(got[r]) & set(ei[r])) / k for r in range(rows)]))
+            return bool(np.array_equal(got, want[1]) and np.array_equal(depths.cpu().numpy(), want[3]))
+        return bool(np.array_equal(got, ei))
+
+    def cpu_step(O, r0, batch):
+        h = host0()
+        sl = slice(r0, r0 + batch)
+        if approx:
+            O.top_dynamic_k(h[sl], k, k)
+        else:
+            O.top_k(h[sl], k)
+        return h[sl].shape[0]
+
+    w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
+    return w
+
+
+def _sort_c2(torch, np, _lib, dev, s_handle, gen, nbuf):
+    w = Workload()
+    rows, cols = 256, 4096
+    nb = nbuf or 16
+    keys = [((torch.randn((rows, cols), generator=gen, device=dev) * 16).round() / 16).to(torch.bfloat16)
+            for _ in range(nb)]
+    vals = [torch.randn((rows, cols), generator=gen, device=dev) for _ in range(nb)]
+    sk = torch.empty((rows, cols), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((rows, cols), dtype=torch.int32, device=dev)
+    g = torch.empty((rows, cols), dtype=torch.float32, device=dev)
+    w.metric = "rows/s + achieved HBM GB/s (% peak): sort_c2"
+    w.rows, w.dtype, w.shape = rows, "bf16", (rows, cols)
+    w.alg_bytes = 20971520  # sort: 2 MiB keys in, 2 MiB keys + 4 MiB indices out; gather: 3 x 4 MiB
+    w.workload = ("tumpy.argsort (stable, packed bf16 path) of bf16 keys [256,4096] = round(16 z)/16, then "
+                  "tumpy.take_along_axis of an f32 [256,4096] array by the indices")
+    w.kernel = "sort_rows_kernel<u32, 4> + gather_row_lds_kernel<u32>"
+    w.cpu_batch = 16
+
+    def launch(i):
+        kx, vx = keys[i % nb], vals[i % nb]
+        _lib.check(_lib.LIB.tallax_sort_rows(kx.data_ptr(), _lib.BF16, rows, cols, 0, 0, None, idx.data_ptr(),
+                                             sk.data_ptr(), _lib.BF16, None, 0, None, 0, s_handle), "sort")
+        _lib.check(_lib.LIB.tallax_take_along_axis(vx.data_ptr(), _lib.F32, rows, cols, idx.data_ptr(), rows, cols,
+                                                   1, g.data_ptr(), s_handle), "gather")
+
+    def host0(O):
+        if not hasattr(w, "h0"):
+            w.h0 = (O.bf16_bits_to_f32(keys[0].view(torch.int16).cpu().numpy().view(np.uint16)),
+                    vals[0].cpu().numpy())
+        return w.h0
+
+    def parity(O):
+        hk, hv = host0(O)
+        launch(0)
+        torch.cuda.synchronize()
+        (_, want_idx), _ = O.sort([hk], 1, is_stable=True, return_argsort=True, dtypes=["bf16"])
+        return bool(np.array_equal(idx.cpu().numpy(), want_idx) and
+                    np.array_equal(g.cpu().numpy(), O.take_along_axis(hv, want_idx, 1)))
+
+    def cpu_step(O, r0, batch):
+        hk, hv = host0(O)
+        sl = slice(r0, r0 + batch)
+        (_, ii), _ = O.sort([hk[sl]], 1, is_stable=True, return_argsort=True, dtypes=["bf16"])
+        O.take_along_axis(hv[sl], ii, 1)
+        return hk[sl].shape[0]
+
+    w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
+    return w
+
+
+def _prefill_c5(torch, np, _lib, dev, s_handle, gen, nbuf):
+    w = Workload()
+    rows, cols, k, p = 1024, 201088, 2048, 0.9
+    nb = nbuf or 2
+    bufs = [torch.randn((rows, cols), generator=gen, device=dev) * 2.0 for _ in range(nb)]
+    probs = torch.empty((rows, k), dtype=torch.float32, device=dev)
+    idx = torch.empty((rows, k), dtype=torch.int32, device=dev)
+    cum = torch.empty((rows, k), dtype=torch.float32, device=dev)
+    cut = torch.empty(rows, dtype=torch.int32, device=dev)
+    w.metric = "rows/s + achieved HBM GB/s (% peak): prefill_c5"
+    w.rows, w.shape = rows, (rows, cols)
+    w.alg_bytes = rows * cols * 4 + 3 * rows * k * 4 + rows * 4
+    w.workload = ("softmax -> top-2048 (indices) -> inclusive cumsum -> cutoff #(cumsum < 0.9): f32 "
+                  "[1024,201088] ~ N(0, sigma=2), fused (tallax_softmax_topk_cumsum)")
+    w.kernel = "softmax_topk_kernel"
+    w.cpu_batch = 2
+    sample = 64  # rows checked against the float64 truth (keeps the check to seconds)
+
+    def launch(i):
+        x = bufs[i % nb]
+        _lib.check(_lib.LIB.tallax_softmax_topk_cumsum(x.data_ptr(), rows, cols, k, p, probs.data_ptr(),
+                                                       idx.data_ptr(), cum.data_ptr(), cut.data_ptr(), s_handle),
+                   "softmax_topk_cumsum")
+
+    def host0():
+        if not hasattr(w, "h0"):
+            w.h0 = bufs[0][:sample].cpu().numpy()
+        return w.h0
+
+    def parity(O):
+        h = host0()
+        launch(0)
+        torch.cuda.synchronize()
+        ii, p64, c64, _ = O.softmax_topk_cumsum_f64(h, k, p)
+        gp = probs[:sample].cpu().numpy()
+        ok = bool(np.array_equal(idx[:sample].cpu().numpy(), ii))
+        ok = ok and bool(np.all(np.abs(gp - p64) <= 1e-5 * np.abs(p64) + 1e-30))
+        return ok and bool(np.all(np.abs(cum[:sample].cpu().numpy() - c64) <= 1e-5 * c64))
+
+    def cpu_step(O, r0, batch):
+        h = host0()
+        r0 = r0 % h.shape[0]
+        O.softmax_topk_cumsum_f64(h[r0:r0 + batch], k, p)
+        return h[r0:r0 + batch].shape[0]
+
+    w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
+    return w
 
 
 def main() -> int:
@@ -112,141 +364,64 @@ def main() -> int:
         return 0
 
     if args.config == "sampler":
-        rows, cols, dt_name, sigma = 256, 128256, "bf16", 3.0
-        tdt = torch.bfloat16
-        rng = np.random.default_rng(5)
-        temp = rng.uniform(0.5, 1.5, rows).astype(np.float32)
-        topk = rng.integers(1, 1025, rows).astype(np.int32)
-        topp = rng.uniform(0.7, 1.0, rows).astype(np.float32)
-        d_temp = torch.from_numpy(temp).to(dev)
-        d_topk = torch.from_numpy(topk).to(dev)
-        d_topp = torch.from_numpy(topp).to(dev)
-        key = (0, 1234)
-        d_key = torch.tensor(key, dtype=torch.int32, device=dev)
-        out = torch.empty(rows, dtype=torch.int32, device=dev)
-        need = _lib.LIB.tallax_sample_workspace_size(rows, cols, _lib.BF16)
-        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
-        alg_bytes = rows * cols * 2 + rows * 12 + 8 + rows * 4
-        workload = ("fused top-k/top-p/temperature/Gumbel sampler (sampling.sample): bf16 logits "
-                    "[256,128256] ~ N(0,3), top_k U{1..1024} (clamped to 128), top_p U[0.7,1), "
-                    "T U[0.5,1.5), threefry key (0,1234)")
-        kernel_name = _lib.select_plan(rows, cols, _lib.BF16)["kernel"].replace("SAMPLE", "true")
-        bufs = [(torch.randn((rows, cols), generator=gen, device=dev) * sigma).to(tdt) for _ in range(args.nbuf)]
-
-        def launch(x):
-            _lib.check(_lib.LIB.tallax_fused_topk_topp_sample(
-                x.data_ptr(), _lib.BF16, rows, cols, d_topk.data_ptr(), d_topp.data_ptr(), d_temp.data_ptr(),
-                d_key.data_ptr(), 0, -1e12, out.data_ptr(), ws.data_ptr(), ws.numel(), s_handle), "sample")
+        w = _sampler(torch, np, _lib, dev, s_handle, gen, args.nbuf)
+    elif args.config.startswith("topk"):
+        w = _topk(torch, np, _lib, dev, s_handle, gen, args.nbuf, args.config)
+    elif args.config == "sort_c2":
+        w = _sort_c2(torch, np, _lib, dev, s_handle, gen, args.nbuf)
     else:
-        if args.config == "topk_c3":
-            rows, cols, k = 128, 151936, 50
-            workload = ("exact top-k (tax.top_k) k=50: f32 [128,151936] ~ N(0, sigma=2) + 32 spikes/row at 8.0")
-        else:
-            rows, cols, k = 8, 32768, 64
-            workload = "exact top-k (tax.top_k) k=64: f32 [8,32768] ~ N(0,1)"
-        dt_name, tdt = "f32", torch.float32
-        kernel_name = _lib.select_plan(rows, cols, _lib.F32)["kernel"].replace("SAMPLE", "false")
-        need = _lib.LIB.tallax_topk_workspace_size(rows, cols, k, _lib.F32)
-        ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
-        vals = torch.empty((rows, k), dtype=tdt, device=dev)
-        idx = torch.empty((rows, k), dtype=torch.int32, device=dev)
-        alg_bytes = rows * cols * 4 + rows * k * 8
-        bufs = []
-        for b in range(args.nbuf):
-            x = torch.randn((rows, cols), generator=gen, device=dev) * (2.0 if args.config == "topk_c3" else 1.0)
-            if args.config == "topk_c3":
-                sp = torch.rand((rows, cols), generator=gen, device=dev).argsort(dim=1)[:, :32]
-                x.scatter_(1, sp, 8.0)
-            bufs.append(x.contiguous())
-
-        def launch(x):
-            _lib.check(_lib.LIB.tallax_topk(x.data_ptr(), _lib.F32, rows, cols, k, vals.data_ptr(),
-                                            idx.data_ptr(), ws.data_ptr(), ws.numel(), s_handle), "top_k")
+        w = _prefill_c5(torch, np, _lib, dev, s_handle, gen, args.nbuf)
     torch.cuda.synchronize()
 
-    # ---- parity of the benchmarked kernel on buffer 0 (outside the timed region)
-    parity = None
-    host0 = None
+    O = None
     if not args.no_parity or not args.no_cpu_baseline:
-        from oracle import tallax_oracle as O
-        if tdt == torch.bfloat16:
-            host0 = O.bf16_bits_to_f32(bufs[0].view(torch.int16).cpu().numpy().view(np.uint16))
-        else:
-            host0 = bufs[0].cpu().numpy()
+        from oracle import tallax_oracle as O  # the checker and the CPU baseline only
+    parity = None
     if not args.no_parity:
-        launch(bufs[0])
-        torch.cuda.synchronize()
-        if args.config == "sampler":
-            want = O.sample(key, host0, topk, topp, temp, dtype="bf16")
-            parity = bool(np.array_equal(out.cpu().numpy(), want))
-        else:
-            ov, oi = O.top_k(host0, k)
-            parity = bool(np.array_equal(idx.cpu().numpy(), oi))
-        print(f"bench: parity of {args.config} vs oracle on buffer 0: {parity}", file=sys.stderr, flush=True)
+        parity = w.parity(O)
+        print(f"bench: parity of {args.config} vs oracle: {parity}", file=sys.stderr, flush=True)
 
-    # ---- warmup
     for s in range(args.warmup):
-        launch(bufs[s % len(bufs)])
+        w.launch(s)
     torch.cuda.synchronize()
 
-    # ---- whole-job timing
+    # ---- timed region: K back-to-back steps
     t0 = time.perf_counter()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for s in range(args.steps):
-        launch(bufs[s % len(bufs)])
+        w.launch(s)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = e0.elapsed_time(e1)
     total_s = max(wall, gpu_ms / 1e3)
     ms_per_step = total_s * 1e3 / args.steps
-
-    # ---- kernel duration: events around each launch on the launch stream
-    n_ev = min(args.steps, 200)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
-    for s in range(n_ev):
-        starts[s].record(stream)
-        launch(bufs[s % len(bufs)])
-        ends[s].record(stream)
-    torch.cuda.synchronize()
-    durs_us = sorted(a.elapsed_time(b) * 1e3 for a, b in zip(starts, ends))
-    # Average launch duration: HIP events on the launch stream around the K
-    # back-to-back launches of the timed region (per-launch event pairs add
-    # their own packets to every launch, so they are reported separately).
+    # average launch duration from HIP events on the launch stream around the
+    # K back-to-back launches (per-launch event pairs would add their own
+    # packets to every launch)
     kern_us = gpu_ms * 1e3 / args.steps
-    achieved = alg_bytes / (kern_us * 1e-6) / 1e9
+    achieved = w.alg_bytes / (kern_us * 1e-6) / 1e9
 
     # ---- CPU baseline: the numpy oracle on a bounded sample of the same workload
     cpu = None
     if not args.no_cpu_baseline:
-        rows_done = 0
-        t_cpu = 0.0
-        batch = 16
-        r0 = 0
+        rows_done, t_cpu, r0 = 0, 0.0, 0
         while t_cpu < args.cpu_seconds:
-            sl = slice(r0, r0 + batch)
             t = time.perf_counter()
-            if args.config == "sampler":
-                O.sample(key, host0[sl], topk[sl], topp[sl], temp[sl], dtype="bf16", dim0_offset=r0)
-            else:
-                O.top_k(host0[sl], k)
+            rows_done += w.cpu_step(O, r0, w.cpu_batch)
             t_cpu += time.perf_counter() - t
-            rows_done += host0[sl].shape[0]
-            r0 = (r0 + batch) % rows
+            r0 = (r0 + w.cpu_batch) % w.rows
         cpu = {"value": rows_done / t_cpu, "unit": "rows/s", "cores": 1, "kind": "port",
-               "sample": f"{rows_done} rows ({batch}-row batches) of the same {dt_name} [{rows},{cols}] "
+               "sample": f"{rows_done} rows ({w.cpu_batch}-row batches) of the same [{w.shape[0]},{w.shape[1]}] "
                          f"workload through the numpy oracle (oracle/tallax_oracle.py), single thread, "
                          f"{t_cpu:.1f} s"}
 
     copy_gbs, _ = _copy_rate(torch, dev, stream, 10, 3)
-    rows_per_s = rows * args.steps / total_s
     rec = {
-        "metric": "rows/s + achieved HBM GB/s (% peak): fused top-k/top-p @256x128256 bf16"
-                  if args.config == "sampler" else f"rows/s + achieved HBM GB/s (% peak): {args.config}",
-        "value": rows_per_s,
+        "metric": w.metric,
+        "value": w.rows * args.steps / total_s,
         "unit": "rows/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -255,20 +430,20 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if dt_name == "bf16" else "f32",
-        "data": f"synthetic (torch.randn on device, seed 4; {args.nbuf} rotating input buffers)",
-        "config": {"workload": workload, "rows": rows, "cols": cols, "parallelism": "single GPU"},
+        "dtype": w.dtype,
+        "data": "synthetic (torch.randn on device, seed 4; rotating input buffers)",
+        "config": {"workload": w.workload, "rows": w.shape[0], "cols": w.shape[1], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": _measured_traffic(args.config),
                      "measured_copy_GBs": copy_gbs, "frac_of_copy": achieved / copy_gbs,
-                     "kernel": kernel_name, "kernel_avg_us": kern_us,
-                     "event_pair_median_us": durs_us[len(durs_us) // 2],
-                     "algorithmic_bytes_per_launch": alg_bytes},
+                     "kernel": w.kernel, "kernel_avg_us": kern_us,
+                     "algorithmic_bytes_per_launch": w.alg_bytes},
         "cpu_baseline": cpu,
         "parity_vs_oracle": parity,
         "wall_ms_per_step": wall * 1e3 / args.steps,
-        "gpu_event_ms_per_step": gpu_ms / args.steps,
     }
+    if hasattr(w, "recall"):
+        rec["recall_at_k_vs_exact"] = w.recall
     print(json.dumps(rec), flush=True)
     return 0
 

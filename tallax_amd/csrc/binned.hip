@@ -103,20 +103,32 @@ __global__ __launch_bounds__(kBinNT) void binned_lists_kernel(BinArgs a) {
   }
   // slice s of bin b: columns b + NB * (s + S * i), in index order
   const int64_t base = row * a.cols;
-  const int64_t step = (int64_t)NB * S;
-  for (int64_t j = (int64_t)s * NB + b; j < a.cols; j += step) {
-    float x = load_val(a.x, a.dtype, base + j);
-    if (x > v[MC - 1]) {  // strict: ties keep the earlier (lower) index; NaN never enters
-      int32_t xi = (int32_t)j;
+  const int step = NB * S;  // = kBinNT
+  // eight loads in flight per thread, then the inserts in index order
+  constexpr int U = 8;
+  const int j0 = s * NB + b;
+  for (int64_t jb = j0; jb < a.cols; jb += (int64_t)U * step) {
+    float xs[U];
 #pragma unroll
-      for (int r = 0; r < MC; ++r) {
-        const bool sw = x > v[r];
-        const float tv = v[r];
-        const int32_t ti = id[r];
-        v[r] = sw ? x : tv;
-        id[r] = sw ? xi : ti;
-        x = sw ? tv : x;
-        xi = sw ? ti : xi;
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = jb + (int64_t)u * step;
+      xs[u] = j < a.cols ? load_val(a.x, a.dtype, base + j) : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float x = xs[u];
+      if (x > v[MC - 1]) {  // strict: ties keep the earlier (lower) index; NaN never enters
+        int32_t xi = (int32_t)(jb + (int64_t)u * step);
+#pragma unroll
+        for (int r = 0; r < MC; ++r) {
+          const bool sw = x > v[r];
+          const float tv = v[r];
+          const int32_t ti = id[r];
+          v[r] = sw ? x : tv;
+          id[r] = sw ? xi : ti;
+          x = sw ? tv : x;
+          xi = sw ? ti : xi;
+        }
       }
     }
   }

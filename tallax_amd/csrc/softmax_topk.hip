@@ -69,7 +69,7 @@ __device__ void pf_sort_desc(uint64_t* pool, int n) {
     v[r] = i < n ? pool[i] : 0ull;
   }
   __syncthreads();
-  block_bitonic_sort<uint64_t, E>(v, pool, kPfNT * E, true);
+  block_bitonic_sort_c<uint64_t, E, kPfNT * E, true>(v, pool);
 #pragma unroll
   for (int r = 0; r < E; ++r) pool[t * E + r] = v[r];
   __syncthreads();
@@ -94,12 +94,18 @@ __global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
   float m = -INFINITY;
   bool bad = false;
   uint32_t top[4] = {0u, 0u, 0u, 0u};
+  // interior vectors (all four elements inside the row) skip the bounds tests
+  const int64_t v_lo = rv.mis ? 1 : 0;
+  const int64_t v_hi = (a.cols + rv.mis) / 4;  // vectors [v_lo, v_hi) are interior
   auto pass1_vec = [&](const uint4 q, int64_t v) {
     const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+    const bool inner = v >= v_lo && v < v_hi;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t e = v * 4 - rv.mis + i;
-      if (e < 0 || e >= a.cols) continue;
+      if (!inner) {
+        const int64_t e = v * 4 - rv.mis + i;
+        if (e < 0 || e >= a.cols) continue;
+      }
       const float x = __uint_as_float(d[i]);
       m = fmaxf(m, x);
       bad = bad || (x != x) || x == INFINITY;
@@ -116,13 +122,14 @@ __global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
     }
   };
   {
+    constexpr int U = 8;  // loads in flight per thread
     int64_t v = t;
-    for (; v + 3 * kPfNT < nv; v += 4 * kPfNT) {
-      const uint4 q0 = rv.base[v], q1 = rv.base[v + kPfNT], q2 = rv.base[v + 2 * kPfNT], q3 = rv.base[v + 3 * kPfNT];
-      pass1_vec(q0, v);
-      pass1_vec(q1, v + kPfNT);
-      pass1_vec(q2, v + 2 * kPfNT);
-      pass1_vec(q3, v + 3 * kPfNT);
+    for (; v + (U - 1) * kPfNT < nv; v += U * kPfNT) {
+      uint4 q[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) q[u] = rv.base[v + u * kPfNT];
+#pragma unroll
+      for (int u = 0; u < U; ++u) pass1_vec(q[u], v + u * kPfNT);
     }
     for (; v < nv; v += kPfNT) pass1_vec(rv.base[v], v);
   }
@@ -135,7 +142,7 @@ __global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
   }
   // threshold: the k-th largest of the 4096 per-thread keys
   uint32_t* keys = (uint32_t*)pool;
-  block_bitonic_sort<uint32_t, 4>(top, keys, kPfNT * 4, true);
+  block_bitonic_sort_c<uint32_t, 4, kPfNT * 4, true>(top, keys);
   if (t == (k - 1) / 4) s_t0 = top[(k - 1) % 4];
   if (t == 0) s_cnt = 0;
   __syncthreads();
@@ -153,10 +160,11 @@ __global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
     const uint32_t d[4] = {q.x, q.y, q.z, q.w};
     float vs = 0.0f;
     uint32_t mask = 0;
+    const bool inner = v >= v_lo && v < v_hi;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t e = v * 4 - rv.mis + i;
-      const bool live = e >= 0 && e < a.cols;
+      const bool live = inner || (e >= 0 && e < a.cols);
       const float x = __uint_as_float(d[i]);
       vs += live ? pf_exp(x, m) : 0.0f;
       mask |= (live && select_key(d[i]) >= t0 ? 1u : 0u) << i;
@@ -190,13 +198,14 @@ __global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
   };
   __syncthreads();  // the key sort above used the pool
   {
+    constexpr int U = 8;
     int64_t v = t;
-    for (; v + 3 * kPfNT < nv; v += 4 * kPfNT) {
-      const uint4 q0 = rv.base[v], q1 = rv.base[v + kPfNT], q2 = rv.base[v + 2 * kPfNT], q3 = rv.base[v + 3 * kPfNT];
-      pass2_vec(q0, v);
-      pass2_vec(q1, v + kPfNT);
-      pass2_vec(q2, v + 2 * kPfNT);
-      pass2_vec(q3, v + 3 * kPfNT);
+    for (; v + (U - 1) * kPfNT < nv; v += U * kPfNT) {
+      uint4 q[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) q[u] = rv.base[v + u * kPfNT];
+#pragma unroll
+      for (int u = 0; u < U; ++u) pass2_vec(q[u], v + u * kPfNT);
     }
     for (; v < nv; v += kPfNT) pass2_vec(rv.base[v], v);
   }

@@ -91,8 +91,8 @@ struct RecT<uint32_t> {  // bf16 keys: (key >> 16) << 16 | tie (tie < 2^16)
   __device__ static uint32_t tie(uint32_t r) { return r & 0xFFFFu; }
 };
 
-template <typename R, int E>
-__global__ __launch_bounds__(1024) void sort_rows_kernel(SortArgs a) {
+template <typename R, int E, int P>
+__global__ __launch_bounds__(P / E) void sort_rows_kernel(SortArgs a) {
   using RT = RecT<R>;
   extern __shared__ __align__(16) unsigned char smem[];
   R* lds = (R*)smem;
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(1024) void sort_rows_kernel(SortArgs a) {
       v[r] = ~(R)0;  // padding: after every real record
     }
   }
-  block_bitonic_sort<R, E>(v, lds, a.P, false);
+  block_bitonic_sort_c<R, E, P, false>(v, lds);
   // outputs
 #pragma unroll
   for (int r = 0; r < E; ++r) {
@@ -141,21 +141,32 @@ __global__ __launch_bounds__(1024) void sort_rows_kernel(SortArgs a) {
   }
 }
 
-template <typename R, int E>
+template <typename R, int E, int P>
 static int launch_sort(const SortArgs& a, int64_t rows, hipStream_t s) {
-  const int nt = a.P / E;
-  const size_t lds = (size_t)a.P * sizeof(R);
+  const size_t lds = (size_t)P * sizeof(R);
   if (lds > 64 * 1024) {
-    static const hipError_t attr = hipFuncSetAttribute((const void*)sort_rows_kernel<R, E>,
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       (int)(kSortMaxCols * sizeof(R)));
+    static const hipError_t attr = hipFuncSetAttribute((const void*)sort_rows_kernel<R, E, P>,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) {
       set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr));
       return kHipError;
     }
   }
-  hipLaunchKernelGGL((sort_rows_kernel<R, E>), dim3((unsigned)rows), dim3(nt), lds, s, a);
+  hipLaunchKernelGGL((sort_rows_kernel<R, E, P>), dim3((unsigned)rows), dim3(P / E), lds, s, a);
   return kOk;
+}
+
+template <typename R>
+static int launch_sort_p(const SortArgs& a, int64_t rows, hipStream_t s) {
+  switch (a.P) {
+    case 256: return launch_sort<R, 4, 256>(a, rows, s);
+    case 512: return launch_sort<R, 4, 512>(a, rows, s);
+    case 1024: return launch_sort<R, 4, 1024>(a, rows, s);
+    case 2048: return launch_sort<R, 4, 2048>(a, rows, s);
+    case 4096: return launch_sort<R, 4, 4096>(a, rows, s);
+    case 8192: return launch_sort<R, 8, 8192>(a, rows, s);
+    default: return launch_sort<R, 32, 16384>(a, rows, s);
+  }
 }
 
 }  // namespace tx
@@ -197,16 +208,7 @@ int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols,
   a.aux = aux; a.aux_dtype = aux_dtype; a.aux_out = aux_out; a.aux_out_dtype = aux_out_dtype;
   // bf16 keys on the packed path fit (16-bit key | 16-bit tie) in one u32
   const bool narrow = key_dtype == kBF16 && !perm_in && cols <= 65536;
-  int st;
-  if (narrow) {
-    if (P <= 4096) st = launch_sort<uint32_t, 4>(a, rows, stream);
-    else if (P == 8192) st = launch_sort<uint32_t, 8>(a, rows, stream);
-    else st = launch_sort<uint32_t, 16>(a, rows, stream);
-  } else {
-    if (P <= 4096) st = launch_sort<uint64_t, 4>(a, rows, stream);
-    else if (P == 8192) st = launch_sort<uint64_t, 8>(a, rows, stream);
-    else st = launch_sort<uint64_t, 16>(a, rows, stream);
-  }
+  const int st = narrow ? launch_sort_p<uint32_t>(a, rows, stream) : launch_sort_p<uint64_t>(a, rows, stream);
   if (st) return st;
   return launch_status("tallax_sort_rows");
 }

@@ -88,4 +88,41 @@ __device__ __forceinline__ void block_bitonic_sort(R v[E], R* lds, int P, bool d
   }
 }
 
+// The same network with P known at compile time: every stage is unrolled,
+// so stride tests and lane distances fold to constants.
+template <typename R, int E, int P, bool DESC>
+__device__ __forceinline__ void block_bitonic_sort_c(R v[E], R* lds) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int size = 2; size <= P; size <<= 1) {
+#pragma unroll
+    for (int stride = size >> 1; stride >= 1; stride >>= 1) {
+      if (stride < E) {
+#pragma unroll
+        for (int r = 0; r < E; ++r) {
+          if ((r & stride) == 0) {
+            const int i = t * E + r;
+            cx_pair(v[r], v[r | stride], ((i & size) == 0) != DESC);
+          }
+        }
+      } else if (stride < kWave * E) {
+        bsort_lane_stage<R, E>(v, stride / E, size, t, DESC);
+      } else {
+#pragma unroll
+        for (int r = 0; r < E; ++r) lds[t * E + r] = v[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < E; ++r) {
+          const int i = t * E + r;
+          const R o = lds[i ^ stride];
+          const bool asc = ((i & size) == 0) != DESC;
+          const bool lower = (i & stride) == 0;
+          v[r] = cx(v[r], o, lower != asc);
+        }
+        __syncthreads();
+      }
+    }
+  }
+}
+
 }  // namespace tx
