@@ -104,8 +104,9 @@ __global__ __launch_bounds__(kBinNT) void binned_lists_kernel(BinArgs a) {
   // slice s of bin b: columns b + NB * (s + S * i), in index order
   const int64_t base = row * a.cols;
   const int step = NB * S;  // = kBinNT
-  // eight loads in flight per thread, then the inserts in index order
-  constexpr int U = 8;
+  // 16 loads in flight per thread (one workgroup per row: each CU needs deep
+  // memory-level parallelism), then the inserts in index order
+  constexpr int U = MC <= 8 ? 16 : 8;
   const int j0 = s * NB + b;
   for (int64_t jb = j0; jb < a.cols; jb += (int64_t)U * step) {
     float xs[U];

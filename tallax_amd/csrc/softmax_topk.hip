@@ -15,14 +15,14 @@
 //   * cumsum over the k sorted probabilities in the reference's tile order
 //     (128-position tiles, Hillis-Steele inside, sequential carry);
 //   * cutoff = #(cumsum < p).
-// A row holding NaN or +inf gives NaN probabilities (as jax.nn.softmax does),
-// indices 0..k-1 and cutoff 0.
+// A row holding NaN or +inf, or only -inf, gives NaN probabilities (as
+// jax.nn.softmax does), indices 0..k-1 and cutoff 0.
 //
 // One 1024-thread workgroup per row, two streaming passes:
-//   pass 1: the row maximum and each thread's four largest select keys; the
-//           k-th largest of those 4096 keys, T0, has at least k elements >= it;
-//   pass 2: exp-sum, and every element with key >= T0 appended to LDS
-//           (expected ~k + 4 % for Gaussian rows);
+//   pass 1: the row maximum and each thread's four largest values; the k-th
+//           largest of those 4096, T0, has at least k elements >= it;
+//   pass 2: exp-sum, and every element >= T0 appended to LDS (expected
+//           ~k + 4 % for Gaussian rows);
 // then a workgroup bitonic sort of the candidates, the outputs, the tile
 // scan and the cutoff.  If the candidates overflow (heavy ties), the k-th
 // composite is found by bisection over the row instead.
@@ -54,9 +54,9 @@ struct PfArgs {
   int32_t* out_cutoff;
 };
 
-__device__ __forceinline__ float pf_exp(float x, float m) {
-#pragma clang fp contract(off)
-  return __builtin_amdgcn_exp2f((x - m) * 1.44269504088896341f);
+// exp(x - m) as 2^(x log2 e - m log2 e), mc = m log2 e (v_exp_f32)
+__device__ __forceinline__ float pf_exp(float x, float mc) {
+  return __builtin_amdgcn_exp2f(__builtin_fmaf(x, 1.44269504088896341f, -mc));
 }
 
 template <int E>
@@ -75,7 +75,10 @@ __device__ void pf_sort_desc(uint64_t* pool, int n) {
   __syncthreads();
 }
 
-__global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
+// 8 waves per SIMD: two row workgroups share a CU, so one streams while the
+// other sorts
+__global__ __launch_bounds__(kPfNT) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void softmax_topk_kernel(PfArgs a) {
   extern __shared__ __align__(16) uint64_t pool[];  // kPfCap records
   __shared__ float redf[kPfNW];
   __shared__ int redi[kPfNW];
@@ -90,33 +93,47 @@ __global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
   const int64_t nv = (a.cols + rv.mis + 3) / 4;
   const int k = a.k;
 
-  // ---- pass 1: maximum, NaN / +inf, per-thread top-4 select keys ----------
-  float m = -INFINITY;
-  bool bad = false;
-  uint32_t top[4] = {0u, 0u, 0u, 0u};
+  // ---- pass 1: maximum and per-thread top-4 values -------------------------
+  // (v_max_f32 ignores NaN; rows holding NaN or +inf are recognised after pass
+  // 2, where their exp-sum comes out NaN)
   // interior vectors (all four elements inside the row) skip the bounds tests
   const int64_t v_lo = rv.mis ? 1 : 0;
   const int64_t v_hi = (a.cols + rv.mis) / 4;  // vectors [v_lo, v_hi) are interior
-  auto pass1_vec = [&](const uint4 q, int64_t v) {
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-    const bool inner = v >= v_lo && v < v_hi;
+  float m = -INFINITY;
+  float top[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  auto live_mask = [&](int64_t v) -> uint32_t {
+    if (v >= v_lo && v < v_hi) return 0xFu;
+    uint32_t live = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (!inner) {
-        const int64_t e = v * 4 - rv.mis + i;
-        if (e < 0 || e >= a.cols) continue;
-      }
-      const float x = __uint_as_float(d[i]);
-      m = fmaxf(m, x);
-      bad = bad || (x != x) || x == INFINITY;
-      uint32_t key = select_key(d[i]);
-      if (key > top[3]) {
+      const int64_t e = v * 4 - rv.mis + i;
+      live |= (e >= 0 && e < a.cols ? 1u : 0u) << i;
+    }
+    return live;
+  };
+  // the four values of a vector, dead slots as NaN (ignored by max and by >)
+  auto vec_vals = [&](uint4 q, uint32_t live, float xs[4]) {
+    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool sw = key > top[r];
-          const uint32_t tv = top[r];
-          top[r] = sw ? key : tv;
-          key = sw ? tv : key;
+    for (int i = 0; i < 4; ++i) xs[i] = __uint_as_float(((live >> i) & 1u) ? d[i] : 0x7FC00000u);
+  };
+  auto pass1_vec = [&](uint4 q, int64_t v) {
+    float xs[4];
+    vec_vals(q, live_mask(v), xs);
+    const float vm = fmaxf(fmaxf(xs[0], xs[1]), fmaxf(xs[2], xs[3]));
+    m = fmaxf(m, vm);
+    if (vm > top[3]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float x = xs[i];
+        if (x > top[3]) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const bool sw = x > top[r];
+            const float tv = top[r];
+            top[r] = sw ? x : tv;
+            x = sw ? tv : x;
+          }
         }
       }
     }
@@ -135,41 +152,43 @@ __global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
   }
 #pragma unroll
   for (int d = kWave / 2; d >= 1; d >>= 1) m = fmaxf(m, lane_xor_f(m, d));
-  const bool wbad = __ballot(bad) != 0ull;
-  if (l == 0) {
-    redf[w] = m;
-    redi[w] = wbad ? 1 : 0;
-  }
-  // threshold: the k-th largest of the 4096 per-thread keys
+  if (l == 0) redf[w] = m;
+  // threshold: the k-th largest of the 4096 per-thread values (as select keys)
+  uint32_t tk[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) tk[r] = select_key(__float_as_uint(top[r]));
   uint32_t* keys = (uint32_t*)pool;
-  block_bitonic_sort_c<uint32_t, 4, kPfNT * 4, true>(top, keys);
-  if (t == (k - 1) / 4) s_t0 = top[(k - 1) % 4];
+  block_bitonic_sort_c<uint32_t, 4, kPfNT * 4, true>(tk, keys);
+  if (t == (k - 1) / 4) s_t0 = tk[(k - 1) % 4];
   if (t == 0) s_cnt = 0;
   __syncthreads();
   m = redf[0];
-  bool row_bad = redi[0] != 0;
-  for (int i = 1; i < kPfNW; ++i) {
-    m = fmaxf(m, redf[i]);
-    row_bad = row_bad || redi[i] != 0;
-  }
-  const uint32_t t0 = s_t0 > 1u ? s_t0 : 1u;  // >= 1: dead slots (key 0) never pass
+  for (int i = 1; i < kPfNW; ++i) m = fmaxf(m, redf[i]);
+  // candidates: x >= T0 as floats (NaN never passes)
+  const float t0f = s_t0 >= 0x007FFFFFu ? __uint_as_float(key_to_bits(s_t0)) : -INFINITY;
 
   // ---- pass 2: exp-sum and candidates -----------------------------------------
   float s = 0.0f;
-  auto pass2_vec = [&](const uint4 q, int64_t v) {
-    const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+  const float mc = m * 1.44269504088896341f;
+  const bool fin = m != -INFINITY;  // else the live elements are all -inf or NaN
+  auto pass2_vec = [&](uint4 q, int64_t v) {
+    const uint32_t live = live_mask(v);
+    float xs[4];
+    vec_vals(q, live, xs);
     float vs = 0.0f;
-    uint32_t mask = 0;
-    const bool inner = v >= v_lo && v < v_hi;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t e = v * 4 - rv.mis + i;
-      const bool live = inner || (e >= 0 && e < a.cols);
-      const float x = __uint_as_float(d[i]);
-      vs += live ? pf_exp(x, m) : 0.0f;
-      mask |= (live && select_key(d[i]) >= t0 ? 1u : 0u) << i;
+      // a real NaN / +inf makes the sum NaN, as in jax.nn.softmax
+      const float e = fin ? pf_exp(xs[i], mc) : (xs[i] != xs[i] ? xs[i] : __builtin_nanf(""));
+      vs += ((live >> i) & 1u) ? e : 0.0f;
     }
     s += vs;
+    const float vm = fmaxf(fmaxf(xs[0], xs[1]), fmaxf(xs[2], xs[3]));
+    uint32_t mask = 0;
+    if (vm >= t0f) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mask |= (xs[i] >= t0f ? 1u : 0u) << i;
+    }
     const uint64_t any = __ballot(mask != 0u);
     if (any) {
       for (;;) {
@@ -180,7 +199,7 @@ __global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
         if (hc) {
           const int i = __builtin_ctz(mask);
           mask &= mask - 1u;
-          c = make_comp(select_key(d[i]), (uint32_t)(v * 4 - rv.mis + i));
+          c = make_comp(select_key(__float_as_uint(xs[i])), (uint32_t)(v * 4 - rv.mis + i));
         }
         // one atomic per wave step, issued by the first active lane (lanes
         // may have left the vector loop already)
@@ -216,6 +235,9 @@ __global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
   s = 0.0f;
   for (int i = 0; i < kPfNW; ++i) s += redf[i];
   const int n = s_cnt;
+  // NaN or +inf in the row, or a row of -inf only, makes the sum NaN, as it
+  // makes jax.nn.softmax NaN
+  const bool row_bad = s != s;
 
   // ---- the k largest composites, sorted ---------------------------------------
   if (n <= kPfCap) {
@@ -269,7 +291,7 @@ __global__ __launch_bounds__(kPfNT) void softmax_topk_kernel(PfArgs a) {
   for (int p = t; p < k; p += kPfNT) {
     const uint64_t c = pool[p];
     int32_t idx = comp_idx(c);
-    float pr = pf_exp(__uint_as_float(key_to_bits(comp_key(c))), m) / s;
+    float pr = pf_exp(__uint_as_float(key_to_bits(comp_key(c))), mc) / s;
     if (row_bad) {
       idx = p;
       pr = NAN;
