@@ -11,26 +11,26 @@
 //     sampling.py:283-290), then top_p_and_sample_arrays (sampling.py:65-115).
 //
 // Design (each element is read from HBM exactly once):
-//   Kernel A, seg_select_kernel: a row is cut into `nseg` segments, one
-//   256-thread workgroup each, sized so that ~4 workgroups run per CU.  A
-//   workgroup streams its segment in tiles of 256 x V 16-byte vectors held in
-//   registers, prefetching tile t+1 while it filters tile t:
-//     - every element becomes a monotone 32-bit select key;
-//     - tile 0 sets a lower bound L on the segment's k-th key: each wave sorts
-//       its 64 per-thread maxima (wave64 bitonic network) and L is the minimum
-//       over the 4 waves of their ceil(k/4)-th largest maximum, so at least k
+//   Kernel A, seg_select_kernel: one workgroup per (segment, row).  A row is
+//   either one segment of a 512-thread workgroup (up to 32 16-byte vectors per
+//   thread, no second kernel) or `nseg` segments of 256 threads, sized so that
+//   ~4 workgroups run per CU.  Every load of the segment is issued up front
+//   into registers, then:
+//     - each thread takes the maximum of its elements as a monotone key
+//       (integer max over raw bits, packed for bf16 pairs);
+//     - a lower bound L on the segment's k-th key: each wave sorts its 64
+//       per-thread maxima (wave64 bitonic network) and L is the minimum over
+//       the waves of their ceil(k/waves)-th largest maximum, so at least k
 //       elements are >= L;
-//     - elements passing the current filter become candidates (u64 composite
-//       key << 32 | ~index), appended by wave-level stream compaction
+//     - vectors whose maximum reaches L are staged through LDS and their
+//       passing elements become candidates (composite key, value descending
+//       then index ascending), appended by wave-level stream compaction
 //       (ballot + mbcnt) to a per-wave LDS region of 256 slots;
-//     - after tile 0, and whenever a wave region holds more than 128, the
-//       candidates are cut to their exact top-k and the filter tightens to
-//       "key > key of the k-th" (later elements have larger indices, so an
-//       equal key can no longer win a tie);
-//     - a tile that would overflow a region (heavy ties) contributes its
-//       exact top-k instead, found by bisection on the composite key.
-//   Selection sorts 128-element runs with a wave64 bitonic network and merges
-//   runs with bitonic merge-and-discard (tx_wave_sort.h).
+//     - if a region overflows (heavy ties), the same staged rounds run a
+//       bisection for the exact k-th composite and collect only those >= it.
+//   Selection compacts the candidates, sorts 64- or 128-element runs with a
+//   wave64 bitonic network and merges runs with bitonic merge-and-discard
+//   (tx_wave_sort.h), giving the segment's sorted top-128.
 //   Kernel B, seg_merge_kernel (only when nseg > 1): one wave per row merges
 //   the segment lists and writes (values, indices) or runs the sampler tail.
 //   The kernel boundary orders the workspace writes before the reads, so no
