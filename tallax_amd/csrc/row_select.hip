@@ -31,8 +31,10 @@
 //   Selection compacts the candidates, sorts 64- or 128-element runs with a
 //   wave64 bitonic network and merges runs with bitonic merge-and-discard
 //   (tx_wave_sort.h), giving the segment's sorted top-128.
-//   Kernel B, seg_merge_kernel (only when nseg > 1): one wave per row merges
-//   the segment lists and writes (values, indices) or runs the sampler tail.
+//   Kernel B, seg_merge_kernel (only when nseg > 1): one 4-wave workgroup per
+//   row loads every segment list at once, merges them (merge-and-discard per
+//   wave, then a tree through LDS) and writes (values, indices) or runs the
+//   sampler tail.
 //   The kernel boundary orders the workspace writes before the reads, so no
 //   device-scope fence (an L2 write-back on gfx950) is ever issued.
 #include <float.h>
@@ -769,24 +771,52 @@ void seg_select_kernel(SelArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel B: one wave per row merges the segment lists and finishes the row.
+// Kernel B: one workgroup of kMergeNT threads per row merges the segment
+// lists and finishes the row.  Wave w loads lists w, w + NW, ... all at once
+// (they were written by other CUs, so every load is a full memory latency),
+// folds them with merge-and-discard, and the per-wave lists are merged as a
+// binary tree through LDS.
 // ---------------------------------------------------------------------------
+constexpr int kMergeNT = 256;
 template <int DT, bool SAMPLE>
-__global__ __launch_bounds__(kWave) void seg_merge_kernel(SelArgs a) {
-  __shared__ uint64_t list[kRun];
+__global__ __launch_bounds__(kMergeNT) void seg_merge_kernel(SelArgs a) {
+  constexpr int NW = kMergeNT / kWave;
+  constexpr int PER = kMaxSeg / NW;  // lists per wave, at most
+  __shared__ uint64_t tree[NW][kRun];
   __shared__ float sg[kRun];
   const int64_t row = blockIdx.x;
-  const int l = lane_id();
+  const int w = threadIdx.x / kWave, l = lane_id();
   const uint64_t* src = a.ws_lists + (size_t)row * a.nseg * kRun;
-  uint64_t acc[2] = {src[l], src[kWave + l]};
-  for (int s = 1; s < a.nseg; ++s) {
-    const uint64_t b[2] = {src[s * kRun + l], src[s * kRun + kWave + l]};
-    wave_merge128_desc(acc, b);
+  uint64_t b[PER][2];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int sgi = w + i * NW;
+    b[i][0] = sgi < a.nseg ? src[sgi * kRun + l] : 0ull;
+    b[i][1] = sgi < a.nseg ? src[sgi * kRun + kWave + l] : 0ull;
   }
-  list[l] = acc[0];
-  list[kWave + l] = acc[1];
+  uint64_t acc[2] = {b[0][0], b[0][1]};
+#pragma unroll
+  for (int i = 1; i < PER; ++i) {
+    if (w + i * NW < a.nseg) wave_merge128_desc(acc, b[i]);
+  }
+#pragma unroll
+  for (int st = 1; st < NW; st <<= 1) {
+    if ((w & (2 * st - 1)) == st) {
+      tree[w][l] = acc[0];
+      tree[w][kWave + l] = acc[1];
+    }
+    __syncthreads();
+    if ((w & (2 * st - 1)) == 0) {
+      const uint64_t c[2] = {tree[w + st][l], tree[w + st][kWave + l]};
+      wave_merge128_desc(acc, c);
+    }
+  }
+  if (w == 0) {
+    tree[0][l] = acc[0];
+    tree[0][kWave + l] = acc[1];
+  }
   __syncthreads();
-  finalize_row<DT, SAMPLE>(a, row, list, sg);
+  finalize_row<DT, SAMPLE>(a, row, tree[0], sg);
 }
 
 // Standalone top_p_and_sample (sampling.py:210-269) on already-sorted
@@ -914,7 +944,7 @@ static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const c
   }
   int st = launch_status(what);
   if (st || a.nseg == 1) return st;
-  hipLaunchKernelGGL((seg_merge_kernel<DT, SAMPLE>), dim3((unsigned)a.rows), dim3(kWave), 0, s, a);
+  hipLaunchKernelGGL((seg_merge_kernel<DT, SAMPLE>), dim3((unsigned)a.rows), dim3(kMergeNT), 0, s, a);
   return launch_status(what);
 }
 
