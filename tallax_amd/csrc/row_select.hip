@@ -394,7 +394,8 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
       const uint64_t c = list[i];
       const uint32_t kk = comp_key(c);
       const int32_t idx = comp_idx(c);
-      uint32_t b = kk > inel ? T::load_bits(rowp, idx) : T::kMinBits;
+      // the key fixes the value except the sign of a zero: only zeros are reloaded
+      uint32_t b = kk > inel ? (kk == 0x80000000u ? T::load_bits(rowp, idx) : key_to_bits(kk)) : T::kMinBits;
       if (a.k_rows && i >= a.k_rows[row]) b = __float_as_uint(a.replace_in_dtype);
       T::store(a.out_vals, row * a.k + i, b);
       a.out_idx[row * a.k + i] = idx;
