@@ -28,19 +28,80 @@ namespace tx {
 
 // axis 1, rows whose values fit in LDS: the row is staged once, then every
 // output of the row gathers from LDS (each value byte read from HBM once).
+// When the value row, the index row and the output row are 16-byte aligned and
+// whole 16-byte blocks, the staging reads, the index reads and the output
+// writes are 16 bytes per lane, and a thread issues all of its staging and
+// index loads (kGatherBatch blocks of each) before waiting for any of them.
+constexpr int kGatherNT = 256;
+constexpr int kGatherBatch = 4;
 template <typename T>
-__global__ __launch_bounds__(256) void gather_row_lds_kernel(const T* __restrict__ val, int64_t vcols,
-                                                             const int32_t* __restrict__ idx, int64_t icols,
-                                                             T* __restrict__ out) {
+__global__ __launch_bounds__(kGatherNT) void gather_row_lds_kernel(const T* __restrict__ val, int64_t vcols,
+                                                                   const int32_t* __restrict__ idx,
+                                                                   int64_t icols, T* __restrict__ out) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* row_vals = (T*)smem;
   const int64_t r = blockIdx.x;
+  const int t = threadIdx.x;
   const T* vr = val + r * vcols;
-  for (int64_t j = threadIdx.x; j < vcols; j += blockDim.x) row_vals[j] = vr[j];
-  __syncthreads();
   const int32_t* ir = idx + r * icols;
   T* orow = out + r * icols;
-  for (int64_t j = threadIdx.x; j < icols; j += blockDim.x) {
+  constexpr int EPV = 16 / (int)sizeof(T);  // values per 16-byte block
+  const bool vec = (((uintptr_t)vr | (uintptr_t)ir | (uintptr_t)orow) & 15u) == 0 && vcols % EPV == 0 &&
+                   icols % EPV == 0;
+  if (vec) {
+    const uint4* v4 = (const uint4*)vr;
+    const uint4* i4 = (const uint4*)ir;
+    const int64_t nv = vcols / EPV;  // value blocks
+    const int64_t ni = icols / 4;    // index blocks (4 indices each)
+    // the first batch of index loads is issued before the staging loads
+    uint4 iv[kGatherBatch];
+#pragma unroll
+    for (int u = 0; u < kGatherBatch; ++u) {
+      const int64_t b = (int64_t)u * kGatherNT + t;
+      if (b < ni) iv[u] = i4[b];
+    }
+    for (int64_t b0 = 0; b0 < nv; b0 += (int64_t)kGatherBatch * kGatherNT) {
+      uint4 sv[kGatherBatch];
+#pragma unroll
+      for (int u = 0; u < kGatherBatch; ++u) {
+        const int64_t b = b0 + (int64_t)u * kGatherNT + t;
+        if (b < nv) sv[u] = v4[b];
+      }
+#pragma unroll
+      for (int u = 0; u < kGatherBatch; ++u) {
+        const int64_t b = b0 + (int64_t)u * kGatherNT + t;
+        if (b < nv) ((uint4*)row_vals)[b] = sv[u];
+      }
+    }
+    __syncthreads();
+    for (int64_t ib = 0; ib < ni; ib += (int64_t)kGatherBatch * kGatherNT) {
+      if (ib > 0) {
+#pragma unroll
+        for (int u = 0; u < kGatherBatch; ++u) {
+          const int64_t b = ib + (int64_t)u * kGatherNT + t;
+          if (b < ni) iv[u] = i4[b];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kGatherBatch; ++u) {
+        const int64_t b = ib + (int64_t)u * kGatherNT + t;
+        if (b >= ni) continue;
+        const int32_t q[4] = {(int32_t)iv[u].x, (int32_t)iv[u].y, (int32_t)iv[u].z, (int32_t)iv[u].w};
+        T o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = (q[e] >= 0 && (int64_t)q[e] < vcols) ? row_vals[q[e]] : (T)0;
+        if (sizeof(T) == 4) {
+          ((uint4*)orow)[b] = make_uint4((uint32_t)o[0], (uint32_t)o[1], (uint32_t)o[2], (uint32_t)o[3]);
+        } else {
+          ((uint2*)orow)[b] = make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+        }
+      }
+    }
+    return;
+  }
+  for (int64_t j = t; j < vcols; j += kGatherNT) row_vals[j] = vr[j];
+  __syncthreads();
+  for (int64_t j = t; j < icols; j += kGatherNT) {
     const int32_t i = ir[j];
     orow[j] = (i >= 0 && (int64_t)i < vcols) ? row_vals[i] : (T)0;
   }
@@ -219,10 +280,10 @@ int tallax_take_along_axis(const void* values, int dtype, int64_t vrows, int64_t
     if (vcols * es <= 64 * 1024 && irows <= 2147483647) {
       const size_t lds = (size_t)vcols * es;
       if (es == 2)
-        hipLaunchKernelGGL(gather_row_lds_kernel<uint16_t>, dim3((unsigned)irows), dim3(256), lds, stream,
+        hipLaunchKernelGGL(gather_row_lds_kernel<uint16_t>, dim3((unsigned)irows), dim3(kGatherNT), lds, stream,
                            (const uint16_t*)values, vcols, indices, icols, (uint16_t*)out);
       else
-        hipLaunchKernelGGL(gather_row_lds_kernel<uint32_t>, dim3((unsigned)irows), dim3(256), lds, stream,
+        hipLaunchKernelGGL(gather_row_lds_kernel<uint32_t>, dim3((unsigned)irows), dim3(kGatherNT), lds, stream,
                            (const uint32_t*)values, vcols, indices, icols, (uint32_t*)out);
     } else if (es == 2) {
       hipLaunchKernelGGL(gather_row_kernel<uint16_t>, dim3(grid_for(total)), dim3(256), 0, stream,
