@@ -38,6 +38,12 @@ int tallax_testing_lane_ops(uint32_t* out, tallax_stream_t stream);
  * out[3] vectors per segment.  Host only: no device work. */
 int tallax_testing_select_plan(int64_t rows, int64_t cols, int dtype, int32_t* out);
 
+// Path of tallax_top_dynamic_k for later calls in this process: 0 (default)
+// settles rows from the exact kernel's per-segment top-128 candidates where
+// they suffice and scans the rest; 1 scans every row.  Both give the same
+// results; tests run both.  Returns TALLAX_INVALID_ARGUMENT for other values.
+int tallax_testing_binned_mode(int mode);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -50,6 +50,7 @@ _SIGNATURES = {
     "tallax_testing_gumbel": ([ctypes.c_uint32, ctypes.c_uint32, _c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
     "tallax_testing_lane_ops": ([_c_p, _c_p], _c_int),
     "tallax_testing_select_plan": ([_c_i64, _c_i64, _c_int, _c_p], _c_int),
+    "tallax_testing_binned_mode": ([_c_int], _c_int),
 }
 
 

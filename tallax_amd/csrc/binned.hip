@@ -68,6 +68,10 @@ struct BinArgs {
   float* st_pivot;         // [rows][nsteps]
   int32_t* st_count;       // [rows][nsteps]
   int32_t* upper;          // [1]
+  // candidate path
+  const uint64_t* lists;   // [rows][nseg][128] per-segment sorted top-128 composites
+  int nseg;
+  int32_t* covered;        // [rows] 1: the candidates settled the row, 0: it was scanned
 };
 
 __device__ __forceinline__ float load_val(const void* x, int dt, int64_t i) {
@@ -81,9 +85,10 @@ __device__ __forceinline__ bool ahead(float va, int32_t ia, float vb, int32_t ib
   return va > vb || (va == vb && (uint32_t)ia < (uint32_t)ib);
 }
 
+// Full scan of one row by a kBinNT-thread workgroup; smem holds
+// kBinNT * MC * 8 bytes.
 template <int MC>
-__global__ __launch_bounds__(kBinNT) void binned_lists_kernel(BinArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
+__device__ __forceinline__ void scan_row(const BinArgs& a, int64_t row, unsigned char* smem) {
   const int NB = a.num_bins;
   const int S = kBinNT / NB;  // slices per bin
   float* sv = (float*)smem;                         // [S][MC][NB]
@@ -92,7 +97,6 @@ __global__ __launch_bounds__(kBinNT) void binned_lists_kernel(BinArgs a) {
   __shared__ int red_i[kBinNT / kWave];
   const int t = threadIdx.x;
   const int b = t % NB, s = t / NB;
-  const int64_t row = blockIdx.x;
   const float lo = dtype_min_f(a.dtype);
   float v[MC];
   int32_t id[MC];
@@ -202,27 +206,46 @@ __global__ __launch_bounds__(kBinNT) void binned_lists_kernel(BinArgs a) {
   }
 }
 
-__global__ __launch_bounds__(256) void binned_finish_kernel(BinArgs a) {
-  __shared__ int red[256 / kWave];
+template <int MC>
+__global__ __launch_bounds__(kBinNT) void binned_lists_kernel(BinArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  scan_row<MC>(a, blockIdx.x, smem);
+}
+
+// Depths, cutoffs, valid and depth_upper from the per-step statistics, one
+// thread per row: a row's depth is m - 1 at its first converged step (max_k
+// if none); a block of block_token rows evaluates steps until all of its rows
+// converged, and its cutoff is the pivot of the last step evaluated.
+constexpr int kFinishNT = 1024;
+__device__ __forceinline__ void finish_rows(const BinArgs& a) {
+  __shared__ int fcs[kFinishNT];
+  __shared__ int red[kFinishNT / kWave];
   const int t = threadIdx.x;
-  const int64_t nblk = a.rows / a.block_token;
   int gmax = 0;
-  for (int64_t bk = t; bk < nblk; bk += blockDim.x) {
-    const int64_t r0 = bk * a.block_token;
-    for (int i = 0; i < a.block_token; ++i) a.out_depths[r0 + i] = a.max_k;
-    for (int q = 0; q < a.nsteps; ++q) {
-      const int m = a.steps[q];
-      bool all = true;
-      for (int i = 0; i < a.block_token; ++i) {
-        const int64_t r = r0 + i;
-        const bool conv = a.st_count[r * a.nsteps + q] >= a.k_rows[r];
-        if (conv && a.out_depths[r] == a.max_k) a.out_depths[r] = m - 1;
-        a.out_cutoff[r] = a.st_pivot[r * a.nsteps + q];
-        all = all && conv;
-      }
-      if (all) break;
+  // chunks of whole blocks of rows
+  const int per = kFinishNT / a.block_token * a.block_token;
+  for (int64_t r0 = 0; r0 < a.rows; r0 += per) {
+    const int64_t r = r0 + t;
+    int fc = a.nsteps;
+    const bool live = t < per && r < a.rows;
+    if (live) {
+      const int kr = a.k_rows[r];
+      for (int q = a.nsteps - 1; q >= 0; --q)
+        if (a.st_count[r * a.nsteps + q] >= kr) fc = q;
     }
-    for (int i = 0; i < a.block_token; ++i) gmax = max(gmax, a.out_depths[r0 + i]);
+    fcs[t] = fc;
+    __syncthreads();
+    if (live) {
+      const int b0 = t / a.block_token * a.block_token;
+      int qb = 0;
+      for (int i = 0; i < a.block_token; ++i) qb = max(qb, fcs[b0 + i]);
+      const int last = qb < a.nsteps - 1 ? qb : a.nsteps - 1;
+      const int depth = fc < a.nsteps ? a.steps[fc] - 1 : a.max_k;
+      a.out_depths[r] = depth;
+      a.out_cutoff[r] = a.st_pivot[r * a.nsteps + last];
+      gmax = max(gmax, depth);
+    }
+    __syncthreads();
   }
   const int l = lane_id();
 #pragma unroll
@@ -231,7 +254,7 @@ __global__ __launch_bounds__(256) void binned_finish_kernel(BinArgs a) {
   __syncthreads();
   if (t == 0) {
     int g = 0;
-    for (int i = 0; i < (int)(blockDim.x / kWave); ++i) g = max(g, red[i]);
+    for (int i = 0; i < kFinishNT / kWave; ++i) g = max(g, red[i]);
     a.out_valid[0] = (g < a.steps[a.nsteps - 1] || a.steps[a.nsteps - 1] == a.max_k) ? 1 : 0;
     int up = a.gsched[a.ngs - 1];
     for (int i = 0; i + 1 < a.ngs; ++i) {
@@ -244,6 +267,194 @@ __global__ __launch_bounds__(256) void binned_finish_kernel(BinArgs a) {
   }
 }
 
+__global__ __launch_bounds__(kFinishNT) void binned_finish_kernel(BinArgs a) { finish_rows(a); }
+
+// ---------------------------------------------------------------------------
+// Candidate path.  The segment kernel of the exact top-k gives every segment's
+// sorted top-128 composites (value descending, index ascending).  With T0 the
+// largest of the segments' 128th composites, every element whose composite is
+// >= T0 is among them, since it is >= its own segment's 128th composite.  So
+// the set C = {candidates >= T0} is complete, and per bin the
+// entries of C are the bin's largest ones, ranked exactly as in the reference's
+// per-bin lists.  A row is settled from C when
+//   * every schedule step's pivot (the max over bins of the m-th largest) is
+//     the m-th entry of some bin of C with a key strictly above T0's, so that
+//     every element >= the pivot is in C (and bins with fewer than m entries in
+//     C have their m-th largest below it);
+//   * no bin overflows its LDS bucket;
+//   * at least max_k entries of C sit at ranks below min(depth, buf), so the
+//     final top-max_k of the first depth_upper ranks of every bin (depth_upper
+//     >= depth) are all in C.
+// Its per-bin lists are then written with the ranks C leaves open as fillers,
+// which rank below every entry the final selection can return.  Other rows
+// are left to the full scan.
+// ---------------------------------------------------------------------------
+constexpr int kCandNT = 1024;
+constexpr int kCandBucketBytes = 64 * 1024;
+constexpr int kCandRank = 16;  // ranks kept per bin (>= buf and every step depth)
+
+__host__ __device__ inline int cand_bucket_cap(int nb) {
+  const int c = kCandBucketBytes / 8 / nb;
+  return c < 32 ? c : 32;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) {
+    const uint64_t o = shfl_xor_u64(v, d);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// One workgroup per row (thread t handles bin t for the per-bin steps).  A row
+// the candidates do not settle is scanned in full by the same workgroup.
+template <int MC>
+__global__ __launch_bounds__(kCandNT) void binned_cand_kernel(BinArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NW = kCandNT / kWave;
+  const int NB = a.num_bins;
+  const int BC = cand_bucket_cap(NB);
+  const int EC = BC < kCandRank ? BC : kCandRank;
+  uint64_t* bucket = (uint64_t*)smem;               // [NB][BC]
+  uint64_t* ranked = bucket + (size_t)NB * BC;      // [NB][EC]
+  int* cnt = (int*)(ranked + (size_t)NB * EC);      // [NB]
+  __shared__ unsigned long long s_t0;
+  __shared__ unsigned long long s_red64[kMaxSteps][NW];
+  __shared__ int s_redi[kMaxSteps][NW];
+  __shared__ unsigned long long s_piv[kMaxSteps];
+  __shared__ int s_cnt[kMaxSteps];
+  __shared__ int s_bad, s_nd;
+  const int t = threadIdx.x, w = t / kWave, l = lane_id();
+  const int64_t row = blockIdx.x;
+  const int n = a.nseg * 128;
+  const uint64_t* lst = a.lists + (size_t)row * n;
+  const uint32_t inel = ineligible_key_max(a.dtype);
+  for (int b = t; b < NB; b += kCandNT) cnt[b] = 0;
+  if (t == 0) s_bad = 0;
+  // every candidate of the row is loaded at once (n <= 32 * 128 = 4 * kCandNT)
+  constexpr int U = 4;
+  uint64_t c[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int e = u * kCandNT + t;
+    c[u] = e < n ? lst[e] : 0ull;
+  }
+  if (w == 0) {  // T0: the largest of the segments' 128th composites (nseg <= 64)
+    const uint64_t v = wave_max_u64(l < a.nseg ? lst[l * 128 + 127] : 0ull);
+    if (l == 0) s_t0 = v;
+  }
+  __syncthreads();
+  const uint64_t t0 = s_t0;
+  int bin[U], pos[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    pos[u] = -1;
+    bin[u] = 0;
+    if (c[u] != 0ull && c[u] >= t0 && comp_key(c[u]) > inel) {
+      bin[u] = (int)((uint32_t)comp_idx(c[u]) % (uint32_t)NB);
+      pos[u] = atomicAdd(&cnt[bin[u]], 1);
+      if (pos[u] < BC) bucket[(size_t)bin[u] * BC + pos[u]] = c[u];
+    }
+  }
+  __syncthreads();
+  // rank of each entry inside its bin's bucket
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (pos[u] < 0 || pos[u] >= BC) continue;
+    const int nb = cnt[bin[u]] < BC ? cnt[bin[u]] : BC;
+    const uint64_t* bk = bucket + (size_t)bin[u] * BC;
+    int r = 0;
+    for (int j = 0; j < nb; ++j) r += bk[j] > c[u] ? 1 : 0;
+    if (r < EC) ranked[(size_t)bin[u] * EC + r] = c[u];
+  }
+  __syncthreads();
+  // per-step pivot: the largest m-th entry over bins (thread t = bin t)
+  const bool hb = t < NB;
+  const int cb_raw = hb ? cnt[t] : 0;
+  const int cb = cb_raw < EC ? cb_raw : EC;
+  if (__ballot(cb_raw > BC) && l == 0) s_bad = 1;
+  for (int q = 0; q < a.nsteps; ++q) {
+    const int m = a.steps[q];
+    const uint64_t v = wave_max_u64((hb && m <= EC && cb >= m) ? ranked[(size_t)t * EC + m - 1] : 0ull);
+    if (l == 0) s_red64[q][w] = v;
+  }
+  __syncthreads();
+  if (t < a.nsteps) {
+    uint64_t v = 0ull;
+    for (int i = 0; i < NW; ++i) v = s_red64[t][i] > v ? s_red64[t][i] : v;
+    s_piv[t] = v;
+  }
+  __syncthreads();
+  // per-step count: entries of ranks < m - 1 with a value >= the pivot
+  for (int q = 0; q < a.nsteps; ++q) {
+    const uint32_t pk = comp_key((uint64_t)s_piv[q]);
+    const int lim = a.steps[q] - 1 < cb ? a.steps[q] - 1 : cb;
+    int cq = 0;
+    for (int i = 0; i < lim; ++i) cq += comp_key(ranked[(size_t)t * EC + i]) >= pk ? 1 : 0;
+    cq = wave_sum_i(cq);
+    if (l == 0) s_redi[q][w] = cq;
+  }
+  __syncthreads();
+  if (t < a.nsteps) {
+    int v = 0;
+    for (int i = 0; i < NW; ++i) v += s_redi[t][i];
+    s_cnt[t] = v;
+  }
+  __syncthreads();
+  // coverage of the steps, the row's depth and the entries below min(depth, buf)
+  bool ok = s_bad == 0;
+  int depth = a.max_k;
+  for (int q = 0; q < a.nsteps; ++q) {
+    const uint64_t pv = s_piv[q];
+    ok = ok && pv != 0ull && comp_key(pv) > comp_key(t0);
+    if (depth == a.max_k && s_cnt[q] >= a.k_rows[row]) depth = a.steps[q] - 1;
+  }
+  const int dm = depth < a.buf ? depth : a.buf;
+  {
+    const int v = wave_sum_i(cb < dm ? cb : dm);
+    if (l == 0) s_redi[0][w] = v;
+  }
+  __syncthreads();
+  if (t == 0) {
+    int v = 0;
+    for (int i = 0; i < NW; ++i) v += s_redi[0][i];
+    s_nd = v;
+  }
+  __syncthreads();
+  ok = ok && s_nd >= a.max_k && dm <= EC;
+  if (t == 0) a.covered[row] = ok ? 1 : 0;
+  if (ok) {
+    if (t < a.nsteps) {
+      a.st_pivot[row * a.nsteps + t] = __uint_as_float(key_to_bits(comp_key((uint64_t)s_piv[t])));
+      a.st_count[row * a.nsteps + t] = s_cnt[t];
+    }
+    const float lo = dtype_min_f(a.dtype);
+    for (int e = t; e < a.buf * NB; e += kCandNT) {
+      const int r = e / NB, b = e % NB;
+      const int cbb = cnt[b] < EC ? cnt[b] : EC;
+      float v = lo;
+      int32_t id = -1;
+      if (r < cbb) {
+        const uint64_t x = ranked[(size_t)b * EC + r];
+        v = __uint_as_float(key_to_bits(comp_key(x)));
+        id = comp_idx(x);
+      }
+      a.lv[((size_t)row * a.buf + r) * NB + b] = v;
+      a.li[((size_t)row * a.buf + r) * NB + b] = id;
+    }
+  } else {
+    __syncthreads();  // the scan reuses the LDS
+    scan_row<MC>(a, row, smem);
+  }
+}
+
+__host__ __device__ inline size_t cand_lds_bytes(int nb) {
+  const int bc = cand_bucket_cap(nb);
+  const int ec = bc < kCandRank ? bc : kCandRank;
+  return (size_t)nb * bc * 8 + (size_t)nb * ec * 8 + (size_t)nb * 4;
+}
+
 // composite of a list entry: value descending then index ascending; fillers
 // (index -1) after every real entry
 __device__ __forceinline__ uint64_t entry_comp(float v, int32_t i) {
@@ -251,47 +462,105 @@ __device__ __forceinline__ uint64_t entry_comp(float v, int32_t i) {
   return make_comp(select_key(__float_as_uint(v)), (uint32_t)i);
 }
 
-__global__ __launch_bounds__(1024) void binned_select_kernel(BinArgs a) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  uint64_t* lds = (uint64_t*)smem;
-  const int t = threadIdx.x;
-  const int NT = blockDim.x;
+// Top max_k of the first depth_upper ranks of every bin: each wave sorts
+// 128-entry runs of the superset (wave64 bitonic network) and folds them into
+// its own top-128 by merge-and-discard; the per-wave lists are merged as a
+// binary tree through LDS.
+// With INLINE (rows <= kFinishNT), every workgroup first recomputes the
+// finish step for all rows (a few values per row) to get depth_upper, and
+// writes its own row's depth and cutoff (workgroup 0 also `valid`), which
+// saves a kernel launch; otherwise binned_finish_kernel ran before.
+constexpr int kSelNT = 1024;
+static_assert(kSelNT == kFinishNT, "the inline finish step uses one thread per row");
+template <bool INLINE>
+__global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
+  constexpr int NW = kSelNT / kWave;
+  __shared__ uint64_t tree[NW][128];
+  __shared__ int fcs[kSelNT];
+  __shared__ int red[NW];
+  const int t = threadIdx.x, w = t / kWave, l = lane_id();
   const int64_t row = blockIdx.x;
   const int NB = a.num_bins;
-  const int up = a.upper[0] < a.buf ? a.upper[0] : a.buf;
-  const int n = up * NB;
-  int P = 1;
-  while (P < n) P <<= 1;
-  for (int i = t; i < P; i += NT) {
-    uint64_t c = 0;
-    if (i < n) {
-      const int r = i / NB, b = i % NB;
-      c = entry_comp(a.lv[((size_t)row * a.buf + r) * NB + b], a.li[((size_t)row * a.buf + r) * NB + b]);
+  int upper_v;
+  if (INLINE) {
+    int fc = a.nsteps;
+    const bool live = t < a.rows;
+    if (live) {
+      const int kr = a.k_rows[t];
+      for (int q = a.nsteps - 1; q >= 0; --q)
+        if (a.st_count[(int64_t)t * a.nsteps + q] >= kr) fc = q;
     }
-    lds[i] = c;
-  }
-  __syncthreads();
-  // bitonic sort, descending
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride >= 1; stride >>= 1) {
-      for (int i = t; i < P; i += NT) {
-        const int j = i ^ stride;
-        if (j > i) {
-          const uint64_t x = lds[i], y = lds[j];
-          const bool desc = (i & size) == 0;
-          if ((x < y) == desc) {
-            lds[i] = y;
-            lds[j] = x;
-          }
-        }
+    fcs[t] = fc;
+    int g = live ? (fc < a.nsteps ? a.steps[fc] - 1 : a.max_k) : 0;
+#pragma unroll
+    for (int d = kWave / 2; d >= 1; d >>= 1) g = max(g, (int)lane_xor((uint32_t)g, d));
+    if (l == 0) red[w] = g;
+    __syncthreads();
+    g = 0;
+    for (int i = 0; i < NW; ++i) g = max(g, red[i]);
+    int up = a.gsched[a.ngs - 1];
+    for (int i = 0; i + 1 < a.ngs; ++i) {
+      if (a.gsched[i] < g && g <= a.gsched[i + 1]) {
+        up = a.gsched[i + 1];
+        break;
       }
-      __syncthreads();
+    }
+    upper_v = up;
+    if (t == 0) {
+      const int r = (int)row;
+      const int b0 = r / a.block_token * a.block_token;
+      int qb = 0;
+      for (int i = 0; i < a.block_token; ++i) qb = max(qb, fcs[b0 + i]);
+      const int last = qb < a.nsteps - 1 ? qb : a.nsteps - 1;
+      const int fr = fcs[r];
+      a.out_depths[row] = fr < a.nsteps ? a.steps[fr] - 1 : a.max_k;
+      a.out_cutoff[row] = a.st_pivot[row * a.nsteps + last];
+      if (row == 0) a.out_valid[0] = (g < a.steps[a.nsteps - 1] || a.steps[a.nsteps - 1] == a.max_k) ? 1 : 0;
+    }
+  } else {
+    upper_v = a.upper[0];
+  }
+  const int up = upper_v < a.buf ? upper_v : a.buf;
+  const int n = up * NB;
+  const int nr = (n + 127) / 128;
+  const float* lv = a.lv + (size_t)row * a.buf * NB;  // rank-major: entry e = rank * NB + bin
+  const int32_t* li = a.li + (size_t)row * a.buf * NB;
+  uint64_t acc[2] = {0ull, 0ull};
+  for (int r = w; r < nr; r += NW) {
+    uint64_t c[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int e = r * 128 + h * kWave + l;
+      c[h] = e < n ? entry_comp(lv[e], li[e]) : 0ull;
+    }
+    wave_sort128_desc(c);
+    if (r == w) {
+      acc[0] = c[0];
+      acc[1] = c[1];
+    } else {
+      wave_merge128_desc(acc, c);
     }
   }
+#pragma unroll
+  for (int st = 1; st < NW; st <<= 1) {
+    if ((w & (2 * st - 1)) == st) {
+      tree[w][l] = acc[0];
+      tree[w][kWave + l] = acc[1];
+    }
+    __syncthreads();
+    if ((w & (2 * st - 1)) == 0) {
+      const uint64_t b[2] = {tree[w + st][l], tree[w + st][kWave + l]};
+      wave_merge128_desc(acc, b);
+    }
+  }
+  if (w != 0) return;
   const float lo = dtype_min_f(a.dtype);
   const int kr = a.k_rows[row];
-  for (int p = t; p < a.max_k; p += NT) {
-    const uint64_t c = p < P ? lds[p] : 0ull;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int p = h * kWave + l;
+    if (p >= a.max_k) continue;
+    const uint64_t c = acc[h];
     float v = lo;
     int32_t id = -1;
     if (c != 0ull) {
@@ -316,8 +585,13 @@ static int log2_ceil(int x) {
 
 static int bin_buf(int max_m) { return max_m > 1 ? (max_m > (1 << log2_ceil(max_m - 1)) ? max_m : (1 << log2_ceil(max_m - 1))) : max_m; }
 
+// Workspace: candidate lists [rows][kMaxSegLists][128] u64, covered flags,
+// per-bin lists (values, indices), per-step pivots and counts, depth_upper.
+constexpr int kMaxSegLists = 32;
 static size_t bin_ws(int64_t rows, int num_bins, int buf, int nsteps) {
   size_t b = 0;
+  b += (size_t)rows * kMaxSegLists * 128 * 8;  // candidate lists
+  b += align_up((size_t)rows * 4, 256);         // covered
   b += (size_t)rows * buf * num_bins * 4;  // lv
   b += (size_t)rows * buf * num_bins * 4;  // li
   b += (size_t)rows * nsteps * 4;          // pivots
@@ -330,7 +604,17 @@ static size_t bin_ws(int64_t rows, int num_bins, int buf, int nsteps) {
 
 using namespace tx;
 
+// Path selection (test hook): 0 = candidates where they settle a row, then the
+// full scan for the rest; 1 = the full scan for every row.
+static int g_binned_mode = 0;
+
 extern "C" {
+
+int tallax_testing_binned_mode(int mode) {
+  if (mode != 0 && mode != 1) return kInvalidArgument;
+  g_binned_mode = mode;
+  return kOk;
+}
 
 size_t tallax_top_dynamic_k_workspace_size(int64_t rows, int num_bins, const int32_t* schedule, int num_steps) {
   if (rows < 0 || num_bins <= 0 || !schedule || num_steps <= 0 || num_steps > kMaxSteps) return 0;
@@ -401,6 +685,10 @@ int tallax_top_dynamic_k(const void* x, int dtype, int64_t rows, int64_t cols, c
   a.out_vals = out_vals; a.out_idx = out_idx; a.out_valid = out_valid; a.out_depths = out_depths;
   a.out_cutoff = out_cutoff;
   char* w = (char*)workspace;
+  uint64_t* lists = (uint64_t*)w;
+  w += (size_t)rows * kMaxSegLists * 128 * 8;
+  int32_t* covered = (int32_t*)w;
+  w += align_up((size_t)rows * 4, 256);
   a.lv = (float*)w;
   w += (size_t)rows * buf * num_bins * 4;
   a.li = (int32_t*)w;
@@ -411,37 +699,62 @@ int tallax_top_dynamic_k(const void* x, int dtype, int64_t rows, int64_t cols, c
   w += (size_t)rows * num_steps * 4;
   a.upper = (int32_t*)w;
   if (rows > 2147483647) { set_error("too many rows"); return kUnsupported; }
-  // kernel 1
-  const int S = kBinNT / num_bins;
+  // candidate path: per-segment top-128 lists, then one kernel that settles
+  // each row from them (or scans it); otherwise the scan kernel.  The finish
+  // step runs inside the select kernel for up to kFinishNT rows, else in its
+  // own kernel.
+  int nseg = 0, maxv = 0;
+  int64_t vps = 0;
+  const int min_seg = (num_bins * max_m + 127) / 128;
+  const bool cand = g_binned_mode == 0 && max_m <= kCandRank &&
+                    segment_lists_plan(cols, dtype, min_seg < 2 ? 2 : min_seg, &nseg, &maxv, &vps) == kOk &&
+                    nseg <= kMaxSegLists;
   const int mc = buf <= 8 ? 8 : 16;
-  const size_t lds = (size_t)S * mc * num_bins * 8;  // = kBinNT * mc * 8 <= 128 KiB
-  static const hipError_t attr8 = hipFuncSetAttribute((const void*)binned_lists_kernel<8>,
-                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
-  static const hipError_t attr16 = hipFuncSetAttribute((const void*)binned_lists_kernel<16>,
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
-  if (attr8 != hipSuccess || attr16 != hipSuccess) {
-    set_error("hipFuncSetAttribute failed");
-    return kHipError;
+  const size_t lds_scan = (size_t)kBinNT * mc * 8;  // <= 128 KiB
+  int st = kOk;
+  if (cand) {
+    a.lists = lists;
+    a.nseg = nseg;
+    a.covered = covered;
+    st = launch_segment_lists(x, dtype, rows, cols, nseg, maxv, vps, lists, stream);
+    if (st) return st;
+    const size_t lds_c = cand_lds_bytes(num_bins) > lds_scan ? cand_lds_bytes(num_bins) : lds_scan;
+    static const hipError_t attr_c8 = hipFuncSetAttribute((const void*)binned_cand_kernel<8>,
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024);
+    static const hipError_t attr_c16 = hipFuncSetAttribute((const void*)binned_cand_kernel<16>,
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024);
+    if (attr_c8 != hipSuccess || attr_c16 != hipSuccess) { set_error("hipFuncSetAttribute failed"); return kHipError; }
+    if (mc == 8)
+      hipLaunchKernelGGL(binned_cand_kernel<8>, dim3((unsigned)rows), dim3(kCandNT), lds_c, stream, a);
+    else
+      hipLaunchKernelGGL(binned_cand_kernel<16>, dim3((unsigned)rows), dim3(kCandNT), lds_c, stream, a);
+    st = launch_status("tallax_top_dynamic_k");
+    if (st) return st;
+    if (rows > kFinishNT) {
+      hipLaunchKernelGGL(binned_finish_kernel, dim3(1), dim3(kFinishNT), 0, stream, a);
+      st = launch_status("tallax_top_dynamic_k");
+      if (st) return st;
+    }
+  } else {
+    static const hipError_t attr8 = hipFuncSetAttribute((const void*)binned_lists_kernel<8>,
+                                                        hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    static const hipError_t attr16 = hipFuncSetAttribute((const void*)binned_lists_kernel<16>,
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+    if (attr8 != hipSuccess || attr16 != hipSuccess) { set_error("hipFuncSetAttribute failed"); return kHipError; }
+    if (mc == 8)
+      hipLaunchKernelGGL(binned_lists_kernel<8>, dim3((unsigned)rows), dim3(kBinNT), lds_scan, stream, a);
+    else
+      hipLaunchKernelGGL(binned_lists_kernel<16>, dim3((unsigned)rows), dim3(kBinNT), lds_scan, stream, a);
+    st = launch_status("tallax_top_dynamic_k");
+    if (st) return st;
+    hipLaunchKernelGGL(binned_finish_kernel, dim3(1), dim3(kFinishNT), 0, stream, a);
+    st = launch_status("tallax_top_dynamic_k");
+    if (st) return st;
   }
-  if (mc == 8)
-    hipLaunchKernelGGL(binned_lists_kernel<8>, dim3((unsigned)rows), dim3(kBinNT), lds, stream, a);
+  if (cand && rows <= kFinishNT)
+    hipLaunchKernelGGL(binned_select_kernel<true>, dim3((unsigned)rows), dim3(kSelNT), 0, stream, a);
   else
-    hipLaunchKernelGGL(binned_lists_kernel<16>, dim3((unsigned)rows), dim3(kBinNT), lds, stream, a);
-  int st = launch_status("tallax_top_dynamic_k");
-  if (st) return st;
-  hipLaunchKernelGGL(binned_finish_kernel, dim3(1), dim3(256), 0, stream, a);
-  st = launch_status("tallax_top_dynamic_k");
-  if (st) return st;
-  // kernel 3: the superset is at most gsched[last] * num_bins entries
-  const int max_up = a.gsched[a.ngs - 1] < buf ? a.gsched[a.ngs - 1] : buf;
-  int P = 1;
-  while (P < max_up * num_bins) P <<= 1;
-  const size_t lds3 = (size_t)P * 8;
-  if (lds3 > 160 * 1024) { set_error("superset of %d entries does not fit LDS", P); return kUnsupported; }
-  static const hipError_t attr3 = hipFuncSetAttribute((const void*)binned_select_kernel,
-                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-  if (attr3 != hipSuccess) { set_error("hipFuncSetAttribute failed"); return kHipError; }
-  hipLaunchKernelGGL(binned_select_kernel, dim3((unsigned)rows), dim3(1024), lds3, stream, a);
+    hipLaunchKernelGGL(binned_select_kernel<false>, dim3((unsigned)rows), dim3(kSelNT), 0, stream, a);
   return launch_status("tallax_top_dynamic_k");
 }
 

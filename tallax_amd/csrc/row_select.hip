@@ -70,6 +70,7 @@ struct SelArgs {
   const int32_t* k_rows;  // optional: positions >= k_rows[row] get replace_in_dtype
   // segment lists: rows * nseg * kRun composites
   uint64_t* ws_lists;
+  int lists_only;  // write the segment list even when a row is one segment
   // sampler
   const int32_t* top_k;
   const float* top_p;
@@ -763,7 +764,7 @@ void seg_select_kernel(SelArgs a) {
   block_select(sh, (const int*)sh.wc);
   for (int i = tid; i < kRun; i += NT) sh.list64[i] = S::to_global(sh.list[i], seg_e0);
   __syncthreads();
-  if (a.nseg == 1) {
+  if (a.nseg == 1 && !a.lists_only) {
     finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_g);
   } else {
     uint64_t* dst = a.ws_lists + ((size_t)row * a.nseg + seg) * kRun;
@@ -947,6 +948,53 @@ static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const c
   if (st || a.nseg == 1) return st;
   hipLaunchKernelGGL((seg_merge_kernel<DT, SAMPLE>), dim3((unsigned)a.rows), dim3(kMergeNT), 0, s, a);
   return launch_status(what);
+}
+
+// Sorted top-128 composites (select key << 32 | ~column) of every segment of
+// every row into lists[rows][nseg][128], for callers that build on
+// per-segment candidates (the binned top-k).  Segments are 256 threads x maxv
+// vectors, maxv in {4, 8, 16}; a row is cut into at least min_seg segments
+// when its length allows, at most kMaxSeg.  Returns kUnsupported when the row
+// needs more segments than that.
+int segment_lists_plan(int64_t cols, int dt, int min_seg, int* nseg_out, int* maxv_out, int64_t* vps_out) {
+  const int vec = dt == kF32 ? 4 : 8;
+  const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
+  int64_t nseg = (nv + (int64_t)kNT * 16 - 1) / ((int64_t)kNT * 16);
+  if (nseg < min_seg) nseg = min_seg;
+  if (nseg > nv) nseg = nv;
+  if (nseg < 1) nseg = 1;
+  if (nseg > kMaxSeg) return kUnsupported;
+  const int64_t vps = (nv + nseg - 1) / nseg;
+  int maxv = 4;
+  while ((int64_t)kNT * maxv < vps) maxv *= 2;
+  if (maxv > 16) return kUnsupported;
+  *nseg_out = (int)((nv + vps - 1) / vps);
+  *maxv_out = maxv;
+  *vps_out = vps;
+  return kOk;
+}
+
+int launch_segment_lists(const void* x, int dt, int64_t rows, int64_t cols, int nseg, int maxv, int64_t vps,
+                         uint64_t* lists, hipStream_t s) {
+  SelArgs a = {};
+  a.x = x;
+  a.rows = rows;
+  a.cols = cols;
+  a.k = kRun;
+  a.nseg = nseg;
+  a.vps = vps;
+  a.ws_lists = lists;
+  a.lists_only = 1;
+  if (dt == kF32) {
+    if (maxv == 16) launch_a<kF32, 16, kNT, false>(a, s);
+    else if (maxv == 8) launch_a<kF32, 8, kNT, false>(a, s);
+    else launch_a<kF32, 4, kNT, false>(a, s);
+  } else {
+    if (maxv == 16) launch_a<kBF16, 16, kNT, false>(a, s);
+    else if (maxv == 8) launch_a<kBF16, 8, kNT, false>(a, s);
+    else launch_a<kBF16, 4, kNT, false>(a, s);
+  }
+  return launch_status("segment lists");
 }
 
 static float round_to_bf16(float f) {

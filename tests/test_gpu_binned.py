@@ -17,6 +17,17 @@ def _log(msg):
     print(msg, flush=True)
 
 
+@pytest.fixture(params=[0, 1], ids=["candidates", "scan"])
+def binned_mode(request):
+    """Runs a test once with the candidate path (rows settled from the exact
+    kernel's per-segment top-128 where they suffice, the rest scanned) and
+    once with the full scan for every row; both must match the oracle."""
+    from tallax_amd import _lib
+    assert _lib.LIB.tallax_testing_binned_mode(request.param) == 0
+    yield request.param
+    assert _lib.LIB.tallax_testing_binned_mode(0) == 0
+
+
 def _check(got, want):
     gv, gi, gvalid, gd, gc = got
     wv, wi, wvalid, wd, wc = want
@@ -27,7 +38,7 @@ def _check(got, want):
     assert np.array_equal(bits(from_dev_vals(gv)), bits(wv))
 
 
-def test_config3_approx_and_recall(gpu):
+def test_config3_approx_and_recall(gpu, binned_mode):
     from tallax_amd import tax
     _log("config 3 approximate: f32 [128,151936] + spikes, k=50")
     rng = np.random.default_rng(3)
@@ -53,8 +64,9 @@ def test_config3_approx_and_recall(gpu):
     (12, 3000, 20, 64, 4, (3, 6)),
     (8, 300, 32, 128, 8, (2, 4, 9)),     # short rows: fillers at depth
     (16, 50000, 8, 512, 8, (2,)),        # unconverged rows: approximate, valid False
+    (16, 151936, 50, 128, 8, None),      # config-3 rows with heavy ties: candidates and scan mixed
 ])
-def test_top_dynamic_k_parity(gpu, dtype, rows, cols, max_k, num_bins, block_token, schedule):
+def test_top_dynamic_k_parity(gpu, binned_mode, dtype, rows, cols, max_k, num_bins, block_token, schedule):
     from tallax_amd import tax
     _log(f"top_dynamic_k {dtype} [{rows},{cols}] max_k={max_k} bins={num_bins} bt={block_token} sched={schedule}")
     rng = np.random.default_rng(rows * cols + max_k)
@@ -95,3 +107,38 @@ def test_top_dynamic_k_errors(gpu):
         tax.top_dynamic_k(x, 4, 4, block_token=8)
     with pytest.raises(NotImplementedError):
         tax.top_dynamic_k(x[:8], 4, 129)
+
+
+def test_candidates_settle_config3_rows(gpu):
+    """White-box: on config 3 the per-segment candidates settle every row (the
+    covered flag follows the candidate lists at the front of the workspace)."""
+    import ctypes
+    from tallax_amd import _lib, schedule as sch
+    rng = np.random.default_rng(3)
+    rows, cols = 128, 151936
+    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    for r in range(rows):
+        x[r, rng.choice(cols, 32, replace=False)] = 8.0
+    xd = torch.from_numpy(x).to(gpu)
+    steps = sch.topm_schedule(50, 128, 8, None)
+    arr = (ctypes.c_int32 * len(steps))(*steps)
+    need = _lib.LIB.tallax_top_dynamic_k_workspace_size(rows, 128, arr, len(steps))
+    ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
+    k = torch.full((rows,), 50, dtype=torch.int32, device=gpu)
+    vals = torch.empty((rows, 50), dtype=torch.float32, device=gpu)
+    idx = torch.empty((rows, 50), dtype=torch.int32, device=gpu)
+    valid = torch.empty(1, dtype=torch.int32, device=gpu)
+    depths = torch.empty(rows, dtype=torch.int32, device=gpu)
+    cutoff = torch.empty(rows, dtype=torch.float32, device=gpu)
+    _lib.check(_lib.LIB.tallax_top_dynamic_k(
+        xd.data_ptr(), _lib.F32, rows, cols, k.data_ptr(), 50, 8, 128, arr, len(steps), 0, 0.0, vals.data_ptr(),
+        idx.data_ptr(), valid.data_ptr(), depths.data_ptr(), cutoff.data_ptr(), ws.data_ptr(), need,
+        _lib.stream_of(xd)), "top_dynamic_k")
+    torch.cuda.synchronize()
+    off = rows * 32 * 128 * 8
+    covered = ws[off:off + rows * 4].view(torch.int32).cpu().numpy()
+    _log(f"rows settled by candidates: {int(covered.sum())} of {rows}")
+    assert covered.sum() == rows
+    want = O.top_dynamic_k(x, 50, 50)
+    assert np.array_equal(idx.cpu().numpy(), want[1])
+    assert np.array_equal(depths.cpu().numpy(), want[3])
