@@ -290,12 +290,20 @@ __global__ __launch_bounds__(kFinishNT) void binned_finish_kernel(BinArgs a) { f
 // are left to the full scan.
 // ---------------------------------------------------------------------------
 constexpr int kCandNT = 1024;
-constexpr int kCandBucketBytes = 64 * 1024;
+constexpr int kCandLdsBytes = 128 * 1024;
 constexpr int kCandRank = 16;  // ranks kept per bin (>= buf and every step depth)
 
+// Per bin: a bucket of cap entries and a ranked list of min(cap, kCandRank)
+// entries, each padded by one entry so that lanes reading their own bins
+// spread over the LDS banks, plus a counter.
+__host__ __device__ inline size_t cand_bin_bytes(int cap) {
+  const int ec = cap < kCandRank ? cap : kCandRank;
+  return (size_t)(cap + 1) * 8 + (size_t)(ec + 1) * 8 + 4;
+}
 __host__ __device__ inline int cand_bucket_cap(int nb) {
-  const int c = kCandBucketBytes / 8 / nb;
-  return c < 32 ? c : 32;
+  int c = 32;
+  while (c > 1 && (size_t)nb * cand_bin_bytes(c) > (size_t)kCandLdsBytes) --c;
+  return c;
 }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
@@ -316,9 +324,10 @@ __global__ __launch_bounds__(kCandNT) void binned_cand_kernel(BinArgs a) {
   const int NB = a.num_bins;
   const int BC = cand_bucket_cap(NB);
   const int EC = BC < kCandRank ? BC : kCandRank;
-  uint64_t* bucket = (uint64_t*)smem;               // [NB][BC]
-  uint64_t* ranked = bucket + (size_t)NB * BC;      // [NB][EC]
-  int* cnt = (int*)(ranked + (size_t)NB * EC);      // [NB]
+  const int BS = BC + 1, ES = EC + 1;               // padded strides
+  uint64_t* bucket = (uint64_t*)smem;               // [NB][BS]
+  uint64_t* ranked = bucket + (size_t)NB * BS;      // [NB][ES]
+  int* cnt = (int*)(ranked + (size_t)NB * ES);      // [NB]
   __shared__ unsigned long long s_t0;
   __shared__ unsigned long long s_red64[kMaxSteps][NW];
   __shared__ int s_redi[kMaxSteps][NW];
@@ -354,7 +363,7 @@ __global__ __launch_bounds__(kCandNT) void binned_cand_kernel(BinArgs a) {
     if (c[u] != 0ull && c[u] >= t0 && comp_key(c[u]) > inel) {
       bin[u] = (int)((uint32_t)comp_idx(c[u]) % (uint32_t)NB);
       pos[u] = atomicAdd(&cnt[bin[u]], 1);
-      if (pos[u] < BC) bucket[(size_t)bin[u] * BC + pos[u]] = c[u];
+      if (pos[u] < BC) bucket[(size_t)bin[u] * BS + pos[u]] = c[u];
     }
   }
   __syncthreads();
@@ -363,42 +372,59 @@ __global__ __launch_bounds__(kCandNT) void binned_cand_kernel(BinArgs a) {
   for (int u = 0; u < U; ++u) {
     if (pos[u] < 0 || pos[u] >= BC) continue;
     const int nb = cnt[bin[u]] < BC ? cnt[bin[u]] : BC;
-    const uint64_t* bk = bucket + (size_t)bin[u] * BC;
+    const uint64_t* bk = bucket + (size_t)bin[u] * BS;
     int r = 0;
-    for (int j = 0; j < nb; ++j) r += bk[j] > c[u] ? 1 : 0;
-    if (r < EC) ranked[(size_t)bin[u] * EC + r] = c[u];
+    for (int j0 = 0; j0 < nb; j0 += 8) {  // 8 LDS reads in flight per batch
+      uint64_t x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = j0 + j < nb ? bk[j0 + j] : 0ull;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r += x[j] > c[u] ? 1 : 0;
+    }
+    if (r < EC) ranked[(size_t)bin[u] * ES + r] = c[u];
   }
   __syncthreads();
-  // per-step pivot: the largest m-th entry over bins (thread t = bin t)
+  // per-step pivot: the largest m-th entry over bins (thread t = bin t; only
+  // the waves holding bins take part in the per-bin steps)
+  const int nbw = (NB + kWave - 1) / kWave;
+  const bool bw = w < nbw;
   const bool hb = t < NB;
   const int cb_raw = hb ? cnt[t] : 0;
   const int cb = cb_raw < EC ? cb_raw : EC;
-  if (__ballot(cb_raw > BC) && l == 0) s_bad = 1;
-  for (int q = 0; q < a.nsteps; ++q) {
-    const int m = a.steps[q];
-    const uint64_t v = wave_max_u64((hb && m <= EC && cb >= m) ? ranked[(size_t)t * EC + m - 1] : 0ull);
-    if (l == 0) s_red64[q][w] = v;
+  uint32_t rk[kCandRank];
+  if (bw) {
+    if (__ballot(cb_raw > BC) && l == 0) s_bad = 1;
+    for (int q = 0; q < a.nsteps; ++q) {
+      const int m = a.steps[q];
+      const uint64_t v = wave_max_u64((hb && m <= EC && cb >= m) ? ranked[(size_t)t * ES + m - 1] : 0ull);
+      if (l == 0) s_red64[q][w] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < kCandRank; ++i) rk[i] = (hb && i < cb) ? comp_key(ranked[(size_t)t * ES + i]) : 0u;
   }
   __syncthreads();
   if (t < a.nsteps) {
     uint64_t v = 0ull;
-    for (int i = 0; i < NW; ++i) v = s_red64[t][i] > v ? s_red64[t][i] : v;
+    for (int i = 0; i < nbw; ++i) v = s_red64[t][i] > v ? s_red64[t][i] : v;
     s_piv[t] = v;
   }
   __syncthreads();
   // per-step count: entries of ranks < m - 1 with a value >= the pivot
-  for (int q = 0; q < a.nsteps; ++q) {
-    const uint32_t pk = comp_key((uint64_t)s_piv[q]);
-    const int lim = a.steps[q] - 1 < cb ? a.steps[q] - 1 : cb;
-    int cq = 0;
-    for (int i = 0; i < lim; ++i) cq += comp_key(ranked[(size_t)t * EC + i]) >= pk ? 1 : 0;
-    cq = wave_sum_i(cq);
-    if (l == 0) s_redi[q][w] = cq;
+  if (bw) {
+    for (int q = 0; q < a.nsteps; ++q) {
+      const uint32_t pk = comp_key((uint64_t)s_piv[q]);
+      const int lim = a.steps[q] - 1 < cb ? a.steps[q] - 1 : cb;
+      int cq = 0;
+#pragma unroll
+      for (int i = 0; i < kCandRank; ++i) cq += (i < lim && rk[i] >= pk) ? 1 : 0;
+      cq = wave_sum_i(cq);
+      if (l == 0) s_redi[q][w] = cq;
+    }
   }
   __syncthreads();
   if (t < a.nsteps) {
     int v = 0;
-    for (int i = 0; i < NW; ++i) v += s_redi[t][i];
+    for (int i = 0; i < nbw; ++i) v += s_redi[t][i];
     s_cnt[t] = v;
   }
   __syncthreads();
@@ -411,14 +437,14 @@ __global__ __launch_bounds__(kCandNT) void binned_cand_kernel(BinArgs a) {
     if (depth == a.max_k && s_cnt[q] >= a.k_rows[row]) depth = a.steps[q] - 1;
   }
   const int dm = depth < a.buf ? depth : a.buf;
-  {
+  if (bw) {
     const int v = wave_sum_i(cb < dm ? cb : dm);
     if (l == 0) s_redi[0][w] = v;
   }
   __syncthreads();
   if (t == 0) {
     int v = 0;
-    for (int i = 0; i < NW; ++i) v += s_redi[0][i];
+    for (int i = 0; i < nbw; ++i) v += s_redi[0][i];
     s_nd = v;
   }
   __syncthreads();
@@ -436,7 +462,7 @@ __global__ __launch_bounds__(kCandNT) void binned_cand_kernel(BinArgs a) {
       float v = lo;
       int32_t id = -1;
       if (r < cbb) {
-        const uint64_t x = ranked[(size_t)b * EC + r];
+        const uint64_t x = ranked[(size_t)b * ES + r];
         v = __uint_as_float(key_to_bits(comp_key(x)));
         id = comp_idx(x);
       }
@@ -449,11 +475,7 @@ __global__ __launch_bounds__(kCandNT) void binned_cand_kernel(BinArgs a) {
   }
 }
 
-__host__ __device__ inline size_t cand_lds_bytes(int nb) {
-  const int bc = cand_bucket_cap(nb);
-  const int ec = bc < kCandRank ? bc : kCandRank;
-  return (size_t)nb * bc * 8 + (size_t)nb * ec * 8 + (size_t)nb * 4;
-}
+__host__ __device__ inline size_t cand_lds_bytes(int nb) { return (size_t)nb * cand_bin_bytes(cand_bucket_cap(nb)); }
 
 // composite of a list entry: value descending then index ascending; fillers
 // (index -1) after every real entry
@@ -481,6 +503,22 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
   const int t = threadIdx.x, w = t / kWave, l = lane_id();
   const int64_t row = blockIdx.x;
   const int NB = a.num_bins;
+  // this wave's 128-entry runs of all buf ranks are loaded before depth_upper is known
+  constexpr int kPre = 2;  // runs per wave prefetched
+  const int nall = a.buf * NB;
+  const float* lv = a.lv + (size_t)row * a.buf * NB;  // rank-major: entry e = rank * NB + bin
+  const int32_t* li = a.li + (size_t)row * a.buf * NB;
+  float pv[kPre][2];
+  int32_t pi[kPre][2];
+#pragma unroll
+  for (int k = 0; k < kPre; ++k) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int e = (w + k * NW) * 128 + h * kWave + l;
+      pv[k][h] = e < nall ? lv[e] : 0.0f;
+      pi[k][h] = e < nall ? li[e] : -1;
+    }
+  }
   int upper_v;
   if (INLINE) {
     int fc = a.nsteps;
@@ -523,15 +561,18 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
   const int up = upper_v < a.buf ? upper_v : a.buf;
   const int n = up * NB;
   const int nr = (n + 127) / 128;
-  const float* lv = a.lv + (size_t)row * a.buf * NB;  // rank-major: entry e = rank * NB + bin
-  const int32_t* li = a.li + (size_t)row * a.buf * NB;
   uint64_t acc[2] = {0ull, 0ull};
   for (int r = w; r < nr; r += NW) {
     uint64_t c[2];
+    const int k = (r - w) / NW;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int e = r * 128 + h * kWave + l;
-      c[h] = e < n ? entry_comp(lv[e], li[e]) : 0ull;
+      if (k < kPre) {
+        c[h] = e < n ? entry_comp(k == 0 ? pv[0][h] : pv[1][h], k == 0 ? pi[0][h] : pi[1][h]) : 0ull;
+      } else {
+        c[h] = e < n ? entry_comp(lv[e], li[e]) : 0ull;
+      }
     }
     wave_sort128_desc(c);
     if (r == w) {
@@ -541,14 +582,14 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
       wave_merge128_desc(acc, c);
     }
   }
-#pragma unroll
-  for (int st = 1; st < NW; st <<= 1) {
+  const int nwr = nr < NW ? nr : NW;  // waves holding a list
+  for (int st = 1; st < nwr; st <<= 1) {
     if ((w & (2 * st - 1)) == st) {
       tree[w][l] = acc[0];
       tree[w][kWave + l] = acc[1];
     }
     __syncthreads();
-    if ((w & (2 * st - 1)) == 0) {
+    if ((w & (2 * st - 1)) == 0 && w + st < nwr) {
       const uint64_t b[2] = {tree[w + st][l], tree[w + st][kWave + l]};
       wave_merge128_desc(acc, b);
     }
