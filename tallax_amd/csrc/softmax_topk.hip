@@ -18,11 +18,14 @@
 // A row holding NaN or +inf, or only -inf, gives NaN probabilities (as
 // jax.nn.softmax does), indices 0..k-1 and cutoff 0.
 //
-// One 1024-thread workgroup per row, two streaming passes:
-//   pass 1: the row maximum and each thread's four largest values; the k-th
-//           largest of those 4096, T0, has at least k elements >= it;
-//   pass 2: exp-sum, and every element >= T0 appended to LDS (expected
-//           ~k + 4 % for Gaussian rows);
+// One 1024-thread workgroup per row, two workgroups per CU:
+//   pass 1 (one streaming read): the row maximum, the exp-sum (online, per
+//           thread), each thread's four largest values and, per 64-byte
+//           group, the high 16 bits of the group maximum's select key (LDS);
+//           the k-th largest of the 4096 per-thread values, T0, has at least
+//           k elements >= it;
+//   pass 2: only the groups whose maximum can reach T0 are read again, and
+//           their elements >= T0 appended to LDS (~k + 4 % for Gaussian rows);
 // then a workgroup bitonic sort of the candidates, the outputs, the tile
 // scan and the cutoff.  If the candidates overflow (heavy ties), the k-th
 // composite is found by bisection over the row instead.
@@ -40,7 +43,8 @@ namespace tx {
 
 constexpr int kPfNT = 1024;
 constexpr int kPfNW = kPfNT / kWave;
-constexpr int kPfCap = 8192;   // candidate records in LDS
+constexpr int kPfCapMax = 8192;        // candidate records in LDS, at most
+constexpr int kPfLdsBytes = 80 * 1024;  // two row workgroups per CU
 constexpr int kPfMaxK = 4096;
 
 struct PfArgs {
@@ -48,6 +52,8 @@ struct PfArgs {
   int64_t rows, cols;
   int k;
   float p;
+  int cap;      // candidate records in the LDS pool
+  int use_sum;  // 1: pass 1 writes group maxima, pass 2 re-reads only the groups that can hold candidates
   float* out_probs;
   int32_t* out_idx;
   float* out_cum;
@@ -79,7 +85,7 @@ __device__ void pf_sort_desc(uint64_t* pool, int n) {
 // other sorts
 __global__ __launch_bounds__(kPfNT) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void softmax_topk_kernel(PfArgs a) {
-  extern __shared__ __align__(16) uint64_t pool[];  // kPfCap records
+  extern __shared__ __align__(16) uint64_t pool[];  // a.cap records, then the group maxima / probabilities
   __shared__ float redf[kPfNW];
   __shared__ int redi[kPfNW];
   __shared__ uint32_t s_t0;
@@ -93,13 +99,20 @@ void softmax_topk_kernel(PfArgs a) {
   const int64_t nv = (a.cols + rv.mis + 3) / 4;
   const int k = a.k;
 
-  // ---- pass 1: maximum and per-thread top-4 values -------------------------
-  // (v_max_f32 ignores NaN; rows holding NaN or +inf are recognised after pass
-  // 2, where their exp-sum comes out NaN)
-  // interior vectors (all four elements inside the row) skip the bounds tests
+  // ---- pass 1: maximum, exp-sum, per-thread top-4 values, group maxima --------
+  // The exp-sum is kept per thread relative to the thread's running maximum
+  // (rescaled when it rises) and combined at the end.  v_max_f32 ignores NaN;
+  // a NaN or +inf makes the sum NaN, as it makes jax.nn.softmax NaN.
+  // A group is the 64 bytes (4 vectors) read by one quad of lanes; its
+  // maximum, as the high 16 bits of the select key, goes to summ[] so that
+  // pass 2 re-reads only groups that can hold an element >= T0.  The loops
+  // advance a quad at a time, so the quad exchange always sees all four lanes.
   const int64_t v_lo = rv.mis ? 1 : 0;
   const int64_t v_hi = (a.cols + rv.mis) / 4;  // vectors [v_lo, v_hi) are interior
-  float m = -INFINITY;
+  uint16_t* summ = (uint16_t*)(pool + a.cap);  // [ceil(nv / 4)] group maxima, later the probabilities
+  const bool use_sum = a.use_sum != 0;
+  constexpr float kLog2e = 1.44269504088896341f;
+  float m = -INFINITY, s = 0.0f;
   float top[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
   auto live_mask = [&](int64_t v) -> uint32_t {
     if (v >= v_lo && v < v_hi) return 0xFu;
@@ -118,10 +131,22 @@ void softmax_topk_kernel(PfArgs a) {
     for (int i = 0; i < 4; ++i) xs[i] = __uint_as_float(((live >> i) & 1u) ? d[i] : 0x7FC00000u);
   };
   auto pass1_vec = [&](uint4 q, int64_t v) {
+    const uint32_t live = v < nv ? live_mask(v) : 0u;
     float xs[4];
-    vec_vals(q, live_mask(v), xs);
+    vec_vals(q, live, xs);
     const float vm = fmaxf(fmaxf(xs[0], xs[1]), fmaxf(xs[2], xs[3]));
-    m = fmaxf(m, vm);
+    if (vm > m) {
+      s = s * __builtin_amdgcn_exp2f((m - vm) * kLog2e);  // m = -inf: s was 0 (or NaN)
+      m = vm;
+    }
+    const float mc = m * kLog2e;
+    float vs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float e = xs[i] == -INFINITY ? 0.0f : pf_exp(xs[i], mc);
+      vs += ((live >> i) & 1u) ? e : 0.0f;
+    }
+    s += vs;
     if (vm > top[3]) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -137,22 +162,32 @@ void softmax_topk_kernel(PfArgs a) {
         }
       }
     }
+    if (use_sum) {
+      float gm = fmaxf(vm, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(vm), 0xB1, 0xF, 0xF, false)));
+      gm = fmaxf(gm, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(gm), 0x4E, 0xF, 0xF, false)));
+      if ((l & 3) == 0 && v < nv) summ[v >> 2] = (uint16_t)(select_key(__float_as_uint(gm)) >> 16);
+    }
   };
   {
-    constexpr int U = 8;  // loads in flight per thread
-    int64_t v = t;
-    for (; v + (U - 1) * kPfNT < nv; v += U * kPfNT) {
+    constexpr int U = 6;  // loads in flight per thread
+    const int64_t vq = (int64_t)t - (l & 3);  // the quad's first vector
+    int64_t i = 0;
+    for (; vq + i + (int64_t)(U - 1) * kPfNT + 3 < nv; i += (int64_t)U * kPfNT) {
       uint4 q[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) q[u] = rv.base[v + u * kPfNT];
+      for (int u = 0; u < U; ++u) q[u] = rv.base[t + i + u * kPfNT];
 #pragma unroll
-      for (int u = 0; u < U; ++u) pass1_vec(q[u], v + u * kPfNT);
+      for (int u = 0; u < U; ++u) pass1_vec(q[u], t + i + u * kPfNT);
     }
-    for (; v < nv; v += kPfNT) pass1_vec(rv.base[v], v);
+    for (; vq + i < nv; i += kPfNT) {
+      const int64_t v = t + i;
+      pass1_vec(v < nv ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u), v);
+    }
   }
+  float M = m;
 #pragma unroll
-  for (int d = kWave / 2; d >= 1; d >>= 1) m = fmaxf(m, lane_xor_f(m, d));
-  if (l == 0) redf[w] = m;
+  for (int d = kWave / 2; d >= 1; d >>= 1) M = fmaxf(M, lane_xor_f(M, d));
+  if (l == 0) redf[w] = M;
   // threshold: the k-th largest of the 4096 per-thread values (as select keys)
   uint32_t tk[4];
 #pragma unroll
@@ -162,27 +197,21 @@ void softmax_topk_kernel(PfArgs a) {
   if (t == (k - 1) / 4) s_t0 = tk[(k - 1) % 4];
   if (t == 0) s_cnt = 0;
   __syncthreads();
-  m = redf[0];
-  for (int i = 1; i < kPfNW; ++i) m = fmaxf(m, redf[i]);
+  M = redf[0];
+  for (int i = 1; i < kPfNW; ++i) M = fmaxf(M, redf[i]);
+  const float mc = M * kLog2e;
+  // the exp-sum: thread sums rescaled to the row maximum (a thread that saw
+  // only -inf / dead slots contributes 0, or its NaN)
+  s = m == -INFINITY ? s : s * __builtin_amdgcn_exp2f((m - M) * kLog2e);
   // candidates: x >= T0 as floats (NaN never passes)
   const float t0f = s_t0 >= 0x007FFFFFu ? __uint_as_float(key_to_bits(s_t0)) : -INFINITY;
+  const uint16_t q0 = (uint16_t)(s_t0 >> 16);
 
-  // ---- pass 2: exp-sum and candidates -----------------------------------------
-  float s = 0.0f;
-  const float mc = m * 1.44269504088896341f;
-  const bool fin = m != -INFINITY;  // else the live elements are all -inf or NaN
+  // ---- pass 2: candidates ---------------------------------------------------------
   auto pass2_vec = [&](uint4 q, int64_t v) {
     const uint32_t live = live_mask(v);
     float xs[4];
     vec_vals(q, live, xs);
-    float vs = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      // a real NaN / +inf makes the sum NaN, as in jax.nn.softmax
-      const float e = fin ? pf_exp(xs[i], mc) : (xs[i] != xs[i] ? xs[i] : __builtin_nanf(""));
-      vs += ((live >> i) & 1u) ? e : 0.0f;
-    }
-    s += vs;
     const float vm = fmaxf(fmaxf(xs[0], xs[1]), fmaxf(xs[2], xs[3]));
     uint32_t mask = 0;
     if (vm >= t0f) {
@@ -210,13 +239,40 @@ void softmax_topk_kernel(PfArgs a) {
         if (hc) {
           const int off = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bm >> 32),
                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)bm, 0u));
-          if (off < kPfCap) pool[off] = c;
+          if (off < a.cap) pool[off] = c;
         }
       }
     }
   };
   __syncthreads();  // the key sort above used the pool
-  {
+  if (use_sum) {
+    // this thread's own vectors t + u * kPfNT (u < 64) in groups that can hold
+    // a candidate, re-read in batches of U
+    uint64_t todo = 0;
+    for (int u = 0; (int64_t)t + (int64_t)u * kPfNT < nv; ++u)
+      todo |= (summ[((int64_t)t + (int64_t)u * kPfNT) >> 2] >= q0 ? 1ull : 0ull) << u;
+    constexpr int U = 4;
+    while (__ballot(todo != 0ull)) {
+      uint4 q[U];
+      int32_t vv[U];  // nv < 2^31
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        vv[j] = -1;
+        if (todo) {
+          const int u = __builtin_ctzll(todo);
+          todo &= todo - 1ull;
+          vv[j] = t + u * kPfNT;
+          q[j] = rv.base[vv[j]];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        if (__ballot(vv[j] >= 0))
+          pass2_vec(vv[j] >= 0 ? q[j] : make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u),
+                    vv[j] >= 0 ? vv[j] : 0);
+      }
+    }
+  } else {
     constexpr int U = 8;
     int64_t v = t;
     for (; v + (U - 1) * kPfNT < nv; v += U * kPfNT) {
@@ -235,12 +291,12 @@ void softmax_topk_kernel(PfArgs a) {
   s = 0.0f;
   for (int i = 0; i < kPfNW; ++i) s += redf[i];
   const int n = s_cnt;
-  // NaN or +inf in the row, or a row of -inf only, makes the sum NaN, as it
-  // makes jax.nn.softmax NaN
-  const bool row_bad = s != s;
+  // NaN or +inf in the row, or a row of -inf only, makes the probabilities NaN,
+  // as it makes jax.nn.softmax NaN
+  const bool row_bad = s != s || M == -INFINITY;
 
   // ---- the k largest composites, sorted ---------------------------------------
-  if (n <= kPfCap) {
+  if (n <= a.cap) {
     if (n <= kPfNT) pf_sort_desc<1>(pool, n);
     else if (n <= 2 * kPfNT) pf_sort_desc<2>(pool, n);
     else if (n <= 4 * kPfNT) pf_sort_desc<4>(pool, n);
@@ -278,7 +334,7 @@ void softmax_topk_kernel(PfArgs a) {
         const int64_t e = v * 4 - rv.mis + i;
         if (e >= 0 && e < a.cols) {
           const uint64_t c = make_comp(select_key(d[i]), (uint32_t)e);
-          if (c >= prefix) pool[atomicAdd(&s_cnt, 1)] = c;  // exactly k <= kPfCap of them
+          if (c >= prefix) pool[atomicAdd(&s_cnt, 1)] = c;  // exactly k <= a.cap of them
         }
       }
     }
@@ -287,7 +343,7 @@ void softmax_topk_kernel(PfArgs a) {
   }
 
   // ---- probabilities, indices, cumsum, cutoff -----------------------------------
-  float* probs = (float*)(pool + kPfMaxK);  // k floats after the first k records
+  float* probs = (float*)summ;  // k floats (the group maxima are no longer needed)
   for (int p = t; p < k; p += kPfNT) {
     const uint64_t c = pool[p];
     int32_t idx = comp_idx(c);
@@ -364,9 +420,25 @@ int tallax_softmax_topk_cumsum(const float* logits, int64_t rows, int64_t cols, 
   PfArgs a = {};
   a.x = logits; a.rows = rows; a.cols = cols; a.k = k; a.p = p;
   a.out_probs = out_probs; a.out_idx = out_idx; a.out_cum = out_cumsum; a.out_cutoff = out_cutoff;
-  const size_t lds = (size_t)kPfCap * 8;
+  // LDS: the candidate pool, then the group maxima of pass 1 (reused for the k
+  // probabilities).  The group maxima need nv / 4 halfwords and one vector per
+  // bit of a 64-bit mask per thread; longer rows re-read everything in pass 2.
+  const int64_t nv_max = (cols + 6) / 4;
+  const int64_t ngroups = (nv_max + 3) / 4;
+  bool use_sum = nv_max <= 64 * (int64_t)kPfNT && ngroups * 2 <= 48 * 1024;
+  size_t region2 = align_up(use_sum ? (size_t)(ngroups * 2 > k * 4 ? ngroups * 2 : k * 4) : (size_t)k * 4, 16);
+  int cap = (int)((kPfLdsBytes - region2) / 8) / 1024 * 1024;
+  if (cap > kPfCapMax) cap = kPfCapMax;
+  if (use_sum && cap < 4096) {
+    use_sum = false;
+    region2 = align_up((size_t)k * 4, 16);
+    cap = kPfCapMax;
+  }
+  a.cap = cap;
+  a.use_sum = use_sum ? 1 : 0;
+  const size_t lds = (size_t)cap * 8 + region2;
   static const hipError_t attr = hipFuncSetAttribute((const void*)softmax_topk_kernel,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, kPfLdsBytes);
   if (attr != hipSuccess) { set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr)); return kHipError; }
   hipLaunchKernelGGL(softmax_topk_kernel, dim3((unsigned)rows), dim3(kPfNT), lds, stream, a);
   return launch_status("tallax_softmax_topk_cumsum");

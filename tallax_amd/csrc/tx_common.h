@@ -149,9 +149,11 @@ struct RowVec {
   const uint4* base;  // aligned-down start
   int mis;            // number of leading elements of the first block outside the row
   __device__ __forceinline__ RowVec(const void* row_ptr) {
-    const uintptr_t a = (uintptr_t)row_ptr;
-    base = (const uint4*)(a - (a & 15u));
-    mis = (int)((a & 15u) / ES);
+    const uint32_t off = (uint32_t)(uintptr_t)row_ptr & 15u;
+    // pointer arithmetic (not an integer round trip) keeps the pointer's
+    // provenance, so loads through it compile to global_load, not flat_load
+    base = (const uint4*)((const char*)row_ptr - off);
+    mis = (int)(off / ES);
   }
 };
 
