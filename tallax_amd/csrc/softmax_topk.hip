@@ -20,18 +20,26 @@
 //
 // One 1024-thread workgroup per row, two workgroups per CU:
 //   pass 1 (one streaming read): the row maximum, the exp-sum (online, per
-//           thread), each thread's four largest values and, per 64-byte
-//           group, the high 16 bits of the group maximum's select key (LDS);
-//           the k-th largest of the 4096 per-thread values, T0, has at least
-//           k elements >= it;
-//   pass 2: only the groups whose maximum can reach T0 are read again, and
-//           their elements >= T0 appended to LDS (~k + 4 % for Gaussian rows);
+//           thread) and, per 64-byte group of the row, the high 16 bits of
+//           the group maximum's select key, kept in LDS with a 256-bin
+//           histogram of their top byte;
+//   threshold: the k-th largest group prefix q0 (the histogram, then one of
+//           the low byte inside the crossing bin).  At least k groups reach
+//           q0, so at least k elements have a key >= q0 << 16: that is T0;
+//   pass 2: the groups that reach q0 (~k of them for Gaussian rows) are
+//           listed, spread evenly over the workgroup and read again; their
+//           elements >= T0 are appended to LDS;
 // then a workgroup bitonic sort of the candidates, the outputs, the tile
-// scan and the cutoff.  If the candidates overflow (heavy ties), the k-th
-// composite is found by bisection over the row instead.
+// scan and the cutoff.  Rows too long for the group summary (over 24 Ki
+// groups) keep each thread's four largest values in pass 1 instead, take T0
+// as the k-th largest of those 4096 and read the whole row again.  If the
+// candidates overflow (heavy ties), the k-th composite is found by bisection
+// over the row instead.
 #include <float.h>
 #include <math.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "tallax_hip.h"
 #include "tx_block_sort.h"
@@ -43,17 +51,20 @@ namespace tx {
 
 constexpr int kPfNT = 1024;
 constexpr int kPfNW = kPfNT / kWave;
-constexpr int kPfCapMax = 8192;        // candidate records in LDS, at most
-constexpr int kPfLdsBytes = 80 * 1024;  // two row workgroups per CU
+constexpr int kPfCapMax = 8192;          // candidate records in LDS, at most
+constexpr int kPfDynBytes = 76 * 1024;   // dynamic LDS: two row workgroups (with their static LDS) per CU
 constexpr int kPfMaxK = 4096;
+constexpr int kPfMaxGroups = 24 * 1024;  // 16-bit group maxima in LDS, 24 per thread at most
+constexpr int kPfBuckets = 512;          // key buckets of the candidate rank sort
+constexpr int kPfRankMax = 128;          // largest bucket the rank sort takes (else bitonic)
 
 struct PfArgs {
   const float* x;
   int64_t rows, cols;
   int k;
   float p;
-  int cap;      // candidate records in the LDS pool
-  int use_sum;  // 1: pass 1 writes group maxima, pass 2 re-reads only the groups that can hold candidates
+  int cap;   // candidate records in the LDS pool
+  int cap2;  // records that fit the region after the pool
   float* out_probs;
   int32_t* out_idx;
   float* out_cum;
@@ -81,15 +92,45 @@ __device__ void pf_sort_desc(uint64_t* pool, int n) {
   __syncthreads();
 }
 
+// For 256 counters h[] in LDS, the largest bin b whose suffix count
+// sum(h[b..255]) is >= need (-1 if none); *above = sum(h[b+1..255]).  One
+// whole wave calls it.
+__device__ __forceinline__ int pf_crossing_bin(const uint32_t* h, uint32_t need, uint32_t* above) {
+  const int l = lane_id();
+  const uint4 hv = ((const uint4*)h)[l];  // bins 4l .. 4l + 3
+  const uint32_t hs[4] = {hv.x, hv.y, hv.z, hv.w};
+  uint32_t incl = hv.x + hv.y + hv.z + hv.w;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+  uint32_t suf = (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1) - incl;  // bins of higher lanes
+  int cnt = 0;
+#pragma unroll
+  for (int j = 3; j >= 0; --j) {
+    suf += hs[j];
+    cnt += suf >= need ? 1 : 0;
+  }
+  const int b = wave_sum_i(cnt) - 1;  // suffix counts fall with b: the bins that reach need are 0..b
+  uint32_t ab = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ab += 4 * l + j > b ? hs[j] : 0u;
+  *above = (uint32_t)wave_sum_i((int)ab);
+  return b;
+}
+
 // 8 waves per SIMD: two row workgroups share a CU, so one streams while the
-// other sorts
+// other sorts.  SUMM: group summary and histogram threshold (rows of at most
+// kPfMaxGroups groups); otherwise per-thread top-4 and a full second read.
+template <bool SUMM>
 __global__ __launch_bounds__(kPfNT) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void softmax_topk_kernel(PfArgs a) {
-  extern __shared__ __align__(16) uint64_t pool[];  // a.cap records, then the group maxima / probabilities
+  extern __shared__ __align__(16) uint64_t pool[];  // a.cap records, then the group maxima / list / probabilities
+  __shared__ __align__(16) uint32_t hist_all[kPfBuckets];  // the two threshold histograms, later the sort buckets
+  uint32_t* hist = hist_all;
+  uint32_t* hist2 = hist_all + 256;
   __shared__ float redf[kPfNW];
   __shared__ int redi[kPfNW];
-  __shared__ uint32_t s_t0;
-  __shared__ int s_cnt;
+  __shared__ uint32_t s_t0, s_above;
+  __shared__ int s_cnt, s_bin;
   __shared__ float s_cum_carry[kPfMaxK / 128];
   __shared__ float s_tile_sum[kPfMaxK / 128];
   const int t = threadIdx.x, w = t / kWave, l = lane_id();
@@ -98,22 +139,37 @@ void softmax_topk_kernel(PfArgs a) {
   const RowVec<4> rv(xr);
   const int64_t nv = (a.cols + rv.mis + 3) / 4;
   const int k = a.k;
-
-  // ---- pass 1: maximum, exp-sum, per-thread top-4 values, group maxima --------
-  // The exp-sum is kept per thread relative to the thread's running maximum
-  // (rescaled when it rises) and combined at the end.  v_max_f32 ignores NaN;
-  // a NaN or +inf makes the sum NaN, as it makes jax.nn.softmax NaN.
-  // A group is the 64 bytes (4 vectors) read by one quad of lanes; its
-  // maximum, as the high 16 bits of the select key, goes to summ[] so that
-  // pass 2 re-reads only groups that can hold an element >= T0.  The loops
-  // advance a quad at a time, so the quad exchange always sees all four lanes.
   const int64_t v_lo = rv.mis ? 1 : 0;
-  const int64_t v_hi = (a.cols + rv.mis) / 4;  // vectors [v_lo, v_hi) are interior
-  uint16_t* summ = (uint16_t*)(pool + a.cap);  // [ceil(nv / 4)] group maxima, later the probabilities
-  const bool use_sum = a.use_sum != 0;
+  const int64_t v_hi = (a.cols + rv.mis) / 4;  // vectors [v_lo, v_hi) lie wholly inside the row
+  const int ngroups = (int)((nv + 3) / 4);     // group g = vectors 4g .. 4g + 3 (SUMM: <= kPfMaxGroups)
+  uint16_t* summ = (uint16_t*)(pool + a.cap);
   constexpr float kLog2e = 1.44269504088896341f;
-  float m = -INFINITY, s = 0.0f;
+  if (SUMM) {
+    if (t < 256) {
+      hist[t] = 0u;
+      hist2[t] = 0u;
+    }
+    __syncthreads();
+  }
+
+  // ---- pass 1: maximum, exp-sum, group maxima (or per-thread top-4) ------------
+  // The exp-sum is kept per thread as s = sum 2^(x log2 e - mc) for the
+  // thread's running maximum m, mc = fl(m log2 e) (0 while m is -inf, so that
+  // -inf elements add exactly 0).  When m rises, s is rescaled by 2^(mc_old -
+  // mc_new), and at the end by 2^(mc - fl(M log2 e)): the rounding of each mc
+  // cancels, so the sum matches the numerators 2^(x log2 e - fl(M log2 e)) of
+  // the probabilities even where |M log2 e| is large.  v_max_f32 ignores NaN;
+  // a NaN or +inf makes the sum NaN, as it makes jax.nn.softmax NaN.
+  float m = -INFINITY, s = 0.0f, mc = 0.0f;
   float top[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  auto raise_max = [&](float vm) {
+    if (vm > m) {
+      const float mcn = vm * kLog2e;
+      s = m == -INFINITY ? s : s * __builtin_amdgcn_exp2f(mc - mcn);  // m = -inf: s is 0 (or NaN)
+      m = vm;
+      mc = mcn;
+    }
+  };
   auto live_mask = [&](int64_t v) -> uint32_t {
     if (v >= v_lo && v < v_hi) return 0xFu;
     uint32_t live = 0;
@@ -124,29 +180,24 @@ void softmax_topk_kernel(PfArgs a) {
     }
     return live;
   };
-  // the four values of a vector, dead slots as NaN (ignored by max and by >)
+  // the four values of a vector, dead slots as NaN (ignored by max and by >=)
   auto vec_vals = [&](uint4 q, uint32_t live, float xs[4]) {
     const uint32_t d[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) xs[i] = __uint_as_float(((live >> i) & 1u) ? d[i] : 0x7FC00000u);
   };
-  auto pass1_vec = [&](uint4 q, int64_t v) {
-    const uint32_t live = v < nv ? live_mask(v) : 0u;
-    float xs[4];
-    vec_vals(q, live, xs);
-    const float vm = fmaxf(fmaxf(xs[0], xs[1]), fmaxf(xs[2], xs[3]));
-    if (vm > m) {
-      s = s * __builtin_amdgcn_exp2f((m - vm) * kLog2e);  // m = -inf: s was 0 (or NaN)
-      m = vm;
-    }
-    const float mc = m * kLog2e;
-    float vs = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float e = xs[i] == -INFINITY ? 0.0f : pf_exp(xs[i], mc);
-      vs += ((live >> i) & 1u) ? e : 0.0f;
-    }
-    s += vs;
+  // maximum over a quad of lanes (the four vectors of a group); all four lanes call it together
+  auto group_max = [&](float vm) {
+    float gm = fmaxf(vm, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(vm), 0xB1, 0xF, 0xF, false)));
+    return fmaxf(gm, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(gm), 0x4E, 0xF, 0xF, false)));
+  };
+  // lane 0 of a quad, v its vector: the group's 16-bit prefix and its histogram count
+  auto put_group = [&](float gm, int64_t v) {
+    const uint32_t q16 = select_key(__float_as_uint(gm)) >> 16;
+    summ[v >> 2] = (uint16_t)q16;
+    atomicAdd(&hist[q16 >> 8], 1u);
+  };
+  auto top4 = [&](const float xs[4], float vm) {
     if (vm > top[3]) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -162,50 +213,135 @@ void softmax_topk_kernel(PfArgs a) {
         }
       }
     }
-    if (use_sum) {
-      float gm = fmaxf(vm, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(vm), 0xB1, 0xF, 0xF, false)));
-      gm = fmaxf(gm, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(gm), 0x4E, 0xF, 0xF, false)));
-      if ((l & 3) == 0 && v < nv) summ[v >> 2] = (uint16_t)(select_key(__float_as_uint(gm)) >> 16);
+  };
+  // any vector (row edges, tail); every thread of the workgroup calls it together
+  auto step1 = [&](int64_t v) {
+    const uint32_t live = v < nv ? live_mask(v) : 0u;
+    const uint4 q = v < nv ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u);
+    float xs[4];
+    vec_vals(q, live, xs);
+    const float vm = fmaxf(fmaxf(xs[0], xs[1]), fmaxf(xs[2], xs[3]));
+    raise_max(vm);
+    float vs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float e = pf_exp(xs[i], mc);
+      vs += ((live >> i) & 1u) ? e : 0.0f;
+    }
+    s += vs;
+    if constexpr (SUMM) {
+      const float gm = group_max(vm);
+      if ((l & 3) == 0 && v < nv) put_group(gm, v);
+    } else {
+      top4(xs, vm);
+    }
+  };
+  // vectors i0 + t + u * kPfNT (u < U), all wholly inside the row
+  auto batch1 = [&](int64_t i0, auto u_const) {
+    constexpr int U = decltype(u_const)::value;
+    uint4 q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) q[u] = rv.base[i0 + t + u * kPfNT];
+    float vm[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      vm[u] = fmaxf(fmaxf(__uint_as_float(q[u].x), __uint_as_float(q[u].y)),
+                    fmaxf(__uint_as_float(q[u].z), __uint_as_float(q[u].w)));
+    float bm = vm[0];
+#pragma unroll
+    for (int u = 1; u < U; ++u) bm = fmaxf(bm, vm[u]);
+    raise_max(bm);
+    float vs[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].x), mc);
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].y), mc);
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].z), mc);
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].w), mc);
+    }
+    s += vs[0] + vs[1];
+    if constexpr (SUMM) {
+      float gm[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) gm[u] = group_max(vm[u]);
+      if ((l & 3) == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) put_group(gm[u], i0 + t + u * kPfNT);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float xs[4] = {__uint_as_float(q[u].x), __uint_as_float(q[u].y), __uint_as_float(q[u].z),
+                             __uint_as_float(q[u].w)};
+        top4(xs, vm[u]);
+      }
     }
   };
   {
-    constexpr int U = 6;  // loads in flight per thread
-    const int64_t vq = (int64_t)t - (l & 3);  // the quad's first vector
+    // the loops are uniform over the workgroup, so quads always see all four lanes
     int64_t i = 0;
-    for (; vq + i + (int64_t)(U - 1) * kPfNT + 3 < nv; i += (int64_t)U * kPfNT) {
-      uint4 q[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) q[u] = rv.base[t + i + u * kPfNT];
-#pragma unroll
-      for (int u = 0; u < U; ++u) pass1_vec(q[u], t + i + u * kPfNT);
+    if (rv.mis) {  // the first vector holds elements before the row
+      step1(t);
+      i = kPfNT;
     }
-    for (; vq + i < nv; i += kPfNT) {
-      const int64_t v = t + i;
-      pass1_vec(v < nv ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u), v);
-    }
+    for (; i + 6 * kPfNT <= v_hi; i += 6 * kPfNT) batch1(i, std::integral_constant<int, 6>());
+    for (; i + kPfNT <= v_hi; i += kPfNT) batch1(i, std::integral_constant<int, 1>());
+    for (; i < nv; i += kPfNT) step1(i + t);
   }
   float M = m;
 #pragma unroll
   for (int d = kWave / 2; d >= 1; d >>= 1) M = fmaxf(M, lane_xor_f(M, d));
   if (l == 0) redf[w] = M;
-  // threshold: the k-th largest of the 4096 per-thread values (as select keys)
-  uint32_t tk[4];
+  if constexpr (!SUMM) {
+    // threshold: the k-th largest of the 4096 per-thread values (as select keys)
+    uint32_t tk[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) tk[r] = select_key(__float_as_uint(top[r]));
-  uint32_t* keys = (uint32_t*)pool;
-  block_bitonic_sort_c<uint32_t, 4, kPfNT * 4, true>(tk, keys);
-  if (t == (k - 1) / 4) s_t0 = tk[(k - 1) % 4];
+    for (int r = 0; r < 4; ++r) tk[r] = select_key(__float_as_uint(top[r]));
+    uint32_t* keys = (uint32_t*)pool;
+    block_bitonic_sort_c<uint32_t, 4, kPfNT * 4, true>(tk, keys);
+    if (t == (k - 1) / 4) s_t0 = tk[(k - 1) % 4];
+  }
   if (t == 0) s_cnt = 0;
   __syncthreads();
-  M = redf[0];
-  for (int i = 1; i < kPfNW; ++i) M = fmaxf(M, redf[i]);
-  const float mc = M * kLog2e;
+  M = l < kPfNW ? redf[l] : -INFINITY;
+#pragma unroll
+  for (int d = kPfNW / 2; d >= 1; d >>= 1) M = fmaxf(M, lane_xor_f(M, d));
+  M = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(M)));
+  const float mcM = M * kLog2e;
   // the exp-sum: thread sums rescaled to the row maximum (a thread that saw
   // only -inf / dead slots contributes 0, or its NaN)
-  s = m == -INFINITY ? s : s * __builtin_amdgcn_exp2f((m - M) * kLog2e);
-  // candidates: x >= T0 as floats (NaN never passes)
+  s = m == -INFINITY ? s : s * __builtin_amdgcn_exp2f(mc - mcM);
+
+  if constexpr (SUMM) {
+    // the k-th largest group prefix: top byte from the histogram, low byte
+    // from a histogram of the groups in the crossing bin
+    if (w == 0) {
+      uint32_t above;
+      const int b = pf_crossing_bin(hist, (uint32_t)k, &above);
+      if (l == 0) {
+        s_bin = b;
+        s_above = above;
+        s_t0 = 0u;  // fewer than k groups: every element is a candidate
+      }
+    }
+    __syncthreads();
+    const int b = s_bin;
+    if (b >= 0) {
+      for (int g = t; g < ngroups; g += kPfNT) {
+        const uint32_t q = summ[g];
+        if ((q >> 8) == (uint32_t)b) atomicAdd(&hist2[q & 255u], 1u);
+      }
+      __syncthreads();
+      if (w == 0) {
+        uint32_t above2;
+        const int b2 = pf_crossing_bin(hist2, (uint32_t)k - s_above, &above2);  // >= 0: hist[b] >= k - above
+        if (l == 0) s_t0 = (((uint32_t)b << 8) | (uint32_t)b2) << 16;
+      }
+      __syncthreads();
+    }
+  }
+  // candidates: key >= T0, i.e. x >= t0f as floats (NaN never passes)
   const float t0f = s_t0 >= 0x007FFFFFu ? __uint_as_float(key_to_bits(s_t0)) : -INFINITY;
-  const uint16_t q0 = (uint16_t)(s_t0 >> 16);
 
   // ---- pass 2: candidates ---------------------------------------------------------
   auto pass2_vec = [&](uint4 q, int64_t v) {
@@ -244,32 +380,75 @@ void softmax_topk_kernel(PfArgs a) {
       }
     }
   };
-  __syncthreads();  // the key sort above used the pool
-  if (use_sum) {
-    // this thread's own vectors t + u * kPfNT (u < 64) in groups that can hold
-    // a candidate, re-read in batches of U
-    uint64_t todo = 0;
-    for (int u = 0; (int64_t)t + (int64_t)u * kPfNT < nv; ++u)
-      todo |= (summ[((int64_t)t + (int64_t)u * kPfNT) >> 2] >= q0 ? 1ull : 0ull) << u;
-    constexpr int U = 4;
-    while (__ballot(todo != 0ull)) {
+  if constexpr (SUMM) {
+    // list the groups that reach q0 (in place of the summary: every thread
+    // reads its groups before the barrier of the scan, then writes)
+    const uint32_t q0 = s_t0 >> 16;
+    uint32_t mine = 0;  // bit j: group t + j * kPfNT
+    for (int g = t, j = 0; g < ngroups; g += kPfNT, ++j) mine |= (summ[g] >= q0 ? 1u : 0u) << j;
+    const int c = __popc(mine);
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+    if (l == kWave - 1) redi[w] = incl;
+    __syncthreads();
+    int off = incl - c, nlist = 0;
+    for (int i = 0; i < kPfNW; ++i) {
+      const int r = redi[i];
+      off += i < w ? r : 0;
+      nlist += r;
+    }
+    uint16_t* list = summ;
+    while (mine) {
+      const int j = __builtin_ctz(mine);
+      mine &= mine - 1u;
+      list[off++] = (uint16_t)(t + j * kPfNT);
+    }
+    __syncthreads();
+    // quad q reads list entries q, q + 256, ...: lane j of the quad vector j
+    // of the group.  Per batch, each lane's candidates get consecutive pool
+    // slots from a wave prefix sum and one atomic per wave.
+    constexpr int U = 6;
+    constexpr int kQuads = kPfNT / 4;
+    const int quad = t >> 2, ql = t & 3;
+    for (int e0 = 0; e0 < nlist; e0 += U * kQuads) {
       uint4 q[U];
       int32_t vv[U];  // nv < 2^31
 #pragma unroll
       for (int j = 0; j < U; ++j) {
-        vv[j] = -1;
-        if (todo) {
-          const int u = __builtin_ctzll(todo);
-          todo &= todo - 1ull;
-          vv[j] = t + u * kPfNT;
-          q[j] = rv.base[vv[j]];
-        }
+        const int e = e0 + quad + j * kQuads;
+        vv[j] = e < nlist ? (int32_t)list[e] * 4 + ql : -1;
+        if (vv[j] >= nv) vv[j] = -1;  // past the last vector of a partial group
+        q[j] = vv[j] >= 0 ? rv.base[vv[j]] : make_uint4(0u, 0u, 0u, 0u);
       }
+      uint32_t cm = 0;  // bit 4 j + i: element i of vector j is a candidate
 #pragma unroll
       for (int j = 0; j < U; ++j) {
-        if (__ballot(vv[j] >= 0))
-          pass2_vec(vv[j] >= 0 ? q[j] : make_uint4(0x7FC00000u, 0x7FC00000u, 0x7FC00000u, 0x7FC00000u),
-                    vv[j] >= 0 ? vv[j] : 0);
+        const uint32_t live = vv[j] >= 0 ? live_mask(vv[j]) : 0u;
+        const uint32_t d[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cm |= (((live >> i) & 1u) && __uint_as_float(d[i]) >= t0f ? 1u : 0u) << (4 * j + i);
+      }
+      const int c = __popc(cm);
+      int incl = c;
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+      const int wtot = __builtin_amdgcn_readlane(incl, kWave - 1);
+      if (wtot) {
+        int base = 0;
+        if (l == 0) base = atomicAdd(&s_cnt, wtot);
+        int off = __builtin_amdgcn_readfirstlane(base) + incl - c;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+          const uint32_t d[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if ((cm >> (4 * j + i)) & 1u) {
+              if (off < a.cap) pool[off] = make_comp(select_key(d[i]), (uint32_t)(vv[j] * 4 - rv.mis + i));
+              ++off;
+            }
+          }
+        }
       }
     }
   } else {
@@ -296,7 +475,68 @@ void softmax_topk_kernel(PfArgs a) {
   const bool row_bad = s != s || M == -INFINITY;
 
   // ---- the k largest composites, sorted ---------------------------------------
-  if (n <= a.cap) {
+  // Candidates have keys in [lo, hi] (hi: the row maximum's).  Bucket b
+  // holds keys with (hi-side first) offset ((key - lo) >> shift) = 511 - b,
+  // so buckets run in descending key order; each candidate's place is its
+  // bucket's start plus the number of larger composites in its bucket.
+  // Buckets larger than kPfRankMax (ties, near-ties) use the bitonic sort.
+  bool ranked = false;
+  if (n <= a.cap && n <= a.cap2) {
+    const uint32_t lo = s_t0 >= 0x007FFFFFu ? s_t0 : 0x007FFFFFu;
+    const uint32_t hi = select_key(__float_as_uint(M));
+    const uint32_t range = hi > lo ? hi - lo : 0u;
+    const int shift = range >= (uint32_t)kPfBuckets ? 32 - __clz((int)(range / kPfBuckets)) : 0;  // range >> shift < kPfBuckets
+    auto bucket = [&](uint64_t c) -> int {
+      const uint32_t key = comp_key(c);
+      const uint32_t o = key > lo ? (key - lo) >> shift : 0u;
+      return kPfBuckets - 1 - (int)(o < (uint32_t)kPfBuckets ? o : (uint32_t)(kPfBuckets - 1));
+    };
+    uint32_t* bk = hist_all;
+    if (t < kPfBuckets) bk[t] = 0u;
+    __syncthreads();
+    for (int i = t; i < n; i += kPfNT) atomicAdd(&bk[bucket(pool[i])], 1u);
+    __syncthreads();
+    // exclusive scan of the bucket counts, and the largest count
+    const int c = t < kPfBuckets ? (int)bk[t] : 0;
+    int incl = c, mx = c;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+#pragma unroll
+    for (int d = kWave / 2; d >= 1; d >>= 1) mx = max(mx, (int)lane_xor((uint32_t)mx, d));
+    if (l == kWave - 1) {
+      redi[w] = incl;
+      redf[w] = __int_as_float(mx);
+    }
+    __syncthreads();
+    int off = incl - c, mxall = 0;
+    for (int i = 0; i < kPfNW; ++i) {
+      off += i < w ? redi[i] : 0;
+      mxall = max(mxall, __float_as_int(redf[i]));
+    }
+    if (t < kPfBuckets) bk[t] = (uint32_t)off;
+    __syncthreads();
+    if (mxall <= kPfRankMax) {
+      ranked = true;
+      uint64_t* pool2 = (uint64_t*)summ;  // n <= a.cap2 records
+      for (int i = t; i < n; i += kPfNT) {
+        const uint64_t cc = pool[i];
+        pool2[atomicAdd(&bk[bucket(cc)], 1u)] = cc;
+      }
+      __syncthreads();  // bk[b] is now the end of bucket b
+      for (int i = t; i < n; i += kPfNT) {
+        const uint64_t cc = pool2[i];
+        const int b = bucket(cc);
+        const int s0 = b ? (int)bk[b - 1] : 0, e0 = (int)bk[b];
+        if (s0 >= k) continue;
+        int r = s0;
+        for (int j = s0; j < e0; ++j) r += pool2[j] > cc ? 1 : 0;
+        if (r < k) pool[r] = cc;
+      }
+      __syncthreads();
+    }
+  }
+  if (ranked) {
+  } else if (n <= a.cap) {
     if (n <= kPfNT) pf_sort_desc<1>(pool, n);
     else if (n <= 2 * kPfNT) pf_sort_desc<2>(pool, n);
     else if (n <= 4 * kPfNT) pf_sort_desc<4>(pool, n);
@@ -347,7 +587,7 @@ void softmax_topk_kernel(PfArgs a) {
   for (int p = t; p < k; p += kPfNT) {
     const uint64_t c = pool[p];
     int32_t idx = comp_idx(c);
-    float pr = pf_exp(__uint_as_float(key_to_bits(comp_key(c))), mc) / s;
+    float pr = pf_exp(__uint_as_float(key_to_bits(comp_key(c))), mcM) / s;
     if (row_bad) {
       idx = p;
       pr = NAN;
@@ -420,27 +660,31 @@ int tallax_softmax_topk_cumsum(const float* logits, int64_t rows, int64_t cols, 
   PfArgs a = {};
   a.x = logits; a.rows = rows; a.cols = cols; a.k = k; a.p = p;
   a.out_probs = out_probs; a.out_idx = out_idx; a.out_cum = out_cumsum; a.out_cutoff = out_cutoff;
-  // LDS: the candidate pool, then the group maxima of pass 1 (reused for the k
-  // probabilities).  The group maxima need nv / 4 halfwords and one vector per
-  // bit of a 64-bit mask per thread; longer rows re-read everything in pass 2.
-  const int64_t nv_max = (cols + 6) / 4;
+  // LDS: the candidate pool, then the group maxima of pass 1 (in place of
+  // which pass 2 lists the groups it reads; later the k probabilities).  The
+  // pool holds at least 3 Ki records, and the sorts' working set (up to 8 Ki
+  // records, 64 KiB) always fits the whole region.
+  const int64_t nv_max = (cols + 6) / 4;  // vectors of a row at any alignment
   const int64_t ngroups = (nv_max + 3) / 4;
-  bool use_sum = nv_max <= 64 * (int64_t)kPfNT && ngroups * 2 <= 48 * 1024;
-  size_t region2 = align_up(use_sum ? (size_t)(ngroups * 2 > k * 4 ? ngroups * 2 : k * 4) : (size_t)k * 4, 16);
-  int cap = (int)((kPfLdsBytes - region2) / 8) / 1024 * 1024;
+  const bool summ = ngroups <= kPfMaxGroups;
+  const size_t region2 = align_up(summ && ngroups * 2 > (int64_t)k * 4 ? (size_t)ngroups * 2 : (size_t)k * 4, 16);
+  int cap = (int)((kPfDynBytes - region2) / 8) / 1024 * 1024;
   if (cap > kPfCapMax) cap = kPfCapMax;
-  if (use_sum && cap < 4096) {
-    use_sum = false;
-    region2 = align_up((size_t)k * 4, 16);
-    cap = kPfCapMax;
-  }
   a.cap = cap;
-  a.use_sum = use_sum ? 1 : 0;
+  a.cap2 = (int)(region2 / 8);
   const size_t lds = (size_t)cap * 8 + region2;
-  static const hipError_t attr = hipFuncSetAttribute((const void*)softmax_topk_kernel,
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, kPfLdsBytes);
-  if (attr != hipSuccess) { set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr)); return kHipError; }
-  hipLaunchKernelGGL(softmax_topk_kernel, dim3((unsigned)rows), dim3(kPfNT), lds, stream, a);
+  static const hipError_t attr1 = hipFuncSetAttribute((const void*)softmax_topk_kernel<true>,
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize, kPfDynBytes);
+  static const hipError_t attr0 = hipFuncSetAttribute((const void*)softmax_topk_kernel<false>,
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize, kPfDynBytes);
+  if (attr1 != hipSuccess || attr0 != hipSuccess) {
+    set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr1 != hipSuccess ? attr1 : attr0));
+    return kHipError;
+  }
+  if (summ)
+    hipLaunchKernelGGL(softmax_topk_kernel<true>, dim3((unsigned)rows), dim3(kPfNT), lds, stream, a);
+  else
+    hipLaunchKernelGGL(softmax_topk_kernel<false>, dim3((unsigned)rows), dim3(kPfNT), lds, stream, a);
   return launch_status("tallax_softmax_topk_cumsum");
 }
 

@@ -48,6 +48,30 @@ def test_prefill_parity(gpu, rows, cols, k, sigma):
     assert not bad.any()
 
 
+@pytest.mark.parametrize("case", ["negative", "wide", "mixed", "near_ties"])
+def test_prefill_key_ranges(gpu, case):
+    """Candidate key ranges that stress the bucketed rank sort: all-negative
+    rows, a very wide range, mixed signs around zero, and values on a fine
+    grid (many equal keys per bucket, some buckets over the rank-sort limit)."""
+    _log(f"softmax_topk_cumsum key range case {case}")
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((12, 30001)).astype(np.float32)
+    if case == "negative":
+        x = x * 2.0 - 300.0
+    elif case == "wide":
+        x = x * 40.0
+    elif case == "mixed":
+        x = x * 1e-3
+    else:
+        x = np.round(x * 2.0 * 256.0) / 256.0
+    x = x.astype(np.float32)
+    gp, gi, gc, gcut = _run(x, 1024, 0.9, gpu)
+    idx, p64, c64, cut64 = O.softmax_topk_cumsum_f64(x, 1024, 0.9)
+    assert np.array_equal(gi, idx)
+    assert np.all(np.abs(gp - p64) <= 1e-5 * np.abs(p64) + 1e-30)
+    assert np.array_equal(bits(gc), bits(O.cumsum(gp, 1)))
+
+
 def test_prefill_ties_fallback_and_nonfinite(gpu):
     """Heavy ties overflow the candidate buffer and take the exact bisection
     path; rows with NaN / +inf give NaN probabilities and indices 0..k-1."""
