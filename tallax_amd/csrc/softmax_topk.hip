@@ -130,7 +130,7 @@ void softmax_topk_kernel(PfArgs a) {
   __shared__ float redf[kPfNW];
   __shared__ int redi[kPfNW];
   __shared__ uint32_t s_t0, s_above;
-  __shared__ int s_cnt, s_bin;
+  __shared__ int s_cnt, s_bin, s_next;
   __shared__ float s_cum_carry[kPfMaxK / 128];
   __shared__ float s_tile_sum[kPfMaxK / 128];
   const int t = threadIdx.x, w = t / kWave, l = lane_id();
@@ -149,6 +149,7 @@ void softmax_topk_kernel(PfArgs a) {
       hist[t] = 0u;
       hist2[t] = 0u;
     }
+    if (t == 0) s_next = 0;
     __syncthreads();
   }
 
@@ -277,7 +278,71 @@ void softmax_topk_kernel(PfArgs a) {
       }
     }
   };
-  {
+  // SUMM rows: waves claim wave-batches of 6 x 64 vectors (vectors c * 384 +
+  // lane + 64 u, all inside the row) from an LDS counter, so that they end
+  // pass 1 together; lane j of a quad holds vector j of a group.
+  const float ninf = -INFINITY;
+  auto batchW = [&](int32_t base) {
+    constexpr int U = 6;
+    uint4 q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) q[u] = rv.base[base + l + kWave * u];
+    float vm[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      vm[u] = raw_max3(__uint_as_float(q[u].x), __uint_as_float(q[u].y),
+                       raw_max3(__uint_as_float(q[u].z), __uint_as_float(q[u].w), ninf));
+    float bm = vm[0];
+#pragma unroll
+    for (int u = 1; u < U; ++u) bm = raw_max(bm, vm[u]);
+    raise_max(bm);
+    float vs[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].x), mc);
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].y), mc);
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].z), mc);
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].w), mc);
+    }
+    s += vs[0] + vs[1];
+    float gm[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float g = raw_max(vm[u], __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(vm[u]), 0xB1, 0xF, 0xF, false)));
+      gm[u] = raw_max(g, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(g), 0x4E, 0xF, 0xF, false)));
+    }
+    if ((l & 3) == 0) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        // select key of the group maximum (never NaN: the maxima start from -inf), -0 as +0
+        const uint32_t b = __float_as_uint(gm[u] + 0.0f);
+        const uint32_t key = b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
+        summ[(base + l + kWave * u) >> 2] = (uint16_t)(key >> 16);
+        atomicAdd(&hist[key >> 24], 1u);
+      }
+    }
+  };
+  if constexpr (SUMM) {
+    constexpr int kWB = 6 * kWave;  // vectors of a wave-batch
+    const int c0 = rv.mis ? 1 : 0;  // the first vector holds elements before the row
+    const int cfull = (int)(v_hi / kWB);
+    for (;;) {
+      int c = 0;
+      if (l == 0) c = atomicAdd(&s_next, 1);
+      c = __builtin_amdgcn_readfirstlane(c) + c0;
+      if (c >= cfull) break;
+      batchW(c * kWB);
+    }
+    // the rest, in chunks of 64 vectors: [0, 384) when the row starts
+    // unaligned, and from the last whole wave-batch to the end
+    const int lo_cov = c0 * 6, hi_cov = (cfull > c0 ? cfull : c0) * 6;
+    const int h_hi = (int)((nv + kWave - 1) / kWave);
+    const int nrest = lo_cov + (h_hi - hi_cov);
+    for (int r = w; r < nrest; r += kPfNW) {
+      const int h = r < lo_cov ? r : hi_cov + (r - lo_cov);
+      step1((int64_t)h * kWave + l);
+    }
+  } else {
     // the loops are uniform over the workgroup, so quads always see all four lanes
     int64_t i = 0;
     if (rv.mis) {  // the first vector holds elements before the row

@@ -59,6 +59,22 @@ __device__ __forceinline__ int32_t comp_idx(uint64_t c) { return (int32_t)(~(uin
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// v_max_f32 / v_max3_f32 on the operands as they are.  fmaxf makes the
+// compiler quiet every operand first (one v_max_f32 x, x each, since the
+// hardware returns NaN for a signalling NaN); these skip that.  A quiet NaN
+// operand is ignored, a signalling NaN may give NaN: use them where any NaN
+// in the data already makes the result NaN.
+__device__ __forceinline__ float raw_max(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float raw_max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Value of lane (lane ^ d) for d in {1, 2, 4, 8, 16, 32}, with VALU lane
 // exchanges only (no LDS-unit round trip):
 //   d = 1, 2   DPP quad_perm [1,0,3,2] / [2,3,0,1];
