@@ -25,6 +25,7 @@
 #include "tx_common.h"
 #include "tx_host.h"
 #include "tx_block_sort.h"
+#include "tx_scan.h"
 #include "tx_wave_sort.h"
 
 namespace tx {
@@ -141,6 +142,163 @@ __global__ __launch_bounds__(P / E) void sort_rows_kernel(SortArgs a) {
   }
 }
 
+// bf16 keys (records of a 16-bit key and a 16-bit tie): a stable LSD radix
+// sort on the key, four passes of 4-bit digits.  The records start in
+// ascending tie order (position p holds tie p), so sorting by key alone,
+// stably, is the ascending record order the bitonic network gives.
+//   * each thread holds E consecutive records; per pass it counts its digits
+//     in its own packed LDS counters (word j * NT + t: digit j in the low
+//     half, digit j + 8 in the high half); the value before its increment is
+//     the record's rank among the thread's earlier records of that digit;
+//   * a raking exclusive scan over the words in (j, t) order gives, per
+//     half, the count of earlier (digit, thread) pairs; the high halves then
+//     add the number of records with digit < 8;
+//   * records move to their ranks through LDS and are read back in order.
+constexpr int kRadixNT = 1024;
+
+template <int E>
+__global__ __launch_bounds__(kRadixNT) void radix_sort_rows_kernel(SortArgs a) {
+  using RT = RecT<uint32_t>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint32_t* cnt = (uint32_t*)smem;       // 8 * kRadixNT counter words
+  uint32_t* buf = cnt + 8 * kRadixNT;    // cols records
+  __shared__ uint32_t wsum[kRadixNT / kWave];
+  const int t = threadIdx.x, l = lane_id(), w = t / kWave;
+  const int n = (int)a.cols;
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * a.cols;
+  uint32_t v[E];
+  // the E keys of positions t E .. t E + E - 1 (ties descending: original
+  // indices n - 1 - p, read in one piece when the row allows)
+  const bool vec = E == 4 && (n & 3) == 0 && (((uintptr_t)a.key + (uintptr_t)base * 2) & 7) == 0;
+  if (vec && t * E < n) {
+    const int i0 = a.ties_desc ? n - 4 - t * E : t * E;
+    const uint2 q = *(const uint2*)((const uint16_t*)a.key + base + i0);
+    const uint32_t h[4] = {q.x << 16, q.x & 0xFFFF0000u, q.y << 16, q.y & 0xFFFF0000u};
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const int i = a.ties_desc ? n - 1 - (t * E + r) : t * E + r;
+      uint32_t k = sort_order_bits(&h[a.ties_desc ? 3 - r : r], kF32, 0);
+      if (a.descending) k = ~k;
+      v[r] = RT::make(k, a.ties_desc ? 0xFFFFu - (uint32_t)i : (uint32_t)i);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const int p = t * E + r;
+      v[r] = 0u;
+      if (p < n) {
+        const int i = a.ties_desc ? n - 1 - p : p;  // ascending ties either way
+        uint32_t k = sort_order_bits(a.key, a.key_dtype, base + i);
+        if (a.descending) k = ~k;
+        v[r] = RT::make(k, a.ties_desc ? 0xFFFFu - (uint32_t)i : (uint32_t)i);
+      }
+    }
+  }
+#pragma unroll 1
+  for (int sh = 16; sh < 32; sh += 4) {
+    // this thread's own counters (nobody else reads them before the barrier below)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) cnt[j * kRadixNT + t] = 0u;
+    uint32_t lr[E];
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      lr[r] = 0u;
+      if (t * E + r < n) {
+        const uint32_t d = (v[r] >> sh) & 15u;
+        const uint32_t hs = (d >> 3) * 16u;
+        lr[r] = (atomicAdd(&cnt[(d & 7u) * kRadixNT + t], 1u << hs) >> hs) & 0xFFFFu;
+      }
+    }
+    __syncthreads();  // every thread's counts are in
+    // raking exclusive scan: thread t takes words 8t .. 8t + 7
+    const uint4 wa = ((const uint4*)cnt)[2 * t], wb = ((const uint4*)cnt)[2 * t + 1];
+    uint32_t x[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    uint32_t run = 0u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t c = x[j];
+      x[j] = run;
+      run += c;
+    }
+    uint32_t incl = run;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+    if (l == kWave - 1) wsum[w] = incl;
+    __syncthreads();
+    uint32_t pre = incl - run, tot = 0u;
+#pragma unroll
+    for (int i = 0; i < kRadixNT / kWave; ++i) {
+      const uint32_t s = wsum[i];
+      pre += i < w ? s : 0u;
+      tot += s;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] += pre;
+    ((uint4*)cnt)[2 * t] = make_uint4(x[0], x[1], x[2], x[3]);
+    ((uint4*)cnt)[2 * t + 1] = make_uint4(x[4], x[5], x[6], x[7]);
+    __syncthreads();
+    const uint32_t below8 = tot & 0xFFFFu;  // records with digit < 8
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      if (t * E + r < n) {
+        const uint32_t d = (v[r] >> sh) & 15u;
+        const uint32_t word = cnt[(d & 7u) * kRadixNT + t];
+        const uint32_t dest = (d >> 3) ? (word >> 16) + below8 : (word & 0xFFFFu);
+        buf[dest + lr[r]] = v[r];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < E; ++r)
+      if (t * E + r < n) v[r] = buf[t * E + r];
+  }
+  const uint32_t tie_mask = 0xFFFFu;
+  if (vec && ((uintptr_t)(a.perm_out + base) & 15) == 0 && t * E < n) {
+    int32_t pp[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t tie = RT::tie(v[r]);
+      pp[r] = a.ties_desc ? (int)(tie_mask - tie) : (int)tie;
+    }
+    *(int4*)(a.perm_out + base + t * E) = make_int4(pp[0], pp[1], pp[2], pp[3]);
+  }
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int i = t * E + r;
+    if (i >= n) continue;
+    const uint32_t tie = RT::tie(v[r]);
+    const int pos = a.ties_desc ? (int)(tie_mask - tie) : (int)tie;
+    if (!(vec && ((uintptr_t)(a.perm_out + base) & 15) == 0)) a.perm_out[base + i] = pos;
+    if (a.key_out) {
+      uint32_t k = RT::key(v[r]);
+      if (a.descending) k = ~k;
+      k &= 0xFFFF0000u;  // rebuild the full order bits of a bf16 key from its high half
+      if (k < 0x80000000u) k |= 0xFFFFu;
+      else if (k > 0xFF800000u) k = 0xFFFFFFFEu;
+      store_sorted(a.key_out, a.key_out_dtype, a.key_dtype, base + i, k);
+    }
+    if (a.aux_out) {
+      const uint32_t u = sort_order_bits(a.aux, a.aux_dtype, base + pos);
+      store_sorted(a.aux_out, a.aux_out_dtype, a.aux_dtype, base + i, u);
+    }
+  }
+}
+
+template <int E>
+static int launch_radix(const SortArgs& a, int64_t rows, hipStream_t s) {
+  const size_t lds = (size_t)8 * kRadixNT * 4 + (size_t)a.cols * 4;
+  static const hipError_t attr = hipFuncSetAttribute((const void*)radix_sort_rows_kernel<E>,
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     8 * kRadixNT * 4 + 4 * kRadixNT * 4);
+  if (attr != hipSuccess) {
+    set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr));
+    return kHipError;
+  }
+  hipLaunchKernelGGL((radix_sort_rows_kernel<E>), dim3((unsigned)rows), dim3(kRadixNT), lds, s, a);
+  return kOk;
+}
+
 template <typename R, int E, int P>
 static int launch_sort(const SortArgs& a, int64_t rows, hipStream_t s) {
   const size_t lds = (size_t)P * sizeof(R);
@@ -208,7 +366,9 @@ int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols,
   a.aux = aux; a.aux_dtype = aux_dtype; a.aux_out = aux_out; a.aux_out_dtype = aux_out_dtype;
   // bf16 keys on the packed path fit (16-bit key | 16-bit tie) in one u32
   const bool narrow = key_dtype == kBF16 && !perm_in && cols <= 65536;
-  const int st = narrow ? launch_sort_p<uint32_t>(a, rows, stream) : launch_sort_p<uint64_t>(a, rows, stream);
+  // bf16 rows up to 4096: radix sort; longer ones: the bitonic network
+  const int st = narrow ? (cols <= 4 * kRadixNT ? launch_radix<4>(a, rows, stream) : launch_sort_p<uint32_t>(a, rows, stream))
+                        : launch_sort_p<uint64_t>(a, rows, stream);
   if (st) return st;
   return launch_status("tallax_sort_rows");
 }
