@@ -19,22 +19,23 @@
 // jax.nn.softmax does), indices 0..k-1 and cutoff 0.
 //
 // One 1024-thread workgroup per row, two workgroups per CU:
-//   pass 1 (one streaming read): the row maximum, the exp-sum (online, per
-//           thread) and, per 64-byte group of the row, the high 16 bits of
-//           the group maximum's select key, kept in LDS with a 256-bin
-//           histogram of their top byte;
+//   pass 1 (one streaming read, waves claiming 6 x 64-vector batches from an
+//           LDS counter): the row maximum, the exp-sum (online, per thread)
+//           and, per 64-byte group of the row, the high 16 bits of the group
+//           maximum's select key, kept in LDS with a 256-bin histogram of
+//           their top byte;
 //   threshold: the k-th largest group prefix q0 (the histogram, then one of
 //           the low byte inside the crossing bin).  At least k groups reach
 //           q0, so at least k elements have a key >= q0 << 16: that is T0;
 //   pass 2: the groups that reach q0 (~k of them for Gaussian rows) are
 //           listed, spread evenly over the workgroup and read again; their
 //           elements >= T0 are appended to LDS;
-// then a workgroup bitonic sort of the candidates, the outputs, the tile
-// scan and the cutoff.  Rows too long for the group summary (over 24 Ki
-// groups) keep each thread's four largest values in pass 1 instead, take T0
-// as the k-th largest of those 4096 and read the whole row again.  If the
-// candidates overflow (heavy ties), the k-th composite is found by bisection
-// over the row instead.
+// then a bucketed rank sort of the candidates (a bitonic network when a key
+// bucket is large), the outputs, the tile scan and the cutoff.  Rows too long
+// for the group summary (over 24 Ki groups) keep each thread's four largest
+// values in pass 1 instead, take T0 as the k-th largest of those 4096 and
+// read the whole row again.  If the candidates overflow (heavy ties), the
+// k-th composite is found by bisection over the row instead.
 #include <float.h>
 #include <math.h>
 #include <stdint.h>

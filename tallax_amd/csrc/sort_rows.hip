@@ -18,7 +18,9 @@
 // padded to P = 2^m >= cols with the largest record and sorted ascending by a
 // bitonic network.  Each thread holds E consecutive records in registers;
 // strides < E are exchanged within the thread, strides < 64 E across lanes
-// with DPP / v_permlane*_swap, larger strides through LDS.
+// with DPP / v_permlane*_swap, larger strides through LDS.  bf16 rows of up
+// to 4096 elements use a stable LSD radix sort instead (see
+// radix_sort_rows_kernel).
 #include <stdint.h>
 
 #include "tallax_hip.h"
