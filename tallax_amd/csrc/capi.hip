@@ -1,6 +1,9 @@
 // Library-wide C-ABI helpers: error reporting and version.
 #include <string.h>
 
+#include <mutex>
+#include <vector>
+
 #include "tx_host.h"
 
 namespace tx {
@@ -12,6 +15,25 @@ void set_error(const char* fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
+}
+
+hipError_t set_dynamic_lds_limit(const void* kernel, int bytes) {
+  struct Done {
+    int dev;
+    const void* kernel;
+    int bytes;
+  };
+  static std::mutex mu;
+  static std::vector<Done> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const Done& d : done)
+    if (d.dev == dev && d.kernel == kernel && d.bytes >= bytes) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.push_back({dev, kernel, bytes});
+  return e;
 }
 
 }  // namespace tx
