@@ -105,10 +105,10 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 # ---------------------------------------------------------------------------
-# Workspace: one zero-initialised byte buffer per device, grown on demand.
-# The kernels leave their arrival counters at zero when they finish, so the
-# buffer never needs clearing between calls.  Calls that overlap on one
-# device (different streams) must pass their own workspace.
+# Workspace: one byte buffer per device, grown on demand.  No kernel reads
+# workspace contents it did not write in the same call, so the buffer never
+# needs clearing.  Calls that overlap on one device (different streams) must
+# pass their own workspace.
 # ---------------------------------------------------------------------------
 _ws_lock = threading.Lock()
 _ws: dict[int, torch.Tensor] = {}

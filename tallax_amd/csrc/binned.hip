@@ -760,8 +760,8 @@ int tallax_top_dynamic_k(const void* x, int dtype, int64_t rows, int64_t cols, c
     st = launch_segment_lists(x, dtype, rows, cols, nseg, maxv, vps, lists, stream);
     if (st) return st;
     const size_t lds_c = cand_lds_bytes(num_bins) > lds_scan ? cand_lds_bytes(num_bins) : lds_scan;
-    const hipError_t attr_c8 = set_dynamic_lds_limit((const void*)binned_cand_kernel<8>, 144 * 1024);
-    const hipError_t attr_c16 = set_dynamic_lds_limit((const void*)binned_cand_kernel<16>, 144 * 1024);
+    const hipError_t attr_c8 = set_dynamic_lds_limit((const void*)binned_cand_kernel<8>, 144 * 1024, stream);
+    const hipError_t attr_c16 = set_dynamic_lds_limit((const void*)binned_cand_kernel<16>, 144 * 1024, stream);
     if (attr_c8 != hipSuccess || attr_c16 != hipSuccess) { set_error("hipFuncSetAttribute failed"); return kHipError; }
     if (mc == 8)
       hipLaunchKernelGGL(binned_cand_kernel<8>, dim3((unsigned)rows), dim3(kCandNT), lds_c, stream, a);
@@ -775,8 +775,8 @@ int tallax_top_dynamic_k(const void* x, int dtype, int64_t rows, int64_t cols, c
       if (st) return st;
     }
   } else {
-    const hipError_t attr8 = set_dynamic_lds_limit((const void*)binned_lists_kernel<8>, 128 * 1024);
-    const hipError_t attr16 = set_dynamic_lds_limit((const void*)binned_lists_kernel<16>, 128 * 1024);
+    const hipError_t attr8 = set_dynamic_lds_limit((const void*)binned_lists_kernel<8>, 128 * 1024, stream);
+    const hipError_t attr16 = set_dynamic_lds_limit((const void*)binned_lists_kernel<16>, 128 * 1024, stream);
     if (attr8 != hipSuccess || attr16 != hipSuccess) { set_error("hipFuncSetAttribute failed"); return kHipError; }
     if (mc == 8)
       hipLaunchKernelGGL(binned_lists_kernel<8>, dim3((unsigned)rows), dim3(kBinNT), lds_scan, stream, a);

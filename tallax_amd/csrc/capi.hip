@@ -17,7 +17,7 @@ void set_error(const char* fmt, ...) {
   va_end(ap);
 }
 
-hipError_t set_dynamic_lds_limit(const void* kernel, int bytes) {
+hipError_t set_dynamic_lds_limit(const void* kernel, int bytes, hipStream_t stream) {
   struct Done {
     int dev;
     const void* kernel;
@@ -25,13 +25,17 @@ hipError_t set_dynamic_lds_limit(const void* kernel, int bytes) {
   };
   static std::mutex mu;
   static std::vector<Done> done;
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) return e;
+  int dev = cur;
+  if (stream && hipStreamGetDevice(stream, &dev) != hipSuccess) dev = cur;
   std::lock_guard<std::mutex> lock(mu);
   for (const Done& d : done)
     if (d.dev == dev && d.kernel == kernel && d.bytes >= bytes) return hipSuccess;
+  if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return e;
   e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (dev != cur) (void)hipSetDevice(cur);
   if (e == hipSuccess) done.push_back({dev, kernel, bytes});
   return e;
 }

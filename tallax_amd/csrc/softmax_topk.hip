@@ -739,8 +739,8 @@ int tallax_softmax_topk_cumsum(const float* logits, int64_t rows, int64_t cols, 
   a.cap = cap;
   a.cap2 = (int)(region2 / 8);
   const size_t lds = (size_t)cap * 8 + region2;
-  const hipError_t attr1 = set_dynamic_lds_limit((const void*)softmax_topk_kernel<true>, kPfDynBytes);
-  const hipError_t attr0 = set_dynamic_lds_limit((const void*)softmax_topk_kernel<false>, kPfDynBytes);
+  const hipError_t attr1 = set_dynamic_lds_limit((const void*)softmax_topk_kernel<true>, kPfDynBytes, stream);
+  const hipError_t attr0 = set_dynamic_lds_limit((const void*)softmax_topk_kernel<false>, kPfDynBytes, stream);
   if (attr1 != hipSuccess || attr0 != hipSuccess) {
     set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr1 != hipSuccess ? attr1 : attr0));
     return kHipError;

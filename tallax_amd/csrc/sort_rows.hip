@@ -290,7 +290,7 @@ __global__ __launch_bounds__(kRadixNT) void radix_sort_rows_kernel(SortArgs a) {
 template <int E>
 static int launch_radix(const SortArgs& a, int64_t rows, hipStream_t s) {
   const size_t lds = (size_t)8 * kRadixNT * 4 + (size_t)a.cols * 4;
-  const hipError_t attr = set_dynamic_lds_limit((const void*)radix_sort_rows_kernel<E>, 8 * kRadixNT * 4 + 4 * kRadixNT * 4);
+  const hipError_t attr = set_dynamic_lds_limit((const void*)radix_sort_rows_kernel<E>, 8 * kRadixNT * 4 + 4 * kRadixNT * 4, s);
   if (attr != hipSuccess) {
     set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr));
     return kHipError;
@@ -303,7 +303,7 @@ template <typename R, int E, int P>
 static int launch_sort(const SortArgs& a, int64_t rows, hipStream_t s) {
   const size_t lds = (size_t)P * sizeof(R);
   if (lds > 64 * 1024) {
-    const hipError_t attr = set_dynamic_lds_limit((const void*)sort_rows_kernel<R, E, P>, (int)lds);
+    const hipError_t attr = set_dynamic_lds_limit((const void*)sort_rows_kernel<R, E, P>, (int)lds, s);
     if (attr != hipSuccess) {
       set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr));
       return kHipError;

@@ -29,9 +29,10 @@ inline int launch_status(const char* what) {
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Raise a kernel's dynamic-LDS limit to `bytes` on the current device (the
-// attribute is per device; each (device, kernel) pair is set once).
-hipError_t set_dynamic_lds_limit(const void* kernel, int bytes);
+// Raise a kernel's dynamic-LDS limit to `bytes` on the device of `stream`
+// (the current device for the null stream).  The attribute is per device;
+// each (device, kernel) pair is set once.
+hipError_t set_dynamic_lds_limit(const void* kernel, int bytes, hipStream_t stream);
 
 // Per-segment sorted top-128 composites of every row (row_select.hip):
 // plan the segments (at least min_seg per row), then launch the segment kernel

@@ -30,6 +30,7 @@ def _run(x, k, p, gpu):
     (24, 50001, 1000, 1.0),      # ragged, odd length
     (16, 3000, 2048, 4.0),       # candidates ~ all of the row
     (8, 129, 100, 2.0),
+    (4, 400003, 256, 2.0),       # over 24 Ki groups: per-thread top-4 and a full second read
 ])
 def test_prefill_parity(gpu, rows, cols, k, sigma):
     _log(f"softmax_topk_cumsum [{rows},{cols}] k={k} sigma={sigma}")
