@@ -14,6 +14,9 @@ samples one token for each of the 256 rows.
   sort_c2        bf16 keys [256,4096] (multiples of 1/16) stable argsort, then
                  take_along_axis of an f32 [256,4096] array
   prefill_c5     f32 [1024,201088] softmax -> top-2048 -> cumsum -> cutoff p=0.9
+  sort_wide      tax.sort of f32 [1024,201088] probabilities, descending stable
+                 argsort with keys: the reference's own route for config 5's
+                 sort (rows > 16384: chunk radix sorts + merge passes)
   copy           torch's device copy of 256 MiB (the counter calibration)
 
 Timing: inputs are resident in HBM before the timed region; steps rotate
@@ -36,7 +39,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak, GB/s
 COPY_BYTES = 256 << 20  # calibration copy: 256 MiB read + 256 MiB written per launch
-CONFIGS = ["sampler", "topk_c3", "topk_c3_approx", "topk_c1", "sort_c2", "prefill_c5", "copy"]
+CONFIGS = ["sampler", "topk_c3", "topk_c3_approx", "topk_c1", "sort_c2", "prefill_c5", "sort_wide", "copy"]
 
 
 def _copy_rate(torch, dev, stream, steps, warmup):
@@ -334,6 +337,54 @@ def _prefill_c5(torch, np, _lib, dev, s_handle, gen, nbuf):
     return w
 
 
+def _sort_wide(torch, np, _lib, dev, s_handle, gen, nbuf):
+    w = Workload()
+    rows, cols = 1024, 201088
+    nb = nbuf or 2
+    bufs = [torch.softmax(torch.randn((rows, cols), generator=gen, device=dev) * 2.0, dim=1) for _ in range(nb)]
+    keys = torch.empty((rows, cols), dtype=torch.float32, device=dev)
+    perm = torch.empty((rows, cols), dtype=torch.int32, device=dev)
+    nws = int(_lib.LIB.tallax_sort_rows_workspace_size(rows, cols))
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev)
+    w.metric = "rows/s + achieved HBM GB/s (% peak): sort_wide"
+    w.rows, w.shape = rows, (rows, cols)
+    w.alg_bytes = rows * cols * 12  # keys in; sorted keys and int32 indices out
+    w.workload = ("tax.sort(p, num_keys=1, is_stable=True, return_argsort=True, descending=True) of f32 "
+                  "[1024,201088] softmax(N(0, sigma=2)) rows: the reference's sort route for config 5 "
+                  "(rows > 16384: chunk radix sorts + merge passes through the workspace)")
+    w.kernel = "sort_chunks_kernel<f32> + 4 merge_runs_kernel passes"
+    w.cpu_batch = 1
+    sample = 4  # rows checked against the oracle
+
+    def launch(i):
+        x = bufs[i % nb]
+        _lib.check(_lib.LIB.tallax_sort_rows_ws(x.data_ptr(), _lib.F32, rows, cols, 1, 0, None, perm.data_ptr(),
+                                                keys.data_ptr(), _lib.F32, None, 0, None, 0, ws.data_ptr(), nws,
+                                                s_handle), "sort")
+
+    def host0():
+        if not hasattr(w, "h0"):
+            w.h0 = bufs[0][:sample].cpu().numpy()
+        return w.h0
+
+    def parity(O):
+        h = host0()
+        launch(0)
+        torch.cuda.synchronize()
+        (sk, si), _ = O.sort([h], 1, is_stable=True, return_argsort=True, descending=True)
+        return bool(np.array_equal(perm[:sample].cpu().numpy(), si) and
+                    np.array_equal(keys[:sample].cpu().numpy().view(np.uint32), sk.view(np.uint32)))
+
+    def cpu_step(O, r0, batch):
+        h = host0()
+        r0 = r0 % h.shape[0]
+        O.sort([h[r0:r0 + batch]], 1, is_stable=True, return_argsort=True, descending=True)
+        return h[r0:r0 + batch].shape[0]
+
+    w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
+    return w
+
+
 def main() -> int:
     args = _parse()
     if args.gpus != 1:
@@ -369,6 +420,8 @@ def main() -> int:
         w = _topk(torch, np, _lib, dev, s_handle, gen, args.nbuf, args.config)
     elif args.config == "sort_c2":
         w = _sort_c2(torch, np, _lib, dev, s_handle, gen, args.nbuf)
+    elif args.config == "sort_wide":
+        w = _sort_wide(torch, np, _lib, dev, s_handle, gen, args.nbuf)
     else:
         w = _prefill_c5(torch, np, _lib, dev, s_handle, gen, args.nbuf)
     torch.cuda.synchronize()

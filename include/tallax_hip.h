@@ -169,12 +169,21 @@ int tallax_cumsum(const void* x, int dtype, int64_t rows, int64_t cols, int axis
  * key_out = the sorted keys decoded (f32 keys: f32; int32: int32; bf16: bf16
  * with NaN 0x7FFF, or f32 with NaN 0x7FFFFFFE, chosen by key_out_dtype);
  * optional aux / aux_out: a second key gathered by perm_out and decoded the
- * same way.  cols <= 16384.
+ * same way.  tallax_sort_rows takes rows of up to 16384 elements (one
+ * workgroup sorts a row in LDS); tallax_sort_rows_ws takes any cols < 2^31
+ * and uses `workspace` for longer rows (the reference's HBM substage route,
+ * sort.py:574-758): at least tallax_sort_rows_workspace_size(rows, cols)
+ * bytes, 0 for cols <= 16384, no initial contents needed.
  * ---------------------------------------------------------------------- */
 int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols, int descending,
                      int ties_descending, const int32_t* perm_in, int32_t* perm_out, void* key_out,
                      int key_out_dtype, const void* aux, int aux_dtype, void* aux_out, int aux_out_dtype,
                      tallax_stream_t stream);
+size_t tallax_sort_rows_workspace_size(int64_t rows, int64_t cols);
+int tallax_sort_rows_ws(const void* key, int key_dtype, int64_t rows, int64_t cols, int descending,
+                        int ties_descending, const int32_t* perm_in, int32_t* perm_out, void* key_out,
+                        int key_out_dtype, const void* aux, int aux_dtype, void* aux_out, int aux_out_dtype,
+                        void* workspace, size_t workspace_bytes, tallax_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Prefill-scale softmax -> top-k -> cumsum -> top-p cutoff, fused (BASELINE

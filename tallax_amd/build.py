@@ -28,6 +28,7 @@ SOURCES = [
     "row_select.hip",
     "scan_gather.hip",
     "sort_rows.hip",
+    "sort_wide.hip",
     "binned.hip",
     "softmax_topk.hip",
     "testing.hip",

@@ -28,54 +28,12 @@
 #include "tx_host.h"
 #include "tx_block_sort.h"
 #include "tx_scan.h"
+#include "tx_sort_keys.h"
 #include "tx_wave_sort.h"
 
 namespace tx {
 
 constexpr int kSortMaxCols = 16384;
-
-struct SortArgs {
-  const void* key;
-  int key_dtype;
-  int64_t cols;
-  int P;            // padded length, power of two
-  int descending;
-  int ties_desc;    // ties by descending original index
-  const int32_t* perm_in;  // optional: sort key[perm_in] with position ties, compose
-  int32_t* perm_out;
-  void* key_out;
-  int key_out_dtype;
-  const void* aux;  // optional second key, output gathered by the final permutation
-  int aux_dtype;
-  void* aux_out;
-  int aux_out_dtype;
-};
-
-// sortable order of a key as an unsigned 32-bit value (standardised floats)
-__device__ __forceinline__ uint32_t sort_order_bits(const void* p, int dtype, int64_t i) {
-  if (dtype == kI32) return (uint32_t)((const int32_t*)p)[i] ^ 0x80000000u;
-  uint32_t b = dtype == kBF16 ? ((uint32_t)((const uint16_t*)p)[i]) << 16 : ((const uint32_t*)p)[i];
-  if ((b & 0x7FFFFFFFu) > 0x7F800000u) b = 0x7FFFFFFEu;  // NaN: sortable_int_to_float(INT32_MAX - 1)
-  if ((b & 0x7FFFFFFFu) == 0u) b = 0u;                   // -0 -> +0
-  const int32_t s = (int32_t)b < 0 ? (int32_t)(b ^ 0x7FFFFFFFu) : (int32_t)b;
-  return (uint32_t)s ^ 0x80000000u;
-}
-// standardised value bits back from the sortable order
-__device__ __forceinline__ uint32_t order_to_value_bits(uint32_t u) {
-  const int32_t s = (int32_t)(u ^ 0x80000000u);
-  return s < 0 ? ((uint32_t)s ^ 0x7FFFFFFFu) : (uint32_t)s;
-}
-__device__ __forceinline__ void store_sorted(void* out, int out_dtype, int in_dtype, int64_t i, uint32_t u) {
-  if (in_dtype == kI32) {
-    ((int32_t*)out)[i] = (int32_t)(u ^ 0x80000000u);
-    return;
-  }
-  const uint32_t b = order_to_value_bits(u);
-  if (out_dtype == kBF16)
-    ((uint16_t*)out)[i] = (uint16_t)(b >> 16);
-  else
-    ((uint32_t*)out)[i] = b;
-}
 
 template <typename R>
 struct RecT;
@@ -322,7 +280,7 @@ static int launch_sort_p(const SortArgs& a, int64_t rows, hipStream_t s) {
     case 2048: return launch_sort<R, 4, 2048>(a, rows, s);
     case 4096: return launch_sort<R, 4, 4096>(a, rows, s);
     case 8192: return launch_sort<R, 8, 8192>(a, rows, s);
-    default: return launch_sort<R, 32, 16384>(a, rows, s);
+    default: return launch_sort<R, 16, 16384>(a, rows, s);
   }
 }
 
@@ -332,10 +290,14 @@ using namespace tx;
 
 extern "C" {
 
-int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols, int descending,
-                     int ties_descending, const int32_t* perm_in, int32_t* perm_out, void* key_out,
-                     int key_out_dtype, const void* aux, int aux_dtype, void* aux_out, int aux_out_dtype,
-                     hipStream_t stream) {
+size_t tallax_sort_rows_workspace_size(int64_t rows, int64_t cols) {
+  return sort_wide_workspace_bytes(rows, cols);
+}
+
+int tallax_sort_rows_ws(const void* key, int key_dtype, int64_t rows, int64_t cols, int descending,
+                        int ties_descending, const int32_t* perm_in, int32_t* perm_out, void* key_out,
+                        int key_out_dtype, const void* aux, int aux_dtype, void* aux_out, int aux_out_dtype,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (!key || !perm_out) { set_error("null pointer argument"); return kInvalidArgument; }
   for (int d : {key_dtype, aux ? aux_dtype : kF32}) {
     if (d != kF32 && d != kBF16 && d != kI32) { set_error("dtype %d not supported", d); return kUnsupported; }
@@ -348,21 +310,21 @@ int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols,
   if (aux_out && !out_ok(aux_dtype, aux_out_dtype)) { set_error("aux_out dtype %d invalid for aux dtype %d", aux_out_dtype, aux_dtype); return kInvalidArgument; }
   if (rows < 0 || cols < 0) { set_error("negative extent"); return kInvalidArgument; }
   if (rows == 0 || cols == 0) return kOk;
-  if (cols > kSortMaxCols) {
-    set_error("rows of %lld elements exceed this build's in-LDS sort limit of %d", (long long)cols, kSortMaxCols);
-    return kUnsupported;
-  }
   if (rows > 2147483647) { set_error("too many rows"); return kUnsupported; }
   SortArgs a = {};
   a.key = key; a.key_dtype = key_dtype; a.cols = cols;
   int P = 256;
-  while (P < cols) P <<= 1;
+  while (P < cols && P <= kSortMaxCols) P <<= 1;  // the in-LDS network's padded length
   a.P = P;
   a.descending = descending != 0;
   a.ties_desc = ties_descending != 0;
   a.perm_in = perm_in; a.perm_out = perm_out;
   a.key_out = key_out; a.key_out_dtype = key_out_dtype;
   a.aux = aux; a.aux_dtype = aux_dtype; a.aux_out = aux_out; a.aux_out_dtype = aux_out_dtype;
+  if (cols > kSortMaxCols) {  // longer than one workgroup's LDS: chunk sorts + merge passes
+    const int st = launch_sort_wide(a, rows, workspace, workspace_bytes, stream);
+    return st ? st : launch_status("tallax_sort_rows");
+  }
   // bf16 keys on the packed path fit (16-bit key | 16-bit tie) in one u32
   const bool narrow = key_dtype == kBF16 && !perm_in && cols <= 65536;
   // bf16 rows up to 4096: radix sort; longer ones: the bitonic network
@@ -370,6 +332,14 @@ int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols,
                         : launch_sort_p<uint64_t>(a, rows, stream);
   if (st) return st;
   return launch_status("tallax_sort_rows");
+}
+
+int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols, int descending,
+                     int ties_descending, const int32_t* perm_in, int32_t* perm_out, void* key_out,
+                     int key_out_dtype, const void* aux, int aux_dtype, void* aux_out, int aux_out_dtype,
+                     hipStream_t stream) {
+  return tallax_sort_rows_ws(key, key_dtype, rows, cols, descending, ties_descending, perm_in, perm_out, key_out,
+                             key_out_dtype, aux, aux_dtype, aux_out, aux_out_dtype, nullptr, 0, stream);
 }
 
 }  // extern "C"

@@ -88,41 +88,55 @@ __device__ __forceinline__ void block_bitonic_sort(R v[E], R* lds, int P, bool d
   }
 }
 
-// The same network with P known at compile time: every stage is unrolled,
-// so stride tests and lane distances fold to constants.
-template <typename R, int E, int P, bool DESC>
-__device__ __forceinline__ void block_bitonic_sort_c(R v[E], R* lds) {
+// The same network with P known at compile time.  Each (size, stride) stage
+// is its own template instance, reached by compile-time recursion rather than
+// by unrolling the nested size / stride loops: the loops' trip counts grow
+// as log^2 P and the unroller gives up on them for P = 16384, which left the
+// register array indexed at run time (VGPR indexing or scratch).  Here every
+// record index is a constant.
+template <typename R, int E, int SIZE, int STRIDE, bool DESC>
+__device__ __forceinline__ void bitonic_stage_c(R (&v)[E], R* lds) {
   const int t = threadIdx.x;
+  if constexpr (STRIDE < E) {
 #pragma unroll
-  for (int size = 2; size <= P; size <<= 1) {
-#pragma unroll
-    for (int stride = size >> 1; stride >= 1; stride >>= 1) {
-      if (stride < E) {
-#pragma unroll
-        for (int r = 0; r < E; ++r) {
-          if ((r & stride) == 0) {
-            const int i = t * E + r;
-            cx_pair(v[r], v[r | stride], ((i & size) == 0) != DESC);
-          }
-        }
-      } else if (stride < kWave * E) {
-        bsort_lane_stage<R, E>(v, stride / E, size, t, DESC);
-      } else {
-#pragma unroll
-        for (int r = 0; r < E; ++r) lds[t * E + r] = v[r];
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < E; ++r) {
-          const int i = t * E + r;
-          const R o = lds[i ^ stride];
-          const bool asc = ((i & size) == 0) != DESC;
-          const bool lower = (i & stride) == 0;
-          v[r] = cx(v[r], o, lower != asc);
-        }
-        __syncthreads();
+    for (int r = 0; r < E; ++r) {
+      if ((r & STRIDE) == 0) {
+        const int i = t * E + r;
+        cx_pair(v[r], v[r | STRIDE], ((i & SIZE) == 0) != DESC);
       }
     }
+  } else if constexpr (STRIDE < kWave * E) {
+    bsort_lane_stage<R, E>(v, STRIDE / E, SIZE, t, DESC);
+  } else {
+#pragma unroll
+    for (int r = 0; r < E; ++r) lds[t * E + r] = v[r];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const int i = t * E + r;
+      const R o = lds[i ^ STRIDE];
+      const bool asc = ((i & SIZE) == 0) != DESC;
+      const bool lower = (i & STRIDE) == 0;
+      v[r] = cx(v[r], o, lower != asc);
+    }
+    __syncthreads();
   }
+}
+
+template <typename R, int E, int P, int SIZE, int STRIDE, bool DESC>
+__device__ __forceinline__ void bitonic_from_c(R (&v)[E], R* lds) {
+  bitonic_stage_c<R, E, SIZE, STRIDE, DESC>(v, lds);
+  if constexpr (STRIDE > 1) {
+    bitonic_from_c<R, E, P, SIZE, STRIDE / 2, DESC>(v, lds);
+  } else if constexpr (SIZE < P) {
+    bitonic_from_c<R, E, P, SIZE * 2, SIZE, DESC>(v, lds);
+  }
+}
+
+template <typename R, int E, int P, bool DESC>
+__device__ __forceinline__ void block_bitonic_sort_c(R (&v)[E], R* lds) {
+  static_assert((P & (P - 1)) == 0 && P >= 2 && P % E == 0, "P: a power of two, E records per thread");
+  bitonic_from_c<R, E, P, 2, 1, DESC>(v, lds);
 }
 
 }  // namespace tx

@@ -41,4 +41,27 @@ int segment_lists_plan(int64_t cols, int dt, int min_seg, int* nseg_out, int* ma
 int launch_segment_lists(const void* x, int dt, int64_t rows, int64_t cols, int nseg, int maxv, int64_t vps,
                          uint64_t* lists, hipStream_t s);
 
+// Arguments of a row sort (sort_rows.hip, sort_wide.hip).
+struct SortArgs {
+  const void* key;
+  int key_dtype;
+  int64_t cols;
+  int P;            // padded length, power of two (in-LDS sorts)
+  int descending;
+  int ties_desc;    // ties by descending original index
+  const int32_t* perm_in;  // optional: sort key[perm_in] with position ties, compose
+  int32_t* perm_out;
+  void* key_out;
+  int key_out_dtype;
+  const void* aux;  // optional second key, output gathered by the final permutation
+  int aux_dtype;
+  void* aux_out;
+  int aux_out_dtype;
+};
+
+// Rows longer than one workgroup's LDS holds (sort_wide.hip): chunk sorts and
+// merge passes through a workspace of sort_wide_workspace_bytes bytes.
+size_t sort_wide_workspace_bytes(int64_t rows, int64_t cols);
+int launch_sort_wide(const SortArgs& a, int64_t rows, void* ws, size_t ws_bytes, hipStream_t s);
+
 }  // namespace tx

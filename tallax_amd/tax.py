@@ -153,8 +153,11 @@ def sort(operand, num_keys: int, is_stable: bool = False, return_argsort: bool =
         int32 indices are appended last.
     Non-stable ties are ordered by ascending index (the reference leaves that
     order to its network).  Keys: float32, bfloat16, int32; up to two keys;
-    rows of up to 16384 elements.  `num_vmem_substages`, `block_token` and
-    `interpret` are TPU tuning knobs, accepted and ignored.
+    rows of any length below 2^31.  Rows longer than 16384 elements (the
+    reference's HBM substage route, sort.py:574-758) are sorted in chunks and
+    merged through a device workspace of 8 or 16 bytes per element.
+    `num_vmem_substages`, `block_token` and `interpret` are TPU tuning knobs,
+    accepted and ignored.
     """
     del num_vmem_substages, block_token, interpret
     operands = list(operand) if isinstance(operand, (list, tuple)) else [operand]
@@ -195,21 +198,25 @@ def sort(operand, num_keys: int, is_stable: bool = False, return_argsort: bool =
     outs = [None] * len(ops)
     k0 = ops[0]
     out0 = torch.empty(shape, dtype=key_out_dtype(k0), device=dev)
+    # rows longer than 16384: a per-call workspace (the caching allocator recycles it)
+    nws = int(_lib.LIB.tallax_sort_rows_workspace_size(rows, cols))
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws else None
+    ws_ptr = ws.data_ptr() if ws is not None else None
     if num_keys == 1:
-        _lib.check(_lib.LIB.tallax_sort_rows(
+        _lib.check(_lib.LIB.tallax_sort_rows_ws(
             k0.data_ptr(), _lib.dtype_code(k0), rows, cols, int(bool(descending)), int(ties_desc), None,
-            perm.data_ptr(), out0.data_ptr(), _lib.dtype_code(out0), None, 0, None, 0, stream), "sort")
+            perm.data_ptr(), out0.data_ptr(), _lib.dtype_code(out0), None, 0, None, 0, ws_ptr, nws, stream), "sort")
     else:  # stable LSD passes: by key 1, then by key 0 with position ties
         k1 = ops[1]
         perm1 = torch.empty(shape, dtype=torch.int32, device=dev)
-        _lib.check(_lib.LIB.tallax_sort_rows(
+        _lib.check(_lib.LIB.tallax_sort_rows_ws(
             k1.data_ptr(), _lib.dtype_code(k1), rows, cols, int(bool(descending)), 0, None, perm1.data_ptr(),
-            None, 0, None, 0, None, 0, stream), "sort")
+            None, 0, None, 0, None, 0, ws_ptr, nws, stream), "sort")
         out1 = torch.empty(shape, dtype=key_out_dtype(k1), device=dev)
-        _lib.check(_lib.LIB.tallax_sort_rows(
+        _lib.check(_lib.LIB.tallax_sort_rows_ws(
             k0.data_ptr(), _lib.dtype_code(k0), rows, cols, int(bool(descending)), 0, perm1.data_ptr(),
             perm.data_ptr(), out0.data_ptr(), _lib.dtype_code(out0), k1.data_ptr(), _lib.dtype_code(k1),
-            out1.data_ptr(), _lib.dtype_code(out1), stream), "sort")
+            out1.data_ptr(), _lib.dtype_code(out1), ws_ptr, nws, stream), "sort")
         outs[1] = out1
     outs[0] = out0
     for i in range(num_keys, len(ops)):

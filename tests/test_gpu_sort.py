@@ -127,3 +127,104 @@ def test_tumpy_axes_and_errors(gpu):
         tax.sort([xd[0], xd[1, :2]], num_keys=1)
     with pytest.raises(ValueError):
         tax.sort(xd, num_keys=1)   # 3D
+
+
+# Rows longer than 16384 (the reference's HBM substage route, sort.py:574-758):
+# chunk sorts + merge passes through the workspace.  1, 2, 3 and 5 merge
+# passes; ragged last chunks; the packed bf16 route up to 65536.
+WIDE_COLS = [16385, 32768, 50001, 65536, 65537, 262147]
+WIDE_MODES = [(False, True, True), (True, True, True), (True, False, True), (False, False, False)]
+
+
+@pytest.mark.parametrize("cols", WIDE_COLS)
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "i32"])
+@pytest.mark.parametrize("descending,stable,argsort", WIDE_MODES)
+def test_sort_wide_rows(gpu, cols, dtype, descending, stable, argsort):
+    from tallax_amd import tax
+    _log(f"wide sort {dtype} cols={cols} desc={descending} stable={stable} argsort={argsort}")
+    rng = np.random.default_rng(cols + 7 * descending + 3 * stable)
+    rows = 3
+    if dtype == "i32":
+        x = rng.integers(-50, 50, (rows, cols)).astype(np.int32)
+        x[0] = rng.integers(-2**31, 2**31, cols, dtype=np.int64).astype(np.int32)
+        xd = torch.from_numpy(x).to(gpu)
+        host = x
+    else:
+        x = np.round(rng.standard_normal((rows, cols)) * 8).astype(np.float32) / 8
+        x[1] = _special_row(rng, cols)
+        x[2, : cols // 2] = 0.5  # a long run of ties across chunk boundaries
+        xd = to_dev(x, dtype, gpu)
+        host = O.round_to_dtype(x, dtype)
+    got = tax.sort(xd, num_keys=1, is_stable=stable, return_argsort=argsort, descending=descending)
+    torch.cuda.synchronize()
+    want, path = O.sort([host], 1, is_stable=stable, return_argsort=argsort, descending=descending,
+                        dtypes=[dtype])
+    assert len(got) == len(want)
+    if dtype == "bf16":
+        assert got[0].dtype == (torch.bfloat16 if path == "packed" else torch.float32)
+    for g, w in zip(got, want):
+        assert _same(_host(g), w)
+
+
+def test_sort_wide_constant_and_nan_rows(gpu):
+    from tallax_amd import tax
+    cols = 40000
+    x = np.zeros((3, cols), np.float32)
+    x[0] = 1.25
+    x[1] = np.nan
+    x[2, ::2] = -0.0
+    xd = torch.from_numpy(x).to(gpu)
+    for desc in (False, True):
+        got = tax.sort(xd, num_keys=1, is_stable=True, return_argsort=True, descending=desc)
+        torch.cuda.synchronize()
+        want, _ = O.sort([x], 1, is_stable=True, return_argsort=True, descending=desc)
+        for g, w in zip(got, want):
+            assert _same(_host(g), w)
+        assert np.array_equal(got[1][0].cpu().numpy(), np.arange(cols, dtype=np.int32))
+
+
+def test_sort_wide_prefill_shape_descending(gpu):
+    """The reference's route for config 5's sort: softmax probabilities of a
+    201088-wide row, descending argsort (sort.py:843 pads at the front)."""
+    from tallax_amd import tax
+    rng = np.random.default_rng(6)
+    z = (rng.standard_normal((2, 201088)) * 2).astype(np.float32)
+    p = np.exp(z - z.max(axis=1, keepdims=True))
+    p = (p / p.sum(axis=1, keepdims=True)).astype(np.float32)
+    got = tax.sort(torch.from_numpy(p).to(gpu), num_keys=1, is_stable=True, return_argsort=True, descending=True)
+    torch.cuda.synchronize()
+    want, _ = O.sort([p], 1, is_stable=True, return_argsort=True, descending=True)
+    for g, w in zip(got, want):
+        assert _same(_host(g), w)
+
+
+@pytest.mark.parametrize("descending", [False, True])
+def test_sort_wide_two_keys_with_payloads(gpu, descending):
+    from tallax_amd import tax
+    rng = np.random.default_rng(19)
+    rows, cols = 2, 70000
+    k0 = rng.integers(0, 4, (rows, cols)).astype(np.int32)
+    k1 = np.round(rng.standard_normal((rows, cols)) * 2).astype(np.float32) / 2
+    k1[0, ::13] = np.nan
+    pay_f = rng.standard_normal((rows, cols)).astype(np.float32)
+    pay_b = rng.standard_normal((rows, cols)).astype(np.float32)
+    ops = [torch.from_numpy(k0).to(gpu), torch.from_numpy(k1).to(gpu), torch.from_numpy(pay_f).to(gpu),
+           to_dev(pay_b, "bf16", gpu)]
+    got = tax.sort(ops, num_keys=2, return_argsort=True, descending=descending)
+    torch.cuda.synchronize()
+    want, _ = O.sort([k0, k1, pay_f, O.round_to_dtype(pay_b, "bf16")], 2, return_argsort=True,
+                     descending=descending, dtypes=["i32", "f32", "f32", "bf16"])
+    for g, w in zip(got, want):
+        assert _same(_host(g), w)
+
+
+def test_tumpy_flattened_wide(gpu):
+    from tallax_amd import tumpy
+    rng = np.random.default_rng(23)
+    x = np.round(rng.standard_normal((4, 30000)) * 4).astype(np.float32) / 4
+    xd = torch.from_numpy(x).to(gpu)
+    a = tumpy.argsort(xd, axis=None)
+    s = tumpy.sort(xd, axis=None)
+    torch.cuda.synchronize()
+    assert np.array_equal(a.cpu().numpy(), np.argsort(x.reshape(-1), kind="stable"))
+    assert np.array_equal(s.cpu().numpy(), np.sort(x.reshape(-1)))
