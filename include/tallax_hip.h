@@ -118,6 +118,19 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
                                   tallax_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Top-p mask over already-selected, descending candidates, along axis 0.
+ * Replaces top_p_mask(*, topk_logits, p, replace_val, axis=0) --
+ * tallax/_src/sampling.py:25-62: probs = exp(l - l[0]) / sum, inclusive
+ * cumsum in the (8, 128)-tile order of cumsum_arrays (cumsum.py:32-63),
+ * t = #(cumsum < p), threshold l[t] (0.0 when t == k, the out-of-range
+ * gather), keep l >= threshold, replace_val elsewhere.
+ * topk_logits, out [k, cols] f32 (column b sorted descending); top_p [cols]
+ * f32; 1 <= k <= 128 (the sampler's candidate count, sampling.py:283-290).
+ * ---------------------------------------------------------------------- */
+int tallax_top_p_mask(const float* topk_logits, int64_t k, int64_t cols, const float* top_p, double replace_val,
+                      float* out, tallax_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Top-p filter + temperature + Gumbel-max sampling over already-selected,
  * descending candidates.
  * Replaces top_p_and_sample(topk_logits, topk_idx, rng_key, top_p,

@@ -850,6 +850,30 @@ __global__ __launch_bounds__(kWave) void top_p_sample_kernel(const void* logits,
   if (l == 0) out[row] = tok;
 }
 
+// Standalone top_p_mask (sampling.py:25-62), axis 0: f32 candidates
+// [K, cols] sorted descending down each column, K <= 128; one wave per column
+// (position p = h * 64 + lane).  Keeps v >= the threshold of top_p_threshold,
+// writes replace_f32 elsewhere.
+__global__ __launch_bounds__(kWave) void top_p_mask_kernel(const float* logits, int64_t cols, int K,
+                                                           const float* top_p, float replace_f32, float* out) {
+  const int64_t b = blockIdx.x;
+  const int l = lane_id();
+  float v[2], e[2];
+  const float v0 = logits[b];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int p = h * kWave + l;
+    v[h] = p < K ? logits[(int64_t)p * cols + b] : 0.0f;
+    e[h] = p < K ? candidate_exp(v[h], v0) : 0.0f;
+  }
+  const float thr = top_p_threshold(v, e, K, top_p[b]);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int p = h * kWave + l;
+    if (p < K) out[(int64_t)p * cols + b] = v[h] >= thr ? v[h] : replace_f32;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
@@ -1156,6 +1180,18 @@ int tallax_top_p_and_sample(const void* topk_logits, int dtype, const int32_t* t
                        topk_idx, rows, (int)k, rng_key, top_p, temperature, (uint32_t)vocab_size, rf,
                        dim0_offset, out_tokens);
   return launch_status("tallax_top_p_and_sample");
+}
+
+int tallax_top_p_mask(const float* topk_logits, int64_t k, int64_t cols, const float* top_p, double replace_val,
+                      float* out, hipStream_t stream) {
+  if (!topk_logits || !top_p || !out) { set_error("null pointer argument"); return kInvalidArgument; }
+  if (k < 1 || cols < 0) { set_error("bad extents k=%lld cols=%lld", (long long)k, (long long)cols); return kInvalidArgument; }
+  if (k > kMaxK) { set_error("k=%lld > 128 candidates per column is not supported", (long long)k); return kUnsupported; }
+  if (cols > 2147483647) { set_error("too many columns"); return kUnsupported; }
+  if (cols == 0) return kOk;
+  hipLaunchKernelGGL(top_p_mask_kernel, dim3((unsigned)cols), dim3(kWave), 0, stream, topk_logits, cols, (int)k,
+                     top_p, (float)replace_val, out);
+  return launch_status("tallax_top_p_mask");
 }
 
 }  // extern "C"

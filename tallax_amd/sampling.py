@@ -4,7 +4,7 @@
 does the per-row top-k (clamped to 128, as the reference's max_k=128), the
 top-p filter, temperature and Gumbel-max draw.  `top_p_and_sample`
 (sampling.py:210-269) runs the same tail on candidates the caller already
-selected.
+selected, and `top_p_mask` (sampling.py:25-62) only its top-p filter.
 
 Operands are torch tensors on a ROCm device; the rng key is the two uint32
 words of a threefry key (what `jax.random.key_data(key)` holds), as a device
@@ -80,6 +80,34 @@ def sample(rng_key: Any, logits: torch.Tensor, tpu_sampling_metadata: Any,
     return out
 
 
+def top_p_mask(*, topk_logits: torch.Tensor, p: Any, replace_val: float, axis: int) -> torch.Tensor:
+    """Top-p filter of descending candidates along axis 0.
+
+    Reference: top_p_mask(*, topk_logits, p, replace_val, axis)
+    (sampling.py:25-62).  topk_logits [k, B] float32, each column sorted
+    descending, k <= 128 (the sampler's candidate count); p a scalar or [B].
+    probs = softmax down each column, inclusive cumsum in the reference's tile
+    order, t = #(cumsum < p); values >= the t-th (0.0 when t == k) are kept,
+    ties included, the rest become replace_val.  Returns a new [k, B] tensor.
+    Raises NotImplementedError for axis != 0, as the reference does.
+    """
+    if axis != 0:
+        raise NotImplementedError("topp_mask only supports axis=0")
+    _lib.require_cuda(topk_logits)
+    if topk_logits.ndim != 2:
+        raise ValueError("topk_logits must be 2D [k, batch]")
+    if topk_logits.dtype != torch.float32:
+        raise NotImplementedError("top_p_mask takes float32 candidates (the sampler casts to float32 first)")
+    k, cols = topk_logits.shape
+    dev = topk_logits.device
+    logits = topk_logits.contiguous()
+    tp = _per_row(p, cols, torch.float32, dev)
+    out = torch.empty_like(logits)
+    _lib.check(_lib.LIB.tallax_top_p_mask(logits.data_ptr(), k, cols, tp.data_ptr(), float(replace_val),
+                                          out.data_ptr(), _lib.stream_of(logits)), "top_p_mask")
+    return out
+
+
 def top_p_and_sample(topk_logits: torch.Tensor, topk_idx: torch.Tensor, rng_key: Any,
                      top_p: Any, temperature: Any, *, vocab_size: int, replace_val: float,
                      interpret: bool = False, dim0_offset: int = 0) -> torch.Tensor:
@@ -120,4 +148,4 @@ class SamplingMetadata:
         self.temperature = temperature
 
 
-__all__: Sequence[str] = ["sample", "top_p_and_sample", "SamplingMetadata"]
+__all__: Sequence[str] = ["sample", "top_p_mask", "top_p_and_sample", "SamplingMetadata"]

@@ -215,3 +215,40 @@ def test_top_p_and_sample_parity(gpu, k, dtype):
     torch.cuda.synchronize()
     want = O.top_p_and_sample(L, I, key, tp, tt, 50000, -1e12)
     assert np.array_equal(tok.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("k", [128, 100, 64, 9, 1])
+def test_top_p_mask_parity(gpu, k):
+    """sampling.top_p_mask (sampling.py:25-62, axis 0) against the oracle, bit
+    for bit: random columns, ties at the threshold, p = 1 (t may reach k: the
+    out-of-range gather keeps everything >= 0.0), tiny p (only the maximum and
+    its ties survive), and a constant column."""
+    from tallax_amd import sampling
+    rng = np.random.default_rng(500 + k)
+    B = 257
+    L = -np.sort(-(np.round(rng.standard_normal((k, B)) * 4) / 4).astype(np.float32), axis=0)
+    L[:, 1] = 0.75  # constant column
+    p = rng.uniform(0.3, 1.0, B).astype(np.float32)
+    p[2], p[3], p[4] = 1.0, np.float32(1e-7), 0.0
+    got = sampling.top_p_mask(topk_logits=torch.from_numpy(L).to(gpu), p=torch.from_numpy(p), replace_val=-1e12,
+                              axis=0)
+    torch.cuda.synchronize()
+    want = O.top_p_mask(L, p, -1e12)
+    assert got.dtype == torch.float32 and tuple(got.shape) == (k, B)
+    assert np.array_equal(got.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    # scalar p broadcasts over the columns
+    got2 = sampling.top_p_mask(topk_logits=torch.from_numpy(L).to(gpu), p=0.9, replace_val=-5.0, axis=0)
+    torch.cuda.synchronize()
+    want2 = O.top_p_mask(L, np.full(B, 0.9, np.float32), -5.0)
+    assert np.array_equal(got2.cpu().numpy().view(np.uint32), want2.view(np.uint32))
+
+
+def test_top_p_mask_errors(gpu):
+    from tallax_amd import sampling
+    x = torch.zeros((8, 4), device=gpu)
+    with pytest.raises(NotImplementedError):
+        sampling.top_p_mask(topk_logits=x, p=0.9, replace_val=0.0, axis=1)
+    with pytest.raises(NotImplementedError):
+        sampling.top_p_mask(topk_logits=torch.zeros((129, 4), device=gpu), p=0.9, replace_val=0.0, axis=0)
+    with pytest.raises(NotImplementedError):
+        sampling.top_p_mask(topk_logits=x.to(torch.bfloat16), p=0.9, replace_val=0.0, axis=0)
