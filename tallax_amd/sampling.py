@@ -12,6 +12,7 @@ tensor of dtype int32/uint32 or a host sequence of two ints.
 """
 from __future__ import annotations
 
+import numbers
 from typing import Any, Sequence
 
 import torch
@@ -37,6 +38,9 @@ def _key_tensor(rng_key: Any, device: torch.device) -> torch.Tensor:
 
 
 def _per_row(v: Any, rows: int, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    if isinstance(v, numbers.Number):
+        # filled on the device: no host-to-device copy, so the call can be graph-captured
+        return torch.full((rows,), v, dtype=dtype, device=device)
     t = v if isinstance(v, torch.Tensor) else torch.tensor(v, dtype=dtype)
     t = t.to(device=device, dtype=dtype)
     if t.ndim == 0:

@@ -7,6 +7,8 @@ keyword arguments of the reference (`interpret`, `block_token`,
 """
 from __future__ import annotations
 
+import numbers
+
 import torch
 
 from . import _lib
@@ -53,6 +55,9 @@ def top_k(logits: torch.Tensor, k: int, block_token: int = 8, num_bins: int = NU
 
 
 def _k_rows(k, rows: int, device) -> torch.Tensor:
+    if isinstance(k, numbers.Integral):
+        # filled on the device: no host-to-device copy, so the call can be graph-captured
+        return torch.full((rows,), int(k), dtype=torch.int32, device=device)
     t = k if isinstance(k, torch.Tensor) else torch.tensor(k, dtype=torch.int32)
     t = t.to(device=device, dtype=torch.int32)
     if t.ndim == 0:
