@@ -53,9 +53,10 @@ namespace tx {
 constexpr int kPfNT = 1024;
 constexpr int kPfNW = kPfNT / kWave;
 constexpr int kPfCapMax = 8192;          // candidate records in LDS, at most
-constexpr int kPfDynBytes = 76 * 1024;   // dynamic LDS: two row workgroups (with their static LDS) per CU
+constexpr int kPfDynBytes = 75 * 1024;   // dynamic LDS: two row workgroups (with their static LDS) per CU
 constexpr int kPfMaxK = 4096;
 constexpr int kPfMaxGroups = 24 * 1024;  // 16-bit group maxima in LDS, 24 per thread at most
+constexpr int kPfMaxBatches = kPfMaxGroups * 4 / (6 * 64) + 1;  // wave-batches of pass 1, at most
 constexpr int kPfBuckets = 512;          // key buckets of the candidate rank sort
 constexpr int kPfRankMax = 128;          // largest bucket the rank sort takes (else bitonic)
 
@@ -132,6 +133,7 @@ void softmax_topk_kernel(PfArgs a) {
   __shared__ int redi[kPfNW];
   __shared__ uint32_t s_t0, s_above;
   __shared__ int s_cnt, s_bin, s_next;
+  __shared__ float s_bmc[kPfMaxBatches], s_bsum[kPfMaxBatches];  // per wave-batch: reference mc, exp-sum
   __shared__ float s_cum_carry[kPfMaxK / 128];
   __shared__ float s_tile_sum[kPfMaxK / 128];
   const int t = threadIdx.x, w = t / kWave, l = lane_id();
@@ -281,10 +283,17 @@ void softmax_topk_kernel(PfArgs a) {
   };
   // SUMM rows: waves claim wave-batches of 6 x 64 vectors (vectors c * 384 +
   // lane + 64 u, all inside the row) from an LDS counter, so that they end
-  // pass 1 together; lane j of a quad holds vector j of a group.
+  // pass 1 together; lane j of a quad holds vector j of a group.  Which wave
+  // takes which batch varies from run to run, so a batch's exp-sum is formed
+  // in the wave (reference mc_c = fl(M_c log2 e) for the batch maximum M_c,
+  // lane sums added in a fixed tree) and kept per batch; the batches are
+  // merged in batch order at the end, so the row's sum does not depend on
+  // the claiming.
   const float ninf = -INFINITY;
-  auto batchW = [&](int32_t base) {
+  float mb = -INFINITY;  // this lane's maximum over its batches
+  auto batchW = [&](int32_t c) {
     constexpr int U = 6;
+    const int32_t base = c * (6 * kWave);
     uint4 q[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) q[u] = rv.base[base + l + kWave * u];
@@ -296,16 +305,24 @@ void softmax_topk_kernel(PfArgs a) {
     float bm = vm[0];
 #pragma unroll
     for (int u = 1; u < U; ++u) bm = raw_max(bm, vm[u]);
-    raise_max(bm);
+    mb = raw_max(mb, bm);
+    float wm = bm;
+#pragma unroll
+    for (int d = kWave / 2; d >= 1; d >>= 1) wm = raw_max(wm, lane_xor_f(wm, d));
+    const float mcc = wm == -INFINITY ? 0.0f : wm * kLog2e;  // -inf elements add exactly 0
     float vs[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      vs[u & 1] += pf_exp(__uint_as_float(q[u].x), mc);
-      vs[u & 1] += pf_exp(__uint_as_float(q[u].y), mc);
-      vs[u & 1] += pf_exp(__uint_as_float(q[u].z), mc);
-      vs[u & 1] += pf_exp(__uint_as_float(q[u].w), mc);
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].x), mcc);
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].y), mcc);
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].z), mcc);
+      vs[u & 1] += pf_exp(__uint_as_float(q[u].w), mcc);
     }
-    s += vs[0] + vs[1];
+    const float bsum = wave_sum_f(vs[0] + vs[1]);  // lane 0's value: a fixed order
+    if (l == 0) {
+      s_bmc[c] = mcc;
+      s_bsum[c] = bsum;
+    }
     float gm[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -323,16 +340,16 @@ void softmax_topk_kernel(PfArgs a) {
       }
     }
   };
+  constexpr int kWB = 6 * kWave;  // vectors of a wave-batch
+  const int c0 = rv.mis ? 1 : 0;  // the first vector holds elements before the row
+  const int cfull = (int)(v_hi / kWB);
   if constexpr (SUMM) {
-    constexpr int kWB = 6 * kWave;  // vectors of a wave-batch
-    const int c0 = rv.mis ? 1 : 0;  // the first vector holds elements before the row
-    const int cfull = (int)(v_hi / kWB);
     for (;;) {
       int c = 0;
       if (l == 0) c = atomicAdd(&s_next, 1);
       c = __builtin_amdgcn_readfirstlane(c) + c0;
       if (c >= cfull) break;
-      batchW(c * kWB);
+      batchW(c);
     }
     // the rest, in chunks of 64 vectors: [0, 384) when the row starts
     // unaligned, and from the last whole wave-batch to the end
@@ -354,7 +371,7 @@ void softmax_topk_kernel(PfArgs a) {
     for (; i + kPfNT <= v_hi; i += kPfNT) batch1(i, std::integral_constant<int, 1>());
     for (; i < nv; i += kPfNT) step1(i + t);
   }
-  float M = m;
+  float M = fmaxf(m, mb);
 #pragma unroll
   for (int d = kWave / 2; d >= 1; d >>= 1) M = fmaxf(M, lane_xor_f(M, d));
   if (l == 0) redf[w] = M;
@@ -377,6 +394,13 @@ void softmax_topk_kernel(PfArgs a) {
   // the exp-sum: thread sums rescaled to the row maximum (a thread that saw
   // only -inf / dead slots contributes 0, or its NaN)
   s = m == -INFINITY ? s : s * __builtin_amdgcn_exp2f(mc - mcM);
+  if constexpr (SUMM) {
+    // the wave-batch sums, rescaled the same way, each thread taking batches in a fixed order
+    for (int c = c0 + t; c < cfull; c += kPfNT) {
+      const float bsum = s_bsum[c];
+      s += bsum != 0.0f ? bsum * __builtin_amdgcn_exp2f(s_bmc[c] - mcM) : bsum;
+    }
+  }
 
   if constexpr (SUMM) {
     // the k-th largest group prefix: top byte from the histogram, low byte
