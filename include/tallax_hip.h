@@ -118,6 +118,32 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
                                   tallax_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Vocabulary-sharded sampling, the two compute steps of the reference's
+ * partitioned sampler (tallax/_src/sampling.py:300-321: per-shard
+ * _top_k_arrays(logits, 128), indices to the global frame, all_gather, then
+ * bitonic_top_k of the gathered lists, the k mask and top_p_and_sample).
+ * tallax_shard_candidates: the shard x [rows, cols] (f32/bf16, cols >= 128,
+ * its first column is global column col_offset) -> candidates [rows, 128]
+ * u64, its sorted top-128 as composites (select key << 32 | ~global column;
+ * larger = earlier, ties to the lowest column).  Workspace:
+ * tallax_shard_candidates_workspace_size bytes (0 for whole-row plans).
+ * tallax_sample_from_candidates: candidates [rows, nlists, 128] u64 (the
+ * lists of nlists <= 32 shards side by side per row, i.e. what an all-gather
+ * along axis 1 gives) -> out_tokens [rows] int32: their merged top-128 (the
+ * global top-128, ties to the lowest column), positions >= top_k[row]
+ * replaced by replace_val in the logits dtype, then the sampler tail with
+ * vocab = the total vocabulary.  The tokens equal tallax_fused_topk_topp_sample
+ * on the unsharded logits.
+ * ---------------------------------------------------------------------- */
+size_t tallax_shard_candidates_workspace_size(int64_t rows, int64_t cols, int dtype);
+int tallax_shard_candidates(const void* x, int dtype, int64_t rows, int64_t cols, int64_t col_offset,
+                            uint64_t* candidates, void* workspace, size_t workspace_bytes, tallax_stream_t stream);
+int tallax_sample_from_candidates(const uint64_t* candidates, int64_t nlists, int dtype, int64_t rows,
+                                  int64_t vocab, const int32_t* top_k, const float* top_p, const float* temperature,
+                                  const uint32_t* rng_key, int64_t dim0_offset, double replace_val,
+                                  int32_t* out_tokens, tallax_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Top-p mask over already-selected, descending candidates, along axis 0.
  * Replaces top_p_mask(*, topk_logits, p, replace_val, axis=0) --
  * tallax/_src/sampling.py:25-62: probs = exp(l - l[0]) / sum, inclusive

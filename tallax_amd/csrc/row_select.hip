@@ -71,6 +71,8 @@ struct SelArgs {
   // segment lists: rows * nseg * kRun composites
   uint64_t* ws_lists;
   int lists_only;  // write the segment list even when a row is one segment
+  int64_t col_offset;   // added to every column index of a written list (a vocabulary shard's first column)
+  uint64_t* out_lists;  // merge kernel, lists_only: the merged list of each row, [rows][128]
   // sampler
   const int32_t* top_k;
   const float* top_p;
@@ -389,8 +391,8 @@ template <int DT, bool SAMPLE>
 __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list, float* sg) {
   using T = ElemT<DT>;
   const uint32_t inel = ineligible_key_max(DT);
-  const char* rowp = (const char*)a.x + (size_t)(row * a.cols) * T::ES;
   if (!SAMPLE) {
+    const char* rowp = (const char*)a.x + (size_t)(row * a.cols) * T::ES;
     for (int i = threadIdx.x; i < a.k; i += blockDim.x) {
       const uint64_t c = list[i];
       const uint32_t kk = comp_key(c);
@@ -768,7 +770,8 @@ void seg_select_kernel(SelArgs a) {
     finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_g);
   } else {
     uint64_t* dst = a.ws_lists + ((size_t)row * a.nseg + seg) * kRun;
-    for (int i = tid; i < kRun; i += NT) dst[i] = sh.list64[i];
+    // ~(idx + off) = ~idx - off without a borrow into the key (idx + off < 2^31); empty slots stay 0
+    for (int i = tid; i < kRun; i += NT) dst[i] = sh.list64[i] ? sh.list64[i] - (uint64_t)a.col_offset : 0ull;
   }
 }
 
@@ -818,6 +821,10 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge_kernel(SelArgs a) {
     tree[0][kWave + l] = acc[1];
   }
   __syncthreads();
+  if (!SAMPLE && a.lists_only) {  // the row's merged list (already in the shard's column frame)
+    for (int i = threadIdx.x; i < kRun; i += kMergeNT) a.out_lists[(size_t)row * kRun + i] = tree[0][i];
+    return;
+  }
   finalize_row<DT, SAMPLE>(a, row, tree[0], sg);
 }
 
@@ -1144,6 +1151,66 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
   a.out_tokens = out_tokens;
   return dtype == kF32 ? launch_select<kF32, true>(a, p, stream, "tallax_fused_topk_topp_sample")
                        : launch_select<kBF16, true>(a, p, stream, "tallax_fused_topk_topp_sample");
+}
+
+size_t tallax_shard_candidates_workspace_size(int64_t rows, int64_t cols, int dtype) {
+  return tallax_topk_workspace_size(rows, cols, kMaxK, dtype);
+}
+
+int tallax_shard_candidates(const void* x, int dtype, int64_t rows, int64_t cols, int64_t col_offset,
+                            uint64_t* candidates, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int st = check_common(x, dtype, rows, cols);
+  if (st) return st;
+  if (cols < kMaxK) { set_error("a shard of %lld < 128 columns is not supported", (long long)cols); return kUnsupported; }
+  if (col_offset < 0 || col_offset + cols >= (int64_t)1 << 31) { set_error("column offset %lld out of range", (long long)col_offset); return kInvalidArgument; }
+  if (!candidates) { set_error("null pointer argument"); return kInvalidArgument; }
+  if (rows == 0) return kOk;
+  Plan p;
+  st = plan_rows(rows, cols, dtype, &p);
+  if (st) return st;
+  const size_t need = ws_bytes_for(rows, p);
+  if (workspace_bytes < need || (need && !workspace)) {
+    set_error("workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
+    return kWorkspaceTooSmall;
+  }
+  SelArgs a = {};
+  a.x = x; a.rows = rows; a.cols = cols; a.k = kMaxK;
+  a.nseg = p.nseg; a.vps = p.vps;
+  a.lists_only = 1;
+  a.col_offset = col_offset;
+  // one segment: the segment kernel writes the row's list itself; more: per-segment
+  // lists in the workspace, merged into the output by the merge kernel
+  a.ws_lists = p.nseg == 1 ? candidates : (uint64_t*)workspace;
+  a.out_lists = candidates;
+  return dtype == kF32 ? launch_select<kF32, false>(a, p, stream, "tallax_shard_candidates")
+                       : launch_select<kBF16, false>(a, p, stream, "tallax_shard_candidates");
+}
+
+int tallax_sample_from_candidates(const uint64_t* candidates, int64_t nlists, int dtype, int64_t rows,
+                                  int64_t vocab, const int32_t* top_k, const float* top_p, const float* temperature,
+                                  const uint32_t* rng_key, int64_t dim0_offset, double replace_val,
+                                  int32_t* out_tokens, hipStream_t stream) {
+  if (!candidates || !top_k || !top_p || !temperature || !rng_key || !out_tokens) { set_error("null pointer argument"); return kInvalidArgument; }
+  if (dtype != kF32 && dtype != kBF16) { set_error("dtype %d not supported (f32=0, bf16=1)", dtype); return kUnsupported; }
+  if (nlists < 1 || nlists > kMaxSeg) { set_error("%lld candidate lists per row: 1 to %d are supported", (long long)nlists, kMaxSeg); return nlists < 1 ? kInvalidArgument : kUnsupported; }
+  if (rows < 0 || vocab < kMaxK || vocab >= (int64_t)1 << 31) { set_error("bad shape: rows %lld, vocab %lld", (long long)rows, (long long)vocab); return kInvalidArgument; }
+  if (rows > 2147483647) { set_error("too many rows"); return kUnsupported; }
+  if (rows == 0) return kOk;
+  SelArgs a = {};
+  a.rows = rows; a.cols = vocab; a.k = kMaxK;
+  a.nseg = (int)nlists;
+  a.ws_lists = const_cast<uint64_t*>(candidates);
+  a.top_k = top_k; a.top_p = top_p; a.temperature = temperature; a.rng_key = rng_key;
+  a.dim0_offset = dim0_offset;
+  const float rf = (float)replace_val;
+  a.replace_f32 = rf;
+  a.replace_in_dtype = dtype == kBF16 ? round_to_bf16(rf) : rf;
+  a.out_tokens = out_tokens;
+  if (dtype == kF32)
+    hipLaunchKernelGGL((seg_merge_kernel<kF32, true>), dim3((unsigned)rows), dim3(kMergeNT), 0, stream, a);
+  else
+    hipLaunchKernelGGL((seg_merge_kernel<kBF16, true>), dim3((unsigned)rows), dim3(kMergeNT), 0, stream, a);
+  return launch_status("tallax_sample_from_candidates");
 }
 
 int tallax_testing_select_plan(int64_t rows, int64_t cols, int dtype, int32_t* out) {

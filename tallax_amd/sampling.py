@@ -20,6 +20,7 @@ import torch
 from . import _lib
 
 _SAMPLING_EPS = 1e-5  # sampling.py:22
+NUM_CANDIDATES = 128  # the sampler's top-k width, max_k = NUM_LANES (sampling.py:283-290)
 
 
 def _key_tensor(rng_key: Any, device: torch.device) -> torch.Tensor:
@@ -143,6 +144,63 @@ def top_p_and_sample(topk_logits: torch.Tensor, topk_idx: torch.Tensor, rng_key:
     return out
 
 
+def sample_sharded(rng_key: Any, logit_shards: Sequence[torch.Tensor], tpu_sampling_metadata: Any,
+                   *, replace_val: float = -1e12, dim0_offset: int = 0) -> torch.Tensor:
+    """`sample` over a vocabulary split into column shards, computed the way the
+    reference's partitioned sampler does it, with every shard on this GPU.
+
+    Reference: _top_k_with_sharding's partition (sampling.py:300-321) followed
+    by top_p_and_sample (sampling.py:331-343).  Each shard [B, V_i] (V_i >= 128,
+    consecutive column ranges in order) gives its sorted top-128 as composites
+    in the global column frame (tallax_shard_candidates); the per-shard lists
+    are stacked side by side (what the all-gather of a multi-GPU run
+    delivers: [B, n, 128]); one kernel merges them into the global top-128
+    (ties to the lowest global column, as in `sample`), writes replace_val
+    (in the logits dtype) at positions >= top_k[row] and runs the sampler tail
+    with vocab_size = sum(V_i) (tallax_sample_from_candidates).  The tokens
+    equal `sample` on the concatenated logits.  Here every shard's step runs
+    on this GPU at its real shape; in a multi-GPU run each GPU runs only its
+    own, and the stacking is the collective.  At most 32 shards.
+    """
+    shards = list(logit_shards)
+    if not shards:
+        raise ValueError("sample_sharded needs at least one shard")
+    if len(shards) > 32:
+        raise NotImplementedError(f"{len(shards)} shards: at most 32 are supported")
+    _lib.require_cuda(*shards)
+    rows = shards[0].shape[0]
+    for x in shards:
+        if x.ndim != 2 or x.shape[0] != rows or x.dtype != shards[0].dtype or x.device != shards[0].device:
+            raise ValueError("shards must be 2D [B, V_i] of one dtype and device with the same B")
+    dev = shards[0].device
+    dt = _lib.dtype_code(shards[0])
+    if dt == _lib.I32:
+        raise NotImplementedError("sample_sharded needs float logits")
+    stream = _lib.stream_of(shards[0])
+    lists, off = [], 0
+    for x in shards:
+        xc = x.contiguous()
+        cols = xc.shape[1]
+        need = _lib.LIB.tallax_shard_candidates_workspace_size(rows, cols, dt)
+        ws = _lib.workspace(dev, need)
+        cand = torch.empty((rows, NUM_CANDIDATES), dtype=torch.int64, device=dev)
+        _lib.check(_lib.LIB.tallax_shard_candidates(xc.data_ptr(), dt, rows, cols, off, cand.data_ptr(),
+                                                    ws.data_ptr() if need else None, ws.numel() if need else 0,
+                                                    stream), "sample_sharded (shard)")
+        lists.append(cand)
+        off += cols
+    gathered = torch.stack(lists, 1)  # [B, n, 128]: the all-gather of a multi-GPU run
+    top_k = _per_row(tpu_sampling_metadata.top_k, rows, torch.int32, dev)
+    top_p = _per_row(tpu_sampling_metadata.top_p, rows, torch.float32, dev)
+    temp = _per_row(tpu_sampling_metadata.temperature, rows, torch.float32, dev)
+    key = _key_tensor(rng_key, dev)
+    out = torch.empty(rows, dtype=torch.int32, device=dev)
+    _lib.check(_lib.LIB.tallax_sample_from_candidates(
+        gathered.data_ptr(), len(shards), dt, rows, off, top_k.data_ptr(), top_p.data_ptr(), temp.data_ptr(),
+        key.data_ptr(), int(dim0_offset), float(replace_val), out.data_ptr(), stream), "sample_sharded (merge)")
+    return out
+
+
 class SamplingMetadata:
     """Minimal stand-in for vLLM's TPU sampling metadata (.top_k/.top_p/.temperature)."""
 
@@ -152,4 +210,4 @@ class SamplingMetadata:
         self.temperature = temperature
 
 
-__all__: Sequence[str] = ["sample", "top_p_mask", "top_p_and_sample", "SamplingMetadata"]
+__all__: Sequence[str] = ["sample", "sample_sharded", "top_p_mask", "top_p_and_sample", "SamplingMetadata"]

@@ -252,3 +252,32 @@ def test_top_p_mask_errors(gpu):
         sampling.top_p_mask(topk_logits=torch.zeros((129, 4), device=gpu), p=0.9, replace_val=0.0, axis=0)
     with pytest.raises(NotImplementedError):
         sampling.top_p_mask(topk_logits=x.to(torch.bfloat16), p=0.9, replace_val=0.0, axis=0)
+
+
+@pytest.mark.parametrize("rows,vocab,dtype,widths", [
+    (256, 128256, "bf16", [128256 // 8] * 8),           # 8-way vocab split of config 4: [256, 16032] shards
+    (256, 128256, "bf16", [64128, 64128]),
+    (64, 50000, "f32", [20000, 129, 29871]),            # uneven, a shard barely over 128 columns
+    (32, 32000, "bf16", [32000]),
+])
+def test_sample_sharded_equals_sample(gpu, rows, vocab, dtype, widths):
+    """The vocabulary-sharded composition (per-shard top-128, global indices,
+    concatenation, top-128 merge, k mask, tail: sampling.py:300-321) gives the
+    tokens of the unsharded sampler and of the oracle."""
+    from tallax_amd import sampling
+    assert sum(widths) == vocab
+    x, temp, topk, topp = _sampler_inputs(rows, vocab, seed=rows + len(widths))
+    x[1, :] = 0.5                          # a constant row: ties across shards go to the lowest index
+    x[2, ::1000] = 9.0                     # equal maxima in several shards
+    temp[::13] = 1e-6                      # greedy rows
+    meta = sampling.SamplingMetadata(torch.from_numpy(topk), torch.from_numpy(topp), torch.from_numpy(temp))
+    full = to_dev(x, dtype, gpu)
+    bounds = np.cumsum([0] + widths)
+    shards = [full[:, bounds[i]:bounds[i + 1]].contiguous() for i in range(len(widths))]
+    key = torch.tensor([7, 99], dtype=torch.int32, device=gpu)
+    got = sampling.sample_sharded(key, shards, meta, dim0_offset=5)
+    want = sampling.sample(key, full, meta, dim0_offset=5)
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), want.cpu().numpy())
+    ref = O.sample((7, 99), host_values(x, dtype), topk, topp, temp, dtype=dtype, dim0_offset=5)
+    assert np.array_equal(got.cpu().numpy(), ref)
