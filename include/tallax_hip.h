@@ -219,6 +219,12 @@ int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols,
                      int key_out_dtype, const void* aux, int aux_dtype, void* aux_out, int aux_out_dtype,
                      tallax_stream_t stream);
 size_t tallax_sort_rows_workspace_size(int64_t rows, int64_t cols);
+/* The third and later keys of a multi-key sort (sort.py:912-919 decodes every
+ * key operand): out[r, j] = key[r, perm[r, j]] standardised and decoded as
+ * key_out is (out_dtype as for key_out).  perm [rows, cols] int32 from
+ * tallax_sort_rows; a column outside the row gives 0. */
+int tallax_gather_sort_key(const void* key, int key_dtype, int64_t rows, int64_t cols, const int32_t* perm,
+                           void* out, int out_dtype, tallax_stream_t stream);
 int tallax_sort_rows_ws(const void* key, int key_dtype, int64_t rows, int64_t cols, int descending,
                         int ties_descending, const int32_t* perm_in, int32_t* perm_out, void* key_out,
                         int key_out_dtype, const void* aux, int aux_dtype, void* aux_out, int aux_out_dtype,

@@ -45,6 +45,7 @@ _SIGNATURES = {
     "tallax_sort_rows": ([_c_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _c_p, _c_p, _c_p, _c_int, _c_p, _c_int,
                           _c_p, _c_int, _c_p], _c_int),
     "tallax_sort_rows_workspace_size": ([_c_i64, _c_i64], _c_sz),
+    "tallax_gather_sort_key": ([_c_p, _c_int, _c_i64, _c_i64, _c_p, _c_p, _c_int, _c_p], _c_int),
     "tallax_sort_rows_ws": ([_c_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _c_p, _c_p, _c_p, _c_int, _c_p, _c_int,
                              _c_p, _c_int, _c_p, _c_sz, _c_p], _c_int),
     "tallax_topk_replace": ([_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_p, _c_d, _c_p, _c_p, _c_p, _c_sz, _c_p], _c_int),

@@ -245,6 +245,25 @@ __global__ __launch_bounds__(kRadixNT) void radix_sort_rows_kernel(SortArgs a) {
   }
 }
 
+// out[i] = the key at column perm[i] of the same row, standardised and
+// decoded like the sorted key outputs (store_sorted): the third and later
+// keys of a multi-key sort.  A column outside the row gives 0 bits.
+__global__ __launch_bounds__(256) void gather_sort_key_kernel(const void* key, int key_dtype, int64_t cols,
+                                                              const int32_t* perm, void* out, int out_dtype,
+                                                              int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const int64_t base = i / cols * cols;
+    const int32_t src = perm[i];
+    if (src >= 0 && src < cols) {
+      store_sorted(out, out_dtype, key_dtype, i, sort_order_bits(key, key_dtype, base + src));
+    } else if (out_dtype == kBF16) {
+      ((uint16_t*)out)[i] = 0;
+    } else {
+      ((uint32_t*)out)[i] = 0u;
+    }
+  }
+}
+
 template <int E>
 static int launch_radix(const SortArgs& a, int64_t rows, hipStream_t s) {
   const size_t lds = (size_t)8 * kRadixNT * 4 + (size_t)a.cols * 4;
@@ -332,6 +351,21 @@ int tallax_sort_rows_ws(const void* key, int key_dtype, int64_t rows, int64_t co
                         : launch_sort_p<uint64_t>(a, rows, stream);
   if (st) return st;
   return launch_status("tallax_sort_rows");
+}
+
+int tallax_gather_sort_key(const void* key, int key_dtype, int64_t rows, int64_t cols, const int32_t* perm,
+                           void* out, int out_dtype, hipStream_t stream) {
+  if (!key || !perm || !out) { set_error("null pointer argument"); return kInvalidArgument; }
+  if (key_dtype != kF32 && key_dtype != kBF16 && key_dtype != kI32) { set_error("dtype %d not supported", key_dtype); return kUnsupported; }
+  const bool ok = key_dtype == kBF16 ? (out_dtype == kBF16 || out_dtype == kF32) : out_dtype == key_dtype;
+  if (!ok) { set_error("out dtype %d invalid for key dtype %d", out_dtype, key_dtype); return kInvalidArgument; }
+  if (rows < 0 || cols < 0) { set_error("negative extent"); return kInvalidArgument; }
+  const int64_t n = rows * cols;
+  if (n == 0) return kOk;
+  const int64_t blocks = (n + 255) / 256 < ((int64_t)1 << 20) ? (n + 255) / 256 : ((int64_t)1 << 20);
+  hipLaunchKernelGGL(gather_sort_key_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, key, key_dtype, cols,
+                     perm, out, out_dtype, n);
+  return launch_status("tallax_gather_sort_key");
 }
 
 int tallax_sort_rows(const void* key, int key_dtype, int64_t rows, int64_t cols, int descending,

@@ -157,8 +157,8 @@ def sort(operand, num_keys: int, is_stable: bool = False, return_argsort: bool =
       * non-key operands are permuted unchanged; with return_argsort the
         int32 indices are appended last.
     Non-stable ties are ordered by ascending index (the reference leaves that
-    order to its network).  Keys: float32, bfloat16, int32; up to two keys;
-    rows of any length below 2^31.  Rows longer than 16384 elements (the
+    order to its network).  Keys: float32, bfloat16, int32, any number of
+    them; rows of any length below 2^31.  Rows longer than 16384 elements (the
     reference's HBM substage route, sort.py:574-758) are sorted in chunks and
     merged through a device workspace of 8 or 16 bytes per element.
     `num_vmem_substages`, `block_token` and `interpret` are TPU tuning knobs,
@@ -178,8 +178,6 @@ def sort(operand, num_keys: int, is_stable: bool = False, return_argsort: bool =
     num_keys = int(num_keys)
     if not 1 <= num_keys <= len(operands):
         raise ValueError(f"num_keys={num_keys} must be in [1, {len(operands)}]")
-    if num_keys > 2:
-        raise NotImplementedError("more than two sort keys")
     for x in operands:
         if x.dtype not in _SORT_DTYPES:
             raise NotImplementedError(f"sort operand dtype {x.dtype}")
@@ -211,18 +209,33 @@ def sort(operand, num_keys: int, is_stable: bool = False, return_argsort: bool =
         _lib.check(_lib.LIB.tallax_sort_rows_ws(
             k0.data_ptr(), _lib.dtype_code(k0), rows, cols, int(bool(descending)), int(ties_desc), None,
             perm.data_ptr(), out0.data_ptr(), _lib.dtype_code(out0), None, 0, None, 0, ws_ptr, nws, stream), "sort")
-    else:  # stable LSD passes: by key 1, then by key 0 with position ties
+    else:
+        # stable LSD passes, last key first; each pass sorts key[perm] with
+        # position ties and composes, so the final permutation orders the rows
+        # lexicographically by all keys, ties by ascending index
+        prev = None
+        for i in range(num_keys - 1, 0, -1):
+            ki = ops[i]
+            pi = torch.empty(shape, dtype=torch.int32, device=dev)
+            _lib.check(_lib.LIB.tallax_sort_rows_ws(
+                ki.data_ptr(), _lib.dtype_code(ki), rows, cols, int(bool(descending)), 0,
+                prev.data_ptr() if prev is not None else None, pi.data_ptr(), None, 0, None, 0, None, 0, ws_ptr, nws,
+                stream), "sort")
+            prev = pi
         k1 = ops[1]
-        perm1 = torch.empty(shape, dtype=torch.int32, device=dev)
-        _lib.check(_lib.LIB.tallax_sort_rows_ws(
-            k1.data_ptr(), _lib.dtype_code(k1), rows, cols, int(bool(descending)), 0, None, perm1.data_ptr(),
-            None, 0, None, 0, None, 0, ws_ptr, nws, stream), "sort")
         out1 = torch.empty(shape, dtype=key_out_dtype(k1), device=dev)
         _lib.check(_lib.LIB.tallax_sort_rows_ws(
-            k0.data_ptr(), _lib.dtype_code(k0), rows, cols, int(bool(descending)), 0, perm1.data_ptr(),
+            k0.data_ptr(), _lib.dtype_code(k0), rows, cols, int(bool(descending)), 0, prev.data_ptr(),
             perm.data_ptr(), out0.data_ptr(), _lib.dtype_code(out0), k1.data_ptr(), _lib.dtype_code(k1),
             out1.data_ptr(), _lib.dtype_code(out1), ws_ptr, nws, stream), "sort")
         outs[1] = out1
+        for i in range(2, num_keys):  # further keys: gathered by the final permutation, decoded like keys
+            ki = ops[i]
+            oi = torch.empty(shape, dtype=key_out_dtype(ki), device=dev)
+            _lib.check(_lib.LIB.tallax_gather_sort_key(ki.data_ptr(), _lib.dtype_code(ki), rows, cols,
+                                                       perm.data_ptr(), oi.data_ptr(), _lib.dtype_code(oi), stream),
+                       "sort")
+            outs[i] = oi
     outs[0] = out0
     for i in range(num_keys, len(ops)):
         x = ops[i]

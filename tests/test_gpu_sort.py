@@ -228,3 +228,31 @@ def test_tumpy_flattened_wide(gpu):
     torch.cuda.synchronize()
     assert np.array_equal(a.cpu().numpy(), np.argsort(x.reshape(-1), kind="stable"))
     assert np.array_equal(s.cpu().numpy(), np.sort(x.reshape(-1)))
+
+
+@pytest.mark.parametrize("cols", [3000, 40000])
+@pytest.mark.parametrize("descending", [False, True])
+def test_sort_many_keys(gpu, cols, descending):
+    """Three and four keys (lexicographic, sort.py:768-929): LSD passes with
+    the permutation carried along; the third and later keys come back
+    standardised and decoded like the first two (NaN payload, -0 -> +0,
+    bf16 keys as float32)."""
+    from tallax_amd import tax
+    rng = np.random.default_rng(cols + descending)
+    rows = 3
+    k0 = rng.integers(0, 3, (rows, cols)).astype(np.int32)
+    k1 = np.round(rng.standard_normal((rows, cols))).astype(np.float32)
+    k2 = np.round(rng.standard_normal((rows, cols)) * 2).astype(np.float32) / 2
+    k2[0, ::7] = np.nan
+    k2[1, ::5] = -0.0
+    k3 = np.round(rng.standard_normal((rows, cols)) * 4).astype(np.float32) / 4
+    pay = rng.standard_normal((rows, cols)).astype(np.float32)
+    for nk, ops_h, dts in [(3, [k0, k1, k2, pay], ["i32", "f32", "f32", "f32"]),
+                           (4, [k1, k0, k2, O.round_to_dtype(k3, "bf16"), pay], ["f32", "i32", "f32", "bf16", "f32"])]:
+        ops = [torch.from_numpy(o).to(gpu) if d != "bf16" else to_dev(o, "bf16", gpu) for o, d in zip(ops_h, dts)]
+        got = tax.sort(ops, num_keys=nk, is_stable=True, return_argsort=True, descending=descending)
+        torch.cuda.synchronize()
+        want, _ = O.sort(ops_h, nk, is_stable=True, return_argsort=True, descending=descending, dtypes=dts)
+        assert len(got) == len(want)
+        for g, w in zip(got, want):
+            assert _same(_host(g), w)
