@@ -189,7 +189,7 @@ def _topk(torch, np, _lib, dev, s_handle, gen, nbuf, which):
         valid = torch.empty(1, dtype=torch.int32, device=dev)
         depths = torch.empty(rows, dtype=torch.int32, device=dev)
         cutoff = torch.empty(rows, dtype=torch.float32, device=dev)
-        w.kernel = "binned_lists_kernel<8> + binned_finish_kernel + binned_select_kernel"
+        w.kernel = "seg_select_kernel<f32, 16, 256> (lists) + binned_cand_kernel<8> + binned_select_kernel"
         w.alg_bytes += rows * 12 + 4
 
         def launch(i):
@@ -253,7 +253,7 @@ def _sort_c2(torch, np, _lib, dev, s_handle, gen, nbuf):
     w.alg_bytes = 20971520  # sort: 2 MiB keys in, 2 MiB keys + 4 MiB indices out; gather: 3 x 4 MiB
     w.workload = ("tumpy.argsort (stable, packed bf16 path) of bf16 keys [256,4096] = round(16 z)/16, then "
                   "tumpy.take_along_axis of an f32 [256,4096] array by the indices")
-    w.kernel = "sort_rows_kernel<u32, 4> + gather_row_lds_kernel<u32>"
+    w.kernel = "radix_sort_rows_kernel<4> + gather_row_lds_kernel<u32>"
     w.cpu_batch = 16
 
     def launch(i):
