@@ -2,6 +2,7 @@
 GPU checker: known-answer vectors, an independent implementation (rocRAND),
 float64 numpy, closed forms, brute force and statistics."""
 import json
+import math
 import os
 import shutil
 import subprocess
@@ -351,6 +352,36 @@ def test_sort_oracle_two_keys_and_forced_stable():
     for r in range(3):
         o = np.lexsort([np.arange(50), k1[r], k0[r]])
         assert np.array_equal(c[r], pay[r, o]) and np.array_equal(a[r], k0[r, o])
+
+
+@pytest.mark.parametrize("descending", [False, True])
+def test_sort_oracle_many_keys_brute_force(descending):
+    """Three keys, lexicographic (sort.py:768-929, S1-S2), against Python's
+    sorted() on tuples: float keys standardised (NaN above +inf, -0 == +0),
+    ties by ascending index in both directions; key outputs decoded."""
+    rng = np.random.default_rng(40 + descending)
+    n = 60
+    k0 = rng.integers(-2, 2, (2, n)).astype(np.int32)
+    k1 = rng.integers(-2, 2, (2, n)).astype(np.float32)
+    k1[0, ::9] = np.nan
+    k1[1, ::4] = -0.0
+    k2 = np.round(rng.standard_normal((2, n))).astype(np.float32)
+    pay = rng.standard_normal((2, n)).astype(np.float32)
+    (a, b, c, d, perm), _ = O.sort([k0, k1, k2, pay], 3, is_stable=True, return_argsort=True,
+                                   descending=descending)
+
+    def std(x):  # standardised order of a float key
+        x = float(x)
+        return math.inf * 2 if x != x else (0.0 if x == 0.0 else x)
+
+    sign = -1 if descending else 1
+    for r in range(2):
+        o = sorted(range(n), key=lambda j: (sign * int(k0[r, j]), sign * std(k1[r, j]), sign * std(k2[r, j]), j))
+        assert np.array_equal(perm[r], np.array(o, dtype=np.int32))
+        assert np.array_equal(d[r], pay[r, o]) and np.array_equal(a[r], k0[r, o])
+        got_k1 = b[r]
+        assert np.all(np.isnan(got_k1) == np.isnan(k1[r, o]))
+        assert np.array_equal(got_k1.view(np.uint32) == 0x80000000, np.zeros(n, bool))  # no -0 left
 
 
 # --------------------------------------------------------------------------- approximate top-k
