@@ -47,6 +47,7 @@
 #include "tx_host.h"
 #include "tx_math.h"
 #include "tx_sample.h"
+#include "tx_scan.h"
 #include "tx_wave_sort.h"
 
 namespace tx {
@@ -223,6 +224,28 @@ struct SegShared {
   int red[NW];
   int wc[NW];  // per-wave candidate counts
 };
+
+// Exclusive prefix of v over the threads of the workgroup, in thread order;
+// total = the sum over all.  Every thread must call it.
+template <int NW>
+__device__ __forceinline__ int block_exscan(int v, int* red, int& total) {
+  const int l = lane_id(), w = threadIdx.x / kWave;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+  __syncthreads();
+  if (l == kWave - 1) red[w] = incl;
+  __syncthreads();
+  int pre = 0;
+  total = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const int r = red[i];
+    pre += i < w ? r : 0;
+    total += r;
+  }
+  return pre + incl - v;
+}
 
 template <int NW>
 __device__ __forceinline__ int block_sum(int v, int* red) {
@@ -494,6 +517,157 @@ __device__ __forceinline__ int32_t vec_omax(const uint4 v) {
 }
 
 // ---------------------------------------------------------------------------
+// Heavy ties (a candidate region overflowed, e.g. constant rows or rows of
+// -inf but a few): the k candidates are chosen exactly.  The k-th largest
+// canonical key K comes from a bisection over the key bits, counting
+// straight from registers (one pass over the thread's elements and one
+// block sum per bit); the elements above K are appended, then the first
+// k - #above of key K in slot order: vector j of every thread (threads in
+// order) precedes vector j + 1, so one block scan per vector index until
+// enough are taken (usually at j = 0).  The append passes take the vectors
+// through the thread's own stage slots, kStage at a time, with one loop body
+// per vector.
+//   It is a separate, non-inlined function that loads the segment again, so
+// that its register needs do not weigh on the selection kernel's common path.
+//   The counts use the raw-key order, which equals the canonical order but
+// for -0 (one below +0), positive NaNs (above +inf) and negative NaNs and
+// dead slots (below -inf): per-thread counts of the first two correct the
+// sums, and probes below the key of -inf count every live element, since no
+// canonical key lies between a NaN's and -inf's.
+// Returns this wave's number of appended candidates.  Every thread calls it.
+// ---------------------------------------------------------------------------
+template <int DT, int MAXV, int NT>
+__device__ __attribute__((noinline)) int tie_select(const uint4* base, int64_t s0, int64_t s1, int lbase,
+                                                    int live_lo, int live_hi, uint32_t gbase, int k,
+                                                    typename Sel<DT, (NT * MAXV * ElemT<DT>::VEC > 65535)>::Comp* reg,
+                                                    int* red, uint4* stage) {
+  using T = ElemT<DT>;
+  constexpr bool kWide = NT * MAXV * T::VEC > 65535;
+  using S = Sel<DT, kWide>;
+  using C = typename S::Comp;
+  constexpr bool kBF = DT == kBF16;
+  constexpr int VEC = T::VEC, NW = Geo<NT>::NW, WCAP = Geo<NT>::WCAP;
+  constexpr uint32_t kZeroKey = kBF ? 0x8000u : 0x80000000u;     // canonical key of +-0
+  constexpr uint32_t kNaNKey = kBF ? 0u : 1u;                     // canonical key of every NaN
+  constexpr uint32_t kNegInfKey = kBF ? 0x007Fu : 0x007FFFFFu;    // canonical key of -inf
+  constexpr int kKeyBits = kBF ? 16 : 32;
+  const int tid = threadIdx.x;
+  auto elem_id = [&](int lidx) -> uint32_t { return (kBF && !kWide) ? (uint32_t)lidx : gbase + (uint32_t)lidx; };
+  auto live_bits = [&](int li0) -> uint32_t {
+    uint32_t m = 0;
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) m |= (li0 + q >= live_lo && li0 + q < live_hi ? 1u : 0u) << q;
+    return m;
+  };
+  // the segment again, slots outside the row as all-ones
+  uint4 raw[MAXV];
+#pragma unroll
+  for (int j = 0; j < MAXV; ++j) {
+    const int64_t v = s0 + (int64_t)j * NT + tid;
+    raw[j] = v < s1 ? base[v] : make_uint4(~0u, ~0u, ~0u, ~0u);
+  }
+  int nlive = 0, nposnan = 0, nnegzero = 0;
+#pragma unroll
+  for (int j = 0; j < MAXV; ++j) {
+    const uint32_t lm = live_bits(lbase + j * NT * VEC);
+    uint32_t d[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {  // dead slots become all-ones
+      if (kBF) {
+        d[i] |= ((lm >> (2 * i)) & 1u) ? 0u : 0x0000FFFFu;
+        d[i] |= ((lm >> (2 * i + 1)) & 1u) ? 0u : 0xFFFF0000u;
+      } else {
+        d[i] |= ((lm >> i) & 1u) ? 0u : ~0u;
+      }
+    }
+    raw[j] = make_uint4(d[0], d[1], d[2], d[3]);
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) {
+      const uint32_t bq = elem_bits<DT>(raw[j], q);
+      const bool live = (lm >> q) & 1u;
+      nlive += live ? 1 : 0;
+      nposnan += live && bq > (kBF ? 0x7F80u : 0x7F800000u) && bq < kZeroKey ? 1 : 0;
+      nnegzero += live && bq == kZeroKey ? 1 : 0;
+    }
+  }
+  // live elements whose canonical key is >= P
+  auto count_ge = [&](uint32_t P) -> int {
+    if (P <= kNaNKey) return nlive;
+    const uint32_t pr = P < kNegInfKey ? kNegInfKey : P;
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < MAXV; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t x = dword_of(raw[j], i);
+        if (kBF) {
+          const uint32_t rk = raw_key2_bf16(x);
+          c += ((rk & 0xFFFFu) >= pr ? 1 : 0) + ((rk >> 16) >= pr ? 1 : 0);
+        } else {
+          c += raw_key_f32(x) >= pr ? 1 : 0;
+        }
+      }
+    }
+    return c - nposnan + (P == kZeroKey ? nnegzero : 0);
+  };
+  uint32_t K = 0;
+#pragma unroll 1
+  for (int b = kKeyBits - 1; b >= 0; --b) {
+    const uint32_t probe = K | (1u << b);
+    if (block_sum<NW>(count_ge(probe), red) >= k) K = probe;
+  }
+  const int above = block_sum<NW>(count_ge(K + 1u), red);  // K < the largest key: no wrap
+  int rest = k - above;                                    // >= 1 elements of key K
+  int wcnt = 0;
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+    for (int c = 0; c < (MAXV + kStage - 1) / kStage; ++c) {
+      if (pass == 1 && rest <= 0) break;
+#pragma unroll
+      for (int u = 0; u < kStage; ++u)
+        if (c * kStage + u < MAXV) stage[u * NT + tid] = raw[c * kStage + u];
+#pragma unroll 1
+      for (int u = 0; u < kStage && c * kStage + u < MAXV; ++u) {
+        if (pass == 1 && rest <= 0) break;
+        const int li0 = lbase + (c * kStage + u) * NT * VEC;
+        const uint4 vv = stage[u * NT + tid];
+        const uint32_t lm = live_bits(li0);
+        uint32_t mask = 0;
+        if (pass == 0) {  // above K
+#pragma unroll
+          for (int q = 0; q < VEC; ++q)
+            mask |= (((lm >> q) & 1u) && S::canon(elem_bits<DT>(vv, q)) > K ? 1u : 0u) << q;
+        } else {  // key K, the first `rest` in slot order
+          uint32_t eq = 0;
+#pragma unroll
+          for (int q = 0; q < VEC; ++q)
+            eq |= (((lm >> q) & 1u) && S::canon(elem_bits<DT>(vv, q)) == K ? 1u : 0u) << q;
+          int total = 0;
+          const int before = block_exscan<NW>(__popc(eq), red, total);
+#pragma unroll
+          for (int q = 0; q < VEC; ++q)
+            mask |= (((eq >> q) & 1u) && before + __popc(eq & ((1u << q) - 1u)) < rest ? 1u : 0u) << q;
+          rest -= total;
+        }
+        for (;;) {
+          const bool hc = mask != 0u;
+          if (!__ballot(hc)) break;
+          C cm = 0;
+          if (hc) {
+            const int e = __builtin_ctz(mask);
+            mask &= mask - 1u;
+            cm = S::comp(elem_bits<DT>(vv, e), elem_id(li0 + e));
+          }
+          wave_append<WCAP>(hc, cm, reg, wcnt);
+        }
+      }
+    }
+  }
+  return wcnt;
+}
+
+// ---------------------------------------------------------------------------
 // Kernel A: one workgroup per (segment, row).  The segment (MAXV 16-byte
 // vectors per thread) is loaded into registers with every load issued up
 // front; a per-thread maximum bounds the k-th key from below (L); vectors
@@ -638,9 +812,9 @@ void seg_select_kernel(SelArgs a) {
   // element passes if it is live, its canonical key is >= thr and, with a
   // probe, its composite is >= probe.  Passing elements are appended to the
   // wave's region, or only counted (count_only).
-  auto pass_mask = [&](const uint4 vv, int li0, bool use_probe, C probe) -> uint32_t {
+  auto pass_mask = [&](const uint4 vv, int li0) -> uint32_t {
     uint32_t m = 0;
-    if (pos_thr && !use_probe) {
+    if (pos_thr) {
       // positive threshold: st <= bits <= +inf in the signed view (NaNs excluded);
       // dead slots (all-ones, -1) fail
       const uint32_t span = (uint32_t)(kPosInf - st);
@@ -657,17 +831,11 @@ void seg_select_kernel(SelArgs a) {
       return m;
     }
 #pragma unroll
-    for (int q = 0; q < VEC; ++q) {
-      const uint32_t bits = elem_bits<DT>(vv, q);
-      bool p = S::canon(bits) >= thr;
-      if (use_probe) p = p && S::comp(bits, elem_id(li0 + q)) >= probe;
-      m |= (p ? 1u : 0u) << q;
-    }
+    for (int q = 0; q < VEC; ++q) m |= (S::canon(elem_bits<DT>(vv, q)) >= thr ? 1u : 0u) << q;
     if (li0 < live_lo || li0 + VEC > live_hi) m &= live_mask(li0);
     return m;
   };
-  auto rounds = [&](bool count_only, bool use_probe, C probe, int& wcnt) -> int {
-    int cnt = 0;
+  auto rounds = [&](int& wcnt) {
 #pragma unroll 1
     for (int first = 0;; first += kStage) {
       uint32_t slots = 0;
@@ -694,72 +862,42 @@ void seg_select_kernel(SelArgs a) {
         if (have) {
           vv = stage[i * NT + tid];
           li0 = lbase + (int)((slots >> (5 * i)) & 31u) * NT * VEC;
-          mask = pass_mask(vv, li0, use_probe, probe);
+          mask = pass_mask(vv, li0);
         }
-        if (count_only) {
-          cnt += __popc(mask);
-        } else {
-          for (;;) {
-            const bool hc = mask != 0u;
-            if (!__ballot(hc)) break;
-            C cm = 0;
-            if (hc) {
-              const int e = __builtin_ctz(mask);
-              mask &= mask - 1u;
-              // the element, read back from its staged copy
-              const uint32_t bits = kBF ? (uint32_t)((const uint16_t*)&stage[i * NT + tid])[e]
-                                        : ((const uint32_t*)&stage[i * NT + tid])[e];
-              cm = S::comp(bits, elem_id(li0 + e));
-            }
-            wave_append<WCAP>(hc, cm, reg, wcnt);
+        for (;;) {
+          const bool hc = mask != 0u;
+          if (!__ballot(hc)) break;
+          C cm = 0;
+          if (hc) {
+            const int e = __builtin_ctz(mask);
+            mask &= mask - 1u;
+            // the element, read back from its staged copy
+            const uint32_t bits = kBF ? (uint32_t)((const uint16_t*)&stage[i * NT + tid])[e]
+                                      : ((const uint32_t*)&stage[i * NT + tid])[e];
+            cm = S::comp(bits, elem_id(li0 + e));
           }
+          wave_append<WCAP>(hc, cm, reg, wcnt);
         }
       }
       if (!__ballot(nfl > first + kStage)) break;
     }
-    return cnt;
   };
 
-  // Filter pass; if a region overflows, bisect for the k-th composite among
-  // the passing elements (composites are distinct, so exactly k are >= it)
-  // and collect those.  Control flow is block-uniform.
-  constexpr int kIdxTop = sizeof(C) == 4 ? 15 : 31;  // top bit of the index field
-  constexpr int kKeyTop = sizeof(C) == 4 ? 31 : (kBF ? 47 : 63);
-  // index bits that vary: ~idx has ones above them for every idx < 2^ib
-  int ib = kIdxTop + 1;
-  if (sizeof(C) == 8) {
-    const uint64_t span = (uint64_t)(kBF && !kWide ? live_hi : (uint32_t)(gbase + (uint32_t)live_hi));
-    ib = span <= 1 ? 1 : 64 - __clzll(span - 1);
-    ib = ib > 32 ? 32 : ib;
-  }
-  int phase = 0;  // 0 filter, 1 bisection count, 2 final append
-  int bit = kKeyTop;
-  C prefix = 0;
-#pragma unroll 1
-  for (;;) {
-    const C probe = phase == 1 ? (C)(prefix | ((C)1 << bit)) : prefix;
+  // Filter pass; exact tie selection when a region overflows.  Control flow
+  // is block-uniform.
+  {
     int wcnt = 0;
-    const int cnt = rounds(phase == 1, phase != 0, probe, wcnt);
-    if (phase != 1) {
+    rounds(wcnt);
+    if (l == 0) sh.wc[w] = wcnt;
+    __syncthreads();
+    bool overflow = false;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) overflow |= sh.wc[q] > WCAP;
+    if (overflow) {
+      // its block sums order the reads of sh.wc above before the write below
+      wcnt = tie_select<DT, MAXV, NT>(rv.base, s0, s1, lbase, live_lo, live_hi, gbase, k, reg, sh.red, stage);
       if (l == 0) sh.wc[w] = wcnt;
       __syncthreads();
-      bool overflow = false;
-#pragma unroll
-      for (int q = 0; q < NW; ++q) overflow |= sh.wc[q] > WCAP;
-      if (!overflow || phase == 2) break;  // phase 2 admits exactly k <= WCAP
-      __syncthreads();
-      phase = 1;
-      bit = kKeyTop;
-      prefix = 0;
-    } else {
-      if (block_sum<NW>(cnt, sh.red) >= k) prefix = probe;
-      if (bit == kIdxTop + 1) {  // key resolved: fixed high index bits, then the varying ones
-        if (ib <= kIdxTop) prefix |= (C)((((uint64_t)1 << (kIdxTop + 1)) - 1) & ~(((uint64_t)1 << ib) - 1));
-        bit = ib - 1;
-      } else {
-        --bit;
-      }
-      if (bit < 0) phase = 2;
     }
   }
 

@@ -84,6 +84,14 @@ TOPK_CASES = [
     (8, 65536, 100, "bf16", "strided_hot"), # one thread owns a candidate in every vector
     (8, 65536, 100, "f32", "strided_hot"),
     (16, 128256, 128, "bf16", "normal"),    # vocabulary row of config 4
+    # heavy ties: the exact tie selection (k-th key by bisection, then the
+    # first elements of that key in slot order)
+    (256, 128256, 128, "bf16", "const"),    # constant rows at config 4's shape (whole-row workgroups)
+    (64, 128256, 128, "bf16", "masked5"),   # -inf but 5 values per row (constrained decoding)
+    (8, 151936, 50, "f32", "masked5"),      # the same, segmented rows
+    (4, 40000, 100, "bf16", "tieblock"),    # 60 large values, then a 10000-wide tie block
+    (4, 40000, 100, "f32", "tieblock"),
+    (4, 40000, 100, "f32", "nan_heavy"),    # NaN rows with a few finite, -inf and finfo.min values
 ]
 
 
@@ -108,6 +116,26 @@ def _make(rows, cols, kind, seed):
         return rng.integers(-6, 7, (rows, cols)).astype(np.float32)
     if kind == "const":
         return np.full((rows, cols), 1.5, np.float32)
+    if kind == "masked5":
+        x = np.full((rows, cols), -np.inf, np.float32)
+        for r in range(rows):
+            x[r, rng.choice(cols, 5, replace=False)] = rng.standard_normal(5).astype(np.float32)
+        return x
+    if kind == "tieblock":
+        x = (rng.standard_normal((rows, cols)) * 0.1 - 10).astype(np.float32)
+        for r in range(rows):
+            pos = rng.choice(cols, 10060, replace=False)
+            x[r, pos[:60]] = 100 + rng.random(60).astype(np.float32) * 50
+            x[r, pos[60:]] = 5.0
+        return x
+    if kind == "nan_heavy":
+        x = np.full((rows, cols), np.nan, np.float32)
+        for r in range(rows):
+            pos = rng.choice(cols, 90, replace=False)
+            x[r, pos[:50]] = rng.standard_normal(50).astype(np.float32)
+            x[r, pos[50:70]] = -np.inf
+            x[r, pos[70:]] = np.finfo(np.float32).min
+        return x
     x = rng.standard_normal((rows, cols)).astype(np.float32)
     u = rng.random((rows, cols))
     x[u < 0.05] = np.nan
