@@ -580,32 +580,55 @@ __device__ __attribute__((noinline)) int tie_select(const uint4* base, int64_t s
         d[i] |= ((lm >> i) & 1u) ? 0u : ~0u;
       }
     }
-    raw[j] = make_uint4(d[0], d[1], d[2], d[3]);
+    const uint4 v = make_uint4(d[0], d[1], d[2], d[3]);
 #pragma unroll
     for (int q = 0; q < VEC; ++q) {
-      const uint32_t bq = elem_bits<DT>(raw[j], q);
+      const uint32_t bq = elem_bits<DT>(v, q);
       const bool live = (lm >> q) & 1u;
       nlive += live ? 1 : 0;
       nposnan += live && bq > (kBF ? 0x7F80u : 0x7F800000u) && bq < kZeroKey ? 1 : 0;
       nnegzero += live && bq == kZeroKey ? 1 : 0;
     }
+    // from here on the raw keys (dead slots: 0)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d[i] = kBF ? raw_key2_bf16(d[i]) : raw_key_f32(d[i]);
+    raw[j] = make_uint4(d[0], d[1], d[2], d[3]);
   }
+  // canonical key from a raw key: NaNs (above +inf or below -inf) and -0 differ
+  auto canon_of = [&](uint32_t rk) -> uint32_t {
+    const uint32_t kc = rk == kZeroKey - 1u ? kZeroKey : rk;
+    return rk > (kBF ? 0xFF80u : 0xFF800000u) || rk < kNegInfKey ? kNaNKey : kc;
+  };
+  // composite of an element from its canonical key and slot, as S::comp builds it
+  auto comp_of = [&](uint32_t kc, int lidx) -> C {
+    if constexpr (sizeof(C) == 4) return (C)((kc << 16) | (0xFFFFu - (uint32_t)lidx));
+    else return (C)(((uint64_t)kc << 32) | (uint64_t)(~elem_id(lidx)));
+  };
   // live elements whose canonical key is >= P
   auto count_ge = [&](uint32_t P) -> int {
     if (P <= kNaNKey) return nlive;
     const uint32_t pr = P < kNegInfKey ? kNegInfKey : P;
     int c = 0;
+    if constexpr (kBF) {
+      // both halves at once: sat(rk - (pr - 1)) is 0 exactly when rk < pr; min(., 1) counts
+      const ushort2_t pm1 = __builtin_bit_cast(ushort2_t, (pr - 1u) * 0x10001u);
+      const ushort2_t one = __builtin_bit_cast(ushort2_t, 0x00010001u);
+      ushort2_t acc = __builtin_bit_cast(ushort2_t, 0u);
 #pragma unroll
-    for (int j = 0; j < MAXV; ++j) {
+      for (int j = 0; j < MAXV; ++j) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t x = dword_of(raw[j], i);
-        if (kBF) {
-          const uint32_t rk = raw_key2_bf16(x);
-          c += ((rk & 0xFFFFu) >= pr ? 1 : 0) + ((rk >> 16) >= pr ? 1 : 0);
-        } else {
-          c += raw_key_f32(x) >= pr ? 1 : 0;
+        for (int i = 0; i < 4; ++i) {
+          const ushort2_t rk = __builtin_bit_cast(ushort2_t, dword_of(raw[j], i));
+          acc += __builtin_elementwise_min(__builtin_elementwise_sub_sat(rk, pm1), one);
         }
+      }
+      const uint32_t a2 = __builtin_bit_cast(uint32_t, acc);
+      c = (int)((a2 & 0xFFFFu) + (a2 >> 16));
+    } else {
+#pragma unroll
+      for (int j = 0; j < MAXV; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c += dword_of(raw[j], i) >= pr ? 1 : 0;
       }
     }
     return c - nposnan + (P == kZeroKey ? nnegzero : 0);
@@ -637,12 +660,12 @@ __device__ __attribute__((noinline)) int tie_select(const uint4* base, int64_t s
         if (pass == 0) {  // above K
 #pragma unroll
           for (int q = 0; q < VEC; ++q)
-            mask |= (((lm >> q) & 1u) && S::canon(elem_bits<DT>(vv, q)) > K ? 1u : 0u) << q;
+            mask |= (((lm >> q) & 1u) && canon_of(elem_bits<DT>(vv, q)) > K ? 1u : 0u) << q;
         } else {  // key K, the first `rest` in slot order
           uint32_t eq = 0;
 #pragma unroll
           for (int q = 0; q < VEC; ++q)
-            eq |= (((lm >> q) & 1u) && S::canon(elem_bits<DT>(vv, q)) == K ? 1u : 0u) << q;
+            eq |= (((lm >> q) & 1u) && canon_of(elem_bits<DT>(vv, q)) == K ? 1u : 0u) << q;
           int total = 0;
           const int before = block_exscan<NW>(__popc(eq), red, total);
 #pragma unroll
@@ -657,7 +680,7 @@ __device__ __attribute__((noinline)) int tie_select(const uint4* base, int64_t s
           if (hc) {
             const int e = __builtin_ctz(mask);
             mask &= mask - 1u;
-            cm = S::comp(elem_bits<DT>(vv, e), elem_id(li0 + e));
+            cm = comp_of(canon_of(elem_bits<DT>(vv, e)), li0 + e);
           }
           wave_append<WCAP>(hc, cm, reg, wcnt);
         }
@@ -855,7 +878,8 @@ void seg_select_kernel(SelArgs a) {
 #pragma unroll 1
       for (int i = 0; i < kStage; ++i) {
         const bool have = i < nst;
-        if (!__ballot(have)) break;
+        // a full region means the tie selection takes over: stop appending
+        if (!__ballot(have) || wcnt > WCAP) break;
         uint32_t mask = 0;
         uint4 vv = make_uint4(0u, 0u, 0u, 0u);
         int li0 = 0;
@@ -879,7 +903,7 @@ void seg_select_kernel(SelArgs a) {
           wave_append<WCAP>(hc, cm, reg, wcnt);
         }
       }
-      if (!__ballot(nfl > first + kStage)) break;
+      if (!__ballot(nfl > first + kStage) || wcnt > WCAP) break;
     }
   };
 
