@@ -26,15 +26,16 @@
 //       passing elements become candidates (composite key, value descending
 //       then index ascending), appended by wave-level stream compaction
 //       (ballot + mbcnt) to a per-wave LDS region of 256 slots;
-//     - if a region overflows (heavy ties), the same staged rounds run a
-//       bisection for the exact k-th composite and collect only those >= it.
+//     - if a region overflows (heavy ties), tie_select picks exactly k
+//       candidates instead: the k-th key by bisection counting from
+//       registers, then the first elements of that key in slot order.
 //   Selection compacts the candidates, sorts 64- or 128-element runs with a
 //   wave64 bitonic network and merges runs with bitonic merge-and-discard
 //   (tx_wave_sort.h), giving the segment's sorted top-128.
-//   Kernel B, seg_merge_kernel (only when nseg > 1): one 4-wave workgroup per
-//   row loads every segment list at once, merges them (merge-and-discard per
-//   wave, then a tree through LDS) and writes (values, indices) or runs the
-//   sampler tail.
+//   Kernel B, seg_merge_kernel (only when nseg > 1, or over lists gathered
+//   from vocabulary shards): one 4-wave workgroup per row loads every list at
+//   once, merges them (merge-and-discard per wave, then a tree through LDS)
+//   and writes (values, indices), the merged list, or runs the sampler tail.
 //   The kernel boundary orders the workspace writes before the reads, so no
 //   device-scope fence (an L2 write-back on gfx950) is ever issued.
 #include <float.h>
