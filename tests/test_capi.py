@@ -56,3 +56,26 @@ def test_sort_workspace_contract_without_gpu():
     assert b"workspace" in L.tallax_last_error()
     st = L.tallax_sort_rows_ws(1, 0, 2, 40000, 0, 0, None, 1, None, 0, None, 0, None, 0, 1, 100, None)
     assert st == _lib.WORKSPACE_TOO_SMALL
+
+
+def test_new_entry_points_validate_on_the_host():
+    """Argument checks of the sharded sampler, top_p_mask and the sort-key
+    gather run before any launch (no GPU needed)."""
+    from tallax_amd import _lib
+    L = _lib.LIB
+    # shard candidates: a shard narrower than 128 columns, a negative offset
+    assert L.tallax_shard_candidates(1, 1, 4, 100, 0, 1, None, 0, None) == _lib.UNSUPPORTED
+    assert L.tallax_shard_candidates(1, 1, 4, 1000, -5, 1, None, 0, None) == _lib.INVALID_ARGUMENT
+    assert L.tallax_shard_candidates(1, 1, 4, 1000, 0, None, None, 0, None) == _lib.INVALID_ARGUMENT
+    assert L.tallax_shard_candidates_workspace_size(256, 16032, 1) == 0  # whole rows: no workspace
+    # merge + sample: list counts outside [1, 32], a vocabulary below 128
+    args = (1, 1, 1, 1, 0, -1e12, 1, None)  # top_k, top_p, temperature, key, dim0_offset, replace_val, out, stream
+    assert L.tallax_sample_from_candidates(1, 33, 1, 4, 128256, *args) == _lib.UNSUPPORTED
+    assert L.tallax_sample_from_candidates(1, 0, 1, 4, 128256, *args) == _lib.INVALID_ARGUMENT
+    assert L.tallax_sample_from_candidates(1, 4, 1, 4, 100, *args) == _lib.INVALID_ARGUMENT
+    # top_p_mask: more than 128 candidates per column
+    assert L.tallax_top_p_mask(1, 129, 4, 1, -1e12, 1, None) == _lib.UNSUPPORTED
+    assert L.tallax_top_p_mask(1, 0, 4, 1, -1e12, 1, None) == _lib.INVALID_ARGUMENT
+    # sort-key gather: an output dtype a key cannot decode to
+    assert L.tallax_gather_sort_key(1, _lib.F32, 2, 10, 1, 1, _lib.BF16, None) == _lib.INVALID_ARGUMENT
+    assert L.tallax_gather_sort_key(1, 7, 2, 10, 1, 1, _lib.F32, None) == _lib.UNSUPPORTED
