@@ -118,6 +118,24 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
                                   tallax_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Wide-candidate sampler: sampling.sample (tallax/_src/sampling.py:331-343)
+ * with the top-k width max_k lifted from the reference's 128
+ * (sampling.py:283-290, top_k.py:438-439) to any max_k in [1, 1024], so that
+ * per-row top_k up to 1024 is honoured instead of clamped.  Same algorithm
+ * otherwise: exact top-max_k (value descending, ties to the lowest index),
+ * positions >= top_k[row] replaced by replace_val in the logits dtype, then
+ * top_p_and_sample (sampling.py:65-115) over the max_k candidates.  With
+ * max_k = 128 the tokens equal tallax_fused_topk_topp_sample's.
+ * out_tokens [rows] (or null); out_idx [rows, max_k] int32 and out_vals
+ * [rows, max_k] f32 (each optional) receive the candidates before the k
+ * mask.  max_k <= vocab.  No workspace.
+ * ---------------------------------------------------------------------- */
+int tallax_sample_wide(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t max_k,
+                       const int32_t* top_k, const float* top_p, const float* temperature,
+                       const uint32_t* rng_key, int64_t dim0_offset, double replace_val, int32_t* out_tokens,
+                       int32_t* out_idx, float* out_vals, tallax_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Vocabulary-sharded sampling, the two compute steps of the reference's
  * partitioned sampler (tallax/_src/sampling.py:300-321: per-shard
  * _top_k_arrays(logits, 128), indices to the global frame, all_gather, then

@@ -576,12 +576,21 @@ def take_along_axis(values: np.ndarray, indices: np.ndarray, axis: int) -> np.nd
 # ---------------------------------------------------------------------------
 # top_p_mask / top_p_and_sample / sample (tallax/_src/sampling.py)
 # ---------------------------------------------------------------------------
-def _tree_sum_axis0_128(e: np.ndarray) -> np.ndarray:
-    """Sum over axis 0 (k <= 128 rows) as a stride-halving tree over 128
-    zero-padded slots: x[:64] + x[64:], then x[:32] + x[32:], ..."""
+def _tree_width(k: int) -> int:
+    """Slots of the top-p sum tree: 128 for the reference's k <= 128; the
+    next power of two for the wide-candidate sampler's k <= 1024 (beyond the
+    reference, whose sampler never has more than 128 candidates)."""
+    w = 128
+    while w < k:
+        w *= 2
+    return w
+
+
+def _tree_sum_axis0(e: np.ndarray) -> np.ndarray:
+    """Sum over axis 0 as a stride-halving tree over _tree_width(k) (128 for
+    k <= 128) zero-padded slots: x[:64] + x[64:], then x[:32] + x[32:], ..."""
     k = e.shape[0]
-    assert k <= 128
-    x = np.zeros((128,) + e.shape[1:], dtype=np.float32)
+    x = np.zeros((_tree_width(k),) + e.shape[1:], dtype=np.float32)
     x[:k] = e
     while x.shape[0] > 1:
         h = x.shape[0] // 2
@@ -595,7 +604,7 @@ def top_p_mask(topk_logits: np.ndarray, p: np.ndarray, replace_val: float) -> np
     k = L.shape[0]
     with np.errstate(all="ignore"):
         e = exp_f32(L - L[:1])
-        s = _tree_sum_axis0_128(e)
+        s = _tree_sum_axis0(e)
         probs = e / s
     c = cumsum(probs, axis=0)
     t = (c < np.asarray(p, dtype=np.float32)[None, :]).sum(0)
@@ -624,13 +633,14 @@ def top_p_and_sample(topk_logits, topk_idx, key, top_p, temperature, vocab_size,
 
 
 def sample(key, logits, top_k_per_row, top_p, temperature, dtype: str = "f32",
-           replace_val: float = -1e12, dim0_offset: int = 0) -> np.ndarray:
+           replace_val: float = -1e12, dim0_offset: int = 0, max_k: int = NUM_LANES) -> np.ndarray:
     """sample() (sampling.py:331-343) on one device: exact top-128 (per-row k
     mask with replace_val in the logits dtype, top_k.py:365-369), then
-    top_p_and_sample with replace_val."""
+    top_p_and_sample with replace_val.  max_k != 128 is the wide-candidate
+    sampler (beyond the reference): the same steps with max_k candidates."""
     x = np.asarray(logits, dtype=np.float32)
-    vals, idx = top_k(x, NUM_LANES, dtype)
+    vals, idx = top_k(x, max_k, dtype)
     kr = np.asarray(top_k_per_row, dtype=np.int64)
     rv = round_to_dtype(F32(replace_val), dtype)
-    vals = np.where(np.arange(NUM_LANES)[None, :] < kr[:, None], vals, rv)
+    vals = np.where(np.arange(max_k)[None, :] < kr[:, None], vals, rv)
     return top_p_and_sample(vals, idx, key, top_p, temperature, x.shape[1], replace_val, dim0_offset)

@@ -31,6 +31,7 @@ SOURCES = [
     "sort_wide.hip",
     "binned.hip",
     "softmax_topk.hip",
+    "sample_wide.hip",
     "testing.hip",
 ]
 

@@ -226,40 +226,6 @@ struct SegShared {
   int wc[NW];  // per-wave candidate counts
 };
 
-// Exclusive prefix of v over the threads of the workgroup, in thread order;
-// total = the sum over all.  Every thread must call it.
-template <int NW>
-__device__ __forceinline__ int block_exscan(int v, int* red, int& total) {
-  const int l = lane_id(), w = threadIdx.x / kWave;
-  int incl = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
-  __syncthreads();
-  if (l == kWave - 1) red[w] = incl;
-  __syncthreads();
-  int pre = 0;
-  total = 0;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    const int r = red[i];
-    pre += i < w ? r : 0;
-    total += r;
-  }
-  return pre + incl - v;
-}
-
-template <int NW>
-__device__ __forceinline__ int block_sum(int v, int* red) {
-  v = wave_sum_i(v);
-  __syncthreads();
-  if (lane_id() == 0) red[threadIdx.x / kWave] = v;
-  __syncthreads();
-  int t = 0;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) t += red[i];
-  return t;
-}
-
 // sh.list <- the 128 largest candidates of all wave regions (counts cnt[w] in LDS),
 // descending, zero padded.  Sets of at most 64 per wave use chunk_select;
 // larger ones are sorted per wave region in runs of 128 and the per-wave
@@ -1189,19 +1155,6 @@ int launch_segment_lists(const void* x, int dt, int64_t rows, int64_t cols, int 
     else launch_a<kBF16, 4, kNT, false>(a, s);
   }
   return launch_status("segment lists");
-}
-
-static float round_to_bf16(float f) {
-  uint32_t b;
-  memcpy(&b, &f, 4);
-  if ((b & 0x7fffffffu) > 0x7f800000u) {
-    b = (b | 0x00400000u) & 0xffff0000u;
-  } else {
-    b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
-  }
-  float r;
-  memcpy(&r, &b, 4);
-  return r;
 }
 
 static int check_common(const void* x, int dt, int64_t rows, int64_t cols) {

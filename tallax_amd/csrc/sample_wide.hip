@@ -1,0 +1,385 @@
+// Wide-candidate sampler for gfx950: the fused top-k / top-p / temperature /
+// Gumbel draw of sampling.sample with up to 1024 candidates per row instead
+// of the reference's 128.
+//
+// The reference clamps every row's k to max_k = 128 (sampling.py:283-290,
+// top_k.py:438-439), so requests with top_k in (128, 1024] are cut.  This
+// entry point is the same algorithm with max_k lifted to K <= 1024:
+//   * candidates: the K largest values of the row, value descending, ties to
+//     the lowest index (the order of xla_equivalent_sort(descending=True,
+//     is_stable=True), sort.py:932-970); values the reference's strict-`>`
+//     bins can never admit (NaN, -inf, finfo.min; top_k.py:64,241-243) are
+//     reported as finfo(dtype).min;
+//   * positions >= top_k[row] replaced by replace_val in the logits dtype
+//     (top_k.py:365-369);
+//   * top_p_mask over the K candidates (sampling.py:25-62): numerators
+//     exp(v - v[0]), their sum as a stride-halving tree over
+//     W = max(128, pow2ceil(K)) zero-padded slots, cumsum in 8-position tiles
+//     (cumsum.py:21-53 on axis 0), t = #(cumsum < p), threshold v[t] or 0
+//     when t == K;
+//   * scaled = masked / T plus Gumbel noise on the counter (row * vocab +
+//     token) (sampling.py:97-111, sparse_random.py:49-57), argmax with
+//     max_arrays' tie rule over max(8, pow2ceil(K)) padded slots
+//     (bitonic_top_k.py:43-97), greedy idx[0] when T < 1e-5.
+// With K = 128 the tokens are those of tallax_fused_topk_topp_sample.
+//
+// One 1024-thread workgroup per row:
+//   radix select: histograms of the select key's digits [31:21], [20:10] and
+//     [9:0] (bf16 keys are fixed by their top 16 bits, so two passes), each
+//     pass reading the row again and counting only the elements whose higher
+//     digits match the threshold prefix found so far, until the K-th largest
+//     key is known (or the crossing bin is taken whole);
+//   collect: one more read appends the elements above the threshold, and the
+//     threshold ties in index order (one workgroup scan per 8192-column chunk
+//     that holds a tie, until enough are taken), to LDS: exactly K elements;
+//   a 1024-record bitonic sort of their composites (key << 32 | ~index);
+//   the sampler tail with one candidate per thread.
+// The row is read two (bf16) to four (f32) times; the re-reads of a row just
+// streamed are served mostly from the caches.
+#include <float.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "tallax_hip.h"
+#include "tx_block_sort.h"
+#include "tx_common.h"
+#include "tx_host.h"
+#include "tx_sample.h"
+#include "tx_scan.h"
+
+namespace tx {
+
+constexpr int kSwNT = 1024;
+constexpr int kSwNW = kSwNT / kWave;
+constexpr int kSwMaxK = 1024;           // candidates per row, at most (one per thread)
+constexpr int kSwBins = 2048;           // 11-bit digits
+constexpr int kSwChunk = kSwNT * 8;     // columns per workgroup step: 8 per thread
+
+struct SwArgs {
+  const void* x;
+  int64_t rows, cols;
+  int k;         // candidates per row (K)
+  int vec;       // rows start 16-byte aligned: 8-element vector loads
+  const int32_t* top_k;
+  const float* top_p;
+  const float* temperature;
+  const uint32_t* rng_key;
+  int64_t dim0_offset;
+  float replace_f32;       // top_p_mask's fill (sampling.py:58-60)
+  float replace_in_dtype;  // the k mask's fill, rounded to the logits dtype
+  int32_t* out_tokens;     // [rows], or null
+  int32_t* out_idx;        // [rows, K] candidate columns, or null
+  float* out_vals;         // [rows, K] candidate values (f32), or null
+};
+
+template <int DT>
+__device__ __forceinline__ uint32_t sw_key_at(const char* rowp, int64_t i) {
+  if constexpr (DT == kBF16) return select_key(((uint32_t)((const uint16_t*)rowp)[i]) << 16);
+  else return select_key(((const uint32_t*)rowp)[i]);
+}
+
+// Select keys of columns base .. base+7; returns the mask of those inside the row.
+template <int DT>
+__device__ __forceinline__ uint32_t sw_load8(const char* rowp, int64_t cols, int64_t base, bool vec,
+                                             uint32_t (&k)[8]) {
+  if (vec && base + 8 <= cols) {
+    if constexpr (DT == kBF16) {
+      const uint4 w = *(const uint4*)(rowp + base * 2);
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        k[2 * q] = select_key(ws[q] << 16);
+        k[2 * q + 1] = select_key(ws[q] & 0xFFFF0000u);
+      }
+    } else {
+      const uint4 w0 = *(const uint4*)(rowp + base * 4);
+      const uint4 w1 = *(const uint4*)(rowp + base * 4 + 16);
+      const uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) k[q] = select_key(ws[q]);
+    }
+    return 0xFFu;
+  }
+  uint32_t m = 0;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int64_t i = base + q;
+    k[q] = 0u;
+    if (i < cols) {
+      k[q] = sw_key_at<DT>(rowp, i);
+      m |= 1u << q;
+    }
+  }
+  return m;
+}
+
+// hist[(key >> dsh) & dmask] += 1 over the row's elements whose key >> fsh
+// equals fval (every element when !filt).
+template <int DT>
+__device__ __forceinline__ void sw_hist(const char* rowp, int64_t cols, bool vec, int nchunks, bool filt,
+                                        int fsh, uint32_t fval, int dsh, uint32_t dmask, int* hist) {
+#pragma unroll 2
+  for (int j = 0; j < nchunks; ++j) {
+    const int64_t base = ((int64_t)j * kSwNT + threadIdx.x) * 8;
+    uint32_t k[8];
+    const uint32_t m = sw_load8<DT>(rowp, cols, base, vec, k);
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (((m >> q) & 1u) && (!filt || (k[q] >> fsh) == fval)) atomicAdd(&hist[(k[q] >> dsh) & dmask], 1);
+  }
+}
+
+// The bin holding the need-th largest counted element (bins scanned from the
+// top; thread t owns bins 2047-2t and 2046-2t).  res = {bin, count in higher
+// bins, count in the bin}.  Every thread must call it.
+__device__ __forceinline__ void sw_cross(const int* hist, int need, int* red, int* res) {
+  const int hi = kSwBins - 1 - 2 * (int)threadIdx.x, lo = hi - 1;
+  const int h_hi = hist[hi], h_lo = hist[lo];
+  int total;
+  const int above = block_exscan<kSwNW>(h_hi + h_lo, red, total);
+  if (above < need && need <= above + h_hi + h_lo) {
+    if (need <= above + h_hi) {
+      res[0] = hi; res[1] = above; res[2] = h_hi;
+    } else {
+      res[0] = lo; res[1] = above + h_hi; res[2] = h_lo;
+    }
+  }
+  __syncthreads();
+}
+
+template <int DT>
+__global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
+  constexpr int ES = DT == kBF16 ? 2 : 4;
+  __shared__ int s_hist[kSwBins];
+  __shared__ uint64_t s_list[kSwMaxK];
+  __shared__ float s_v[kSwMaxK];
+  __shared__ float s_e[kSwMaxK];
+  __shared__ float s_tot[kSwMaxK / 8];
+  __shared__ float s_carry[kSwMaxK / 8];
+  __shared__ int s_red[kSwNW];
+  __shared__ int s_res[3];
+  __shared__ int s_cnt;
+  __shared__ float s_sum;
+  __shared__ int32_t s_id0;
+  __shared__ float s_bs[kSwNW];
+  __shared__ uint32_t s_bb[kSwNW];
+  __shared__ int32_t s_bi[kSwNW];
+
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, l = lane_id(), w = t / kWave;
+  const int K = a.k;
+  const char* rowp = (const char*)a.x + (size_t)(row * a.cols) * ES;
+  const bool vec = a.vec != 0;
+  const int nchunks = (int)((a.cols + kSwChunk - 1) / kSwChunk);
+
+  // --- radix select of the K-th largest key ---------------------------------
+  int need = K;          // elements still to take at or below the prefix
+  uint32_t prefix = 0;   // digits found so far
+  int tsh = 0;           // threshold compares key >> tsh with prefix
+  bool take_all = false; // the crossing bin is taken whole
+  constexpr int kPasses = DT == kBF16 ? 2 : 3;
+#pragma unroll 1
+  for (int ps = 0; ps < kPasses; ++ps) {
+    const int bits = ps == 2 ? 10 : 11;
+    const int dsh = ps == 0 ? 21 : ps == 1 ? 10 : 0;
+    for (int i = t; i < kSwBins; i += kSwNT) s_hist[i] = 0;
+    __syncthreads();
+    sw_hist<DT>(rowp, a.cols, vec, nchunks, ps > 0, dsh + bits, prefix, dsh, (1u << bits) - 1u, s_hist);
+    __syncthreads();
+    sw_cross(s_hist, need, s_red, s_res);
+    const int bin = s_res[0], above = s_res[1], cnt = s_res[2];
+    prefix = (prefix << bits) | (uint32_t)bin;
+    need -= above;
+    tsh = dsh;
+    __syncthreads();  // s_res and s_hist are rewritten by the next pass
+    if (need == cnt) {
+      take_all = true;
+      break;
+    }
+  }
+
+  // --- collect exactly K elements into LDS ------------------------------------
+  if (t == 0) s_cnt = 0;
+  __syncthreads();
+  int tie_base = 0;  // threshold ties met so far in index order
+#pragma unroll 1
+  for (int j = 0; j < nchunks; ++j) {
+    const int64_t base = ((int64_t)j * kSwNT + t) * 8;
+    uint32_t k[8];
+    const uint32_t m = sw_load8<DT>(rowp, a.cols, base, vec, k);
+    uint32_t take = 0u, eq = 0u;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint32_t kp = k[q] >> tsh;
+      const bool in = (m >> q) & 1u;
+      take |= (in && kp > prefix ? 1u : 0u) << q;
+      eq |= (in && kp == prefix ? 1u : 0u) << q;
+    }
+    if (take_all) {
+      take |= eq;
+    } else if (tie_base < need) {  // uniform
+      if (__syncthreads_or(eq != 0u)) {
+        int total;
+        const int before = block_exscan<kSwNW>(__popc(eq), s_red, total);
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (((eq >> q) & 1u) && tie_base + before + __popc(eq & ((1u << q) - 1u)) < need) take |= 1u << q;
+        tie_base += total;
+      }
+    }
+    while (take) {
+      const int q = __builtin_ctz(take);
+      take &= take - 1u;
+      const int pos = atomicAdd(&s_cnt, 1);
+      if (pos < kSwMaxK) s_list[pos] = make_comp(k[q], (uint32_t)(base + q));
+    }
+  }
+  __syncthreads();
+
+  // --- sort the K candidates, descending ---------------------------------------
+  uint64_t rec[1];
+  rec[0] = t < K ? s_list[t] : 0ull;
+  __syncthreads();
+  block_bitonic_sort_c<uint64_t, 1, kSwNT, true>(rec, s_list);
+
+  const bool in = t < K;
+  const uint32_t kk = comp_key(rec[0]);
+  const int32_t id = comp_idx(rec[0]);
+  const uint32_t min_bits = DT == kBF16 ? 0xff7f0000u : 0xff7fffffu;  // finfo(dtype).min as f32
+  const float val = __uint_as_float(kk > ineligible_key_max(DT) ? key_to_bits(kk) : min_bits);
+  if (in && a.out_idx) a.out_idx[row * K + t] = id;
+  if (in && a.out_vals) a.out_vals[row * K + t] = val;
+  if (!a.out_tokens) return;  // uniform
+
+  // --- top-p mask, temperature, Gumbel-max (no contraction: built with -ffp-contract=off)
+  const float vv = t < a.top_k[row] ? val : a.replace_in_dtype;
+  s_v[t] = vv;
+  if (t == 0) s_id0 = id;
+  __syncthreads();
+  const float e = in ? candidate_exp(vv, s_v[0]) : 0.0f;
+  s_e[t] = e;
+  int W = 128;
+  while (W < K) W <<= 1;
+  for (int h = W / 2; h >= kWave; h >>= 1) {
+    __syncthreads();
+    if (t < h) s_e[t] = s_e[t] + s_e[t + h];
+  }
+  __syncthreads();
+  if (t < kWave) {
+    float s = s_e[t];
+#pragma unroll
+    for (int d = kWave / 2; d >= 1; d >>= 1) s = s + lane_xor_f(s, d);
+    if (t == 0) s_sum = s;
+  }
+  __syncthreads();
+  float c = in ? e / s_sum : 0.0f;
+#pragma unroll
+  for (int sh = 1; sh < 8; sh <<= 1) {
+    const float u = row_shr_f(c, sh);
+    c = c + ((l & 7) >= sh ? u : 0.0f);
+  }
+  const int g = t >> 3;
+  const int ntiles = (K + 7) >> 3;
+  if ((t & 7) == 7) s_tot[g] = c;
+  __syncthreads();
+  if (t == 0) {
+    float run = s_tot[0];
+    for (int i = 1; i < ntiles; ++i) {
+      s_carry[i] = run;
+      run = run + s_tot[i];
+    }
+  }
+  __syncthreads();
+  if (in && g != 0) c = c + s_carry[g];
+  const int tcount = __syncthreads_count(in && c < a.top_p[row]);
+  const float thr = tcount < K ? s_v[tcount] : 0.0f;
+
+  int P = 8;
+  while (P < K) P <<= 1;
+  int pbits = 0;
+  while ((1 << pbits) < P) ++pbits;
+  const float temp = a.temperature[row];
+  float sc = -INFINITY;
+  uint32_t br = 0u;
+  int32_t tok = 0;
+  if (in) {
+    const float masked = vv >= thr ? vv : a.replace_f32;
+    const float scaled = masked / temp;
+    sc = scaled + candidate_noise(a.rng_key[0], a.rng_key[1], (uint32_t)(row + a.dim0_offset),
+                                  (uint32_t)a.cols, id);
+    tok = id;
+    br = bitrev((uint32_t)t, pbits);
+  } else if (t < P) {
+    sc = -FLT_MAX;
+    tok = INT32_MIN;
+    br = bitrev((uint32_t)t, pbits);
+  }
+  auto reduce = [&]() {
+#pragma unroll
+    for (int d = kWave / 2; d >= 1; d >>= 1) {
+      const float os = lane_xor_f(sc, d);
+      const uint32_t ob = lane_xor(br, d);
+      const int32_t oi = (int32_t)lane_xor((uint32_t)tok, d);
+      if (os > sc || (os == sc && ob > br)) {
+        sc = os;
+        br = ob;
+        tok = oi;
+      }
+    }
+  };
+  reduce();
+  if (l == 0) {
+    s_bs[w] = sc;
+    s_bb[w] = br;
+    s_bi[w] = tok;
+  }
+  __syncthreads();
+  if (t < kWave) {
+    sc = l < kSwNW ? s_bs[l] : -INFINITY;
+    br = l < kSwNW ? s_bb[l] : 0u;
+    tok = l < kSwNW ? s_bi[l] : 0;
+    reduce();
+    if (t == 0) a.out_tokens[row] = temp < 1e-5f ? s_id0 : tok;
+  }
+}
+
+}  // namespace tx
+
+using namespace tx;
+
+extern "C" {
+
+int tallax_sample_wide(const void* logits, int dtype, int64_t rows, int64_t vocab, int64_t max_k,
+                       const int32_t* top_k, const float* top_p, const float* temperature,
+                       const uint32_t* rng_key, int64_t dim0_offset, double replace_val, int32_t* out_tokens,
+                       int32_t* out_idx, float* out_vals, hipStream_t stream) {
+  if (!logits) { set_error("null input pointer"); return kInvalidArgument; }
+  if (dtype != kF32 && dtype != kBF16) { set_error("dtype %d not supported (f32=0, bf16=1)", dtype); return kUnsupported; }
+  if (rows < 0 || vocab <= 0) { set_error("bad shape [%lld, %lld]", (long long)rows, (long long)vocab); return kInvalidArgument; }
+  if (rows > 0x7FFFFFFF || vocab >= (int64_t)1 << 31) { set_error("shape [%lld, %lld] exceeds int32 rows / columns", (long long)rows, (long long)vocab); return kInvalidArgument; }
+  if (max_k < 1 || max_k > kSwMaxK) {
+    set_error("max_k=%lld outside [1, %d]", (long long)max_k, kSwMaxK);
+    return max_k > kSwMaxK ? kUnsupported : kInvalidArgument;
+  }
+  if (max_k > vocab) { set_error("max_k=%lld exceeds the vocabulary %lld", (long long)max_k, (long long)vocab); return kInvalidArgument; }
+  if (!out_tokens && !out_idx && !out_vals) { set_error("no output requested"); return kInvalidArgument; }
+  if (out_tokens && (!top_k || !top_p || !temperature || !rng_key)) { set_error("null sampling parameter pointer"); return kInvalidArgument; }
+  if (rows == 0) return kOk;
+  SwArgs a = {};
+  a.x = logits; a.rows = rows; a.cols = vocab; a.k = (int)max_k;
+  const int es = dtype == kBF16 ? 2 : 4;
+  a.vec = ((uintptr_t)logits % 16 == 0) && ((vocab * es) % 16 == 0);
+  a.top_k = top_k; a.top_p = top_p; a.temperature = temperature; a.rng_key = rng_key;
+  a.dim0_offset = dim0_offset;
+  const float rf = (float)replace_val;
+  a.replace_f32 = rf;
+  a.replace_in_dtype = dtype == kBF16 ? round_to_bf16(rf) : rf;
+  a.out_tokens = out_tokens; a.out_idx = out_idx; a.out_vals = out_vals;
+  if (dtype == kF32)
+    sample_wide_kernel<kF32><<<dim3((unsigned)rows), dim3(kSwNT), 0, stream>>>(a);
+  else
+    sample_wide_kernel<kBF16><<<dim3((unsigned)rows), dim3(kSwNT), 0, stream>>>(a);
+  return launch_status("tallax_sample_wide");
+}
+
+}  // extern "C"

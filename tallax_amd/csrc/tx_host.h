@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <string.h>
 
 namespace tx {
 
@@ -25,6 +26,20 @@ inline int launch_status(const char* what) {
     return kHipError;
   }
   return kOk;
+}
+
+// float -> nearest bfloat16 (ties to even; NaN stays NaN), as a float
+inline float round_to_bf16(float f) {
+  uint32_t b;
+  memcpy(&b, &f, 4);
+  if ((b & 0x7fffffffu) > 0x7f800000u) {
+    b = (b | 0x00400000u) & 0xffff0000u;
+  } else {
+    b = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
+  }
+  float r;
+  memcpy(&r, &b, 4);
+  return r;
 }
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }

@@ -24,6 +24,40 @@ __device__ __forceinline__ int32_t add_in_order<int32_t>(int32_t a, int32_t b) {
   return (int32_t)((uint32_t)a + (uint32_t)b);  // wrapping, as the reference's int32 adds
 }
 
+// Exclusive prefix of v over the threads of the workgroup, in thread order;
+// total = the sum over all.  Every thread must call it.
+template <int NW>
+__device__ __forceinline__ int block_exscan(int v, int* red, int& total) {
+  const int l = lane_id(), w = threadIdx.x / kWave;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+  __syncthreads();
+  if (l == kWave - 1) red[w] = incl;
+  __syncthreads();
+  int pre = 0;
+  total = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    const int r = red[i];
+    pre += i < w ? r : 0;
+    total += r;
+  }
+  return pre + incl - v;
+}
+
+template <int NW>
+__device__ __forceinline__ int block_sum(int v, int* red) {
+  v = wave_sum_i(v);
+  __syncthreads();
+  if (lane_id() == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t += red[i];
+  return t;
+}
+
 // Hillis-Steele inclusive scan of one 128-position tile (p = h * 64 + lane).
 template <typename T>
 __device__ __forceinline__ void hs_scan128(T c[2], int l) {

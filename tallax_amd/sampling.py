@@ -2,7 +2,9 @@
 
 `sample` is the vLLM-facing hook (sampling.py:331-343): one fused HIP kernel
 does the per-row top-k (clamped to 128, as the reference's max_k=128), the
-top-p filter, temperature and Gumbel-max draw.  `top_p_and_sample`
+top-p filter, temperature and Gumbel-max draw.  `sample(..., max_k=K)`
+with 128 < K <= 1024 opts into a wide-candidate kernel that honours per-row
+top_k up to K instead of clamping it to 128.  `top_p_and_sample`
 (sampling.py:210-269) runs the same tail on candidates the caller already
 selected, and `top_p_mask` (sampling.py:25-62) only its top-p filter.
 
@@ -21,6 +23,7 @@ from . import _lib
 
 _SAMPLING_EPS = 1e-5  # sampling.py:22
 NUM_CANDIDATES = 128  # the sampler's top-k width, max_k = NUM_LANES (sampling.py:283-290)
+MAX_WIDE_CANDIDATES = 1024  # widest opt-in candidate list (tallax_sample_wide)
 
 
 def _key_tensor(rng_key: Any, device: torch.device) -> torch.Tensor:
@@ -53,13 +56,18 @@ def _per_row(v: Any, rows: int, dtype: torch.dtype, device: torch.device) -> tor
 
 def sample(rng_key: Any, logits: torch.Tensor, tpu_sampling_metadata: Any,
            *, replace_val: float = -1e12, dim0_offset: int = 0,
-           workspace: torch.Tensor | None = None) -> torch.Tensor:
+           workspace: torch.Tensor | None = None, max_k: int = NUM_CANDIDATES) -> torch.Tensor:
     """Fused top-k -> top-p -> temperature -> Gumbel-max sampler.
 
     Reference: sample(rng_key, logits, tpu_sampling_metadata) (sampling.py:331-343).
     `tpu_sampling_metadata` exposes `.top_k` (int, per row), `.top_p` and
     `.temperature` (float, per row).  The per-row k is clamped to 128 as in
     the reference (max_k=NUM_LANES, sampling.py:283-290).  Returns int32 [rows].
+
+    max_k (opt-in, beyond the reference): the candidate width.  128 is the
+    reference's; any value in [1, 1024] other than 128 runs the wide-candidate
+    kernel, which is the same algorithm with the clamp at max_k (exact
+    top-max_k, then top_p_and_sample over max_k candidates).
     """
     _lib.require_cuda(logits)
     if logits.ndim != 2:
@@ -75,6 +83,9 @@ def sample(rng_key: Any, logits: torch.Tensor, tpu_sampling_metadata: Any,
     if dt == _lib.I32:
         raise NotImplementedError("sample() needs float logits")
     out = torch.empty(rows, dtype=torch.int32, device=dev)
+    if max_k != NUM_CANDIDATES:
+        _wide_candidates(logits, dt, int(max_k), key, top_k, top_p, temp, dim0_offset, replace_val, out)
+        return out
     need = _lib.LIB.tallax_sample_workspace_size(rows, vocab, dt)
     ws = workspace if workspace is not None else _lib.workspace(dev, need)
     _lib.check(_lib.LIB.tallax_fused_topk_topp_sample(
@@ -83,6 +94,38 @@ def sample(rng_key: Any, logits: torch.Tensor, tpu_sampling_metadata: Any,
         ws.data_ptr() if need else None, ws.numel() if need else 0, _lib.stream_of(logits)),
         "sample")
     return out
+
+
+def _wide_candidates(logits, dt, max_k, key, top_k, top_p, temp, dim0_offset, replace_val, out_tokens,
+                     out_idx=None, out_vals=None):
+    rows, vocab = logits.shape
+    _lib.check(_lib.LIB.tallax_sample_wide(
+        logits.data_ptr(), dt, rows, vocab, max_k,
+        top_k.data_ptr() if top_k is not None else None, top_p.data_ptr() if top_p is not None else None,
+        temp.data_ptr() if temp is not None else None, key.data_ptr() if key is not None else None,
+        int(dim0_offset), float(replace_val),
+        out_tokens.data_ptr() if out_tokens is not None else None,
+        out_idx.data_ptr() if out_idx is not None else None,
+        out_vals.data_ptr() if out_vals is not None else None, _lib.stream_of(logits)), "sample(max_k)")
+
+
+def wide_top_k(logits: torch.Tensor, max_k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The candidates of sample(..., max_k): the max_k largest values of each
+    row (value descending, ties to the lowest index; NaN, -inf and finfo.min
+    reported as finfo(dtype).min), as float32 values and int32 columns
+    [rows, max_k], before the per-row k mask.  max_k in [1, 1024]."""
+    _lib.require_cuda(logits)
+    if logits.ndim != 2:
+        raise ValueError("Only 2D inputs supported")
+    logits = logits.contiguous()
+    dt = _lib.dtype_code(logits)
+    if dt == _lib.I32:
+        raise NotImplementedError("wide_top_k needs float logits")
+    rows = logits.shape[0]
+    vals = torch.empty((rows, max_k), dtype=torch.float32, device=logits.device)
+    idx = torch.empty((rows, max_k), dtype=torch.int32, device=logits.device)
+    _wide_candidates(logits, dt, int(max_k), None, None, None, None, 0, -1e12, None, idx, vals)
+    return vals, idx
 
 
 def top_p_mask(*, topk_logits: torch.Tensor, p: Any, replace_val: float, axis: int) -> torch.Tensor:
@@ -210,4 +253,4 @@ class SamplingMetadata:
         self.temperature = temperature
 
 
-__all__: Sequence[str] = ["sample", "sample_sharded", "top_p_mask", "top_p_and_sample", "SamplingMetadata"]
+__all__: Sequence[str] = ["sample", "wide_top_k", "sample_sharded", "top_p_mask", "top_p_and_sample", "SamplingMetadata"]

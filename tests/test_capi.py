@@ -79,3 +79,21 @@ def test_new_entry_points_validate_on_the_host():
     # sort-key gather: an output dtype a key cannot decode to
     assert L.tallax_gather_sort_key(1, _lib.F32, 2, 10, 1, 1, _lib.BF16, None) == _lib.INVALID_ARGUMENT
     assert L.tallax_gather_sort_key(1, 7, 2, 10, 1, 1, _lib.F32, None) == _lib.UNSUPPORTED
+
+
+def test_wide_sampler_validates_on_the_host():
+    """tallax_sample_wide rejects widths outside [1, 1024] or above the
+    vocabulary, and calls with nothing to write, before any launch."""
+    from tallax_amd import _lib
+    L = _lib.LIB
+    par = (1, 1, 1, 1, 0, -1e12)  # top_k, top_p, temperature, key, dim0_offset, replace_val
+    assert L.tallax_sample_wide(1, 1, 4, 128256, 1025, *par, 1, None, None, None) == _lib.UNSUPPORTED
+    assert L.tallax_sample_wide(1, 1, 4, 128256, 0, *par, 1, None, None, None) == _lib.INVALID_ARGUMENT
+    assert L.tallax_sample_wide(1, 1, 4, 500, 501, *par, 1, None, None, None) == _lib.INVALID_ARGUMENT
+    assert L.tallax_sample_wide(1, 1, 4, 128256, 1024, *par, None, None, None, None) == _lib.INVALID_ARGUMENT
+    assert L.tallax_sample_wide(1, 2, 4, 128256, 1024, *par, 1, None, None, None) == _lib.UNSUPPORTED
+    assert L.tallax_sample_wide(1, 1, 4, 128256, 1024, None, 1, 1, 1, 0, -1e12, 1, None, None, None) \
+        == _lib.INVALID_ARGUMENT
+    assert L.tallax_sample_wide(1, 1, 0, 128256, 1024, None, None, None, None, 0, -1e12, None, 1, None, None) \
+        == _lib.OK
+

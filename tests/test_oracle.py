@@ -272,6 +272,52 @@ def test_sampler_replace_and_quirk_threshold_zero():
     assert np.array_equal(m[:, 0], np.array([3.0, 2.0, 1.0, -1e12], np.float32))
 
 
+def test_wide_sampler_oracle_dense_brute_force():
+    """sample(max_k=K) (beyond the reference's 128) against a dense
+    restatement: the top-K set by a stable sort, the k mask, a float64 top-p
+    cut (rows whose cumsum lies within 1e-4 of p are skipped), then
+    argmax(masked / T + gumbel(row, token)) over the whole vocabulary."""
+    rng = np.random.default_rng(21)
+    B, V, K = 12, 3000, 700
+    x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    x[:, ::7] = np.round(x[:, ::7])  # ties
+    kr = rng.integers(150, K + 1, B)
+    p = rng.uniform(0.3, 0.95, B).astype(np.float32)
+    T = rng.uniform(0.5, 1.5, B).astype(np.float32)
+    tok = O.sample((3, 4), x, kr, p, T, max_k=K)
+    checked = 0
+    for b in range(B):
+        order = np.argsort(-x[b].astype(np.float64), kind="stable")[:K]
+        v = x[b, order].astype(np.float64)
+        v[kr[b]:] = -1e12
+        pr = np.exp(v - v[0]); pr /= pr.sum()
+        c = np.cumsum(pr)
+        if np.min(np.abs(c - p[b])) < 1e-4:
+            continue
+        t = int((c < p[b]).sum())
+        keep = v >= v[t]
+        g = O.gumbel((3, 4), (np.full(K, b), order.astype(np.int32)), V).astype(np.float64)
+        score = np.where(keep, v, -1e12) / T[b] + g
+        assert tok[b] == order[np.argmax(score)], b
+        checked += 1
+    assert checked >= 8
+
+
+def test_wide_sampler_oracle_reduces_to_the_reference_width():
+    """With every per-row k <= 128, widening the candidate list only adds
+    masked candidates: sample(max_k=K) == sample() for any K >= 128."""
+    rng = np.random.default_rng(22)
+    B, V = 16, 5000
+    x = (rng.standard_normal((B, V)) * 3).astype(np.float32)
+    kr = rng.integers(1, 129, B)
+    p = rng.uniform(0.5, 1.0, B).astype(np.float32)
+    p[::5] = 1.0
+    T = rng.uniform(0.5, 1.5, B).astype(np.float32)
+    want = O.sample((9, 1), x, kr, p, T)
+    for K in (200, 512, 1024):
+        assert np.array_equal(O.sample((9, 1), x, kr, p, T, max_k=K), want), K
+
+
 # --------------------------------------------------------------------------- take_along_axis
 def test_take_along_axis_oracle_closed_form():
     """gather.py:11-45: in-range indices gather exactly as numpy does; negative
