@@ -39,7 +39,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak, GB/s
 COPY_BYTES = 256 << 20  # calibration copy: 256 MiB read + 256 MiB written per launch
-CONFIGS = ["sampler", "topk_c3", "topk_c3_approx", "topk_c1", "sort_c2", "prefill_c5", "sort_wide", "copy"]
+CONFIGS = ["sampler", "sampler_wide", "topk_c3", "topk_c3_approx", "topk_c1", "sort_c2", "prefill_c5", "sort_wide", "copy"]
 
 
 def _copy_rate(torch, dev, stream, steps, warmup):
@@ -102,7 +102,8 @@ class Workload:
     shape = (0, 0)
 
 
-def _sampler(torch, np, _lib, dev, s_handle, gen, nbuf):
+def _sampler(torch, np, _lib, dev, s_handle, gen, nbuf, max_k=128):
+    """Config 4; max_k > 128 is the opt-in wide-candidate sampler on the same input."""
     w = Workload()
     rows, cols = 256, 128256
     rng = np.random.default_rng(5)
@@ -124,9 +125,19 @@ def _sampler(torch, np, _lib, dev, s_handle, gen, nbuf):
                   "N(0,3), top_k U{1..1024} (clamped to 128), top_p U[0.7,1), T U[0.5,1.5), threefry key (0,1234)")
     w.kernel = _lib.select_plan(rows, cols, _lib.BF16)["kernel"].replace("SAMPLE", "true")
     w.cpu_batch = 16
+    if max_k != 128:
+        w.metric = (f"rows/s + achieved HBM GB/s (% peak): wide-candidate sampler (max_k={max_k}) "
+                    "@256x128256 bf16")
+        w.workload = w.workload.replace("(clamped to 128)", f"(honoured up to max_k={max_k})")
+        w.kernel = "sample_wide_kernel<bf16>"
 
     def launch(i):
         x = bufs[i % len(bufs)]
+        if max_k != 128:
+            _lib.check(_lib.LIB.tallax_sample_wide(
+                x.data_ptr(), _lib.BF16, rows, cols, max_k, d_topk.data_ptr(), d_topp.data_ptr(),
+                d_temp.data_ptr(), d_key.data_ptr(), 0, -1e12, out.data_ptr(), None, None, s_handle), "sample_wide")
+            return
         _lib.check(_lib.LIB.tallax_fused_topk_topp_sample(
             x.data_ptr(), _lib.BF16, rows, cols, d_topk.data_ptr(), d_topp.data_ptr(), d_temp.data_ptr(),
             d_key.data_ptr(), 0, -1e12, out.data_ptr(), ws.data_ptr(), ws.numel(), s_handle), "sample")
@@ -140,12 +151,13 @@ def _sampler(torch, np, _lib, dev, s_handle, gen, nbuf):
         h = host0(O)
         launch(0)
         torch.cuda.synchronize()
-        return bool(np.array_equal(out.cpu().numpy(), O.sample(key, h, topk, topp, temp, dtype="bf16")))
+        return bool(np.array_equal(out.cpu().numpy(), O.sample(key, h, topk, topp, temp, dtype="bf16",
+                                                               max_k=max_k)))
 
     def cpu_step(O, r0, batch):
         h = host0(O)
         sl = slice(r0, r0 + batch)
-        O.sample(key, h[sl], topk[sl], topp[sl], temp[sl], dtype="bf16", dim0_offset=r0)
+        O.sample(key, h[sl], topk[sl], topp[sl], temp[sl], dtype="bf16", dim0_offset=r0, max_k=max_k)
         return h[sl].shape[0]
 
     w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
@@ -416,6 +428,8 @@ def main() -> int:
 
     if args.config == "sampler":
         w = _sampler(torch, np, _lib, dev, s_handle, gen, args.nbuf)
+    elif args.config == "sampler_wide":
+        w = _sampler(torch, np, _lib, dev, s_handle, gen, args.nbuf, max_k=1024)
     elif args.config.startswith("topk"):
         w = _topk(torch, np, _lib, dev, s_handle, gen, args.nbuf, args.config)
     elif args.config == "sort_c2":

@@ -32,14 +32,26 @@ WIDE_TOPK_CASES = [
     (2, 50000, 1024, "f32", "tieblock"),
     (2, 50000, 512, "bf16", "nan_heavy"),
     (2, 40000, 300, "f32", "sorted_asc"),
+    (3, 40000, 1024, "f32", "outlier"),    # K-th value far below the maximum: the whole-row digit passes
+    (3, 40000, 1024, "bf16", "outlier"),
+    (2, 6000, 1024, "bf16", "normal"),     # fewer than K threads hold an element
 ]
+
+
+def _make_wide(rows, cols, kind, seed):
+    if kind == "outlier":
+        x = _make(rows, cols, "normal", seed)
+        x[:, 17] = 1e30
+        x[1:, 40] = -1e30
+        return x
+    return _make(rows, cols, kind, seed)
 
 
 @pytest.mark.parametrize("rows,cols,k,dtype,kind", WIDE_TOPK_CASES)
 def test_wide_top_k_parity(gpu, rows, cols, k, dtype, kind):
     from tallax_amd import sampling
     _log(f"wide_top_k rows={rows} cols={cols} k={k} dtype={dtype} kind={kind}")
-    x = _make(rows, cols, kind, seed=cols + k)
+    x = _make_wide(rows, cols, kind, seed=cols + k)
     xd = to_dev(x, dtype, gpu)
     vals, idx = sampling.wide_top_k(xd, k)
     torch.cuda.synchronize()
