@@ -29,10 +29,12 @@
 //     pass reading the row again and counting only the elements whose higher
 //     digits match the threshold prefix found so far, until the K-th largest
 //     key is known (or the crossing bin is taken whole);
-//   collect: one more read appends the elements above the threshold, and the
-//     threshold ties in index order (one workgroup scan per 8192-column chunk
-//     that holds a tie, until enough are taken), to LDS: exactly K elements;
-//   a 1024-record bitonic sort of their composites (key << 32 | ~index);
+//   collect: one more read appends the elements above the threshold and the
+//     threshold ties to LDS: all ties when they fit a 2048-record list beside
+//     the rest, else the first ones in index order (one workgroup scan per
+//     8192-column chunk that holds a tie, until enough are taken);
+//   a 2048-record bitonic sort of their composites (key << 32 | ~index),
+//     whose first K are the candidates;
 //   the sampler tail with one candidate per thread.
 // The row is read two (bf16) to four (f32) times; the re-reads of a row just
 // streamed are served mostly from the caches.
@@ -52,6 +54,7 @@ namespace tx {
 constexpr int kSwNT = 1024;
 constexpr int kSwNW = kSwNT / kWave;
 constexpr int kSwMaxK = 1024;           // candidates per row, at most (one per thread)
+constexpr int kSwList = 2048;           // collected records, at most (two per thread in the sort)
 constexpr int kSwBins = 2048;           // 11-bit digits
 constexpr int kSwChunk = kSwNT * 8;     // columns per workgroup step: 8 per thread
 
@@ -151,7 +154,7 @@ template <int DT>
 __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   constexpr int ES = DT == kBF16 ? 2 : 4;
   __shared__ int s_hist[kSwBins];
-  __shared__ uint64_t s_list[kSwMaxK];
+  __shared__ uint64_t s_list[kSwList];
   __shared__ float s_v[kSwMaxK];
   __shared__ float s_e[kSwMaxK];
   __shared__ float s_tot[kSwMaxK / 8];
@@ -192,7 +195,10 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
     need -= above;
     tsh = dsh;
     __syncthreads();  // s_res and s_hist are rewritten by the next pass
-    if (need == cnt) {
+    // The crossing bin is taken whole when it is all needed, or when all its
+    // elements fit the list beside the K - need above it: the sort then puts
+    // its ties in index order and the first K records are kept.
+    if (need == cnt || K - need + cnt <= kSwList) {
       take_all = true;
       break;
     }
@@ -231,16 +237,23 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
       const int q = __builtin_ctz(take);
       take &= take - 1u;
       const int pos = atomicAdd(&s_cnt, 1);
-      if (pos < kSwMaxK) s_list[pos] = make_comp(k[q], (uint32_t)(base + q));
+      if (pos < kSwList) s_list[pos] = make_comp(k[q], (uint32_t)(base + q));
     }
   }
   __syncthreads();
 
   // --- sort the K candidates, descending ---------------------------------------
-  uint64_t rec[1];
-  rec[0] = t < K ? s_list[t] : 0ull;
+  const int ncol = min(s_cnt, kSwList);  // K, or more when a tie bin was taken whole
+  uint64_t pair[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) pair[r] = 2 * t + r < ncol ? s_list[2 * t + r] : 0ull;
   __syncthreads();
-  block_bitonic_sort_c<uint64_t, 1, kSwNT, true>(rec, s_list);
+  block_bitonic_sort_c<uint64_t, 2, kSwList, true>(pair, s_list);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) s_list[2 * t + r] = pair[r];
+  __syncthreads();
+  uint64_t rec[1];
+  rec[0] = s_list[t];
 
   const bool in = t < K;
   const uint32_t kk = comp_key(rec[0]);
