@@ -38,11 +38,16 @@ int tallax_testing_lane_ops(uint32_t* out, tallax_stream_t stream);
  * out[3] vectors per segment.  Host only: no device work. */
 int tallax_testing_select_plan(int64_t rows, int64_t cols, int dtype, int32_t* out);
 
-// Path of tallax_top_dynamic_k for later calls in this process: 0 (default)
-// settles rows from the exact kernel's per-segment top-128 candidates where
-// they suffice and scans the rest; 1 scans every row.  Both give the same
-// results; tests run both.  Returns TALLAX_INVALID_ARGUMENT for other values.
-int tallax_testing_binned_mode(int mode);
+/* tallax_top_dynamic_k with its path chosen by `path`: 0 (what
+ * tallax_top_dynamic_k runs) settles rows from the exact kernel's per-segment
+ * top-128 candidates where they suffice and scans the rest; 1 scans every
+ * row.  Both give the same results; tests run both.  Other arguments as
+ * tallax_top_dynamic_k; TALLAX_INVALID_ARGUMENT for another path. */
+int tallax_testing_top_dynamic_k_path(const void* x, int dtype, int64_t rows, int64_t cols, const int32_t* k_rows,
+                                      int max_k, int block_token, int num_bins, const int32_t* schedule,
+                                      int num_steps, int has_replace, double replace_val, void* out_vals,
+                                      int32_t* out_idx, int32_t* out_valid, int32_t* out_depths, float* out_cutoff,
+                                      void* workspace, size_t workspace_bytes, tallax_stream_t stream, int path);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -238,7 +238,12 @@ def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, repla
     depth_upper the power-of-two bucket of the global max depth
     (top_k.py:333-364), ordered by value then lowest index (the reference's
     network order inside ties is not pinned), then truncated to max_k;
-    positions >= k[row] get replace_val in the input dtype when given."""
+    positions >= k[row] get replace_val in the input dtype when given.
+    Ranks at or past the m of a block's last evaluated step are never written
+    for that block's rows: they keep the finfo.min the scratch starts with
+    (top_k.py:241-243, 250-281), so they reach the output only as
+    (finfo.min, -1) fillers (the reference leaves those indices
+    uninitialised)."""
     x = np.asarray(x, dtype=np.float32)
     rows, cols = x.shape
     if rows % block_token:
@@ -250,6 +255,7 @@ def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, repla
     max_m = sched[-1]
     buf = max(max_m, 2 ** log2_ceil(max_m - 1)) if max_m > 1 else max_m
     bv, bi = binned_topm(x, buf, num_bins, dtype)
+    lo = dtype_min(dtype)
     depths = np.full(rows, max_k, np.int32)
     cutoff = np.zeros(rows, np.float32)
     for b0 in range(0, rows, block_token):
@@ -263,6 +269,9 @@ def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, repla
             cutoff[blk] = pivot
             if conv.all():
                 break
+        # ranks >= m (the last step this block evaluated) were never written
+        bv[blk, m:, :] = lo
+        bi[blk, m:, :] = -1
     gmax = int(depths.max())
     valid = bool(gmax < sched[-1] or sched[-1] == max_k)
     gsched = sorted(set(2 ** log2_ceil(s - 1) if s > 1 else s for s in sched))

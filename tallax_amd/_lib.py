@@ -61,7 +61,9 @@ _SIGNATURES = {
     "tallax_testing_gumbel": ([ctypes.c_uint32, ctypes.c_uint32, _c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
     "tallax_testing_lane_ops": ([_c_p, _c_p], _c_int),
     "tallax_testing_select_plan": ([_c_i64, _c_i64, _c_int, _c_p], _c_int),
-    "tallax_testing_binned_mode": ([_c_int], _c_int),
+    "tallax_testing_top_dynamic_k_path": ([_c_p, _c_int, _c_i64, _c_i64, _c_p, _c_int, _c_int, _c_int, _c_p, _c_int,
+                                           _c_int, _c_d, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p, _c_int],
+                                          _c_int),
 }
 
 
@@ -119,10 +121,15 @@ def ptr(t: torch.Tensor | None) -> int | None:
 # Workspace: one byte buffer per device, grown on demand.  No kernel reads
 # workspace contents it did not write in the same call, so the buffer never
 # needs clearing.  Calls that overlap on one device (different streams) must
-# pass their own workspace.
+# pass their own workspace.  A buffer that growth supersedes is kept alive
+# (never returned to the caching allocator), so work already enqueued on it,
+# or a HIP graph captured with its address, never sees its memory reused.
+# Growth is refused while the current stream is capturing: a capturing caller
+# passes workspace= or warms the buffer up eagerly first.
 # ---------------------------------------------------------------------------
 _ws_lock = threading.Lock()
 _ws: dict[int, torch.Tensor] = {}
+_ws_retired: list[torch.Tensor] = []
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
@@ -130,9 +137,28 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     with _ws_lock:
         buf = _ws.get(idx)
         if buf is None or buf.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    f"tallax_amd: the shared workspace of device {idx} must grow to {nbytes} bytes during "
+                    "stream capture; pass workspace= or run the call once before capturing")
+            if buf is not None:
+                _ws_retired.append(buf)
             buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
             _ws[idx] = buf
         return buf
+
+
+def workspace_arg(workspace_t: torch.Tensor | None, device: torch.device, nbytes: int) -> torch.Tensor:
+    """The caller's workspace (checked: a uint8 tensor on `device`, at least
+    nbytes long) or the shared per-device one."""
+    if workspace_t is None:
+        return workspace(device, nbytes)
+    if (not isinstance(workspace_t, torch.Tensor) or workspace_t.device != device
+            or workspace_t.dtype != torch.uint8 or not workspace_t.is_contiguous()):
+        raise ValueError("workspace must be a contiguous uint8 tensor on the operands' device")
+    if workspace_t.numel() < nbytes:
+        raise ValueError(f"workspace of {workspace_t.numel()} bytes is smaller than the {nbytes} required")
+    return workspace_t
 
 
 def require_cuda(*ts: torch.Tensor) -> None:

@@ -14,10 +14,15 @@
 //   * valid = (max depth over all rows < schedule[-1]) or schedule[-1] == max_k;
 //   * the result is the top-128 of the first depth_upper ranks of every bin
 //     (depth_upper = the power-of-two bucket of the global max depth),
-//     truncated to max_k, with replace_val at positions >= k[row].
+//     truncated to max_k, with replace_val at positions >= k[row];
+//   * a block writes only the ranks of the steps it evaluated: ranks at or
+//     past the m of its last evaluated step keep the finfo.min the scratch
+//     starts with (top_k.py:241-243, 250-281), so they count as fillers in
+//     the final selection even where depth_upper reaches past them.
 // The ranks inside a bin are the same whatever the pass structure (each pass
 // extends the exact per-bin top-m), so one scan computes the deepest lists
-// and every step's statistics.
+// and every step's statistics; the select kernel drops the ranks a block
+// never evaluated.
 //
 // Kernels:
 //   binned_lists_kernel  one workgroup per row: thread (bin, slice) scans
@@ -25,7 +30,8 @@
 //                        top-MC list; the slices of a bin are merged through
 //                        LDS; ranks < buf go to the workspace with each
 //                        step's (pivot, count).
-//   binned_finish_kernel one workgroup: depths, cutoffs, valid, depth_upper.
+//   binned_finish_kernel one workgroup: depths, cutoffs, valid, depth_upper
+//                        and each row's last evaluated m.
 //   binned_select_kernel one workgroup per row: bitonic sort of the
 //                        depth_upper * num_bins superset, top-128 out.
 #include <float.h>
@@ -33,6 +39,7 @@
 #include <string.h>
 
 #include "tallax_hip.h"
+#include "tallax_hip_testing.h"
 #include "tx_common.h"
 #include "tx_host.h"
 #include "tx_wave_sort.h"
@@ -68,6 +75,9 @@ struct BinArgs {
   float* st_pivot;         // [rows][nsteps]
   int32_t* st_count;       // [rows][nsteps]
   int32_t* upper;          // [1]
+  int32_t* row_fc;         // [rows] first converged step (nsteps if none)
+  int32_t* blk_last;       // [rows / block_token] last step each block evaluated
+  int32_t* row_mlast;      // [rows] m of the last step the row's block evaluated
   // candidate path
   const uint64_t* lists;   // [rows][nseg][128] per-segment sorted top-128 composites
   int nseg;
@@ -212,40 +222,56 @@ __global__ __launch_bounds__(kBinNT) void binned_lists_kernel(BinArgs a) {
   scan_row<MC>(a, blockIdx.x, smem);
 }
 
-// Depths, cutoffs, valid and depth_upper from the per-step statistics, one
-// thread per row: a row's depth is m - 1 at its first converged step (max_k
-// if none); a block of block_token rows evaluates steps until all of its rows
-// converged, and its cutoff is the pivot of the last step evaluated.
+// Depths, cutoffs, valid, depth_upper and each row's last evaluated m from
+// the per-step statistics: a row's depth is m - 1 at its first converged step
+// (max_k if none); a block of block_token rows evaluates steps until all of
+// its rows converged, and its cutoff is the pivot of the last step evaluated.
+// Three passes over rows, blocks and rows (any block_token); the barriers
+// between them order this workgroup's own global writes and reads.
 constexpr int kFinishNT = 1024;
+
+__device__ __forceinline__ int first_converged(const BinArgs& a, int64_t r) {
+  const int kr = a.k_rows[r];
+  int fc = a.nsteps;
+  for (int q = a.nsteps - 1; q >= 0; --q)
+    if (a.st_count[r * a.nsteps + q] >= kr) fc = q;
+  return fc;
+}
+
+__device__ __forceinline__ int depth_upper_of(const BinArgs& a, int g) {
+  int up = a.gsched[a.ngs - 1];
+  for (int i = 0; i + 1 < a.ngs; ++i) {
+    if (a.gsched[i] < g && g <= a.gsched[i + 1]) {
+      up = a.gsched[i + 1];
+      break;
+    }
+  }
+  return up;
+}
+
 __device__ __forceinline__ void finish_rows(const BinArgs& a) {
-  __shared__ int fcs[kFinishNT];
   __shared__ int red[kFinishNT / kWave];
   const int t = threadIdx.x;
   int gmax = 0;
-  // chunks of whole blocks of rows
-  const int per = kFinishNT / a.block_token * a.block_token;
-  for (int64_t r0 = 0; r0 < a.rows; r0 += per) {
-    const int64_t r = r0 + t;
-    int fc = a.nsteps;
-    const bool live = t < per && r < a.rows;
-    if (live) {
-      const int kr = a.k_rows[r];
-      for (int q = a.nsteps - 1; q >= 0; --q)
-        if (a.st_count[r * a.nsteps + q] >= kr) fc = q;
-    }
-    fcs[t] = fc;
-    __syncthreads();
-    if (live) {
-      const int b0 = t / a.block_token * a.block_token;
-      int qb = 0;
-      for (int i = 0; i < a.block_token; ++i) qb = max(qb, fcs[b0 + i]);
-      const int last = qb < a.nsteps - 1 ? qb : a.nsteps - 1;
-      const int depth = fc < a.nsteps ? a.steps[fc] - 1 : a.max_k;
-      a.out_depths[r] = depth;
-      a.out_cutoff[r] = a.st_pivot[r * a.nsteps + last];
-      gmax = max(gmax, depth);
-    }
-    __syncthreads();
+  for (int64_t r = t; r < a.rows; r += kFinishNT) {
+    const int fc = first_converged(a, r);
+    a.row_fc[r] = fc;
+    const int depth = fc < a.nsteps ? a.steps[fc] - 1 : a.max_k;
+    a.out_depths[r] = depth;
+    gmax = max(gmax, depth);
+  }
+  __syncthreads();
+  const int64_t nblk = a.rows / a.block_token;
+  for (int64_t b = t; b < nblk; b += kFinishNT) {
+    int qb = 0;
+    for (int64_t i = 0; i < a.block_token; ++i) qb = max(qb, a.row_fc[b * a.block_token + i]);
+    a.blk_last[b] = qb < a.nsteps - 1 ? qb : a.nsteps - 1;
+  }
+  __syncthreads();
+  for (int64_t r = t; r < a.rows; r += kFinishNT) {
+    const int last = a.blk_last[r / a.block_token];
+    a.out_cutoff[r] = a.st_pivot[r * a.nsteps + last];
+    a.row_mlast[r] = a.steps[last];
   }
   const int l = lane_id();
 #pragma unroll
@@ -256,14 +282,7 @@ __device__ __forceinline__ void finish_rows(const BinArgs& a) {
     int g = 0;
     for (int i = 0; i < kFinishNT / kWave; ++i) g = max(g, red[i]);
     a.out_valid[0] = (g < a.steps[a.nsteps - 1] || a.steps[a.nsteps - 1] == a.max_k) ? 1 : 0;
-    int up = a.gsched[a.ngs - 1];
-    for (int i = 0; i + 1 < a.ngs; ++i) {
-      if (a.gsched[i] < g && g <= a.gsched[i + 1]) {
-        up = a.gsched[i + 1];
-        break;
-      }
-    }
-    a.upper[0] = up;
+    a.upper[0] = depth_upper_of(a, g);
   }
 }
 
@@ -431,12 +450,24 @@ __global__ __launch_bounds__(kCandNT) void binned_cand_kernel(BinArgs a) {
   // coverage of the steps, the row's depth and the entries below min(depth, buf)
   bool ok = s_bad == 0;
   int depth = a.max_k;
+  bool conv = false;
   for (int q = 0; q < a.nsteps; ++q) {
     const uint64_t pv = s_piv[q];
     ok = ok && pv != 0ull && comp_key(pv) > comp_key(t0);
-    if (depth == a.max_k && s_cnt[q] >= a.k_rows[row]) depth = a.steps[q] - 1;
+    if (!conv && s_cnt[q] >= a.k_rows[row]) {
+      conv = true;
+      depth = a.steps[q] - 1;
+    }
   }
-  const int dm = depth < a.buf ? depth : a.buf;
+  // The final selection reads ranks below R = min(depth_upper, m of the last
+  // step the row's block evaluated).  A converged row has R >= depth
+  // (depth_upper >= min(global max depth, last bucket) >= depth, and its
+  // block ran at least to its converging step m = depth + 1); an unconverged
+  // row's block ran every step, so R >= min(max_k, m_final - 1).  max_k
+  // entries of C below that bound make the final top-max_k come from C.
+  const int mf = a.steps[a.nsteps - 1];
+  int dm = conv ? depth : (a.max_k < mf - 1 ? a.max_k : mf - 1);
+  dm = dm < a.buf ? dm : a.buf;
   if (bw) {
     const int v = wave_sum_i(cb < dm ? cb : dm);
     if (l == 0) s_redi[0][w] = v;
@@ -500,6 +531,7 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
   __shared__ uint64_t tree[NW][128];
   __shared__ int fcs[kSelNT];
   __shared__ int red[NW];
+  __shared__ int s_mlast;
   const int t = threadIdx.x, w = t / kWave, l = lane_id();
   const int64_t row = blockIdx.x;
   const int NB = a.num_bins;
@@ -519,15 +551,10 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
       pi[k][h] = e < nall ? li[e] : -1;
     }
   }
-  int upper_v;
+  int upper_v, mlast;
   if (INLINE) {
-    int fc = a.nsteps;
     const bool live = t < a.rows;
-    if (live) {
-      const int kr = a.k_rows[t];
-      for (int q = a.nsteps - 1; q >= 0; --q)
-        if (a.st_count[(int64_t)t * a.nsteps + q] >= kr) fc = q;
-    }
+    const int fc = live ? first_converged(a, t) : a.nsteps;
     fcs[t] = fc;
     int g = live ? (fc < a.nsteps ? a.steps[fc] - 1 : a.max_k) : 0;
 #pragma unroll
@@ -536,15 +563,9 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
     __syncthreads();
     g = 0;
     for (int i = 0; i < NW; ++i) g = max(g, red[i]);
-    int up = a.gsched[a.ngs - 1];
-    for (int i = 0; i + 1 < a.ngs; ++i) {
-      if (a.gsched[i] < g && g <= a.gsched[i + 1]) {
-        up = a.gsched[i + 1];
-        break;
-      }
-    }
-    upper_v = up;
+    upper_v = depth_upper_of(a, g);
     if (t == 0) {
+      // rows <= kSelNT and block_token divides rows, so the block lies in fcs
       const int r = (int)row;
       const int b0 = r / a.block_token * a.block_token;
       int qb = 0;
@@ -554,11 +575,17 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
       a.out_depths[row] = fr < a.nsteps ? a.steps[fr] - 1 : a.max_k;
       a.out_cutoff[row] = a.st_pivot[row * a.nsteps + last];
       if (row == 0) a.out_valid[0] = (g < a.steps[a.nsteps - 1] || a.steps[a.nsteps - 1] == a.max_k) ? 1 : 0;
+      s_mlast = a.steps[last];
     }
+    __syncthreads();
+    mlast = s_mlast;
   } else {
     upper_v = a.upper[0];
+    mlast = a.row_mlast[row];
   }
-  const int up = upper_v < a.buf ? upper_v : a.buf;
+  // ranks the row's block never evaluated stay fillers
+  const int up0 = upper_v < a.buf ? upper_v : a.buf;
+  const int up = up0 < mlast ? up0 : mlast;
   const int n = up * NB;
   const int nr = (n + 127) / 128;
   uint64_t acc[2] = {0ull, 0ull};
@@ -627,7 +654,8 @@ static int log2_ceil(int x) {
 static int bin_buf(int max_m) { return max_m > 1 ? (max_m > (1 << log2_ceil(max_m - 1)) ? max_m : (1 << log2_ceil(max_m - 1))) : max_m; }
 
 // Workspace: candidate lists [rows][kMaxSegLists][128] u64, covered flags,
-// per-bin lists (values, indices), per-step pivots and counts, depth_upper.
+// per-bin lists (values, indices), per-step pivots and counts, depth_upper,
+// and the finish step's per-row / per-block step indices.
 constexpr int kMaxSegLists = 32;
 static size_t bin_ws(int64_t rows, int num_bins, int buf, int nsteps) {
   size_t b = 0;
@@ -637,7 +665,8 @@ static size_t bin_ws(int64_t rows, int num_bins, int buf, int nsteps) {
   b += (size_t)rows * buf * num_bins * 4;  // li
   b += (size_t)rows * nsteps * 4;          // pivots
   b += (size_t)rows * nsteps * 4;          // counts
-  b += 256;
+  b += 256;                                // depth_upper
+  b += 3 * align_up((size_t)rows * 4, 256);  // row_fc, blk_last, row_mlast
   return align_up(b, 256);
 }
 
@@ -645,17 +674,16 @@ static size_t bin_ws(int64_t rows, int num_bins, int buf, int nsteps) {
 
 using namespace tx;
 
-// Path selection (test hook): 0 = candidates where they settle a row, then the
-// full scan for the rest; 1 = the full scan for every row.
-static int g_binned_mode = 0;
+// Path: 0 = candidates where they settle a row, then the full scan for the
+// rest (the product path); 1 = the full scan for every row (testing entry
+// point only).  Both give the same results.
+static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t cols, const int32_t* k_rows,
+                              int max_k, int block_token, int num_bins, const int32_t* schedule, int num_steps,
+                              int has_replace, double replace_val, void* out_vals, int32_t* out_idx,
+                              int32_t* out_valid, int32_t* out_depths, float* out_cutoff, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream, int mode);
 
 extern "C" {
-
-int tallax_testing_binned_mode(int mode) {
-  if (mode != 0 && mode != 1) return kInvalidArgument;
-  g_binned_mode = mode;
-  return kOk;
-}
 
 size_t tallax_top_dynamic_k_workspace_size(int64_t rows, int num_bins, const int32_t* schedule, int num_steps) {
   if (rows < 0 || num_bins <= 0 || !schedule || num_steps <= 0 || num_steps > kMaxSteps) return 0;
@@ -667,6 +695,32 @@ int tallax_top_dynamic_k(const void* x, int dtype, int64_t rows, int64_t cols, c
                          double replace_val, void* out_vals, int32_t* out_idx, int32_t* out_valid,
                          int32_t* out_depths, float* out_cutoff, void* workspace, size_t workspace_bytes,
                          hipStream_t stream) {
+  return top_dynamic_k_impl(x, dtype, rows, cols, k_rows, max_k, block_token, num_bins, schedule, num_steps,
+                            has_replace, replace_val, out_vals, out_idx, out_valid, out_depths, out_cutoff, workspace,
+                            workspace_bytes, stream, 0);
+}
+
+int tallax_testing_top_dynamic_k_path(const void* x, int dtype, int64_t rows, int64_t cols, const int32_t* k_rows,
+                                      int max_k, int block_token, int num_bins, const int32_t* schedule,
+                                      int num_steps, int has_replace, double replace_val, void* out_vals,
+                                      int32_t* out_idx, int32_t* out_valid, int32_t* out_depths, float* out_cutoff,
+                                      void* workspace, size_t workspace_bytes, hipStream_t stream, int path) {
+  if (path != 0 && path != 1) {
+    set_error("path %d is not 0 (candidates) or 1 (scan)", path);
+    return kInvalidArgument;
+  }
+  return top_dynamic_k_impl(x, dtype, rows, cols, k_rows, max_k, block_token, num_bins, schedule, num_steps,
+                            has_replace, replace_val, out_vals, out_idx, out_valid, out_depths, out_cutoff, workspace,
+                            workspace_bytes, stream, path);
+}
+
+}  // extern "C"
+
+static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t cols, const int32_t* k_rows,
+                              int max_k, int block_token, int num_bins, const int32_t* schedule, int num_steps,
+                              int has_replace, double replace_val, void* out_vals, int32_t* out_idx,
+                              int32_t* out_valid, int32_t* out_depths, float* out_cutoff, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream, int mode) {
   if (!x || !k_rows || !schedule || !out_vals || !out_idx || !out_valid || !out_depths || !out_cutoff) {
     set_error("null pointer argument");
     return kInvalidArgument;
@@ -739,6 +793,12 @@ int tallax_top_dynamic_k(const void* x, int dtype, int64_t rows, int64_t cols, c
   a.st_count = (int32_t*)w;
   w += (size_t)rows * num_steps * 4;
   a.upper = (int32_t*)w;
+  w += 256;
+  a.row_fc = (int32_t*)w;
+  w += align_up((size_t)rows * 4, 256);
+  a.blk_last = (int32_t*)w;
+  w += align_up((size_t)rows * 4, 256);
+  a.row_mlast = (int32_t*)w;
   if (rows > 2147483647) { set_error("too many rows"); return kUnsupported; }
   // candidate path: per-segment top-128 lists, then one kernel that settles
   // each row from them (or scans it); otherwise the scan kernel.  The finish
@@ -747,7 +807,7 @@ int tallax_top_dynamic_k(const void* x, int dtype, int64_t rows, int64_t cols, c
   int nseg = 0, maxv = 0;
   int64_t vps = 0;
   const int min_seg = (num_bins * max_m + 127) / 128;
-  const bool cand = g_binned_mode == 0 && max_m <= kCandRank &&
+  const bool cand = mode == 0 && max_m <= kCandRank &&
                     segment_lists_plan(cols, dtype, min_seg < 2 ? 2 : min_seg, &nseg, &maxv, &vps) == kOk &&
                     nseg <= kMaxSegLists;
   const int mc = buf <= 8 ? 8 : 16;
@@ -794,5 +854,3 @@ int tallax_top_dynamic_k(const void* x, int dtype, int64_t rows, int64_t cols, c
     hipLaunchKernelGGL(binned_select_kernel<false>, dim3((unsigned)rows), dim3(kSelNT), 0, stream, a);
   return launch_status("tallax_top_dynamic_k");
 }
-
-}  // extern "C"

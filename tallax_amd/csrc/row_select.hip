@@ -126,8 +126,6 @@ struct Geo {
   static constexpr int WCAP = 256;
 };
 constexpr int kStage = 6;                  // flagged 16-byte vectors staged per thread
-// Tunable (read once from the environment by the host):
-//   TALLAX_SEL_BLOCKS   workgroups aimed for per launch (default 1024).
 
 // ---------------------------------------------------------------------------
 // Per-dtype selection traits.
@@ -1020,26 +1018,6 @@ struct Plan {
   int64_t vps;
 };
 
-struct Tuning {
-  int target_blocks = kTargetBlocks;
-};
-
-static int env_int(const char* name, int dflt, int lo, int hi) {
-  const char* v = getenv(name);
-  if (!v || !*v) return dflt;
-  const long x = strtol(v, nullptr, 10);
-  return x < lo ? lo : (x > hi ? hi : (int)x);
-}
-
-static const Tuning& tuning() {
-  static const Tuning t = [] {
-    Tuning r;
-    r.target_blocks = env_int("TALLAX_SEL_BLOCKS", r.target_blocks, 1, 1 << 20);
-    return r;
-  }();
-  return t;
-}
-
 // Work split.  A row of nv 16-byte vectors is handled either
 //   * whole by one 512-thread workgroup (up to 32 vectors per thread) when
 //     that gives enough workgroups (>= 128 rows): no merge kernel at all; or
@@ -1062,7 +1040,7 @@ static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
   for (int o = 0; o < 3; ++o) {
     const int64_t per = (int64_t)kNT * kOpts[o];
     const int64_t nseg = (nv + per - 1) / per;
-    if (rows * nseg >= tuning().target_blocks && nseg <= kMaxSeg) { maxv = kOpts[o]; break; }
+    if (rows * nseg >= kTargetBlocks && nseg <= kMaxSeg) { maxv = kOpts[o]; break; }
   }
   int64_t per = (int64_t)kNT * maxv;
   int64_t nseg = (nv + per - 1) / per;

@@ -87,7 +87,7 @@ def sample(rng_key: Any, logits: torch.Tensor, tpu_sampling_metadata: Any,
         _wide_candidates(logits, dt, int(max_k), key, top_k, top_p, temp, dim0_offset, replace_val, out)
         return out
     need = _lib.LIB.tallax_sample_workspace_size(rows, vocab, dt)
-    ws = workspace if workspace is not None else _lib.workspace(dev, need)
+    ws = _lib.workspace_arg(workspace, dev, need)
     _lib.check(_lib.LIB.tallax_fused_topk_topp_sample(
         logits.data_ptr(), dt, rows, vocab, top_k.data_ptr(), top_p.data_ptr(), temp.data_ptr(),
         key.data_ptr(), int(dim0_offset), float(replace_val), out.data_ptr(),
@@ -188,7 +188,8 @@ def top_p_and_sample(topk_logits: torch.Tensor, topk_idx: torch.Tensor, rng_key:
 
 
 def sample_sharded(rng_key: Any, logit_shards: Sequence[torch.Tensor], tpu_sampling_metadata: Any,
-                   *, replace_val: float = -1e12, dim0_offset: int = 0) -> torch.Tensor:
+                   *, replace_val: float = -1e12, dim0_offset: int = 0,
+                   workspace: torch.Tensor | None = None) -> torch.Tensor:
     """`sample` over a vocabulary split into column shards, computed the way the
     reference's partitioned sampler does it, with every shard on this GPU.
 
@@ -203,7 +204,9 @@ def sample_sharded(rng_key: Any, logit_shards: Sequence[torch.Tensor], tpu_sampl
     with vocab_size = sum(V_i) (tallax_sample_from_candidates).  The tokens
     equal `sample` on the concatenated logits.  Here every shard's step runs
     on this GPU at its real shape; in a multi-GPU run each GPU runs only its
-    own, and the stacking is the collective.  At most 32 shards.
+    own, and the stacking is the collective.  At most 32 shards.  `workspace`:
+    a uint8 device tensor large enough for the largest shard, used instead of
+    the shared per-device buffer (the shard steps run in turn on one stream).
     """
     shards = list(logit_shards)
     if not shards:
@@ -225,7 +228,7 @@ def sample_sharded(rng_key: Any, logit_shards: Sequence[torch.Tensor], tpu_sampl
         xc = x.contiguous()
         cols = xc.shape[1]
         need = _lib.LIB.tallax_shard_candidates_workspace_size(rows, cols, dt)
-        ws = _lib.workspace(dev, need)
+        ws = _lib.workspace_arg(workspace, dev, need)
         cand = torch.empty((rows, NUM_CANDIDATES), dtype=torch.int64, device=dev)
         _lib.check(_lib.LIB.tallax_shard_candidates(xc.data_ptr(), dt, rows, cols, off, cand.data_ptr(),
                                                     ws.data_ptr() if need else None, ws.numel() if need else 0,

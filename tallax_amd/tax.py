@@ -47,7 +47,7 @@ def top_k(logits: torch.Tensor, k: int, block_token: int = 8, num_bins: int = NU
     vals = torch.empty((rows, k), dtype=x.dtype, device=x.device)
     idx = torch.empty((rows, k), dtype=torch.int32, device=x.device)
     need = _lib.LIB.tallax_topk_workspace_size(rows, cols, k, dt)
-    ws = workspace if workspace is not None else _lib.workspace(x.device, need)
+    ws = _lib.workspace_arg(workspace, x.device, need)
     _lib.check(_lib.LIB.tallax_topk(
         x.data_ptr(), dt, rows, cols, k, vals.data_ptr(), idx.data_ptr(),
         ws.data_ptr() if need else None, ws.numel() if need else 0, _lib.stream_of(x)), "top_k")
@@ -69,7 +69,7 @@ def _k_rows(k, rows: int, device) -> torch.Tensor:
 
 def top_dynamic_k(logits: torch.Tensor, k, max_k: int, block_token: int = 8, num_bins: int = NUM_LANES,
                   bins_topm_unroll: int = 32, bins_topm_schedule=None, guarantee_convergence: bool = False,
-                  replace_val=None, interpret: bool = False):
+                  replace_val=None, interpret: bool = False, *, workspace: torch.Tensor | None = None):
     """Per-row top-k (k <= max_k <= 128) by binned top-m supersets.
 
     Reference: top_dynamic_k (tallax/_src/top_k.py:385-514).
@@ -83,8 +83,19 @@ def top_dynamic_k(logits: torch.Tensor, k, max_k: int, block_token: int = 8, num
         converged answer, ties to the lowest index, as tax.top_k).
     Positions >= k[row] hold replace_val (in the logits dtype) when given.
     Raises ValueError if rows % block_token != 0 and NotImplementedError for
-    max_k > 128, like the reference.
+    max_k > 128, like the reference.  `workspace` (keyword only): a uint8
+    device tensor of at least the entry point's workspace size, used instead
+    of the shared per-device buffer (for callers that capture graphs or run
+    calls concurrently).
     """
+    return _top_dynamic_k(logits, k, max_k, block_token, num_bins, bins_topm_unroll, bins_topm_schedule,
+                          guarantee_convergence, replace_val, interpret, workspace, None)
+
+
+def _top_dynamic_k(logits, k, max_k, block_token, num_bins, bins_topm_unroll, bins_topm_schedule,
+                   guarantee_convergence, replace_val, interpret, workspace, testing_path):
+    """top_dynamic_k; testing_path 0/1 routes the binned form through the
+    testing entry point that forces the candidate (0) or the scan (1) path."""
     del bins_topm_unroll, interpret
     from . import schedule as sch
     _lib.require_cuda(logits)
@@ -108,7 +119,7 @@ def top_dynamic_k(logits: torch.Tensor, k, max_k: int, block_token: int = 8, num
         if max_k > cols:
             raise ValueError(f"max_k={max_k} exceeds row length {cols}")
         need = _lib.LIB.tallax_topk_workspace_size(rows, cols, max_k, dt)
-        ws = _lib.workspace(dev, need)
+        ws = _lib.workspace_arg(workspace, dev, need)
         if replace_val is None:
             _lib.check(_lib.LIB.tallax_topk(x.data_ptr(), dt, rows, cols, max_k, vals.data_ptr(), idx.data_ptr(),
                                             ws.data_ptr() if need else None, ws.numel() if need else 0, stream),
@@ -123,15 +134,18 @@ def top_dynamic_k(logits: torch.Tensor, k, max_k: int, block_token: int = 8, num
     import ctypes
     arr = (ctypes.c_int32 * len(steps))(*steps)
     need = _lib.LIB.tallax_top_dynamic_k_workspace_size(rows, num_bins, arr, len(steps))
-    ws = _lib.workspace(dev, max(need, 1))
+    ws = _lib.workspace_arg(workspace, dev, max(need, 1))
     valid = torch.empty(1, dtype=torch.int32, device=dev)
     depths = torch.empty(rows, dtype=torch.int32, device=dev)
     cutoff = torch.empty(rows, dtype=torch.float32, device=dev)
-    _lib.check(_lib.LIB.tallax_top_dynamic_k(
-        x.data_ptr(), dt, rows, cols, kr.data_ptr(), max_k, block_token, num_bins, arr, len(steps),
-        int(replace_val is not None), float(replace_val) if replace_val is not None else 0.0, vals.data_ptr(),
-        idx.data_ptr(), valid.data_ptr(), depths.data_ptr(), cutoff.data_ptr(), ws.data_ptr(), ws.numel(),
-        stream), "top_dynamic_k")
+    args = (x.data_ptr(), dt, rows, cols, kr.data_ptr(), max_k, block_token, num_bins, arr, len(steps),
+            int(replace_val is not None), float(replace_val) if replace_val is not None else 0.0, vals.data_ptr(),
+            idx.data_ptr(), valid.data_ptr(), depths.data_ptr(), cutoff.data_ptr(), ws.data_ptr(), ws.numel(),
+            stream)
+    if testing_path is None:
+        _lib.check(_lib.LIB.tallax_top_dynamic_k(*args), "top_dynamic_k")
+    else:
+        _lib.check(_lib.LIB.tallax_testing_top_dynamic_k_path(*args, int(testing_path)), "top_dynamic_k")
     return vals, idx, valid.reshape(()).bool(), depths, cutoff
 
 

@@ -21,11 +21,15 @@ def _log(msg):
 def binned_mode(request):
     """Runs a test once with the candidate path (rows settled from the exact
     kernel's per-segment top-128 where they suffice, the rest scanned) and
-    once with the full scan for every row; both must match the oracle."""
-    from tallax_amd import _lib
-    assert _lib.LIB.tallax_testing_binned_mode(request.param) == 0
-    yield request.param
-    assert _lib.LIB.tallax_testing_binned_mode(0) == 0
+    once with the full scan for every row; both must match the oracle.  The
+    path goes to the testing entry point tallax_testing_top_dynamic_k_path."""
+    return request.param
+
+
+def _dyn(x, k, max_k, path, block_token=8, num_bins=128, bins_topm_schedule=None, replace_val=None):
+    from tallax_amd import tax
+    return tax._top_dynamic_k(x, k, max_k, block_token, num_bins, 32, bins_topm_schedule, False, replace_val,
+                              False, None, path)
 
 
 def _check(got, want):
@@ -46,7 +50,7 @@ def test_config3_approx_and_recall(gpu, binned_mode):
     for r in range(128):
         x[r, rng.choice(151936, 32, replace=False)] = 8.0
     xd = torch.from_numpy(x).to(gpu)
-    got = tax.top_dynamic_k(xd, 50, 50)
+    got = _dyn(xd, 50, 50, binned_mode)
     torch.cuda.synchronize()
     want = O.top_dynamic_k(x, 50, 50)
     _check(got, want)
@@ -63,7 +67,7 @@ def test_config3_approx_and_recall(gpu, binned_mode):
     (8, 5000, 128, 256, 8, None),
     (12, 3000, 20, 64, 4, (3, 6)),
     (8, 300, 32, 128, 8, (2, 4, 9)),     # short rows: fillers at depth
-    (16, 50000, 8, 512, 8, (2,)),        # unconverged rows: approximate, valid False
+    (16, 50000, 8, 512, 8, (2,)),        # one-step schedule
     (16, 151936, 50, 128, 8, None),      # config-3 rows with heavy ties: candidates and scan mixed
 ])
 def test_top_dynamic_k_parity(gpu, binned_mode, dtype, rows, cols, max_k, num_bins, block_token, schedule):
@@ -76,11 +80,77 @@ def test_top_dynamic_k_parity(gpu, binned_mode, dtype, rows, cols, max_k, num_bi
     x[2, 1::4] = O.dtype_min(dtype)
     k = rng.integers(1, max_k + 1, rows).astype(np.int32)
     xd = to_dev(x, dtype, gpu)
-    got = tax.top_dynamic_k(xd, torch.from_numpy(k).to(gpu), max_k, block_token=block_token, num_bins=num_bins,
-                            bins_topm_schedule=schedule, replace_val=-1e12)
+    got = _dyn(xd, torch.from_numpy(k).to(gpu), max_k, binned_mode, block_token=block_token, num_bins=num_bins,
+               bins_topm_schedule=schedule, replace_val=-1e12)
     torch.cuda.synchronize()
     want = O.top_dynamic_k(O.round_to_dtype(x, dtype), k, max_k, block_token=block_token, num_bins=num_bins,
                            schedule=schedule, replace_val=-1e12, dtype=dtype)
+    _check(got, want)
+
+
+_ORACLE_CACHE = {}
+
+
+def _unconverged_rows(rows, cols, num_bins, spike_rows, nspikes, seed):
+    """Untied Gaussian rows; rows in spike_rows get nspikes large distinct
+    values all in bin 0 (columns = 0 mod num_bins), so the per-bin top-(m-1)
+    lists cannot hold k of them at any shallow step: those rows (and their
+    blocks) never converge."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    nspikes = min(nspikes, cols // num_bins)
+    for r in spike_rows:
+        x[r, rng.choice(cols // num_bins, nspikes, replace=False) * num_bins] = 50.0 + rng.random(nspikes)
+    return x
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("replace", [None, -1e12], ids=["no_replace", "replace"])
+@pytest.mark.parametrize("rows,cols,max_k,num_bins,block_token,schedule,spike_rows", [
+    (16, 3000, 32, 64, 8, (3, 6, 12), (5, 6)),           # depth_upper 16 > m_final 12
+    (16, 3000, 32, 64, 4, (2, 3, 6, 12), (9,)),           # blocks stop at different steps
+    (64, 151936, 50, 128, 8, (2, 5, 9), (3, 17, 40)),     # config-3 width, some blocks unconverged
+])
+def test_top_dynamic_k_unconverged_blocks(gpu, binned_mode, dtype, replace, rows, cols, max_k, num_bins,
+                                          block_token, schedule, spike_rows):
+    """Blocks that never converge (depth max_k, valid False) next to blocks
+    that stop early: the ranks a block never evaluated stay finfo.min
+    (top_k.py:241-243, 250-315, 333-364), bit-exact against the oracle, which
+    is pinned by the literal block-by-block restatement in test_oracle.py."""
+    _log(f"top_dynamic_k unconverged {dtype} [{rows},{cols}] max_k={max_k} bins={num_bins} bt={block_token} "
+         f"sched={schedule} replace={replace} path={binned_mode}")
+    x = O.round_to_dtype(_unconverged_rows(rows, cols, num_bins, spike_rows, 2 * max_k, rows + cols), dtype)
+    rng = np.random.default_rng(cols)
+    k = rng.integers(max_k // 2, max_k + 1, rows).astype(np.int32)
+    for r in spike_rows:
+        k[r] = max_k
+    xd = to_dev(x, dtype, gpu)
+    got = _dyn(xd, torch.from_numpy(k).to(gpu), max_k, binned_mode, block_token=block_token, num_bins=num_bins,
+               bins_topm_schedule=schedule, replace_val=replace)
+    torch.cuda.synchronize()
+    key = (dtype, replace, rows, cols, max_k, num_bins, block_token, schedule, spike_rows)
+    if key not in _ORACLE_CACHE:   # the same inputs run on both paths
+        _ORACLE_CACHE[key] = O.top_dynamic_k(x, k, max_k, block_token=block_token, num_bins=num_bins,
+                                             schedule=schedule, replace_val=replace, dtype=dtype)
+    want = _ORACLE_CACHE[key]
+    assert not want[2] and (want[3][list(spike_rows)] == max_k).all()
+    _check(got, want)
+
+
+@pytest.mark.parametrize("rows,block_token", [(2048, 8), (2048, 2048), (1536, 512)])
+def test_top_dynamic_k_many_rows_and_wide_blocks(gpu, binned_mode, rows, block_token):
+    """More rows than one finish workgroup has threads (the separate finish
+    kernel) and blocks wider than it: per-block last steps over any
+    block_token."""
+    _log(f"top_dynamic_k rows={rows} block_token={block_token} path={binned_mode}")
+    cols, max_k, nb, sched = 1000, 16, 32, (2, 4, 7)
+    x = _unconverged_rows(rows, cols, nb, (7, rows - 1), 24, rows + block_token)
+    rng = np.random.default_rng(block_token)
+    k = rng.integers(1, max_k + 1, rows).astype(np.int32)
+    got = _dyn(torch.from_numpy(x).to(gpu), torch.from_numpy(k).to(gpu), max_k, binned_mode,
+               block_token=block_token, num_bins=nb, bins_topm_schedule=sched, replace_val=None)
+    torch.cuda.synchronize()
+    want = O.top_dynamic_k(x, k, max_k, block_token=block_token, num_bins=nb, schedule=sched)
     _check(got, want)
 
 

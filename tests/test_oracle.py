@@ -498,3 +498,157 @@ def test_top_dynamic_k_converged_rows_are_exact():
     v2, i2, valid2, d2, _ = O.top_dynamic_k(x, 50, 50, schedule=(2,))
     assert not valid2 and (d2 == 50).all()
     assert np.all(np.diff(v2, axis=1) <= 0)
+
+
+# A literal restatement of dynamic_top_k_refs (top_k.py:203-370) and its
+# wrapper (top_k.py:433-514), block by block, used only to pin the oracle:
+# scratch values start at finfo.min for each block (:241-243) and indices are
+# uninitialised (here the sentinel _GARBAGE); each schedule step runs
+# binned_top_k (:13-106) with the completed ranks invalidated by index
+# (:53-60) and a strict-> sinking insert (:61-72), only while the block's
+# termination flag is 0 (:250-315); the final top-128 reads the first
+# depth_upper * num_bins scratch columns (:333-364); replace_val at positions
+# >= k (:365-369).  The final order among equal values is the lowest index
+# (BASELINE's tie contract; the reference's network order is unpinned).
+_GARBAGE = 2 ** 31 - 1
+
+
+def _literal_dynamic_top_k(x, k, max_k, block_token, num_bins, schedule, replace_val=None, dtype="f32"):
+    rows, vocab = x.shape
+    lo = O.dtype_min(dtype)
+    kk = np.broadcast_to(np.asarray(k, np.int64), (rows,))
+    sched = (0,) + tuple(sorted(set(schedule)))
+    max_m = sched[-1]
+    buf = max(max_m, 2 ** O.log2_ceil(max_m - 1)) * num_bins
+    sv = np.full((rows, buf), np.nan, np.float32)
+    si = np.full((rows, buf), _GARBAGE, np.int64)
+    depths = np.zeros(rows, np.int32)
+    cutoff = np.zeros(rows, np.float32)
+    nslices = -(-vocab // num_bins)
+    xp = np.full((rows, nslices * num_bins), lo, np.float32)   # pad(val='min'), :96-105
+    xp[:, :vocab] = x
+    for pid in range(rows // block_token):
+        ts = slice(pid * block_token, (pid + 1) * block_token)
+        sv[ts] = lo
+        depths[ts] = max_k
+        flag = 0
+        for completed, m in zip(sched, sched[1:]):
+            if flag != 0:
+                continue
+            vals = [sv[ts, i * num_bins:(i + 1) * num_bins].copy() for i in range(m)]
+            idxs = [si[ts, i * num_bins:(i + 1) * num_bins].copy() for i in range(m)]
+            for s in range(nslices):
+                bv = xp[ts, s * num_bins:(s + 1) * num_bins].copy()
+                bi = np.broadcast_to(s * num_bins + np.arange(num_bins), bv.shape).astype(np.int64).copy()
+                for i in range(completed):
+                    bv = np.where(bi == idxs[i], lo, bv)
+                for i in range(completed, m):
+                    mask = bv > vals[i]
+                    vals[i], bv = np.where(mask, bv, vals[i]), np.where(mask, vals[i], bv)
+                    idxs[i], bi = np.where(mask, bi, idxs[i]), np.where(mask, idxs[i], bi)
+            for i in range(completed, m):
+                sv[ts, i * num_bins:(i + 1) * num_bins] = vals[i]
+                si[ts, i * num_bins:(i + 1) * num_bins] = idxs[i]
+            pivot = vals[m - 1].max(-1)
+            num_larger = sum((v >= pivot[:, None]) for v in vals[:m - 1]).sum(-1) if m > 1 else np.zeros(block_token)
+            flag = 0
+            for i in range(block_token):
+                r = pid * block_token + i
+                contains = num_larger[i] >= kk[r]
+                flag += int(contains)
+                if contains and depths[r] == max_k:
+                    depths[r] = m - 1
+                cutoff[r] = pivot[i]
+            if flag != block_token:
+                flag = 0
+    gts = sorted(set(2 ** O.log2_ceil(s - 1) if s > 1 else s for s in sched))
+    gmax = int(depths.max())
+    valid = bool(gmax < sched[-1] or sched[-1] == max_k)
+    out = None
+    for d_lo, d_up in zip(gts, gts[1:]):
+        if (d_lo < gmax <= d_up) or (d_up == gts[-1] and gmax > d_up):
+            v = sv[:, :d_up * num_bins].astype(np.float64)
+            i = si[:, :d_up * num_bins]
+            order = np.lexsort((i, -v), axis=1)[:, :128]
+            ov = np.take_along_axis(sv[:, :d_up * num_bins], order, 1)
+            oi = np.take_along_axis(i, order, 1)
+            if replace_val is not None:
+                rv = O.round_to_dtype(np.float32(replace_val), dtype)
+                ov = np.where(np.arange(ov.shape[1])[None, :] < kk[:, None], ov, rv).astype(np.float32)
+            oi = np.where(oi == _GARBAGE, -1, oi).astype(np.int32)
+            out = (ov[:, :max_k], oi[:, :max_k])
+    return out, valid, depths, cutoff
+
+
+def _dyn_cases():
+    rng = np.random.default_rng(77)
+    # untied values, so that every output (indices included) is pinned
+    x = (rng.standard_normal((16, 3000)) * 2).astype(np.float32)
+    for r in (5, 6):                       # block 0 cannot converge: 40 spikes in bin 0
+        x[r, rng.choice(3000 // 64, 40, replace=False) * 64] = 50.0 + rng.random(40).astype(np.float32)
+    k = rng.integers(1, 33, 16).astype(np.int32)
+    yield "unconverged block, depth_upper > m_final", x, k, 32, 8, 64, (3, 6, 12)
+    yield "early exit per block", x, np.full(16, 4, np.int32), 32, 4, 64, (2, 3, 6, 12)
+    y = (rng.standard_normal((8, 700)) * 3).astype(np.float32)
+    y[:, ::7] = -np.inf
+    yield "short rows, fillers", y, rng.integers(1, 17, 8).astype(np.int32), 16, 4, 32, (2, 5)
+    z = (rng.standard_normal((8, 4000))).astype(np.float32)
+    yield "k = max_k everywhere", z, np.full(8, 24, np.int32), 24, 8, 128, (2, 4, 7)
+
+
+@pytest.mark.parametrize("replace", [None, -1e12])
+@pytest.mark.parametrize("case", list(_dyn_cases()), ids=lambda c: c[0] if isinstance(c, tuple) else str(c))
+def test_top_dynamic_k_matches_literal_block_restatement(case, replace):
+    """All five outputs of O.top_dynamic_k equal the literal block-by-block
+    restatement of dynamic_top_k_refs, including blocks that stop early, rows
+    that never converge (depth max_k, valid False) and depth_upper buckets
+    past the last step (ranks never written keep finfo.min)."""
+    _, x, k, max_k, bt, nb, sched = case
+    (lv, li), lvalid, ld, lc = _literal_dynamic_top_k(x, k, max_k, bt, nb, sched, replace)
+    ov, oi, ovalid, od, oc = O.top_dynamic_k(x, k, max_k, block_token=bt, num_bins=nb, schedule=sched,
+                                             replace_val=replace)
+    assert ovalid == lvalid
+    assert np.array_equal(od, ld) and np.array_equal(oc.view(np.uint32), lc.view(np.uint32))
+    assert np.array_equal(oi, li)
+    assert np.array_equal(ov.view(np.uint32), lv.view(np.uint32))
+
+
+def _full_depth_variant(x, k, max_k, block_token, num_bins, schedule, replace_val, depths):
+    """The same selection with every rank of the depth_upper bucket filled
+    (what a scan to full depth gives): what the oracle did before it kept
+    never-evaluated ranks at finfo.min."""
+    sch = O.topm_schedule(max_k, num_bins, block_token, schedule)
+    gts = sorted(set(2 ** O.log2_ceil(s - 1) if s > 1 else s for s in sch))
+    gmax, up = int(depths.max()), gts[-1]
+    for a, b in zip(gts, gts[1:]):
+        if a < gmax <= b:
+            up = b
+            break
+    fv, fi = O.binned_topm(x, up, num_bins)
+    sv, si = fv.reshape(len(x), -1), fi.reshape(len(x), -1)
+    order = np.lexsort((np.where(si < 0, 2 ** 40, si), -np.where(si < 0, -np.inf, sv.astype(np.float64))), axis=1)
+    gv = np.take_along_axis(sv, order[:, :max_k], 1)
+    gi = np.take_along_axis(si, order[:, :max_k], 1)
+    if replace_val is not None:
+        gv = np.where(np.arange(max_k)[None, :] < np.asarray(k)[:, None], gv, np.float32(replace_val))
+    return gv.astype(np.float32), gi
+
+
+def test_literal_restatement_reaches_the_unconverged_paths():
+    """The cases above really exercise what they name: a block that never
+    converges (depth max_k, valid False) and blocks that stop before the
+    depth_upper bucket, where the never-written ranks change the result
+    against a full-depth scan: indices with replace_val=None, and values inside
+    the first k[row] positions of an unconverged row with replace_val set."""
+    cases = {c[0]: c for c in _dyn_cases()}
+    _, x, k, max_k, bt, nb, sched = cases["unconverged block, depth_upper > m_final"]
+    for rep in (None, -1e12):
+        (lv, li), valid, d, _ = _literal_dynamic_top_k(x, k, max_k, bt, nb, sched, rep)
+        assert not valid and d[5] == max_k and (d[8:] < max_k).all()
+        fv, fi = _full_depth_variant(x, k, max_k, bt, nb, sched, rep, d)
+        assert (fv.view(np.uint32) != lv.view(np.uint32)).any(axis=1).sum() >= 1
+    _, x, k, max_k, bt, nb, sched = cases["early exit per block"]
+    (lv, li), valid, d, c = _literal_dynamic_top_k(x, k, max_k, bt, nb, sched)
+    assert valid and (d == 1).sum() >= 8
+    fv, fi = _full_depth_variant(x, k, max_k, bt, nb, sched, None, d)
+    assert (fi != li).any(axis=1).sum() >= 4
