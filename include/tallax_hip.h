@@ -118,6 +118,23 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
                                   tallax_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * The fused sampler with no workspace argument and no allocation.
+ * NO COUNTERPART IN THE REFERENCE: for callers that cannot allocate device
+ * memory or pass a workspace (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results as
+ * tallax_fused_topk_topp_sample; the per-segment candidate lists of
+ * segmented rows go to a static device array of 16 MiB that each GPU holds
+ * until the process ends (it calls no hipMalloc/hipFree).  Inputs whose
+ * lists need more (rows x segments x 1 KiB; e.g. f32 rows of 151936 columns
+ * beyond about 1600 rows) return TALLAX_UNSUPPORTED before any launch.  All
+ * calls on one GPU share the array: calls that overlap on one GPU race.
+ * ---------------------------------------------------------------------- */
+int tallax_fused_topk_topp_sample_noalloc(const void* logits, int dtype, int64_t rows, int64_t vocab,
+                                          const int32_t* top_k, const float* top_p, const float* temperature,
+                                          const uint32_t* rng_key, int64_t dim0_offset, double replace_val,
+                                          int32_t* out_tokens, tallax_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Wide-candidate sampler: sampling.sample (tallax/_src/sampling.py:331-343)
  * with the top-k width max_k lifted from the reference's 128
  * (sampling.py:283-290, top_k.py:438-439) to any max_k in [1, 1024], so that

@@ -33,6 +33,8 @@ _SIGNATURES = {
     "tallax_sample_workspace_size": ([_c_i64, _c_i64, _c_int], _c_sz),
     "tallax_fused_topk_topp_sample": (
         [_c_p, _c_int, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_d, _c_p, _c_p, _c_sz, _c_p], _c_int),
+    "tallax_fused_topk_topp_sample_noalloc": (
+        [_c_p, _c_int, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_d, _c_p, _c_p], _c_int),
     "tallax_sample_wide": ([_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_d, _c_p, _c_p,
                             _c_p, _c_p], _c_int),
     "tallax_shard_candidates_workspace_size": ([_c_i64, _c_i64, _c_int], _c_sz),

@@ -43,6 +43,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "tallax_hip.h"
 #include "tx_common.h"
 #include "tx_host.h"
@@ -1215,11 +1217,91 @@ size_t tallax_sample_workspace_size(int64_t rows, int64_t vocab, int dtype) {
   return tallax_topk_workspace_size(rows, vocab, kMaxK, dtype);
 }
 
+}  // extern "C"
+
+// The fused sampler with its workspace given (workspace != nullptr or none
+// needed) or, for the no-allocation entry point (use_scratch), the device
+// scratch array below.
+static int fused_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, const int32_t* top_k,
+                        const float* top_p, const float* temperature, const uint32_t* rng_key, int64_t dim0_offset,
+                        double replace_val, int32_t* out_tokens, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream, bool use_scratch);
+
+// Scratch of tallax_fused_topk_topp_sample_noalloc: the per-segment candidate
+// lists of segmented rows (rows x segments x 1 KiB).  Every GPU the library
+// runs on holds its own copy until the process ends.  In host code the array's
+// name is not a device address: kernels get the per-device address from
+// hipGetSymbolAddress (scratch_address).  Calls on one GPU share it, so calls
+// that overlap there race; no call reads bytes it did not write itself, so
+// nothing needs clearing between calls.
+constexpr size_t kSampleScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kSampleScratchBytes];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the device of `stream` (the current device
+// for the null stream), looked up once per device with that device current.
+static int scratch_address(hipStream_t stream, void** out) {
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) {
+    set_error("hipGetDevice failed");
+    return kHipError;
+  }
+  int dev = cur;
+  if (stream && hipStreamGetDevice(stream, &dev) != hipSuccess) {
+    set_error("hipStreamGetDevice failed");
+    return kHipError;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("device %d outside the %d this build tracks", dev, kMaxDevices);
+    return kUnsupported;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) {
+      set_error("hipSetDevice(%d) failed", dev);
+      return kHipError;
+    }
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p) {
+      set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+      return kHipError;
+    }
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return kOk;
+}
+
+extern "C" {
+
 int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, int64_t vocab,
                                   const int32_t* top_k, const float* top_p, const float* temperature,
                                   const uint32_t* rng_key, int64_t dim0_offset, double replace_val,
                                   int32_t* out_tokens, void* workspace, size_t workspace_bytes,
                                   hipStream_t stream) {
+  return fused_sample(logits, dtype, rows, vocab, top_k, top_p, temperature, rng_key, dim0_offset, replace_val,
+                      out_tokens, workspace, workspace_bytes, stream, false);
+}
+
+int tallax_fused_topk_topp_sample_noalloc(const void* logits, int dtype, int64_t rows, int64_t vocab,
+                                          const int32_t* top_k, const float* top_p, const float* temperature,
+                                          const uint32_t* rng_key, int64_t dim0_offset, double replace_val,
+                                          int32_t* out_tokens, hipStream_t stream) {
+  return fused_sample(logits, dtype, rows, vocab, top_k, top_p, temperature, rng_key, dim0_offset, replace_val,
+                      out_tokens, nullptr, 0, stream, true);
+}
+
+}  // extern "C"
+
+static int fused_sample(const void* logits, int dtype, int64_t rows, int64_t vocab, const int32_t* top_k,
+                        const float* top_p, const float* temperature, const uint32_t* rng_key, int64_t dim0_offset,
+                        double replace_val, int32_t* out_tokens, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream, bool use_scratch) {
   int st = check_common(logits, dtype, rows, vocab);
   if (st) return st;
   if (vocab < kMaxK) { set_error("vocab %lld < 128 is not supported by the fused sampler", (long long)vocab); return kUnsupported; }
@@ -1229,7 +1311,19 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
   st = plan_rows(rows, vocab, dtype, &p);
   if (st) return st;
   const size_t need = ws_bytes_for(rows, p);
-  if (workspace_bytes < need || (need && !workspace)) {
+  if (use_scratch) {
+    if (need > kSampleScratchBytes) {
+      set_error("[%lld, %lld] needs %zu bytes of scratch; the no-allocation sampler holds %zu (pass a workspace to "
+                "tallax_fused_topk_topp_sample instead)", (long long)rows, (long long)vocab, need,
+                kSampleScratchBytes);
+      return kUnsupported;
+    }
+    if (need) {
+      st = scratch_address(stream, &workspace);
+      if (st) return st;
+      workspace_bytes = kSampleScratchBytes;
+    }
+  } else if (workspace_bytes < need || (need && !workspace)) {
     set_error("workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
     return kWorkspaceTooSmall;
   }
@@ -1246,6 +1340,8 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
   return dtype == kF32 ? launch_select<kF32, true>(a, p, stream, "tallax_fused_topk_topp_sample")
                        : launch_select<kBF16, true>(a, p, stream, "tallax_fused_topk_topp_sample");
 }
+
+extern "C" {
 
 size_t tallax_shard_candidates_workspace_size(int64_t rows, int64_t cols, int dtype) {
   return tallax_topk_workspace_size(rows, cols, kMaxK, dtype);

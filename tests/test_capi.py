@@ -97,3 +97,23 @@ def test_wide_sampler_validates_on_the_host():
     assert L.tallax_sample_wide(1, 1, 0, 128256, 1024, None, None, None, None, 0, -1e12, None, 1, None, None) \
         == _lib.OK
 
+
+
+def test_noalloc_sampler_limit_without_gpu():
+    """The no-allocation sampler refuses, on the host and before any device
+    call, inputs whose candidate lists exceed its 16 MiB scratch."""
+    from tallax_amd import _lib
+    L = _lib.LIB
+    rows, vocab = 4096, 151936
+    assert L.tallax_sample_workspace_size(rows, vocab, _lib.F32) > 16 << 20
+    st = L.tallax_fused_topk_topp_sample_noalloc(1, _lib.F32, rows, vocab, 1, 1, 1, 1, 0, -1e12, 1, None)
+    assert st == _lib.UNSUPPORTED
+    assert b"scratch" in L.tallax_last_error()
+
+
+def test_top_dynamic_k_path_hook_rejects_unknown_paths():
+    from tallax_amd import _lib
+    sched = (ctypes.c_int32 * 2)(3, 6)
+    st = _lib.LIB.tallax_testing_top_dynamic_k_path(1, 0, 8, 100, 1, 4, 8, 128, sched, 2, 0, 0.0, 1, 1, 1, 1, 1,
+                                                    1, 1 << 20, None, 7)
+    assert st == _lib.INVALID_ARGUMENT and b"path" in _lib.LIB.tallax_last_error()
