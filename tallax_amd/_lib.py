@@ -179,6 +179,9 @@ def select_plan(rows: int, cols: int, dtype: int) -> dict:
     check(LIB.tallax_testing_select_plan(rows, cols, dtype, out), "select_plan")
     nt, maxv, nseg, vps = list(out)
     dt = {F32: 0, BF16: 1}[dtype]
+    if nt == 1024:
+        name = f"stream_select_kernel<{dt}, {maxv}, SAMPLE>"
+    else:
+        name = f"seg_select_kernel<{dt}, {maxv}, {nt}, SAMPLE>" + (" + seg_merge_kernel" if nseg > 1 else "")
     return {"threads": nt, "vectors_per_thread": maxv, "segments": nseg, "vectors_per_segment": vps,
-            "kernel": f"seg_select_kernel<{dt}, {maxv}, {nt}, SAMPLE>"
-                      + (" + seg_merge_kernel" if nseg > 1 else "")}
+            "kernel": name}

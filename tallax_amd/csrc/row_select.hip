@@ -378,7 +378,7 @@ __device__ __forceinline__ uint32_t elem_bits(const uint4 v, int q) {
 // Outputs of one row from its sorted top-128 list (in LDS).  Called by every
 // thread of the workgroup; sg is a 128-float LDS buffer (sampler only).
 template <int DT, bool SAMPLE>
-__device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list, float* sg) {
+__device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list, float* sg, bool noise_ready = false) {
   using T = ElemT<DT>;
   const uint32_t inel = ineligible_key_max(DT);
   if (!SAMPLE) {
@@ -407,8 +407,9 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
   const int tid = threadIdx.x, l = lane_id();
   // Waves 1-2 compute the Gumbel noise of the 128 candidates while wave 0
   // finds the top-p threshold (a 64-thread block does both in wave 0).
-  const bool split = blockDim.x >= 3 * kWave;
-  if (split && tid >= kWave && tid < kWave + kMaxK) {
+  // (noise_ready: the caller already stored every candidate's noise in sg)
+  const bool split = noise_ready || blockDim.x >= 3 * kWave;
+  if (!noise_ready && split && tid >= kWave && tid < kWave + kMaxK) {
     const int p = tid - kWave;
     sg[p] = candidate_noise(k0, k1, row_ctr, (uint32_t)a.cols, comp_idx(list[p]));
   }
@@ -503,7 +504,7 @@ __device__ __forceinline__ int32_t vec_omax(const uint4 v) {
 // canonical key lies between a NaN's and -inf's.
 // Returns this wave's number of appended candidates.  Every thread calls it.
 // ---------------------------------------------------------------------------
-template <int DT, int MAXV, int NT>
+template <int DT, int MAXV, int NT, int SG = kStage>
 __device__ __attribute__((noinline)) int tie_select(const uint4* base, int64_t s0, int64_t s1, int lbase,
                                                     int live_lo, int live_hi, uint32_t gbase, int k,
                                                     typename Sel<DT, (NT * MAXV * ElemT<DT>::VEC > 65535)>::Comp* reg,
@@ -612,15 +613,15 @@ __device__ __attribute__((noinline)) int tie_select(const uint4* base, int64_t s
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
-    for (int c = 0; c < (MAXV + kStage - 1) / kStage; ++c) {
+    for (int c = 0; c < (MAXV + SG - 1) / SG; ++c) {
       if (pass == 1 && rest <= 0) break;
 #pragma unroll
-      for (int u = 0; u < kStage; ++u)
-        if (c * kStage + u < MAXV) stage[u * NT + tid] = raw[c * kStage + u];
+      for (int u = 0; u < SG; ++u)
+        if (c * SG + u < MAXV) stage[u * NT + tid] = raw[c * SG + u];
 #pragma unroll 1
-      for (int u = 0; u < kStage && c * kStage + u < MAXV; ++u) {
+      for (int u = 0; u < SG && c * SG + u < MAXV; ++u) {
         if (pass == 1 && rest <= 0) break;
-        const int li0 = lbase + (c * kStage + u) * NT * VEC;
+        const int li0 = lbase + (c * SG + u) * NT * VEC;
         const uint4 vv = stage[u * NT + tid];
         const uint32_t lm = live_bits(li0);
         uint32_t mask = 0;
@@ -957,6 +958,379 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge_kernel(SelArgs a) {
   finalize_row<DT, SAMPLE>(a, row, tree[0], sg);
 }
 
+// ---------------------------------------------------------------------------
+// Kernel S (stream_select_kernel): a whole row per 1024-thread workgroup (16
+// waves, 4 per SIMD), V 16-byte vectors per thread, vector j of thread t at
+// row vector j * 1024 + t.
+//   1. Every load is issued up front; as the vectors arrive each thread keeps
+//      their maxima (signed view) -- the only work during the stream.
+//   2. The bound L: the minimum over waves of each wave's 8th largest thread
+//      maximum (a radix search with one ballot per key bit), so at least 128
+//      elements reach L; also the row's largest key M.
+//   3. Vectors whose maximum reaches L are staged in their wave's LDS region
+//      (one ballot per vector index), then each wave takes its staged vectors
+//      one per lane and appends the elements >= L as composites
+//      (canonical key << 32 | ~index).
+//   4. The candidates are put in order by an LDS bucket rank: buckets of
+//      (M - key) >> shift (at most kBuckets), one atomic per candidate for the
+//      histogram and its slot, an exclusive scan, a scatter, and each
+//      candidate's rank = its bucket's start + the larger composites in its
+//      bucket.  The first 128 ranks are the row's top-128 in order.  The
+//      sampler's Gumbel noise of every candidate is computed meanwhile.
+// Rows whose staged vectors or candidates overflow (heavy ties: constant rows,
+// long tie blocks) or that hold fewer than 128 eligible elements take
+// tie_select over the whole row instead.
+// ---------------------------------------------------------------------------
+constexpr int kNTS = 1024;
+constexpr int kStageCap = 128;   // staged vectors per wave
+constexpr int kCandCap = 1024;   // candidates (one per thread in the ranking)
+constexpr int kBuckets = 1024;
+
+struct StreamShared {
+  uint4 vst[kNTS / kWave][kStageCap];      // staged vectors, per wave     32 KiB
+  uint32_t vsi[kNTS / kWave][kStageCap];   // their first element's row index
+  uint64_t cand[kCandCap];                 // candidates, then in bucket order
+  float noise[kCandCap];                   // sampler: Gumbel noise by rank
+  int hist[kBuckets];                      // bucket counts, then bucket starts
+  uint32_t wl[kNTS / kWave];
+  uint32_t wm[kNTS / kWave];
+  int wst[kNTS / kWave];                   // staged vectors per wave
+  int ncand;
+};
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4_t* GlobalVec;
+
+// Loaded in place of vectors past the end of a row: all-ones (negative NaNs)
+// never pass a filter and never raise a maximum.
+static __device__ u32x4_t g_dead_vec = {~0u, ~0u, ~0u, ~0u};
+
+// lanes below this one in the wave
+__device__ __forceinline__ uint64_t lanes_below() {
+  const int l = lane_id();
+  return l == 0 ? 0ull : (~0ull >> (kWave - l));
+}
+
+// The k-th largest of the wave's 64 values (k >= 1), by a radix search over
+// the bits with one ballot per bit: the largest K with #(v >= K) >= k.
+template <int BITS>
+__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k) {
+  uint32_t K = 0;
+#pragma unroll
+  for (int b = BITS - 1; b >= 0; --b) {
+    const uint32_t probe = K | (1u << b);
+    if (__popcll(__ballot(v >= probe)) >= k) K = probe;
+  }
+  return K;
+}
+
+// Wave-wide exclusive prefix of v and the total: scans of the 16-lane rows
+// with DPP row shifts, then the row totals through readlane.
+__device__ __forceinline__ int wave_exscan_i32(int v, int& total) {
+  const int l = lane_id();
+  int x = v;
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31);
+  const int r2 = __builtin_amdgcn_readlane(x, 47), r3 = __builtin_amdgcn_readlane(x, 63);
+  const int row = l >> 4;
+  const int before = (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+  total = r0 + r1 + r2 + r3;
+  return before + x - v;
+}
+
+// Slots q < lo or q >= hi of a 16-byte vector of VEC elements become all-ones.
+template <int DT>
+__device__ __forceinline__ uint4 kill_slots(uint4 x, int lo, int hi) {
+  constexpr int VEC = ElemT<DT>::VEC;
+  uint32_t d[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+  for (int q = 0; q < VEC; ++q) {
+    const bool dead = q < lo || q >= hi;
+    if (DT == kBF16) d[q >> 1] |= dead ? ((q & 1) ? 0xFFFF0000u : 0x0000FFFFu) : 0u;
+    else d[q] |= dead ? ~0u : 0u;
+  }
+  return make_uint4(d[0], d[1], d[2], d[3]);
+}
+
+// Bits q of the elements of vv with canonical key >= thr (thr >= the smallest
+// eligible key, so NaNs and dead slots never pass).
+template <int DT>
+__device__ __forceinline__ uint32_t pass_mask_ge(const uint4 vv, uint32_t thr) {
+  constexpr bool kBF = DT == kBF16;
+  constexpr int VEC = ElemT<DT>::VEC;
+  constexpr uint32_t kZeroKey = kBF ? 0x8000u : 0x80000000u;
+  constexpr int32_t kPosInf = kBF ? 0x7F80 : 0x7F800000;
+  uint32_t m = 0;
+  if (thr > kZeroKey) {  // positive threshold: st <= bits <= +inf in the signed view
+    const int32_t st = (int32_t)(thr - kZeroKey);
+    const uint32_t span = (uint32_t)(kPosInf - st);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t x = dword_of(vv, d);
+      if (kBF) {
+        m |= ((uint32_t)((int32_t)(int16_t)(x & 0xFFFFu) - st) <= span ? 1u : 0u) << (2 * d);
+        m |= ((uint32_t)(((int32_t)x >> 16) - st) <= span ? 1u : 0u) << (2 * d + 1);
+      } else {
+        m |= ((uint32_t)((int32_t)x - st) <= span ? 1u : 0u) << d;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) m |= (Sel<DT, true>::canon(elem_bits<DT>(vv, q)) >= thr ? 1u : 0u) << q;
+  }
+  return m;
+}
+
+template <int DT, int V, bool SAMPLE>
+__global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
+  using T = ElemT<DT>;
+  constexpr int VEC = T::VEC, ES = T::ES, NW = kNTS / kWave;
+  constexpr bool kBF = DT == kBF16;
+  constexpr int KB = kBF ? 16 : 32;  // canonical key bits
+  using ST = Sel<DT, (kNTS * V * VEC > 65535)>;  // the tie path's composites (tie_select's choice)
+  using CT = typename ST::Comp;
+  constexpr uint32_t kZeroKey = kBF ? 0x8000u : 0x80000000u;
+  constexpr int32_t kPosInf = kBF ? 0x7F80 : 0x7F800000;
+  constexpr int32_t kOrdNegInf = kBF ? -32641 : (int32_t)0x807FFFFFu;
+  constexpr uint32_t kFloor = kBF ? 0x0081u : 0x00800001u;  // smallest eligible canonical key
+  __shared__ StreamShared ss;
+  __shared__ SegShared<CT, kNTS> sh;  // tie path, output list
+  __shared__ uint4 stage[2 * kNTS];   // tie path
+  const int tid = threadIdx.x, w = tid / kWave, l = lane_id();
+  const int64_t row = blockIdx.x;
+  const char* rowp = (const char*)a.x + (size_t)(row * a.cols) * ES;
+  const RowVec<ES> rv(rowp);
+  const int nv = (int)((a.cols + rv.mis + VEC - 1) / VEC);  // 1 <= nv <= kNTS * V (host plan)
+  const int cols = (int)a.cols;
+
+  // ---- 1. every load up front (global loads: flat loads would also count
+  // against the LDS counter), vector maxima as the data arrives
+  uint4 raw[V];
+  {
+    const GlobalVec gb = (GlobalVec)rv.base;
+    const GlobalVec dead = (GlobalVec)(uintptr_t)&g_dead_vec;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int v = j * kNTS + tid;
+      const u32x4_t x = *(v < nv ? gb + v : dead);
+      raw[j] = make_uint4(x.x, x.y, x.z, x.w);
+    }
+  }
+  if (tid == 0) ss.ncand = 0;
+  for (int i = tid; i < kBuckets; i += kNTS) ss.hist[i] = 0;
+  {
+    // the row's first vector (misaligned start) and last one (partial end):
+    // dead slots become all-ones, under block-uniform conditions and with
+    // selects of values only (a store guarded per vector would be merged into
+    // a store at a variable index, which would move raw[] to scratch memory)
+    const int tail_live = cols + rv.mis - (nv - 1) * VEC;  // live slots of the last vector, 1..VEC
+    if (rv.mis > 0 || tail_live < VEC) {
+      int tj = -1, lo = 0, hi = VEC;
+      if (tid == 0 && rv.mis > 0) {
+        tj = 0;
+        lo = rv.mis;
+      }
+      if (tid == (nv - 1) % kNTS && tail_live < VEC) {
+        tj = (nv - 1) / kNTS;
+        hi = tail_live;
+      }
+      // the empty asm keeps the masks derived from these values in this block
+      asm volatile("" : "+v"(tj), "+v"(lo), "+v"(hi));
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const uint4 x = raw[j];
+        const uint4 y = kill_slots<DT>(x, lo, hi);
+        const bool t = tj == j;
+        raw[j] = make_uint4(t ? y.x : x.x, t ? y.y : x.y, t ? y.z : x.z, t ? y.w : x.w);
+      }
+    }
+  }
+  int32_t vmax[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) vmax[j] = vec_smax<DT>(raw[j]);
+
+  // ---- 2. the bound L and the row maximum M (canonical keys)
+  int32_t smax = vmax[0];
+#pragma unroll
+  for (int j = 1; j < V; ++j) smax = imax32(smax, vmax[j]);
+  bool ord_view = false;  // some thread's maximum needs the ordered view
+  uint32_t tk;
+  if (smax >= 0 && smax <= kPosInf) {
+    tk = (uint32_t)smax | kZeroKey;
+  } else {
+    int32_t omax = kBF ? -32768 : (int32_t)0x80000000u;
+#pragma unroll
+    for (int j = 0; j < V; ++j) omax = imax32(omax, vec_omax<DT>(raw[j]));
+    if (omax <= kPosInf) {
+      tk = omax < kOrdNegInf ? 0u : (omax == -1 ? kZeroKey : (uint32_t)omax + kZeroKey);
+    } else {  // a positive NaN: canonical maximum element by element
+      tk = 0;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) {
+          const uint32_t kk = Sel<DT, true>::canon(elem_bits<DT>(raw[j], q));
+          tk = kk > tk ? kk : tk;
+        }
+      }
+    }
+  }
+  {
+    const uint32_t wl = wave_kth_largest<KB>(tk, kMaxK / NW);
+    const uint32_t wm = wave_kth_largest<KB>(tk, 1);
+    if (l == 0) {
+      ss.wl[w] = wl;
+      ss.wm[w] = wm;
+    }
+  }
+  __syncthreads();
+  uint32_t L = ss.wl[0], M = ss.wm[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) {
+    L = ss.wl[i] < L ? ss.wl[i] : L;
+    M = ss.wm[i] > M ? ss.wm[i] : M;
+  }
+  const uint32_t thr = L > kFloor ? L : kFloor;
+
+  // ---- 3. stage the vectors that may hold a candidate, then the candidates
+  {
+    const bool pos_thr = thr > kZeroKey;
+    const int32_t st = (int32_t)(thr - kZeroKey);                       // bits, positive threshold
+    const int32_t ot = thr == kZeroKey ? -1 : (int32_t)(thr - kZeroKey);  // ordered view otherwise
+    int wcnt = 0;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const bool f = pos_thr ? vmax[j] >= st : vec_omax<DT>(raw[j]) >= ot;
+      const uint64_t m = __ballot(f);
+      if (m) {
+        if (f) {
+          const int o = wcnt + (int)__popcll(m & lanes_below());
+          if (o < kStageCap) {
+            ss.vst[w][o] = raw[j];
+            ss.vsi[w][o] = (uint32_t)((j * kNTS + tid) * VEC - rv.mis);
+          }
+        }
+        wcnt += (int)__popcll(m);
+      }
+    }
+    if (l == 0) ss.wst[w] = wcnt;
+    // the wave's own region: one staged vector per lane
+    const int nst = wcnt < kStageCap ? wcnt : kStageCap;
+    for (int r0 = 0; r0 < nst; r0 += kWave) {  // wave-uniform
+      const int o = r0 + l;
+      uint32_t pm = 0;
+      uint4 vv = make_uint4(~0u, ~0u, ~0u, ~0u);
+      uint32_t e0 = 0;
+      if (o < nst) {
+        vv = ss.vst[w][o];
+        e0 = ss.vsi[w][o];
+        pm = pass_mask_ge<DT>(vv, thr);
+      }
+      int tot;
+      const int pre = wave_exscan_i32(__popc(pm), tot);
+      if (tot) {
+        int b0 = 0;
+        if (l == 0) b0 = atomicAdd(&ss.ncand, tot);
+        int oc = __shfl(b0, 0) + pre;
+        while (pm) {
+          const int q = __builtin_ctz(pm);
+          pm &= pm - 1u;
+          if (oc < kCandCap) ss.cand[oc] = make_comp(Sel<DT, true>::canon(elem_bits<DT>(vv, q)), e0 + (uint32_t)q);
+          ++oc;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int n = ss.ncand;
+  bool tie = false;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) tie |= ss.wst[i] > kStageCap;
+  // fewer than 128: fewer than 128 eligible elements in the row (thr was the
+  // eligibility floor); more than kCandCap: heavy ties
+  tie = tie || n < kMaxK || n > kCandCap;  // block-uniform
+  if (!tie) {
+    // ---- 4. bucket rank (and the candidates' noise meanwhile)
+    const uint32_t range = M - thr;  // the candidates' keys lie in [thr, M]
+    int shift = 0;
+    while ((range >> shift) >= (uint32_t)kBuckets) ++shift;
+    const bool mine = tid < n;
+    const uint64_t c = mine ? ss.cand[tid] : 0ull;
+    const int b = mine ? (int)((M - comp_key(c)) >> shift) : 0;
+    int slot = 0;
+    if (mine) slot = atomicAdd(&ss.hist[b], 1);
+    float nz = 0.0f;
+    if (SAMPLE && mine)
+      nz = candidate_noise(a.rng_key[0], a.rng_key[1], (uint32_t)(row + a.dim0_offset), (uint32_t)a.cols,
+                           (int32_t)~(uint32_t)c);
+    __syncthreads();
+    const int nb = (int)(range >> shift) + 1;
+    if (w == 0) {  // exclusive scan of the bucket counts, 16 buckets per lane
+      constexpr int PER = kBuckets / kWave;
+      int cnt[PER];
+      int loc = 0;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        cnt[i] = ss.hist[l * PER + i];  // buckets past nb hold 0
+        loc += cnt[i];
+      }
+      int tot;
+      int run = wave_exscan_i32(loc, tot);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        ss.hist[l * PER + i] = run;  // the bucket's start
+        run += cnt[i];
+      }
+    }
+    __syncthreads();
+    int start = 0, end = 0;
+    if (mine) {
+      start = ss.hist[b];
+      end = b + 1 < nb ? ss.hist[b + 1] : n;
+      ss.cand[start + slot] = c;  // every thread read its own entry before the barriers above
+    }
+    __syncthreads();
+    if (mine) {
+      int r = start;
+      for (int i0 = start; i0 < end; i0 += 8) {  // 8 LDS reads in flight
+        uint64_t x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = i0 + u < end ? ss.cand[i0 + u] : 0ull;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) r += x[u] > c ? 1 : 0;
+      }
+      if (r < kMaxK) {
+        const uint32_t k = comp_key(c);
+        uint32_t key = k;
+        if (kBF) key = k >= 0x8000u ? (k << 16) : ((k << 16) | 0xFFFFu);
+        sh.list64[r] = make_comp(key, ~(uint32_t)c);
+        if (SAMPLE) sh.samp_g[r] = nz;
+      }
+    }
+  } else {
+    const int lbase = tid * VEC;
+    const int64_t seg_e0 = -(int64_t)rv.mis;
+    const int live_lo = rv.mis;
+    const int live_hi = cols + rv.mis < nv * VEC ? cols + rv.mis : nv * VEC;
+    const int wcnt = tie_select<DT, V, kNTS, 2>(rv.base, 0, nv, lbase, live_lo, live_hi, (uint32_t)seg_e0, kMaxK,
+                                                sh.cand + w * Geo<kNTS>::WCAP, sh.red, stage);
+    if (l == 0) sh.wc[w] = wcnt;
+    __syncthreads();
+    block_select(sh, (const int*)sh.wc);
+    for (int i = tid; i < kRun; i += kNTS) sh.list64[i] = ST::to_global(sh.list[i], seg_e0);
+  }
+  __syncthreads();
+  if (!a.lists_only) {
+    finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_g, !tie);
+  } else {
+    uint64_t* dst = a.ws_lists + (size_t)row * kRun;
+    for (int i = tid; i < kRun; i += kNTS) dst[i] = sh.list64[i] ? sh.list64[i] - (uint64_t)a.col_offset : 0ull;
+  }
+}
+
 // Standalone top_p_and_sample (sampling.py:210-269) on already-sorted
 // candidates [rows, K], K <= 128: one wave per row.
 template <int DT>
@@ -1014,28 +1388,29 @@ __global__ __launch_bounds__(kWave) void top_p_mask_kernel(const float* logits, 
 // Host side.
 // ---------------------------------------------------------------------------
 struct Plan {
-  int nt;  // threads per workgroup: kNT (segments) or kNTRow (whole rows)
+  int nt;  // threads per workgroup: kNT (segments) or kNTS (whole rows)
   int maxv;
   int nseg;
   int64_t vps;
 };
 
 // Work split.  A row of nv 16-byte vectors is handled either
-//   * whole by one 512-thread workgroup (up to 32 vectors per thread) when
-//     that gives enough workgroups (>= 128 rows): no merge kernel at all; or
+//   * whole by one 1024-thread workgroup of stream_select_kernel (up to 16
+//     vectors per thread) when that gives enough workgroups (>= 128 rows):
+//     no merge kernel at all; or
 //   * in segments of 256 x MAXV vectors, MAXV in {4, 8, 16}: the largest that
 //     still gives ~4 workgroups per CU over the launch, then a per-row merge.
 static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
   const int vec = dt == kF32 ? 4 : 8;
   const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
   static const int kOpts[3] = {16, 8, 4};
-  if (rows >= 128 && nv <= (int64_t)kNTRow * 32) {
-    int maxv = 32;
-    while (maxv > 8 && (int64_t)kNTRow * (maxv / 2) >= nv) maxv /= 2;
-    p->nt = kNTRow;
+  if (rows >= 128 && nv <= (int64_t)kNTS * 16) {
+    int maxv = 16;
+    while (maxv > 4 && (int64_t)kNTS * (maxv / 2) >= nv) maxv /= 2;
+    p->nt = kNTS;
     p->maxv = maxv;
     p->nseg = 1;
-    p->vps = (int64_t)kNTRow * maxv;
+    p->vps = (int64_t)kNTS * maxv;
     return kOk;
   }
   int maxv = 4;
@@ -1075,10 +1450,14 @@ static void launch_a(const SelArgs& a, hipStream_t s) {
 
 template <int DT, bool SAMPLE>
 static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const char* what) {
-  if (p.nt == kNTRow) {
-    if (p.maxv == 32) launch_a<DT, 32, kNTRow, SAMPLE>(a, s);
-    else if (p.maxv == 16) launch_a<DT, 16, kNTRow, SAMPLE>(a, s);
-    else launch_a<DT, 8, kNTRow, SAMPLE>(a, s);
+  if (p.nt == kNTS) {
+    if (p.maxv == 16)
+      hipLaunchKernelGGL((stream_select_kernel<DT, 16, SAMPLE>), dim3((unsigned)a.rows), dim3(kNTS), 0, s, a);
+    else if (p.maxv == 8)
+      hipLaunchKernelGGL((stream_select_kernel<DT, 8, SAMPLE>), dim3((unsigned)a.rows), dim3(kNTS), 0, s, a);
+    else
+      hipLaunchKernelGGL((stream_select_kernel<DT, 4, SAMPLE>), dim3((unsigned)a.rows), dim3(kNTS), 0, s, a);
+    return launch_status(what);
   } else {
     if (p.maxv == 16) launch_a<DT, 16, kNT, SAMPLE>(a, s);
     else if (p.maxv == 8) launch_a<DT, 8, kNT, SAMPLE>(a, s);
