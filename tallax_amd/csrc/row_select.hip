@@ -375,10 +375,38 @@ __device__ __forceinline__ uint32_t elem_bits(const uint4 v, int q) {
   return dword_of(v, q);
 }
 
+// A row's sampler parameters, loaded when the kernel starts so that their
+// memory latency is not paid in the tail.
+struct RowParams {
+  int kr;           // top_k[row]
+  float top_p;
+  float temp;
+  uint32_t k0, k1;  // threefry key
+  uint32_t row_ctr;  // row + dim0_offset
+  uint32_t vocab;
+  float replace_in_dtype, replace_f32;
+};
+template <bool SAMPLE>
+__device__ __forceinline__ RowParams load_row_params(const SelArgs& a, int64_t row) {
+  RowParams rp = {0, 0.0f, 0.0f, 0u, 0u, 0u, 0u, 0.0f, 0.0f};
+  if (SAMPLE) {
+    rp.kr = a.top_k[row];
+    rp.top_p = a.top_p[row];
+    rp.temp = a.temperature[row];
+    rp.k0 = a.rng_key[0];
+    rp.k1 = a.rng_key[1];
+    rp.row_ctr = (uint32_t)(row + a.dim0_offset);
+    rp.vocab = (uint32_t)a.cols;
+    rp.replace_in_dtype = a.replace_in_dtype;
+    rp.replace_f32 = a.replace_f32;
+  }
+  return rp;
+}
+
 // Outputs of one row from its sorted top-128 list (in LDS).  Called by every
 // thread of the workgroup; sg is a 128-float LDS buffer (sampler only).
 template <int DT, bool SAMPLE>
-__device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list, float* sg, bool noise_ready = false) {
+__device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list, float* sg, const RowParams& rp) {
   using T = ElemT<DT>;
   const uint32_t inel = ineligible_key_max(DT);
   if (!SAMPLE) {
@@ -396,22 +424,21 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
     return;
   }
   // value at position p of the top-128, positions >= top_k[row] replaced
-  const int kr = a.top_k[row];
+  const int kr = rp.kr;
   auto value_at = [&](int p) -> float {
     const uint32_t kk = comp_key(list[p]);
     const float val = __uint_as_float(kk > inel ? key_to_bits(kk) : T::kMinBits);
-    return p < kr ? val : a.replace_in_dtype;
+    return p < kr ? val : rp.replace_in_dtype;
   };
-  const uint32_t row_ctr = (uint32_t)(row + a.dim0_offset);
-  const uint32_t k0 = a.rng_key[0], k1 = a.rng_key[1];
+  const uint32_t row_ctr = rp.row_ctr;
+  const uint32_t k0 = rp.k0, k1 = rp.k1;
   const int tid = threadIdx.x, l = lane_id();
   // Waves 1-2 compute the Gumbel noise of the 128 candidates while wave 0
   // finds the top-p threshold (a 64-thread block does both in wave 0).
-  // (noise_ready: the caller already stored every candidate's noise in sg)
-  const bool split = noise_ready || blockDim.x >= 3 * kWave;
-  if (!noise_ready && split && tid >= kWave && tid < kWave + kMaxK) {
+  const bool split = blockDim.x >= 3 * kWave;
+  if (split && tid >= kWave && tid < kWave + kMaxK) {
     const int p = tid - kWave;
-    sg[p] = candidate_noise(k0, k1, row_ctr, (uint32_t)a.cols, comp_idx(list[p]));
+    sg[p] = candidate_noise(k0, k1, row_ctr, rp.vocab, comp_idx(list[p]));
   }
   float v[2], e[2], g[2];
   int32_t id[2];
@@ -424,9 +451,9 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
       v[h] = value_at(p);
       id[h] = comp_idx(list[p]);
       e[h] = candidate_exp(v[h], v0);
-      if (!split) g[h] = candidate_noise(k0, k1, row_ctr, (uint32_t)a.cols, id[h]);
+      if (!split) g[h] = candidate_noise(k0, k1, row_ctr, rp.vocab, id[h]);
     }
-    thr = top_p_threshold(v, e, kMaxK, a.top_p[row]);
+    thr = top_p_threshold(v, e, kMaxK, rp.top_p);
   }
   if (split) __syncthreads();
   if (tid < kWave) {
@@ -434,7 +461,7 @@ __device__ void finalize_row(const SelArgs& a, int64_t row, const uint64_t* list
       g[0] = sg[l];
       g[1] = sg[kWave + l];
     }
-    const int32_t tok = gumbel_argmax(v, id, g, kMaxK, thr, a.temperature[row], a.replace_f32);
+    const int32_t tok = gumbel_argmax(v, id, g, kMaxK, thr, rp.temp, rp.replace_f32);
     if (l == 0) a.out_tokens[row] = tok;
   }
 }
@@ -687,6 +714,7 @@ void seg_select_kernel(SelArgs a) {
   const int seg = blockIdx.x;
   const int64_t row = blockIdx.y;
   const int k = a.k;
+  const RowParams rp = load_row_params<SAMPLE>(a, row);
 
   const char* rowp = (const char*)a.x + (size_t)(row * a.cols) * ES;
   const RowVec<ES> rv(rowp);
@@ -897,7 +925,7 @@ void seg_select_kernel(SelArgs a) {
   for (int i = tid; i < kRun; i += NT) sh.list64[i] = S::to_global(sh.list[i], seg_e0);
   __syncthreads();
   if (a.nseg == 1 && !a.lists_only) {
-    finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_g);
+    finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_g, rp);
   } else {
     uint64_t* dst = a.ws_lists + ((size_t)row * a.nseg + seg) * kRun;
     // ~(idx + off) = ~idx - off without a borrow into the key (idx + off < 2^31); empty slots stay 0
@@ -922,6 +950,7 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge_kernel(SelArgs a) {
   const int64_t row = blockIdx.x;
   const int w = threadIdx.x / kWave, l = lane_id();
   const uint64_t* src = a.ws_lists + (size_t)row * a.nseg * kRun;
+  const RowParams rp = load_row_params<SAMPLE>(a, row);
   uint64_t b[PER][2];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
@@ -955,7 +984,7 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge_kernel(SelArgs a) {
     for (int i = threadIdx.x; i < kRun; i += kMergeNT) a.out_lists[(size_t)row * kRun + i] = tree[0][i];
     return;
   }
-  finalize_row<DT, SAMPLE>(a, row, tree[0], sg);
+  finalize_row<DT, SAMPLE>(a, row, tree[0], sg, rp);
 }
 
 // ---------------------------------------------------------------------------
@@ -975,8 +1004,7 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge_kernel(SelArgs a) {
 //      (M - key) >> shift (at most kBuckets), one atomic per candidate for the
 //      histogram and its slot, an exclusive scan, a scatter, and each
 //      candidate's rank = its bucket's start + the larger composites in its
-//      bucket.  The first 128 ranks are the row's top-128 in order.  The
-//      sampler's Gumbel noise of every candidate is computed meanwhile.
+//      bucket.  The first 128 ranks are the row's top-128 in order.
 // Rows whose staged vectors or candidates overflow (heavy ties: constant rows,
 // long tie blocks) or that hold fewer than 128 eligible elements take
 // tie_select over the whole row instead.
@@ -989,13 +1017,12 @@ constexpr int kBuckets = 1024;
 struct StreamShared {
   uint4 vst[kNTS / kWave][kStageCap];      // staged vectors, per wave     32 KiB
   uint32_t vsi[kNTS / kWave][kStageCap];   // their first element's row index
-  uint64_t cand[kCandCap];                 // candidates, then in bucket order
-  float noise[kCandCap];                   // sampler: Gumbel noise by rank
+  uint64_t cand[kCandCap + 8];             // candidates, then in bucket order (+8: unguarded reads)
   int hist[kBuckets];                      // bucket counts, then bucket starts
   uint32_t wl[kNTS / kWave];
   uint32_t wm[kNTS / kWave];
-  int wst[kNTS / kWave];                   // staged vectors per wave
   int ncand;
+  int ovf;                                 // a wave's staged vectors overflowed its region
 };
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -1011,17 +1038,21 @@ __device__ __forceinline__ uint64_t lanes_below() {
   return l == 0 ? 0ull : (~0ull >> (kWave - l));
 }
 
-// The k-th largest of the wave's 64 values (k >= 1), by a radix search over
-// the bits with one ballot per bit: the largest K with #(v >= K) >= k.
+// The k-th largest (kth) and the largest (top) of the wave's 64 values
+// (k >= 1), by radix searches over the bits with one ballot per bit and
+// search: the largest K with #(v >= K) >= k.
 template <int BITS>
-__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k) {
-  uint32_t K = 0;
+__device__ __forceinline__ void wave_kth_and_max(uint32_t v, int k, uint32_t& kth, uint32_t& top) {
+  uint32_t K = 0, T = 0;
 #pragma unroll
   for (int b = BITS - 1; b >= 0; --b) {
-    const uint32_t probe = K | (1u << b);
-    if (__popcll(__ballot(v >= probe)) >= k) K = probe;
+    const uint32_t pk = K | (1u << b), pt = T | (1u << b);
+    const uint64_t mk = __ballot(v >= pk), mt = __ballot(v >= pt);
+    K = __popcll(mk) >= k ? pk : K;
+    T = mt ? pt : T;
   }
-  return K;
+  kth = K;
+  top = T;
 }
 
 // Wave-wide exclusive prefix of v and the total: scans of the 16-lane rows
@@ -1105,6 +1136,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   const RowVec<ES> rv(rowp);
   const int nv = (int)((a.cols + rv.mis + VEC - 1) / VEC);  // 1 <= nv <= kNTS * V (host plan)
   const int cols = (int)a.cols;
+  const RowParams rp = load_row_params<SAMPLE>(a, row);
 
   // ---- 1. every load up front (global loads: flat loads would also count
   // against the LDS counter), vector maxima as the data arrives
@@ -1119,7 +1151,10 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
       raw[j] = make_uint4(x.x, x.y, x.z, x.w);
     }
   }
-  if (tid == 0) ss.ncand = 0;
+  if (tid == 0) {
+    ss.ncand = 0;
+    ss.ovf = 0;
+  }
   for (int i = tid; i < kBuckets; i += kNTS) ss.hist[i] = 0;
   {
     // the row's first vector (misaligned start) and last one (partial end):
@@ -1179,8 +1214,8 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     }
   }
   {
-    const uint32_t wl = wave_kth_largest<KB>(tk, kMaxK / NW);
-    const uint32_t wm = wave_kth_largest<KB>(tk, 1);
+    uint32_t wl, wm;
+    wave_kth_and_max<KB>(tk, kMaxK / NW, wl, wm);
     if (l == 0) {
       ss.wl[w] = wl;
       ss.wm[w] = wm;
@@ -1201,9 +1236,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     const int32_t st = (int32_t)(thr - kZeroKey);                       // bits, positive threshold
     const int32_t ot = thr == kZeroKey ? -1 : (int32_t)(thr - kZeroKey);  // ordered view otherwise
     int wcnt = 0;
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
-      const bool f = pos_thr ? vmax[j] >= st : vec_omax<DT>(raw[j]) >= ot;
+    auto stage_if = [&](int j, bool f) {
       const uint64_t m = __ballot(f);
       if (m) {
         if (f) {
@@ -1215,8 +1248,15 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
         }
         wcnt += (int)__popcll(m);
       }
+    };
+    if (pos_thr) {  // block-uniform: the signed-view maxima decide
+#pragma unroll
+      for (int j = 0; j < V; ++j) stage_if(j, vmax[j] >= st);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) stage_if(j, vec_omax<DT>(raw[j]) >= ot);
     }
-    if (l == 0) ss.wst[w] = wcnt;
+    if (l == 0 && wcnt > kStageCap) ss.ovf = 1;
     // the wave's own region: one staged vector per lane
     const int nst = wcnt < kStageCap ? wcnt : kStageCap;
     for (int r0 = 0; r0 < nst; r0 += kWave) {  // wave-uniform
@@ -1246,12 +1286,9 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   }
   __syncthreads();
   const int n = ss.ncand;
-  bool tie = false;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) tie |= ss.wst[i] > kStageCap;
   // fewer than 128: fewer than 128 eligible elements in the row (thr was the
   // eligibility floor); more than kCandCap: heavy ties
-  tie = tie || n < kMaxK || n > kCandCap;  // block-uniform
+  const bool tie = ss.ovf != 0 || n < kMaxK || n > kCandCap;  // block-uniform
   if (!tie) {
     // ---- 4. bucket rank (and the candidates' noise meanwhile)
     const uint32_t range = M - thr;  // the candidates' keys lie in [thr, M]
@@ -1262,10 +1299,6 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     const int b = mine ? (int)((M - comp_key(c)) >> shift) : 0;
     int slot = 0;
     if (mine) slot = atomicAdd(&ss.hist[b], 1);
-    float nz = 0.0f;
-    if (SAMPLE && mine)
-      nz = candidate_noise(a.rng_key[0], a.rng_key[1], (uint32_t)(row + a.dim0_offset), (uint32_t)a.cols,
-                           (int32_t)~(uint32_t)c);
     __syncthreads();
     const int nb = (int)(range >> shift) + 1;
     if (w == 0) {  // exclusive scan of the bucket counts, 16 buckets per lane
@@ -1286,28 +1319,28 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
       }
     }
     __syncthreads();
+    // buckets that start at rank >= 128 are not needed any further
     int start = 0, end = 0;
-    if (mine) {
-      start = ss.hist[b];
+    const bool need = mine && (start = ss.hist[b]) < kMaxK;
+    if (need) {
       end = b + 1 < nb ? ss.hist[b + 1] : n;
       ss.cand[start + slot] = c;  // every thread read its own entry before the barriers above
     }
     __syncthreads();
-    if (mine) {
+    if (need) {
       int r = start;
-      for (int i0 = start; i0 < end; i0 += 8) {  // 8 LDS reads in flight
+      for (int i0 = start; i0 < end; i0 += 8) {  // 8 LDS reads in flight (unguarded: the array is padded)
         uint64_t x[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = i0 + u < end ? ss.cand[i0 + u] : 0ull;
+        for (int u = 0; u < 8; ++u) x[u] = ss.cand[i0 + u];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) r += x[u] > c ? 1 : 0;
+        for (int u = 0; u < 8; ++u) r += (i0 + u < end && x[u] > c) ? 1 : 0;
       }
       if (r < kMaxK) {
         const uint32_t k = comp_key(c);
         uint32_t key = k;
         if (kBF) key = k >= 0x8000u ? (k << 16) : ((k << 16) | 0xFFFFu);
         sh.list64[r] = make_comp(key, ~(uint32_t)c);
-        if (SAMPLE) sh.samp_g[r] = nz;
       }
     }
   } else {
@@ -1324,7 +1357,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   }
   __syncthreads();
   if (!a.lists_only) {
-    finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_g, !tie);
+    finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_g, rp);
   } else {
     uint64_t* dst = a.ws_lists + (size_t)row * kRun;
     for (int i = tid; i < kRun; i += kNTS) dst[i] = sh.list64[i] ? sh.list64[i] - (uint64_t)a.col_offset : 0ull;

@@ -61,15 +61,27 @@ __device__ __forceinline__ float top_p_threshold(const float v[2], const float e
       c[h] = c[h] + (ok ? u : 0.0f);
     }
   }
+  // Tile g's total is its last slot (register g / 8, lane 8 (g % 8) + 7).  The
+  // totals are read out first (independent readlanes), then summed in order
+  // (carry_g = t_0 + ... + t_{g-1}, one add after the other), and each lane
+  // picks the carries of its two tiles.
   const int tile0 = l >> 3;  // tile of register 0; register 1 is tile0 + 8
-  float carry0 = 0.0f, carry1 = 0.0f;
-  float run = readlane_f(c[0], 7);
+  float tt[16];
+#pragma unroll
+  for (int g = 0; g < 16; ++g) tt[g] = readlane_f(g < 8 ? c[0] : c[1], (g & 7) * 8 + 7);
+  float carry[16];
+  carry[0] = 0.0f;
+  float run = tt[0];
 #pragma unroll
   for (int g = 1; g < 16; ++g) {
-    if (tile0 == g) carry0 = run;
-    if (tile0 + 8 == g) carry1 = run;
-    const float tsg = readlane_f(g < 8 ? c[0] : c[1], (g & 7) * 8 + 7);
-    run = run + tsg;
+    carry[g] = run;
+    run = run + tt[g];
+  }
+  float carry0 = carry[0], carry1 = carry[8];
+#pragma unroll
+  for (int g = 1; g < 8; ++g) {
+    carry0 = tile0 == g ? carry[g] : carry0;
+    carry1 = tile0 == g ? carry[g + 8] : carry1;
   }
   if (tile0 != 0) c[0] = c[0] + carry0;
   c[1] = c[1] + carry1;
@@ -90,42 +102,34 @@ __device__ __forceinline__ int32_t gumbel_argmax(const float v[2], const int32_t
   while (P < K) P <<= 1;
   int pbits = 0;
   while ((1 << pbits) < P) ++pbits;
-  float best_s = 0.0f;
-  uint32_t best_b = 0;
-  int32_t best_i = 0;
+  // One u64 key per slot: the score as an order-preserving integer (-0 as +0)
+  // above the bit-reversed position, so the largest key is the largest score
+  // with ties to the largest bit-reversed position; slots past P (which
+  // max_arrays never sees) get key 0 and never win.
+  uint64_t best = 0;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int p = h * kWave + l;
-    float sc;
-    int32_t tok = id[h];
+    float sc = -FLT_MAX;  // padding slot of max_arrays (K <= p < P)
     if (p < K) {
       const float masked = v[h] >= thr ? v[h] : mask_val;
       const float scaled = masked / temp;
       sc = scaled + g[h];
-    } else if (p < P) {
-      sc = -FLT_MAX;
-      tok = INT32_MIN;
-    } else {
-      sc = -INFINITY;
     }
-    const uint32_t br = p < P ? bitrev((uint32_t)p, pbits) : 0u;
-    if (h == 0 || sc > best_s || (sc == best_s && br > best_b)) {
-      best_s = sc;
-      best_b = br;
-      best_i = tok;
-    }
+    uint32_t sb = __float_as_uint(sc);
+    sb = sb == 0x80000000u ? 0u : sb;
+    const uint32_t ord = sb ^ ((uint32_t)((int32_t)sb >> 31) | 0x80000000u);
+    const uint64_t key = p < P ? (((uint64_t)ord << 32) | bitrev((uint32_t)p, pbits)) : 0ull;
+    best = key > best ? key : best;
   }
 #pragma unroll
   for (int d = kWave / 2; d >= 1; d >>= 1) {
-    const float os = lane_xor_f(best_s, d);
-    const uint32_t ob = lane_xor(best_b, d);
-    const int32_t oi = (int32_t)lane_xor((uint32_t)best_i, d);
-    if (os > best_s || (os == best_s && ob > best_b)) {
-      best_s = os;
-      best_b = ob;
-      best_i = oi;
-    }
+    const uint64_t o = shfl_xor_u64(best, d);
+    best = o > best ? o : best;
   }
+  const int pw = (int)bitrev((uint32_t)best, pbits);  // the winning slot (uniform)
+  const int32_t wid = (int32_t)readlane_u32((uint32_t)(pw < kWave ? id[0] : id[1]), pw & (kWave - 1));
+  const int32_t best_i = pw < K ? wid : INT32_MIN;
   const int32_t greedy = (int32_t)readlane_u32((uint32_t)id[0], 0);
   return temp < 1e-5f ? greedy : best_i;
 }
