@@ -8,6 +8,9 @@ in [1, 1024], top_p U[0.7,1.0), threefry key data (0, 1234).  A "step"
 samples one token for each of the 256 rows.
 
 --config selects another BASELINE config (each a parity-checked entry point):
+  sampler_masked config 4's sampler on constrained-decoding logits: 3 rows in
+                 4 allow about U{1..600} tokens (the rest -inf), every 4th
+                 row unmasked; also times the unmasked input for comparison
   topk_c3        exact top-k k=50, f32 [128,151936] + 32 spikes/row at 8.0
   topk_c3_approx approximate (binned) top_dynamic_k k=max_k=50, same input
   topk_c1        exact top-k k=64, f32 [8,32768]
@@ -39,7 +42,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak, GB/s
 COPY_BYTES = 256 << 20  # calibration copy: 256 MiB read + 256 MiB written per launch
-CONFIGS = ["sampler", "sampler_wide", "topk_c3", "topk_c3_approx", "topk_c1", "sort_c2", "prefill_c5", "sort_wide", "copy"]
+CONFIGS = ["sampler", "sampler_masked", "sampler_wide", "topk_c3", "topk_c3_approx", "topk_c1", "sort_c2", "prefill_c5", "sort_wide", "copy"]
 
 
 def _copy_rate(torch, dev, stream, steps, warmup):
@@ -102,8 +105,19 @@ class Workload:
     shape = (0, 0)
 
 
-def _sampler(torch, np, _lib, dev, s_handle, gen, nbuf, max_k=128):
-    """Config 4; max_k > 128 is the opt-in wide-candidate sampler on the same input."""
+def _masked_logits(torch, gen, dev, rows, cols):
+    """bf16 N(0,3) logits where rows r % 4 != 3 keep about U{1..600} tokens
+    (each with probability count / cols) and hold -inf elsewhere."""
+    x = torch.randn((rows, cols), generator=gen, device=dev) * 3.0
+    allow = torch.randint(1, 601, (rows, 1), generator=gen, device=dev).float() / cols
+    keep = torch.rand((rows, cols), generator=gen, device=dev) < allow
+    keep[3::4] = True
+    return x.masked_fill(~keep, float("-inf")).to(torch.bfloat16)
+
+
+def _sampler(torch, np, _lib, dev, s_handle, gen, nbuf, max_k=128, masked=False):
+    """Config 4; max_k > 128 is the opt-in wide-candidate sampler on the same
+    input; masked=True runs it on constrained-decoding logits."""
     w = Workload()
     rows, cols = 256, 128256
     rng = np.random.default_rng(5)
@@ -116,8 +130,9 @@ def _sampler(torch, np, _lib, dev, s_handle, gen, nbuf, max_k=128):
     out = torch.empty(rows, dtype=torch.int32, device=dev)
     need = _lib.LIB.tallax_sample_workspace_size(rows, cols, _lib.BF16)
     ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
-    bufs = [(torch.randn((rows, cols), generator=gen, device=dev) * 3.0).to(torch.bfloat16)
-            for _ in range(nbuf or 6)]
+    plain = [(torch.randn((rows, cols), generator=gen, device=dev) * 3.0).to(torch.bfloat16)
+             for _ in range(nbuf or 6)]
+    bufs = [_masked_logits(torch, gen, dev, rows, cols) for _ in range(nbuf or 6)] if masked else plain
     w.metric = "rows/s + achieved HBM GB/s (% peak): fused top-k/top-p @256x128256 bf16"
     w.rows, w.dtype, w.shape = rows, "bf16", (rows, cols)
     w.alg_bytes = rows * cols * 2 + rows * 12 + 8 + rows * 4
@@ -130,9 +145,25 @@ def _sampler(torch, np, _lib, dev, s_handle, gen, nbuf, max_k=128):
                     "@256x128256 bf16")
         w.workload = w.workload.replace("(clamped to 128)", f"(honoured up to max_k={max_k})")
         w.kernel = "sample_wide_kernel<bf16>"
+    if masked:
+        w.metric = "rows/s + achieved HBM GB/s (% peak): fused top-k/top-p @256x128256 bf16, masked rows"
+        w.workload = w.workload.replace("N(0,3)", "N(0,3) with 3 rows in 4 masked to about U{1..600} tokens (-inf "
+                                        "elsewhere)")
 
-    def launch(i):
-        x = bufs[i % len(bufs)]
+        def common_us(steps):   # the same launches on the unmasked logits
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(torch.cuda.current_stream(dev))
+            for i in range(steps):
+                launch(i, plain)
+            e1.record(torch.cuda.current_stream(dev))
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / steps
+        w.common_us = common_us
+
+    def launch(i, src=None):
+        src = bufs if src is None else src
+        x = src[i % len(src)]
         if max_k != 128:
             _lib.check(_lib.LIB.tallax_sample_wide(
                 x.data_ptr(), _lib.BF16, rows, cols, max_k, d_topk.data_ptr(), d_topp.data_ptr(),
@@ -428,6 +459,8 @@ def main() -> int:
 
     if args.config == "sampler":
         w = _sampler(torch, np, _lib, dev, s_handle, gen, args.nbuf)
+    elif args.config == "sampler_masked":
+        w = _sampler(torch, np, _lib, dev, s_handle, gen, args.nbuf, masked=True)
     elif args.config == "sampler_wide":
         w = _sampler(torch, np, _lib, dev, s_handle, gen, args.nbuf, max_k=1024)
     elif args.config.startswith("topk"):
@@ -509,6 +542,10 @@ def main() -> int:
         "parity_vs_oracle": parity,
         "wall_ms_per_step": wall * 1e3 / args.steps,
     }
+    if hasattr(w, "common_us"):
+        cu = w.common_us(args.steps)
+        rec["unmasked_kernel_avg_us"] = cu
+        rec["masked_over_unmasked"] = kern_us / cu
     if hasattr(w, "recall"):
         rec["recall_at_k_vs_exact"] = w.recall
     print(json.dumps(rec), flush=True)

@@ -1005,8 +1005,9 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge_kernel(SelArgs a) {
 //      histogram and its slot, an exclusive scan, a scatter, and each
 //      candidate's rank = its bucket's start + the larger composites in its
 //      bucket.  The first 128 ranks are the row's top-128 in order.
-// Rows whose staged vectors or candidates overflow (heavy ties: constant rows,
-// long tie blocks) or that hold fewer than 128 eligible elements take
+// Rows with fewer than 128 eligible elements rank them and take the rest of
+// the list by class (fill_ineligible).  Rows whose staged vectors or
+// candidates overflow (heavy ties: constant rows, long tie blocks) take
 // tie_select over the whole row instead.
 // ---------------------------------------------------------------------------
 constexpr int kNTS = 1024;
@@ -1113,6 +1114,118 @@ __device__ __forceinline__ uint32_t pass_mask_ge(const uint4 vv, uint32_t thr) {
     for (int q = 0; q < VEC; ++q) m |= (Sel<DT, true>::canon(elem_bits<DT>(vv, q)) >= thr ? 1u : 0u) << q;
   }
   return m;
+}
+
+// Class masks of a 16-byte vector for the ineligible classes: finfo.min
+// elements in bits 0-7, -inf in bits 8-15, NaN in bits 16-23 (all slots,
+// dead ones included).
+template <int DT>
+__device__ __forceinline__ uint32_t ineligible_masks(const uint4 v) {
+  constexpr bool kBF = DT == kBF16;
+  constexpr int VEC = ElemT<DT>::VEC;
+  constexpr uint32_t kMinB = kBF ? 0xFF7Fu : 0xFF7FFFFFu, kNegInfB = kBF ? 0xFF80u : 0xFF800000u;
+  constexpr uint32_t kAbs = kBF ? 0x7FFFu : 0x7FFFFFFFu, kInfAbs = kBF ? 0x7F80u : 0x7F800000u;
+  uint32_t m = 0;
+#pragma unroll
+  for (int q = 0; q < VEC; ++q) {
+    const uint32_t b = elem_bits<DT>(v, q);
+    m |= (b == kMinB ? 1u : 0u) << q;
+    m |= (b == kNegInfB ? 1u : 0u) << (8 + q);
+    m |= ((b & kAbs) > kInfAbs ? 1u : 0u) << (16 + q);
+  }
+  return m;
+}
+
+// The smallest (bits - finfo.min's bits) over the elements of a 16-byte
+// vector, wrapping in the element width: 0 when the vector holds finfo.min,
+// 1 when it holds -inf but not finfo.min, larger otherwise.
+template <int DT>
+__device__ __forceinline__ uint32_t min_offset_from_min(const uint4 v) {
+  if (DT == kBF16) {
+    const ushort2_t fm = __builtin_bit_cast(ushort2_t, 0xFF7FFF7Fu);
+    ushort2_t m = __builtin_bit_cast(ushort2_t, v.x) - fm;
+    m = __builtin_elementwise_min(m, __builtin_bit_cast(ushort2_t, v.y) - fm);
+    m = __builtin_elementwise_min(m, __builtin_bit_cast(ushort2_t, v.z) - fm);
+    m = __builtin_elementwise_min(m, __builtin_bit_cast(ushort2_t, v.w) - fm);
+    const uint32_t mm = __builtin_bit_cast(uint32_t, m);
+    const uint32_t lo = mm & 0xFFFFu, hi = mm >> 16;
+    return lo < hi ? lo : hi;
+  }
+  const uint32_t a = v.x - 0xFF7FFFFFu, b = v.y - 0xFF7FFFFFu, c = v.z - 0xFF7FFFFFu, d = v.w - 0xFF7FFFFFu;
+  const uint32_t ab = a < b ? a : b, cd = c < d ? c : d;
+  return ab < cd ? ab : cd;
+}
+
+// Rows with fewer than 128 eligible elements, all n of them candidates:
+// list[n..127] <- the first 128 - n ineligible elements in composite order --
+// the finfo.min elements, then -inf, then NaN, each class in index order --
+// and zeros where the row has fewer than 128 elements.  pab / pc: this
+// thread's vectors j (bit j) that may hold finfo.min (pab bits 0-15), -inf
+// (pab bits 16-31) or NaN (pc), from the first read; the vectors that
+// hold a class anywhere in the row are read again one at a time (vector j of
+// thread t at row vector j * kNTS + t of the aligned base, nv vectors, the
+// row's first element at slot mis), in order, until the list is full.
+// tmp: 2 * 16 words of LDS.
+template <int DT, int V>
+__device__ __forceinline__ void fill_ineligible(const uint4* row_base, int nv, int mis, int cols, int n, uint32_t pab,
+                                                uint32_t pc, uint64_t* list, int* red, uint32_t* tmp) {
+  constexpr bool kBF = DT == kBF16;
+  constexpr int VEC = ElemT<DT>::VEC, NW = kNTS / kWave;
+  constexpr uint32_t kMinKey = kBF ? 0x0080FFFFu : 0x00800000u;  // global keys of the three classes
+  constexpr uint32_t kNegInfKey = 0x007FFFFFu, kNaNKey = 1u;
+  // the empty asm hides that these addresses equal the first read's: shared,
+  // those would stay live (in registers or spilled) from the kernel's start
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid), "+s"(row_base));
+  const int w = tid / kWave, l = lane_id();
+  const GlobalVec gb = (GlobalVec)row_base;
+  const GlobalVec dead = (GlobalVec)(uintptr_t)&g_dead_vec;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    pab |= lane_xor(pab, d);
+    pc |= lane_xor(pc, d);
+  }
+  if (l == 0) {
+    tmp[w] = pab;
+    tmp[NW + w] = pc;
+  }
+  __syncthreads();
+  pab = 0;
+  pc = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    pab |= tmp[i];
+    pc |= tmp[NW + i];
+  }
+  int r = kMaxK - n, base = n;
+#pragma unroll 1
+  for (int c = 0; c < 3 && r > 0; ++c) {  // block-uniform
+    uint32_t pres = c == 0 ? (pab & 0xFFFFu) : (c == 1 ? pab >> 16 : pc);
+    const uint32_t key = c == 0 ? kMinKey : (c == 1 ? kNegInfKey : kNaNKey);
+    while (pres && r > 0) {  // block-uniform: the vectors that may hold the class, in order
+      const int j = __builtin_ctz(pres);
+      pres &= pres - 1u;
+      const int v = j * kNTS + tid;
+      const u32x4_t x = *(v < nv ? gb + v : dead);
+      const int e0 = v * VEC - mis;
+      uint32_t m = (ineligible_masks<DT>(make_uint4(x.x, x.y, x.z, x.w)) >> (8 * c)) & 0xFFu;
+#pragma unroll
+      for (int q = 0; q < VEC; ++q)  // slots outside the row
+        m &= (uint32_t)(e0 + q) < (uint32_t)cols ? ~0u : ~(1u << q);
+      int total;
+      int p = block_exscan<NW>(__popc(m), red, total);
+      while (m && p < r) {
+        const int q = __builtin_ctz(m);
+        m &= m - 1u;
+        list[base + p] = make_comp(key, (uint32_t)(e0 + q));
+        ++p;
+      }
+      const int took = total < r ? total : r;
+      base += took;
+      r -= took;
+    }
+  }
+  for (int i = base + tid; i < kMaxK; i += kNTS) list[i] = 0ull;
 }
 
 template <int DT, int V, bool SAMPLE>
@@ -1231,6 +1344,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   const uint32_t thr = L > kFloor ? L : kFloor;
 
   // ---- 3. stage the vectors that may hold a candidate, then the candidates
+  uint32_t pab = 0, pc = 0;  // rows with thr at the floor: the vectors holding ineligible classes
   {
     const bool pos_thr = thr > kZeroKey;
     const int32_t st = (int32_t)(thr - kZeroKey);                       // bits, positive threshold
@@ -1255,6 +1369,17 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     } else {
 #pragma unroll
       for (int j = 0; j < V; ++j) stage_if(j, vec_omax<DT>(raw[j]) >= ot);
+      if (thr == kFloor) {  // block-uniform: the row may hold fewer than 128 eligible elements
+        // vectors that hold finfo.min, and those that may hold -inf (cheap
+        // packed tests; NaNs are not tracked: every vector may hold one)
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const uint32_t o = min_offset_from_min<DT>(raw[j]);
+          pab |= (o == 0u ? 1u : 0u) << j;
+          pab |= (o <= 1u ? 1u : 0u) << (16 + j);
+        }
+        pc = (1u << V) - 1u;
+      }
     }
     if (l == 0 && wcnt > kStageCap) ss.ovf = 1;
     // the wave's own region: one staged vector per lane
@@ -1286,10 +1411,24 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   }
   __syncthreads();
   const int n = ss.ncand;
-  // fewer than 128: fewer than 128 eligible elements in the row (thr was the
-  // eligibility floor); more than kCandCap: heavy ties
-  const bool tie = ss.ovf != 0 || n < kMaxK || n > kCandCap;  // block-uniform
-  if (!tie) {
+  // fewer than 128 with thr at the eligibility floor: every eligible element
+  // of the row is a candidate, the rest of the list is ineligible elements
+  const bool fill = ss.ovf == 0 && n < kMaxK && thr == kFloor;  // block-uniform
+  // an overflowing staging region or more than kCandCap candidates: heavy ties
+  const bool tie = !fill && (ss.ovf != 0 || n < kMaxK || n > kCandCap);
+  if (fill) fill_ineligible<DT, V>(rv.base, nv, rv.mis, cols, n, pab, pc, sh.list64, sh.red, &ss.vsi[0][0]);
+  if (tie) {
+    const int lbase = tid * VEC;
+    const int64_t seg_e0 = -(int64_t)rv.mis;
+    const int live_lo = rv.mis;
+    const int live_hi = cols + rv.mis < nv * VEC ? cols + rv.mis : nv * VEC;
+    const int wcnt = tie_select<DT, V, kNTS, 2>(rv.base, 0, nv, lbase, live_lo, live_hi, (uint32_t)seg_e0, kMaxK,
+                                                sh.cand + w * Geo<kNTS>::WCAP, sh.red, stage);
+    if (l == 0) sh.wc[w] = wcnt;
+    __syncthreads();
+    block_select(sh, (const int*)sh.wc);
+    for (int i = tid; i < kRun; i += kNTS) sh.list64[i] = ST::to_global(sh.list[i], seg_e0);
+  } else if (n > 0) {
     // ---- 4. bucket rank (and the candidates' noise meanwhile)
     const uint32_t range = M - thr;  // the candidates' keys lie in [thr, M]
     int shift = 0;
@@ -1343,17 +1482,6 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
         sh.list64[r] = make_comp(key, ~(uint32_t)c);
       }
     }
-  } else {
-    const int lbase = tid * VEC;
-    const int64_t seg_e0 = -(int64_t)rv.mis;
-    const int live_lo = rv.mis;
-    const int live_hi = cols + rv.mis < nv * VEC ? cols + rv.mis : nv * VEC;
-    const int wcnt = tie_select<DT, V, kNTS, 2>(rv.base, 0, nv, lbase, live_lo, live_hi, (uint32_t)seg_e0, kMaxK,
-                                                sh.cand + w * Geo<kNTS>::WCAP, sh.red, stage);
-    if (l == 0) sh.wc[w] = wcnt;
-    __syncthreads();
-    block_select(sh, (const int*)sh.wc);
-    for (int i = tid; i < kRun; i += kNTS) sh.list64[i] = ST::to_global(sh.list[i], seg_e0);
   }
   __syncthreads();
   if (!a.lists_only) {

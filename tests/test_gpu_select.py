@@ -92,7 +92,35 @@ TOPK_CASES = [
     (4, 40000, 100, "bf16", "tieblock"),    # 60 large values, then a 10000-wide tie block
     (4, 40000, 100, "f32", "tieblock"),
     (4, 40000, 100, "f32", "nan_heavy"),    # NaN rows with a few finite, -inf and finfo.min values
+    # whole-row workgroups on masked rows: fewer than 128 eligible values take
+    # the rest of the list by class (finfo.min, -inf, NaN, each in index order)
+    (256, 128256, 128, "bf16", "masked_mix"),
+    (128, 32768, 100, "f32", "masked_mix"),
+    (160, 5003, 128, "bf16", "masked_mix"),
+    (128, 100, 64, "f32", "masked_mix"),    # rows shorter than 128
 ]
+
+
+def _masked_mix(rows, cols, rng):
+    """Rows of -inf with a few allowed values: row r % 8 == 0 allows none,
+    1-3 allow 1..127, 4-5 a few hundred; rows 6 mix finfo.min and NaN in
+    (all ineligible classes, sparse and out of order); rows 7 are unmasked."""
+    x = np.full((rows, cols), -np.inf, np.float32)
+    fmin = np.finfo(np.float32).min
+    for r in range(rows):
+        kind = r % 8
+        if kind == 7:
+            x[r] = rng.standard_normal(cols)
+            continue
+        n = 0 if kind == 0 else (rng.integers(1, 128) if kind <= 3 else rng.integers(128, 600))
+        if kind == 6:
+            n = rng.integers(0, 100)
+            spots = rng.choice(cols, min(cols, 300), replace=False)
+            x[r, spots[: len(spots) // 3]] = fmin
+            x[r, spots[len(spots) // 3: 2 * len(spots) // 3]] = np.nan
+        n = min(n, cols)
+        x[r, rng.choice(cols, n, replace=False)] = (rng.standard_normal(n) * 3).astype(np.float32)
+    return x
 
 
 def _make(rows, cols, kind, seed):
@@ -128,6 +156,8 @@ def _make(rows, cols, kind, seed):
             x[r, pos[:60]] = 100 + rng.random(60).astype(np.float32) * 50
             x[r, pos[60:]] = 5.0
         return x
+    if kind == "masked_mix":
+        return _masked_mix(rows, cols, rng)
     if kind == "nan_heavy":
         x = np.full((rows, cols), np.nan, np.float32)
         for r in range(rows):
@@ -197,12 +227,15 @@ def _sampler_inputs(rows, vocab, seed, sigma=3.0):
     return x, temp, topk, topp
 
 
-@pytest.mark.parametrize("rows,vocab,dtype", [(256, 128256, "bf16"), (64, 32000, "f32"),
-                                              (16, 4096, "bf16"), (8, 131, "f32")])
-def test_fused_sampler_parity(gpu, rows, vocab, dtype):
+@pytest.mark.parametrize("rows,vocab,dtype,masked", [(256, 128256, "bf16", False), (64, 32000, "f32", False),
+                                                     (16, 4096, "bf16", False), (8, 131, "f32", False),
+                                                     (256, 128256, "bf16", True), (128, 32768, "f32", True)])
+def test_fused_sampler_parity(gpu, rows, vocab, dtype, masked):
     from tallax_amd import sampling
-    _log(f"sample rows={rows} vocab={vocab} dtype={dtype}")
+    _log(f"sample rows={rows} vocab={vocab} dtype={dtype} masked={masked}")
     x, temp, topk, topp = _sampler_inputs(rows, vocab, seed=vocab + rows)
+    if masked:   # constrained decoding: most logits -inf
+        x = _masked_mix(rows, vocab, np.random.default_rng(rows))
     temp[::17] = 1e-6      # greedy rows
     topk[1::13] = 1        # top-1 rows
     topp[2::11] = 0.9999999
