@@ -185,13 +185,13 @@ def _sampler(torch, np, _lib, dev, s_handle, gen, nbuf, max_k=128, masked=False)
         return bool(np.array_equal(out.cpu().numpy(), O.sample(key, h, topk, topp, temp, dtype="bf16",
                                                                max_k=max_k)))
 
-    def cpu_step(O, r0, batch):
+    def cpu_job(O, r0, batch):
         h = host0(O)
         sl = slice(r0, r0 + batch)
-        O.sample(key, h[sl], topk[sl], topp[sl], temp[sl], dtype="bf16", dim0_offset=r0, max_k=max_k)
-        return h[sl].shape[0]
+        return ("sample", (key, h[sl], topk[sl], topp[sl], temp[sl]),
+                dict(dtype="bf16", dim0_offset=r0, max_k=max_k))
 
-    w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
+    w.launch, w.parity, w.cpu_job = launch, parity, cpu_job
     return w
 
 
@@ -268,16 +268,12 @@ def _topk(torch, np, _lib, dev, s_handle, gen, nbuf, which):
             return bool(np.array_equal(got, want[1]) and np.array_equal(depths.cpu().numpy(), want[3]))
         return bool(np.array_equal(got, ei))
 
-    def cpu_step(O, r0, batch):
+    def cpu_job(O, r0, batch):
         h = host0()
         sl = slice(r0, r0 + batch)
-        if approx:
-            O.top_dynamic_k(h[sl], k, k)
-        else:
-            O.top_k(h[sl], k)
-        return h[sl].shape[0]
+        return ("top_dynamic_k", (h[sl], k, k), {}) if approx else ("top_k", (h[sl], k), {})
 
-    w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
+    w.launch, w.parity, w.cpu_job = launch, parity, cpu_job
     return w
 
 
@@ -320,14 +316,12 @@ def _sort_c2(torch, np, _lib, dev, s_handle, gen, nbuf):
         return bool(np.array_equal(idx.cpu().numpy(), want_idx) and
                     np.array_equal(g.cpu().numpy(), O.take_along_axis(hv, want_idx, 1)))
 
-    def cpu_step(O, r0, batch):
+    def cpu_job(O, r0, batch):
         hk, hv = host0(O)
         sl = slice(r0, r0 + batch)
-        (_, ii), _ = O.sort([hk[sl]], 1, is_stable=True, return_argsort=True, dtypes=["bf16"])
-        O.take_along_axis(hv[sl], ii, 1)
-        return hk[sl].shape[0]
+        return ("argsort_take", (hk[sl], hv[sl]), {})
 
-    w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
+    w.launch, w.parity, w.cpu_job = launch, parity, cpu_job
     return w
 
 
@@ -370,13 +364,12 @@ def _prefill_c5(torch, np, _lib, dev, s_handle, gen, nbuf):
         ok = ok and bool(np.all(np.abs(gp - p64) <= 1e-5 * np.abs(p64) + 1e-30))
         return ok and bool(np.all(np.abs(cum[:sample].cpu().numpy() - c64) <= 1e-5 * c64))
 
-    def cpu_step(O, r0, batch):
+    def cpu_job(O, r0, batch):
         h = host0()
         r0 = r0 % h.shape[0]
-        O.softmax_topk_cumsum_f64(h[r0:r0 + batch], k, p)
-        return h[r0:r0 + batch].shape[0]
+        return ("softmax_topk_cumsum_f64", (h[r0:r0 + batch], k, p), {})
 
-    w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
+    w.launch, w.parity, w.cpu_job = launch, parity, cpu_job
     return w
 
 
@@ -418,14 +411,73 @@ def _sort_wide(torch, np, _lib, dev, s_handle, gen, nbuf):
         return bool(np.array_equal(perm[:sample].cpu().numpy(), si) and
                     np.array_equal(keys[:sample].cpu().numpy().view(np.uint32), sk.view(np.uint32)))
 
-    def cpu_step(O, r0, batch):
+    def cpu_job(O, r0, batch):
         h = host0()
         r0 = r0 % h.shape[0]
-        O.sort([h[r0:r0 + batch]], 1, is_stable=True, return_argsort=True, descending=True)
-        return h[r0:r0 + batch].shape[0]
+        return ("sort_desc", (h[r0:r0 + batch],), {})
 
-    w.launch, w.parity, w.cpu_step = launch, parity, cpu_step
+    w.launch, w.parity, w.cpu_job = launch, parity, cpu_job
     return w
+
+
+def _cpu_job(job):
+    """One batch of the CPU baseline in a worker process (numpy only): the
+    oracle function the job names on the job's rows; returns the row count."""
+    name, args, kwargs = job
+    from oracle import tallax_oracle as O
+    if name == "argsort_take":
+        keys, vals = args
+        (_, ii), _ = O.sort([keys], 1, is_stable=True, return_argsort=True, dtypes=["bf16"])
+        O.take_along_axis(vals, ii, 1)
+        return keys.shape[0]
+    if name == "sort_desc":
+        O.sort([args[0]], 1, is_stable=True, return_argsort=True, descending=True)
+        return args[0].shape[0]
+    getattr(O, name)(*args, **kwargs)
+    return args[1].shape[0] if name == "sample" else args[0].shape[0]
+
+
+def _cpu_warm(_):
+    from oracle import tallax_oracle  # noqa: F401
+    return 0
+
+
+def _cpu_baseline(w, O, seconds):
+    """The numpy oracle over row batches of the same workload on every host
+    core this process may run on (at most 16, the GPU box's CPU share), one
+    spawned worker process per core: batches are submitted for `seconds`,
+    then the ones in flight finish; rows/s over the wall time of the whole."""
+    import concurrent.futures as cf
+    import multiprocessing as mp
+    cores = max(1, min(len(os.sched_getaffinity(0)), 16))
+    saved = {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS")}
+    for k in saved:
+        os.environ[k] = "1"   # one thread per worker: the pool is the parallelism
+    try:
+        with cf.ProcessPoolExecutor(max_workers=cores, mp_context=mp.get_context("spawn")) as pool:
+            list(pool.map(_cpu_warm, range(cores)))  # workers started and the oracle imported
+            rows_done, r0, pending = 0, 0, set()
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < seconds:
+                while len(pending) < 2 * cores:
+                    pending.add(pool.submit(_cpu_job, w.cpu_job(O, r0, w.cpu_batch)))
+                    r0 = (r0 + w.cpu_batch) % w.rows
+                done, pending = cf.wait(pending, return_when=cf.FIRST_COMPLETED)
+                rows_done += sum(f.result() for f in done)
+            for f in cf.as_completed(pending):
+                rows_done += f.result()
+            wall = time.perf_counter() - t0
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    return {"value": rows_done / wall, "unit": "rows/s", "cores": cores, "kind": "port",
+            "threading": f"process pool (spawn): {cores} single-threaded numpy oracle workers",
+            "sample": f"{rows_done} rows ({w.cpu_batch}-row batches) of the same [{w.shape[0]},{w.shape[1]}] "
+                      f"workload through the numpy oracle (oracle/tallax_oracle.py) on {cores} cores, "
+                      f"{wall:.1f} s wall"}
 
 
 def main() -> int:
@@ -507,16 +559,7 @@ def main() -> int:
     # ---- CPU baseline: the numpy oracle on a bounded sample of the same workload
     cpu = None
     if not args.no_cpu_baseline:
-        rows_done, t_cpu, r0 = 0, 0.0, 0
-        while t_cpu < args.cpu_seconds:
-            t = time.perf_counter()
-            rows_done += w.cpu_step(O, r0, w.cpu_batch)
-            t_cpu += time.perf_counter() - t
-            r0 = (r0 + w.cpu_batch) % w.rows
-        cpu = {"value": rows_done / t_cpu, "unit": "rows/s", "cores": 1, "kind": "port",
-               "sample": f"{rows_done} rows ({w.cpu_batch}-row batches) of the same [{w.shape[0]},{w.shape[1]}] "
-                         f"workload through the numpy oracle (oracle/tallax_oracle.py), single thread, "
-                         f"{t_cpu:.1f} s"}
+        cpu = _cpu_baseline(w, O, args.cpu_seconds)
 
     copy_gbs, _ = _copy_rate(torch, dev, stream, 10, 3)
     rec = {
