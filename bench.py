@@ -21,6 +21,8 @@ samples one token for each of the 256 rows.
                  argsort with keys: the reference's own route for config 5's
                  sort (rows > 16384: chunk radix sorts + merge passes)
   copy           torch's device copy of 256 MiB (the counter calibration)
+  read_calib     read-only kernels over 256 MiB with 16-, 8- and 4-byte loads
+                 (FETCH_SIZE calibration per load width)
 
 Timing: inputs are resident in HBM before the timed region; steps rotate
 over distinct input buffers (more bytes than the 256 MB MALL) so every step
@@ -42,7 +44,8 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak, GB/s
 COPY_BYTES = 256 << 20  # calibration copy: 256 MiB read + 256 MiB written per launch
-CONFIGS = ["sampler", "sampler_masked", "sampler_wide", "topk_c3", "topk_c3_approx", "topk_c1", "sort_c2", "prefill_c5", "sort_wide", "copy"]
+CONFIGS = ["sampler", "sampler_masked", "sampler_wide", "topk_c3", "topk_c3_approx", "topk_c1", "sort_c2", "prefill_c5",
+           "sort_wide", "copy", "read_calib"]
 
 
 def _copy_rate(torch, dev, stream, steps, warmup):
@@ -64,6 +67,32 @@ def _copy_rate(torch, dev, stream, steps, warmup):
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / steps
     return 2 * COPY_BYTES / (us * 1e-6) / 1e9, us
+
+
+def _read_rates(torch, _lib, dev, stream, steps, warmup):
+    """GB/s of the read-only calibration kernel (tallax_testing_read_bytes)
+    over COPY_BYTES with 16-, 8- and 4-byte loads."""
+    bufs = [torch.empty(COPY_BYTES // 4, dtype=torch.int32, device=dev) for _ in range(2)]
+    for b in bufs:
+        b.fill_(7)
+    out = torch.empty(4096, dtype=torch.int32, device=dev)
+    res = {}
+    for width in (16, 8, 4):
+        def go(i):
+            _lib.check(_lib.LIB.tallax_testing_read_bytes(bufs[i % 2].data_ptr(), COPY_BYTES, width, out.data_ptr(),
+                                                          stream.cuda_stream), "read_bytes")
+        for i in range(warmup):
+            go(i)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for i in range(steps):
+            go(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        res[width] = {"GBs": COPY_BYTES / (us * 1e-6) / 1e9, "us": us}
+    return res
 
 
 def _measured_traffic(config):
@@ -90,6 +119,8 @@ def _parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="sampler config: skip the second north-star line (config 3's exact top-k)")
     return ap.parse_args()
 
 
@@ -480,6 +511,30 @@ def _cpu_baseline(w, O, seconds):
                       f"{wall:.1f} s wall"}
 
 
+def _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O):
+    """Config 3 (the second north-star target: exact top-k k=50 of f32
+    [128,151936] + spikes), timed the same way as the main line."""
+    w = _topk(torch, np, _lib, dev, s_handle, gen, None, "topk_c3")
+    parity = None if args.no_parity else w.parity(O)
+    for i in range(args.warmup):
+        w.launch(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(args.steps):
+        w.launch(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    achieved = w.alg_bytes / (us * 1e-6) / 1e9
+    return {"metric": w.metric, "value": w.rows * args.steps / max(wall, us * 1e-6 * args.steps), "unit": "rows/s",
+            "kernel": w.kernel, "kernel_avg_us": us, "achieved_GBs": achieved, "roofline_frac": achieved / PEAK_HBM_GBS,
+            "algorithmic_bytes_per_launch": w.alg_bytes, "traffic": _measured_traffic("topk_c3"),
+            "workload": w.workload, "parity_vs_oracle": parity}
+
+
 def main() -> int:
     args = _parse()
     if args.gpus != 1:
@@ -507,6 +562,16 @@ def main() -> int:
                           "ms_per_step": us / 1e3, "higher_is_better": True, "scaling": "weak",
                           "vs_baseline": None, "dtype": "f32", "data": "synthetic",
                           "config": {"workload": f"torch copy_ of {COPY_BYTES} bytes (f32)"}}), flush=True)
+        return 0
+
+    if args.config == "read_calib":
+        res = _read_rates(torch, _lib, dev, stream, args.steps, args.warmup)
+        print(json.dumps({"metric": "read-only kernel GB/s by load width, calibration", "value": res[16]["GBs"],
+                          "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": res[16]["us"] / 1e3, "higher_is_better": True, "scaling": "weak",
+                          "vs_baseline": None, "dtype": "u32", "data": "synthetic",
+                          "config": {"workload": f"tallax_testing_read_bytes over {COPY_BYTES} bytes"},
+                          "by_width": res}), flush=True)
         return 0
 
     if args.config == "sampler":
@@ -585,6 +650,8 @@ def main() -> int:
         "parity_vs_oracle": parity,
         "wall_ms_per_step": wall * 1e3 / args.steps,
     }
+    if args.config == "sampler" and not args.no_extra:
+        rec["topk_c3"] = _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O)
     if hasattr(w, "common_us"):
         cu = w.common_us(args.steps)
         rec["unmasked_kernel_avg_us"] = cu

@@ -49,6 +49,11 @@ int tallax_testing_top_dynamic_k_path(const void* x, int dtype, int64_t rows, in
                                       int32_t* out_idx, int32_t* out_valid, int32_t* out_depths, float* out_cutoff,
                                       void* workspace, size_t workspace_bytes, tallax_stream_t stream, int path);
 
+/* Reads nbytes of src with `width`-byte loads (4, 8 or 16; src aligned to it,
+ * nbytes a multiple of it) and writes one word per workgroup to out (2048
+ * words): the calibration launch for the FETCH_SIZE counter. */
+int tallax_testing_read_bytes(const void* src, int64_t nbytes, int width, uint32_t* out, tallax_stream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

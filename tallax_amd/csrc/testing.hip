@@ -1,10 +1,13 @@
 // Test hooks: expose the device-side exp/log/Gumbel primitives so that the
-// GPU test suite can pin them bit for bit against the numpy oracle.  These
+// GPU test suite can pin them bit for bit against the numpy oracle, and a
+// read kernel of known traffic for counter calibration.  These
 // entry points have no counterpart in the reference.
 #include "tallax_hip_testing.h"
 #include "tx_common.h"
 #include "tx_host.h"
 #include "tx_math.h"
+
+#include <type_traits>
 
 namespace tx {
 
@@ -37,6 +40,34 @@ __global__ void lane_ops_kernel(uint32_t* out) {
   out[4 * 64 + x] = lane_xor(x, 16);
   out[5 * 64 + x] = lane_xor(x, 32);
   out[6 * 64 + x] = lane_rev(x);
+}
+
+}  // namespace tx
+
+// Reads nbytes (a multiple of W) with W-byte loads, grid-stride, and writes
+// one XOR of the words per workgroup: the counter calibration kernel (the
+// FETCH_SIZE of a launch that reads a known number of bytes with loads of a
+// known width).
+namespace tx {
+
+constexpr int kReadProbeBlocks = 2048;
+template <int W>
+__global__ __launch_bounds__(256) void read_probe_kernel(const void* src, int64_t nbytes, uint32_t* out) {
+  using V = typename std::conditional<W == 16, uint4, typename std::conditional<W == 8, uint2, uint32_t>::type>::type;
+  const V* p = (const V*)src;
+  const int64_t n = nbytes / W;
+  uint32_t acc = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    const V v = p[i];
+    if constexpr (W == 16) acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    else if constexpr (W == 8) acc ^= v.x ^ v.y;
+    else acc ^= v;
+  }
+  acc = (uint32_t)wave_sum_i((int)acc);  // any combination: it only has to be written
+  __shared__ uint32_t red[4];
+  if (lane_id() == 0) red[threadIdx.x / kWave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
 
 }  // namespace tx
@@ -75,6 +106,19 @@ int tallax_testing_gumbel(uint32_t k0, uint32_t k1, const uint32_t* counters, fl
   hipLaunchKernelGGL(tx::gumbel_probe_kernel, dim3(blocks), dim3(256), 0, stream, k0, k1, counters,
                      gumbel_out, bits_out, n);
   return tx::launch_status("tallax_testing_gumbel");
+}
+
+int tallax_testing_read_bytes(const void* src, int64_t nbytes, int width, uint32_t* out, hipStream_t stream) {
+  if ((width != 4 && width != 8 && width != 16) || nbytes <= 0 || nbytes % width || !src || !out ||
+      ((uintptr_t)src % width)) {
+    tx::set_error("bad arguments");
+    return tx::kInvalidArgument;
+  }
+  const dim3 grid(tx::kReadProbeBlocks), block(256);
+  if (width == 16) hipLaunchKernelGGL(tx::read_probe_kernel<16>, grid, block, 0, stream, src, nbytes, out);
+  else if (width == 8) hipLaunchKernelGGL(tx::read_probe_kernel<8>, grid, block, 0, stream, src, nbytes, out);
+  else hipLaunchKernelGGL(tx::read_probe_kernel<4>, grid, block, 0, stream, src, nbytes, out);
+  return tx::launch_status("tallax_testing_read_bytes");
 }
 
 }  // extern "C"
