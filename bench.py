@@ -120,7 +120,8 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
-                    help="sampler config: skip the second north-star line (config 3's exact top-k)")
+                    help="skip the extra measurements: config 3's line in the sampler config, the unmasked "
+                         "comparison in sampler_masked (profiling runs)")
     return ap.parse_args()
 
 
@@ -652,7 +653,7 @@ def main() -> int:
     }
     if args.config == "sampler" and not args.no_extra:
         rec["topk_c3"] = _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O)
-    if hasattr(w, "common_us"):
+    if hasattr(w, "common_us") and not args.no_extra:
         cu = w.common_us(args.steps)
         rec["unmasked_kernel_avg_us"] = cu
         rec["masked_over_unmasked"] = kern_us / cu
