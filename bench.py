@@ -270,7 +270,7 @@ def _topk(torch, np, _lib, dev, s_handle, gen, nbuf, which):
         def launch(i):
             x = bufs[i % len(bufs)]
             _lib.check(_lib.LIB.tallax_top_dynamic_k(
-                x.data_ptr(), _lib.F32, rows, cols, kr.data_ptr(), k, 8, 128, arr, len(steps), 0, 0.0,
+                x.data_ptr(), _lib.F32, rows, cols, kr.data_ptr(), k, 8, 128, arr, len(steps), 0, 0, 0.0,
                 vals.data_ptr(), idx.data_ptr(), valid.data_ptr(), depths.data_ptr(), cutoff.data_ptr(),
                 ws.data_ptr(), ws.numel(), s_handle), "top_dynamic_k")
     else:

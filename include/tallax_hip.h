@@ -66,9 +66,9 @@ int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k,
 /* ------------------------------------------------------------------------
  * Exact top-k with per-row k and a replacement value: top_k(x, k) whose
  * positions >= k_rows[row] hold replace_val (in x's dtype).
- * Replaces top_dynamic_k(logits, k, max_k, guarantee_convergence=True,
- * replace_val) -- tallax/_src/top_k.py:385-514 (replacement :365-369),
- * under the lowest-index tie rule of tax.top_k.  Workspace as tallax_topk
+ * The exact counterpart of top_dynamic_k(logits, k, max_k, replace_val)
+ * -- tallax/_src/top_k.py:385-514 (replacement :365-369) -- for a run that
+ * converges, under the lowest-index tie rule of tax.top_k.  Workspace as tallax_topk
  * (tallax_topk_workspace_size).
  * ---------------------------------------------------------------------- */
 int tallax_topk_replace(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k, const int32_t* k_rows,
@@ -76,24 +76,30 @@ int tallax_topk_replace(const void* x, int dtype, int64_t rows, int64_t cols, in
                         size_t workspace_bytes, tallax_stream_t stream);
 
 /* ------------------------------------------------------------------------
- * Approximate (binned) top-k: top_dynamic_k(..., guarantee_convergence=False).
+ * Binned top-k: top_dynamic_k.
  * Replaces top_dynamic_k -- tallax/_src/top_k.py:385-514 (kernel
- * dynamic_top_k_refs :203-370, binned_top_k :13-106).
+ * dynamic_top_k_refs :203-370, binned_top_k :13-106, and with
+ * guarantee_convergence the bin-packing merge of unconverged blocks,
+ * _merge_unconverged_bins_top_k :108-200, invoked at :317-331).
  * x [rows, cols] f32/bf16; k_rows [rows] int32 (per-row k <= max_k <= 128);
  * rows % block_token == 0; num_bins divides 1024; schedule: the strictly
  * increasing depths m (the reference's bins_topm_schedule without its
  * leading 0; the caller computes the automatic one), deepest <= 16 after
- * power-of-two bucketing.  Outputs: out_vals [rows, max_k] (x's dtype),
- * out_idx [rows, max_k] int32 (-1 where fewer admissible elements exist),
+ * power-of-two bucketing.  guarantee_convergence != 0 with a last depth m
+ * other than max_k needs m >= 2 and num_bins % 128 == 0 (the merge packs
+ * the 2^ceil(log2(ceil(max_k / (m - 1)))) busiest bins).  Outputs:
+ * out_vals [rows, max_k] (x's dtype), out_idx [rows, max_k] int32 (-1 where
+ * fewer admissible elements exist; the merge can also return columns past
+ * the row's end, with finfo.min, where the reference reads past it),
  * out_valid [1] int32 (0/1), out_depths [rows] int32, out_cutoff [rows] f32.
  * Workspace: tallax_top_dynamic_k_workspace_size bytes.
  * ---------------------------------------------------------------------- */
 size_t tallax_top_dynamic_k_workspace_size(int64_t rows, int num_bins, const int32_t* schedule, int num_steps);
 int tallax_top_dynamic_k(const void* x, int dtype, int64_t rows, int64_t cols, const int32_t* k_rows, int max_k,
-                         int block_token, int num_bins, const int32_t* schedule, int num_steps, int has_replace,
-                         double replace_val, void* out_vals, int32_t* out_idx, int32_t* out_valid,
-                         int32_t* out_depths, float* out_cutoff, void* workspace, size_t workspace_bytes,
-                         tallax_stream_t stream);
+                         int block_token, int num_bins, const int32_t* schedule, int num_steps,
+                         int guarantee_convergence, int has_replace, double replace_val, void* out_vals,
+                         int32_t* out_idx, int32_t* out_valid, int32_t* out_depths, float* out_cutoff,
+                         void* workspace, size_t workspace_bytes, tallax_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Fused vLLM-style sampler: top-k (per-row k, clamped to 128) -> top-p ->

@@ -45,7 +45,8 @@ int tallax_testing_select_plan(int64_t rows, int64_t cols, int dtype, int32_t* o
  * tallax_top_dynamic_k; TALLAX_INVALID_ARGUMENT for another path. */
 int tallax_testing_top_dynamic_k_path(const void* x, int dtype, int64_t rows, int64_t cols, const int32_t* k_rows,
                                       int max_k, int block_token, int num_bins, const int32_t* schedule,
-                                      int num_steps, int has_replace, double replace_val, void* out_vals,
+                                      int num_steps, int guarantee_convergence, int has_replace,
+                                      double replace_val, void* out_vals,
                                       int32_t* out_idx, int32_t* out_valid, int32_t* out_depths, float* out_cutoff,
                                       void* workspace, size_t workspace_bytes, tallax_stream_t stream, int path);
 

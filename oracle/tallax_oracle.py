@@ -221,11 +221,73 @@ def binned_topm(x: np.ndarray, m: int, num_bins: int, dtype: str = "f32"):
     return out_v, out_i
 
 
+def list_order(v: np.ndarray, i: np.ndarray) -> np.ndarray:
+    """Row-wise order of (value, index) list entries: select_key descending,
+    then index ascending as an unsigned 32-bit number, so that the scratch
+    fillers (finfo.min, index -1) follow every entry of a value >= finfo.min
+    with a real index (the reference orders them by value; their indices are
+    uninitialised there)."""
+    key = select_key(np.asarray(v, np.float32)).astype(np.int64)
+    iu = np.asarray(i).astype(np.int64) & 0xFFFFFFFF
+    return np.lexsort((iu, -key), axis=-1)
+
+
+def packed_bins(max_k: int, m: int) -> int:
+    """num_packed_bins of _merge_unconverged_bins_top_k (top_k.py:122-124):
+    the smallest power of two >= ceil(max_k / (m - 1))."""
+    if m < 2:
+        raise ValueError(f"the bin-packing merge needs a last schedule depth >= 2, got {m}")
+    return 2 ** log2_ceil(-(-max_k // (m - 1)))
+
+
+def merge_unconverged_bins(x, bv, bi, num_bins, m, max_k, dtype="f32"):
+    """_merge_unconverged_bins_top_k (top_k.py:108-200) on the rows of one
+    block, in place on their rank-major lists bv/bi [R, buf, num_bins]:
+      * pivot = max over bins of rank m-1 (:126); per bin, the count of its
+        ranks < m-1 that are >= pivot (:128-133);
+      * the P = packed_bins(max_k, m) bins of the largest counts (:135-140;
+        the reference's bitonic network leaves the order among equal counts
+        open, and this restatement takes the lowest bin first);
+      * every rank of a chosen bin becomes float32's finfo.min (:147-151,
+        the scratch is 32-bit) with its index kept;
+      * packed position e of ceil(V / (128 num_bins / P)) * 128 holds column
+        (e // P) * num_bins + chosen[e % P] (:153-183: lane L of packed tile
+        j is slice j * 128 / P + L // P of bin chosen[L % P]); columns past
+        the row hold (finfo(dtype).min, column), where the reference reads
+        past the row's end;
+      * rank 0 of bins 0..127 (the first 128 scratch columns) becomes the
+        top-128 (list_order) of the packed entries and those 128 columns
+        (:185-200).
+    Needs num_bins % 128 == 0 (the first 128 columns are rank 0 of 128
+    bins, and 128 bins are ranked at :139)."""
+    if num_bins % NUM_LANES:
+        raise NotImplementedError(f"the bin-packing merge needs num_bins % {NUM_LANES} == 0, got {num_bins}")
+    x = np.asarray(x, np.float32)
+    rows, V = x.shape
+    P = packed_bins(max_k, m)
+    lo = dtype_min(dtype)
+    pivot = bv[:, m - 1, :].max(axis=1)
+    cnt = (bv[:, :m - 1, :] >= pivot[:, None, None]).sum(axis=1)
+    bins = np.broadcast_to(np.arange(num_bins), cnt.shape)
+    chosen = np.lexsort((bins, -cnt), axis=1)[:, :P]
+    for r in range(rows):
+        bv[r][:, chosen[r]] = F32_MIN
+    n = -(-V // (NUM_LANES * (num_bins // P))) * NUM_LANES
+    e = np.arange(n)
+    col = (e // P)[None, :] * num_bins + chosen[:, e % P]
+    pv = np.where(col < V, np.take_along_axis(x, np.minimum(col, V - 1), 1), lo).astype(np.float32)
+    cv = np.concatenate([pv, bv[:, 0, :NUM_LANES]], axis=1)
+    ci = np.concatenate([col.astype(np.int64), bi[:, 0, :NUM_LANES].astype(np.int64)], axis=1)
+    top = list_order(cv, ci)[:, :NUM_LANES]
+    bv[:, 0, :NUM_LANES] = np.take_along_axis(cv, top, 1)
+    bi[:, 0, :NUM_LANES] = np.take_along_axis(ci, top, 1).astype(np.int32)
+
+
 def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, replace_val=None,
-                  dtype: str = "f32"):
-    """top_dynamic_k with guarantee_convergence=False (top_k.py:203-514):
+                  dtype: str = "f32", guarantee_convergence: bool = False):
+    """top_dynamic_k (top_k.py:203-514).  guarantee_convergence=False:
     (vals [R, max_k], idxs [R, max_k] int32, valid bool, depths [R] int32,
-    cutoff_vals [R] f32).
+    cutoff_vals [R] f32); True: (vals, idxs).
 
     For each schedule step m (after the leading 0), evaluated while some row
     of the row's block of `block_token` rows has not converged:
@@ -233,12 +295,17 @@ def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, repla
       that are >= pivot); a row converges when num_larger >= k[row]; depth =
       m - 1 at the first convergence (max_k if never); cutoff = the pivot of
       the last step evaluated (top_k.py:283-320).
+    With guarantee_convergence and a last depth other than max_k, a block
+    that has not converged after its last step goes through
+    merge_unconverged_bins (top_k.py:317-331).  The reference adds no max_k
+    to the schedule, whatever its docstring says (top_k.py:444-450).
     valid = (max depth over all rows < schedule[-1]) or schedule[-1] == max_k.
     The output is the top-128 of the first depth_upper ranks of every bin,
     depth_upper the power-of-two bucket of the global max depth
-    (top_k.py:333-364), ordered by value then lowest index (the reference's
-    network order inside ties is not pinned), then truncated to max_k;
-    positions >= k[row] get replace_val in the input dtype when given.
+    (top_k.py:333-364), in list_order (value, then lowest index: the
+    reference's network order inside ties is not pinned), truncated to
+    max_k and rounded to the dtype; positions >= k[row] get replace_val in
+    the input dtype when given.
     Ranks at or past the m of a block's last evaluated step are never written
     for that block's rows: they keep the finfo.min the scratch starts with
     (top_k.py:241-243, 250-281), so they reach the output only as
@@ -253,6 +320,11 @@ def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, repla
     kk = np.broadcast_to(np.asarray(k, dtype=np.int64), (rows,))
     sched = topm_schedule(max_k, num_bins, block_token, schedule)
     max_m = sched[-1]
+    merge = guarantee_convergence and max_m != max_k
+    if merge:
+        packed_bins(max_k, max_m)
+        if num_bins % NUM_LANES:
+            raise NotImplementedError(f"the bin-packing merge needs num_bins % {NUM_LANES} == 0")
     buf = max(max_m, 2 ** log2_ceil(max_m - 1)) if max_m > 1 else max_m
     bv, bi = binned_topm(x, buf, num_bins, dtype)
     lo = dtype_min(dtype)
@@ -272,6 +344,8 @@ def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, repla
         # ranks >= m (the last step this block evaluated) were never written
         bv[blk, m:, :] = lo
         bi[blk, m:, :] = -1
+        if merge and not conv.all():
+            merge_unconverged_bins(x[blk], bv[blk], bi[blk], num_bins, max_m, max_k, dtype)
     gmax = int(depths.max())
     valid = bool(gmax < sched[-1] or sched[-1] == max_k)
     gsched = sorted(set(2 ** log2_ceil(s - 1) if s > 1 else s for s in sched))
@@ -282,16 +356,15 @@ def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, repla
             break
     sv = bv[:, :upper, :].reshape(rows, -1)
     si = bi[:, :upper, :].reshape(rows, -1)
-    filler = si < 0
-    kv = np.where(filler, -np.inf, sv.astype(np.float64))
-    ki = np.where(filler, np.iinfo(np.int64).max, si.astype(np.int64))
-    order = np.lexsort((ki, -kv), axis=1)[:, :NUM_LANES]
-    vals = np.take_along_axis(sv, order, 1)[:, :max_k].copy()
+    order = list_order(sv, si)[:, :NUM_LANES]
+    vals = round_to_dtype(np.take_along_axis(sv, order, 1)[:, :max_k], dtype).astype(np.float32)
     idxs = np.take_along_axis(si, order, 1)[:, :max_k].copy()
     if replace_val is not None:
         pos = np.arange(vals.shape[1])[None, :]
         rv = round_to_dtype(np.float32(replace_val), dtype)
         vals = np.where(pos < kk[:, None], vals, rv).astype(np.float32)
+    if guarantee_convergence:
+        return vals, idxs
     return vals, idxs, valid, depths, cutoff
 
 

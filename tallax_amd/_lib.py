@@ -55,7 +55,7 @@ _SIGNATURES = {
     "tallax_topk_replace": ([_c_p, _c_int, _c_i64, _c_i64, _c_i64, _c_p, _c_d, _c_p, _c_p, _c_p, _c_sz, _c_p], _c_int),
     "tallax_top_dynamic_k_workspace_size": ([_c_i64, _c_int, _c_p, _c_int], _c_sz),
     "tallax_top_dynamic_k": ([_c_p, _c_int, _c_i64, _c_i64, _c_p, _c_int, _c_int, _c_int, _c_p, _c_int, _c_int,
-                              _c_d, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p], _c_int),
+                              _c_int, _c_d, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p], _c_int),
     "tallax_softmax_topk_cumsum": ([_c_p, _c_i64, _c_i64, _c_int, ctypes.c_float, _c_p, _c_p, _c_p, _c_p, _c_p],
                                    _c_int),
     # test hooks (include/tallax_hip_testing.h)
@@ -65,7 +65,7 @@ _SIGNATURES = {
     "tallax_testing_read_bytes": ([_c_p, _c_i64, _c_int, _c_p, _c_p], _c_int),
     "tallax_testing_select_plan": ([_c_i64, _c_i64, _c_int, _c_p], _c_int),
     "tallax_testing_top_dynamic_k_path": ([_c_p, _c_int, _c_i64, _c_i64, _c_p, _c_int, _c_int, _c_int, _c_p, _c_int,
-                                           _c_int, _c_d, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p, _c_int],
+                                           _c_int, _c_int, _c_d, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p, _c_int],
                                           _c_int),
 }
 

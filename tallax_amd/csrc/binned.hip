@@ -1,5 +1,5 @@
-// Approximate (binned) top-k for gfx950: tax.top_dynamic_k with
-// guarantee_convergence=False.
+// Binned top-k for gfx950: tax.top_dynamic_k, with guarantee_convergence's
+// bin-packing merge of unconverged blocks (binned_merge_kernel).
 //
 // Reference semantics (tallax/_src/top_k.py:13-106, 203-370, 372-514):
 //   * bin b holds the columns j = b (mod num_bins); each bin keeps its m
@@ -32,6 +32,9 @@
 //                        step's (pivot, count).
 //   binned_finish_kernel one workgroup: depths, cutoffs, valid, depth_upper
 //                        and each row's last evaluated m.
+//   binned_merge_kernel  one workgroup per row of an unconverged block
+//                        (guarantee_convergence, last depth != max_k):
+//                        the busiest bins packed whole into rank 0.
 //   binned_select_kernel one workgroup per row: bitonic sort of the
 //                        depth_upper * num_bins superset, top-128 out.
 #include <float.h>
@@ -64,6 +67,8 @@ struct BinArgs {
   int ngs;
   int has_replace;
   float replace_val;       // in the input dtype
+  int merge;               // bin-packing merge of unconverged blocks
+  int num_packed;          // bins packed by the merge (a power of two <= 128)
   void* out_vals;
   int32_t* out_idx;
   int32_t* out_valid;
@@ -508,11 +513,38 @@ __global__ __launch_bounds__(kCandNT) void binned_cand_kernel(BinArgs a) {
 
 __host__ __device__ inline size_t cand_lds_bytes(int nb) { return (size_t)nb * cand_bin_bytes(cand_bucket_cap(nb)); }
 
-// composite of a list entry: value descending then index ascending; fillers
-// (index -1) after every real entry
+// composite of a list entry: value descending then index ascending as an
+// unsigned number, so that a scratch filler (finfo.min, index -1) follows
+// every entry of its value or above with a real index; 0 stays "no entry"
 __device__ __forceinline__ uint64_t entry_comp(float v, int32_t i) {
-  if (i < 0) return 0ull;
   return make_comp(select_key(__float_as_uint(v)), (uint32_t)i);
+}
+
+// float -> bfloat16 bits, nearest even (NaN kept quiet): list values are
+// bfloat16 values except the merge's float32 finfo.min, which becomes -inf
+__device__ __forceinline__ uint16_t bf16_bits_rne(float v) {
+  const uint32_t b = __float_as_uint(v);
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((b | 0x00400000u) >> 16);
+  return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+
+// Binary-tree merge of the sorted top-128 lists held by waves 0..nwr-1
+// (acc, two entries per lane) through LDS; wave 0 ends with the merged list.
+// Every thread of the workgroup must call it.
+template <int NW>
+__device__ __forceinline__ void tree_merge128(uint64_t acc[2], int nwr, uint64_t (*tree)[128]) {
+  const int w = (int)(threadIdx.x / kWave), l = lane_id();
+  for (int st = 1; st < nwr; st <<= 1) {
+    if ((w & (2 * st - 1)) == st) {
+      tree[w][l] = acc[0];
+      tree[w][kWave + l] = acc[1];
+    }
+    __syncthreads();
+    if ((w & (2 * st - 1)) == 0 && w + st < nwr) {
+      const uint64_t b[2] = {tree[w + st][l], tree[w + st][kWave + l]};
+      wave_merge128_desc(acc, b);
+    }
+  }
 }
 
 // Top max_k of the first depth_upper ranks of every bin: each wave sorts
@@ -609,18 +641,7 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
       wave_merge128_desc(acc, c);
     }
   }
-  const int nwr = nr < NW ? nr : NW;  // waves holding a list
-  for (int st = 1; st < nwr; st <<= 1) {
-    if ((w & (2 * st - 1)) == st) {
-      tree[w][l] = acc[0];
-      tree[w][kWave + l] = acc[1];
-    }
-    __syncthreads();
-    if ((w & (2 * st - 1)) == 0 && w + st < nwr) {
-      const uint64_t b[2] = {tree[w + st][l], tree[w + st][kWave + l]};
-      wave_merge128_desc(acc, b);
-    }
-  }
+  tree_merge128<NW>(acc, nr < NW ? nr : NW, tree);  // waves holding a list
   if (w != 0) return;
   const float lo = dtype_min_f(a.dtype);
   const int kr = a.k_rows[row];
@@ -638,10 +659,144 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
     if (a.has_replace && p >= kr) v = a.replace_val;
     const int64_t o = row * a.max_k + p;
     if (a.dtype == kBF16)
-      ((uint16_t*)a.out_vals)[o] = (uint16_t)(__float_as_uint(v) >> 16);
+      ((uint16_t*)a.out_vals)[o] = bf16_bits_rne(v);
     else
       ((float*)a.out_vals)[o] = v;
     a.out_idx[o] = id;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Bin-packing merge of the blocks that did not converge, for
+// guarantee_convergence with a last depth m other than max_k
+// (_merge_unconverged_bins_top_k, top_k.py:108-200, invoked at :317-331).
+// One workgroup per row, after the finish step; rows of converged blocks
+// return at once.
+//   1. per bin b, cnt[b] = #(ranks < m-1 whose value is >= the last step's
+//      pivot); the P bins of the largest counts are chosen (equal counts:
+//      lowest bin first), by a wave sort of (cnt, bin) composites;
+//   2. the packed entries (position e < npk: column (e / P) * NB +
+//      chosen[e % P], or (finfo.min, that column) past the row's end) and
+//      rank 0 of bins 0..127 (float32's finfo.min for chosen bins) are
+//      reduced to their top 128: each wave sorts 128-entry runs and merges
+//      them into its list, skipping runs with nothing above its 128th
+//      entry, then the waves' lists are merged;
+//   3. rank 0 of bins 0..127 takes that top 128, and every other rank of a
+//      chosen bin takes float32's finfo.min with its index kept.
+// ---------------------------------------------------------------------------
+constexpr int kMergeNT = 1024;
+static_assert(kMergeNT >= kBinNT, "one thread per bin");
+__global__ __launch_bounds__(kMergeNT) void binned_merge_kernel(BinArgs a) {
+  constexpr int NW = kMergeNT / kWave;
+  __shared__ uint64_t tree[NW][128];
+  __shared__ int s_chosen[128];
+  __shared__ unsigned char s_isch[kBinNT];
+  const int t = threadIdx.x, w = t / kWave, l = lane_id();
+  const int64_t row = blockIdx.x;
+  const int NB = a.num_bins, P = a.num_packed;
+  const int last = a.nsteps - 1;
+  const int m = a.steps[last];
+  const int64_t b0 = row / a.block_token * a.block_token;
+  int open = 0;
+  for (int64_t i = t; i < a.block_token; i += kMergeNT) open |= a.row_fc[b0 + i] >= a.nsteps ? 1 : 0;
+  if (!__syncthreads_or(open)) return;  // the block converged
+  float* lv = a.lv + (size_t)row * a.buf * NB;  // rank-major: entry rank * NB + bin
+  int32_t* li = a.li + (size_t)row * a.buf * NB;
+  const float pivot = a.st_pivot[row * a.nsteps + last];
+  // 1. counts, as (count, bin) composites in LDS, then the top 128 of them
+  uint64_t* cb = &tree[0][0];  // NB <= NW * 128 entries
+  if (t < NB) {
+    int c = 0;
+    for (int i = 0; i < m - 1; ++i) c += lv[(size_t)i * NB + t] >= pivot ? 1 : 0;
+    cb[t] = make_comp((uint32_t)c, (uint32_t)t);
+    s_isch[t] = 0;
+  }
+  __syncthreads();
+  const int nbr = (NB + 127) / 128;
+  uint64_t acc[2] = {0ull, 0ull};
+  if (w < nbr) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int e = w * 128 + h * kWave + l;
+      acc[h] = e < NB ? cb[e] : 0ull;
+    }
+    wave_sort128_desc(acc);
+  }
+  __syncthreads();  // the tree reuses the counts' LDS
+  tree_merge128<NW>(acc, nbr, tree);
+  if (w == 0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int p = h * kWave + l;
+      if (p < P) {
+        const int b = comp_idx(acc[h]);
+        s_chosen[p] = b;
+        s_isch[b] = 1;
+      }
+    }
+  }
+  __syncthreads();
+  // 2. top 128 of the packed entries and rank 0 of bins 0..127
+  const int64_t V = a.cols;
+  const int64_t npk = (V + (int64_t)128 * (NB / P) - 1) / ((int64_t)128 * (NB / P)) * 128;
+  const int64_t nr = npk / 128 + 1;  // runs; the last one is rank 0 of bins 0..127
+  const float lo = dtype_min_f(a.dtype);
+  const uint32_t lo_key = select_key(__float_as_uint(lo));
+  const int64_t xrow = row * V;
+  auto entry = [&](int64_t e) -> uint64_t {
+    if (e < npk) {
+      const int64_t col = (e / P) * NB + s_chosen[e % P];
+      const uint32_t key = col < V ? select_key(__float_as_uint(load_val(a.x, a.dtype, xrow + col))) : lo_key;
+      return make_comp(key, (uint32_t)col);
+    }
+    const int c = (int)(e - npk);
+    return entry_comp(s_isch[c] ? -FLT_MAX : lv[c], li[c]);
+  };
+  constexpr int U = 4;  // runs loaded per batch
+  acc[0] = acc[1] = 0ull;
+  bool have = false;
+  for (int64_t r0 = w; r0 < nr; r0 += (int64_t)U * NW) {
+    uint64_t c[U][2];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = r0 + (int64_t)u * NW;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) c[u][h] = r < nr ? entry(r * 128 + h * kWave + l) : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (r0 + (int64_t)u * NW >= nr) break;
+      if (have) {
+        const uint64_t a1 = acc[1];
+        const uint64_t thr = ((uint64_t)readlane_u32((uint32_t)(a1 >> 32), kWave - 1) << 32) |
+                             readlane_u32((uint32_t)a1, kWave - 1);
+        if (!__any(c[u][0] > thr || c[u][1] > thr)) continue;
+      }
+      wave_sort128_desc(c[u]);
+      if (!have) {
+        acc[0] = c[u][0];
+        acc[1] = c[u][1];
+        have = true;
+      } else {
+        wave_merge128_desc(acc, c[u]);
+      }
+    }
+  }
+  __syncthreads();  // the tree's LDS held the counts' lists
+  tree_merge128<NW>(acc, nr < NW ? (int)nr : NW, tree);
+  // 3. write back
+  if (w == 0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int p = h * kWave + l;
+      lv[p] = __uint_as_float(key_to_bits(comp_key(acc[h])));
+      li[p] = comp_idx(acc[h]);
+    }
+  }
+  for (int e = t; e < a.buf * P; e += kMergeNT) {
+    const int r = e / P, b = s_chosen[e % P];
+    if (r == 0 && b < 128) continue;  // written above
+    lv[(size_t)r * NB + b] = -FLT_MAX;
   }
 }
 
@@ -679,7 +834,7 @@ using namespace tx;
 // point only).  Both give the same results.
 static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t cols, const int32_t* k_rows,
                               int max_k, int block_token, int num_bins, const int32_t* schedule, int num_steps,
-                              int has_replace, double replace_val, void* out_vals, int32_t* out_idx,
+                              int guarantee_convergence, int has_replace, double replace_val, void* out_vals, int32_t* out_idx,
                               int32_t* out_valid, int32_t* out_depths, float* out_cutoff, void* workspace,
                               size_t workspace_bytes, hipStream_t stream, int mode);
 
@@ -691,18 +846,19 @@ size_t tallax_top_dynamic_k_workspace_size(int64_t rows, int num_bins, const int
 }
 
 int tallax_top_dynamic_k(const void* x, int dtype, int64_t rows, int64_t cols, const int32_t* k_rows, int max_k,
-                         int block_token, int num_bins, const int32_t* schedule, int num_steps, int has_replace,
-                         double replace_val, void* out_vals, int32_t* out_idx, int32_t* out_valid,
-                         int32_t* out_depths, float* out_cutoff, void* workspace, size_t workspace_bytes,
-                         hipStream_t stream) {
+                         int block_token, int num_bins, const int32_t* schedule, int num_steps,
+                         int guarantee_convergence, int has_replace, double replace_val, void* out_vals,
+                         int32_t* out_idx, int32_t* out_valid, int32_t* out_depths, float* out_cutoff,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream) {
   return top_dynamic_k_impl(x, dtype, rows, cols, k_rows, max_k, block_token, num_bins, schedule, num_steps,
-                            has_replace, replace_val, out_vals, out_idx, out_valid, out_depths, out_cutoff, workspace,
+                            guarantee_convergence, has_replace, replace_val, out_vals, out_idx, out_valid, out_depths, out_cutoff, workspace,
                             workspace_bytes, stream, 0);
 }
 
 int tallax_testing_top_dynamic_k_path(const void* x, int dtype, int64_t rows, int64_t cols, const int32_t* k_rows,
                                       int max_k, int block_token, int num_bins, const int32_t* schedule,
-                                      int num_steps, int has_replace, double replace_val, void* out_vals,
+                                      int num_steps, int guarantee_convergence, int has_replace,
+                                      double replace_val, void* out_vals,
                                       int32_t* out_idx, int32_t* out_valid, int32_t* out_depths, float* out_cutoff,
                                       void* workspace, size_t workspace_bytes, hipStream_t stream, int path) {
   if (path != 0 && path != 1) {
@@ -710,15 +866,15 @@ int tallax_testing_top_dynamic_k_path(const void* x, int dtype, int64_t rows, in
     return kInvalidArgument;
   }
   return top_dynamic_k_impl(x, dtype, rows, cols, k_rows, max_k, block_token, num_bins, schedule, num_steps,
-                            has_replace, replace_val, out_vals, out_idx, out_valid, out_depths, out_cutoff, workspace,
-                            workspace_bytes, stream, path);
+                            guarantee_convergence, has_replace, replace_val, out_vals, out_idx, out_valid, out_depths,
+                            out_cutoff, workspace, workspace_bytes, stream, path);
 }
 
 }  // extern "C"
 
 static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t cols, const int32_t* k_rows,
                               int max_k, int block_token, int num_bins, const int32_t* schedule, int num_steps,
-                              int has_replace, double replace_val, void* out_vals, int32_t* out_idx,
+                              int guarantee_convergence, int has_replace, double replace_val, void* out_vals, int32_t* out_idx,
                               int32_t* out_valid, int32_t* out_depths, float* out_cutoff, void* workspace,
                               size_t workspace_bytes, hipStream_t stream, int mode) {
   if (!x || !k_rows || !schedule || !out_vals || !out_idx || !out_valid || !out_depths || !out_cutoff) {
@@ -741,8 +897,28 @@ static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t co
     }
   }
   if (cols >= (int64_t)1 << 31) { set_error("cols must fit int32 indices"); return kInvalidArgument; }
-  if (rows == 0) return kOk;
   const int max_m = schedule[num_steps - 1];
+  // the bin-packing merge runs for guarantee_convergence unless the last
+  // depth is max_k (top_k.py:317-331); the reference derives P from
+  // ceil(max_k / (m - 1)) and reads rank 0 of 128 bins
+  const bool merge = guarantee_convergence != 0 && max_m != max_k;
+  int packed = 0;
+  if (merge) {
+    if (max_m < 2) {
+      set_error("guarantee_convergence needs a last schedule depth >= 2 (or = max_k), got %d", max_m);
+      return kInvalidArgument;
+    }
+    if (num_bins % 128) {
+      set_error("guarantee_convergence needs num_bins %% 128 == 0, got %d", num_bins);
+      return kUnsupported;
+    }
+    packed = 1 << log2_ceil((max_k + max_m - 2) / (max_m - 1));
+    if (cols + (int64_t)128 * num_bins >= (int64_t)1 << 31) {
+      set_error("cols must leave room for the packed columns in int32");
+      return kInvalidArgument;
+    }
+  }
+  if (rows == 0) return kOk;
   const int buf = bin_buf(max_m);
   if (buf > 16) { set_error("schedule depth %d exceeds this build's per-bin list of 16", max_m); return kUnsupported; }
   const size_t need = bin_ws(rows, num_bins, buf, num_steps);
@@ -777,6 +953,8 @@ static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t co
     memcpy(&rv, &u, 4);
   }
   a.replace_val = rv;
+  a.merge = merge ? 1 : 0;
+  a.num_packed = packed;
   a.out_vals = out_vals; a.out_idx = out_idx; a.out_valid = out_valid; a.out_depths = out_depths;
   a.out_cutoff = out_cutoff;
   char* w = (char*)workspace;
@@ -848,7 +1026,17 @@ static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t co
     st = launch_status("tallax_top_dynamic_k");
     if (st) return st;
   }
-  if (cand && rows <= kFinishNT)
+  if (merge) {
+    if (cand && rows <= kFinishNT) {  // the finish step was left to the select kernel
+      hipLaunchKernelGGL(binned_finish_kernel, dim3(1), dim3(kFinishNT), 0, stream, a);
+      st = launch_status("tallax_top_dynamic_k");
+      if (st) return st;
+    }
+    hipLaunchKernelGGL(binned_merge_kernel, dim3((unsigned)rows), dim3(kMergeNT), 0, stream, a);
+    st = launch_status("tallax_top_dynamic_k");
+    if (st) return st;
+  }
+  if (cand && rows <= kFinishNT && !merge)
     hipLaunchKernelGGL(binned_select_kernel<true>, dim3((unsigned)rows), dim3(kSelNT), 0, stream, a);
   else
     hipLaunchKernelGGL(binned_select_kernel<false>, dim3((unsigned)rows), dim3(kSelNT), 0, stream, a);

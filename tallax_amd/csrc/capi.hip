@@ -46,6 +46,6 @@ extern "C" {
 
 const char* tallax_last_error(void) { return tx::g_err; }
 
-int tallax_abi_version(void) { return 1; }
+int tallax_abi_version(void) { return 2; }
 
 }  // extern "C"

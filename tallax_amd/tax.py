@@ -79,8 +79,15 @@ def top_dynamic_k(logits: torch.Tensor, k, max_k: int, block_token: int = 8, num
         num_bins; the schedule (auto from the convergence theory if None)
         decides depths/cutoffs; the result is the top-128 of the first
         depth_upper ranks of every bin, ordered by value then lowest index.
-      * guarantee_convergence=True: (vals, idxs), the exact top-max_k (the
-        converged answer, ties to the lowest index, as tax.top_k).
+      * guarantee_convergence=True: (vals, idxs) of the same algorithm,
+        where a block of rows that has not converged after the last step
+        (when that step's depth m is not max_k) first goes through the
+        bin-packing merge (_merge_unconverged_bins_top_k, top_k.py:108-200):
+        the 2^ceil(log2(ceil(max_k / (m - 1)))) bins with the most entries
+        above the last pivot are packed whole and their top-128 replaces rank
+        0 of bins 0..127.  Like the reference, no max_k step is added to the
+        schedule; this needs m >= 2 and num_bins % 128 == 0 (ValueError /
+        NotImplementedError otherwise).  For the exact answer use tax.top_k.
     Positions >= k[row] hold replace_val (in the logits dtype) when given.
     Raises ValueError if rows % block_token != 0 and NotImplementedError for
     max_k > 128, like the reference.  `workspace` (keyword only): a uint8
@@ -115,22 +122,12 @@ def _top_dynamic_k(logits, k, max_k, block_token, num_bins, bins_topm_unroll, bi
     stream = _lib.stream_of(x)
     vals = torch.empty((rows, max_k), dtype=x.dtype, device=dev)
     idx = torch.empty((rows, max_k), dtype=torch.int32, device=dev)
-    if guarantee_convergence:
-        if max_k > cols:
-            raise ValueError(f"max_k={max_k} exceeds row length {cols}")
-        need = _lib.LIB.tallax_topk_workspace_size(rows, cols, max_k, dt)
-        ws = _lib.workspace_arg(workspace, dev, need)
-        if replace_val is None:
-            _lib.check(_lib.LIB.tallax_topk(x.data_ptr(), dt, rows, cols, max_k, vals.data_ptr(), idx.data_ptr(),
-                                            ws.data_ptr() if need else None, ws.numel() if need else 0, stream),
-                       "top_dynamic_k")
-        else:
-            _lib.check(_lib.LIB.tallax_topk_replace(x.data_ptr(), dt, rows, cols, max_k, kr.data_ptr(),
-                                                    float(replace_val), vals.data_ptr(), idx.data_ptr(),
-                                                    ws.data_ptr() if need else None, ws.numel() if need else 0,
-                                                    stream), "top_dynamic_k")
-        return vals, idx
     steps = sch.topm_schedule(max_k, num_bins, block_token, bins_topm_schedule)
+    if guarantee_convergence and steps[-1] != max_k:
+        if steps[-1] < 2:
+            raise ValueError(f"guarantee_convergence needs a last schedule depth >= 2 (or = max_k), got {steps[-1]}")
+        if num_bins % NUM_LANES:
+            raise NotImplementedError(f"guarantee_convergence needs num_bins % {NUM_LANES} == 0, got {num_bins}")
     import ctypes
     arr = (ctypes.c_int32 * len(steps))(*steps)
     need = _lib.LIB.tallax_top_dynamic_k_workspace_size(rows, num_bins, arr, len(steps))
@@ -139,13 +136,15 @@ def _top_dynamic_k(logits, k, max_k, block_token, num_bins, bins_topm_unroll, bi
     depths = torch.empty(rows, dtype=torch.int32, device=dev)
     cutoff = torch.empty(rows, dtype=torch.float32, device=dev)
     args = (x.data_ptr(), dt, rows, cols, kr.data_ptr(), max_k, block_token, num_bins, arr, len(steps),
-            int(replace_val is not None), float(replace_val) if replace_val is not None else 0.0, vals.data_ptr(),
+            int(bool(guarantee_convergence)), int(replace_val is not None), float(replace_val) if replace_val is not None else 0.0, vals.data_ptr(),
             idx.data_ptr(), valid.data_ptr(), depths.data_ptr(), cutoff.data_ptr(), ws.data_ptr(), ws.numel(),
             stream)
     if testing_path is None:
         _lib.check(_lib.LIB.tallax_top_dynamic_k(*args), "top_dynamic_k")
     else:
         _lib.check(_lib.LIB.tallax_testing_top_dynamic_k_path(*args, int(testing_path)), "top_dynamic_k")
+    if guarantee_convergence:
+        return vals, idx
     return vals, idx, valid.reshape(()).bool(), depths, cutoff
 
 

@@ -114,6 +114,6 @@ def test_noalloc_sampler_limit_without_gpu():
 def test_top_dynamic_k_path_hook_rejects_unknown_paths():
     from tallax_amd import _lib
     sched = (ctypes.c_int32 * 2)(3, 6)
-    st = _lib.LIB.tallax_testing_top_dynamic_k_path(1, 0, 8, 100, 1, 4, 8, 128, sched, 2, 0, 0.0, 1, 1, 1, 1, 1,
+    st = _lib.LIB.tallax_testing_top_dynamic_k_path(1, 0, 8, 100, 1, 4, 8, 128, sched, 2, 0, 0, 0.0, 1, 1, 1, 1, 1,
                                                     1, 1 << 20, None, 7)
     assert st == _lib.INVALID_ARGUMENT and b"path" in _lib.LIB.tallax_last_error()

@@ -1,6 +1,6 @@
-"""GPU parity: tax.top_dynamic_k (approximate, binned) and its exact
-guarantee_convergence=True form through the C ABI against the oracle on
-identical seeded inputs (bit-exact values, indices, valid, depths and
+"""GPU parity: tax.top_dynamic_k (binned, with and without
+guarantee_convergence's bin-packing merge) through the C ABI against the
+oracle on identical seeded inputs (bit-exact values, indices, valid, depths and
 cutoffs), with config 3's recall@50 of the approximate result against the
 exact one reported."""
 import numpy as np
@@ -154,7 +154,75 @@ def test_top_dynamic_k_many_rows_and_wide_blocks(gpu, binned_mode, rows, block_t
     _check(got, want)
 
 
-def test_top_dynamic_k_guaranteed_is_exact(gpu):
+def _merge_rows(rows, cols, num_bins, spike_rows, spike_bins, nspikes, seed, masked_rows=()):
+    """Untied Gaussian rows; rows in spike_rows get nspikes large distinct
+    values spread over the bins spike_bins, so that their blocks cannot
+    converge at a shallow depth and go through the bin-packing merge; rows in
+    masked_rows are -inf but for a few values, with three spikes in bin 3."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    per = cols // num_bins
+    for r in spike_rows:
+        for j, b in enumerate(spike_bins):
+            n = min(nspikes // len(spike_bins), per)
+            x[r, rng.choice(per, n, replace=False) * num_bins + b] = 40.0 + 10 * j + rng.random(n)
+    for r in masked_rows:
+        x[r] = -np.inf
+        x[r, rng.choice(cols, 12, replace=False)] = rng.standard_normal(12)
+        x[r, [3, 3 + num_bins, 3 + 2 * num_bins]] = [9.0, 8.0, 7.0]
+    return x
+
+
+@pytest.mark.parametrize("replace", [None, -1e12], ids=["no_replace", "replace"])
+@pytest.mark.parametrize("dtype,rows,cols,max_k,num_bins,block_token,schedule,spikes,masked", [
+    ("f32", 16, 3000, 32, 128, 8, (3, 6), ((5, 6), (0, 9), 32), ()),          # P = 8
+    ("bf16", 64, 50000, 128, 256, 8, (5, 9), ((3, 17, 40), (0, 1, 2, 3), 300), (41,)),  # the sampler's call, P = 16
+    ("bf16", 8, 700, 16, 256, 4, (2,), ((), (), 0), tuple(range(8))),          # packed slots past the row's end
+    ("f32", 32, 128256, 128, 128, 8, (2,), ((1, 9), (5,), 200), ()),           # P = num_bins: whole rows packed
+])
+def test_top_dynamic_k_merge_parity(gpu, binned_mode, replace, dtype, rows, cols, max_k, num_bins, block_token,
+                                    schedule, spikes, masked):
+    """guarantee_convergence=True with a last depth below max_k: blocks that
+    did not converge go through the bin-packing merge
+    (_merge_unconverged_bins_top_k, top_k.py:108-200), bit-exact against the
+    oracle, which is pinned by the tile-level literal restatement in
+    test_oracle.py.  With P == num_bins the merged rows are the exact top-k."""
+    from tallax_amd import tax
+    _log(f"top_dynamic_k merge {dtype} [{rows},{cols}] max_k={max_k} bins={num_bins} bt={block_token} "
+         f"sched={schedule} replace={replace} path={binned_mode}")
+    x = O.round_to_dtype(_merge_rows(rows, cols, num_bins, *spikes, rows + cols, masked), dtype)
+    rng = np.random.default_rng(cols + 1)
+    k = rng.integers(max_k // 2, max_k + 1, rows).astype(np.int32)
+    for r in spikes[0]:
+        k[r] = max_k
+    xd = to_dev(x, dtype, gpu)
+    gv, gi = tax._top_dynamic_k(xd, torch.from_numpy(k).to(gpu), max_k, block_token, num_bins, 32, schedule, True,
+                                replace, False, None, binned_mode)
+    torch.cuda.synchronize()
+    key = ("merge", dtype, replace, rows, cols, max_k, num_bins, block_token, schedule)
+    if key not in _ORACLE_CACHE:   # the same inputs run on both paths
+        conv = O.top_dynamic_k(x, k, max_k, block_token=block_token, num_bins=num_bins, schedule=schedule,
+                               dtype=dtype)
+        _ORACLE_CACHE[key] = (O.top_dynamic_k(x, k, max_k, block_token=block_token, num_bins=num_bins,
+                                              schedule=schedule, replace_val=replace, dtype=dtype,
+                                              guarantee_convergence=True), conv)
+    (wv, wi), conv = _ORACLE_CACHE[key]
+    unconv = np.repeat((conv[3].reshape(-1, block_token) == max_k).any(axis=1), block_token)
+    _log(f"rows in unconverged blocks: {int(unconv.sum())} of {rows}")
+    assert unconv.any()
+    assert np.array_equal(gi.cpu().numpy(), wi)
+    assert np.array_equal(bits(from_dev_vals(gv)), bits(wv))
+    if O.packed_bins(max_k, schedule[-1]) == num_bins and replace is None:
+        ev, ei = O.top_k(x, max_k, dtype)
+        assert np.array_equal(wi[unconv], ei[unconv])
+
+
+def test_top_dynamic_k_sampler_call_on_config4_is_exact(gpu):
+    """The reference sampler's top-k stage (sampling.py:283-290:
+    top_dynamic_k(max_k=128, guarantee_convergence=True, num_bins=256,
+    bins_topm_schedule=(5, 9), replace_val)) on config 4's logits: every
+    block converges, so the result is the exact top-k inside k[row], which is
+    what the fused sampler computes."""
     from tallax_amd import tax
     rng = np.random.default_rng(4)
     x = (rng.standard_normal((256, 128256)) * 3).astype(np.float32)
@@ -164,10 +232,13 @@ def test_top_dynamic_k_guaranteed_is_exact(gpu):
                                   guarantee_convergence=True, replace_val=-1e12)
     torch.cuda.synchronize()
     hv = O.round_to_dtype(x, "bf16")
+    wv, wi = O.top_dynamic_k(hv, k, 128, num_bins=256, schedule=(5, 9), replace_val=-1e12, dtype="bf16",
+                             guarantee_convergence=True)
+    assert np.array_equal(idx.cpu().numpy(), wi)
+    assert np.array_equal(bits(from_dev_vals(vals)), bits(wv))
     ev, ei = O.top_k(hv, 128, dtype="bf16")
-    ev = np.where(np.arange(128)[None, :] < k[:, None], ev, O.round_to_dtype(np.float32(-1e12), "bf16"))
-    assert np.array_equal(idx.cpu().numpy(), ei)
-    assert np.array_equal(bits(from_dev_vals(vals)), bits(ev))
+    inside = np.arange(128)[None, :] < k[:, None]
+    assert np.array_equal(np.where(inside, wi, -2), np.where(inside, ei, -2))
 
 
 def test_top_dynamic_k_errors(gpu):
@@ -177,6 +248,10 @@ def test_top_dynamic_k_errors(gpu):
         tax.top_dynamic_k(x, 4, 4, block_token=8)
     with pytest.raises(NotImplementedError):
         tax.top_dynamic_k(x[:8], 4, 129)
+    with pytest.raises(ValueError):
+        tax.top_dynamic_k(x[:8], 4, 8, bins_topm_schedule=(1,), guarantee_convergence=True)
+    with pytest.raises(NotImplementedError):
+        tax.top_dynamic_k(x[:8], 4, 8, num_bins=64, bins_topm_schedule=(2,), guarantee_convergence=True)
 
 
 def test_candidates_settle_config3_rows(gpu):
@@ -201,7 +276,7 @@ def test_candidates_settle_config3_rows(gpu):
     depths = torch.empty(rows, dtype=torch.int32, device=gpu)
     cutoff = torch.empty(rows, dtype=torch.float32, device=gpu)
     _lib.check(_lib.LIB.tallax_top_dynamic_k(
-        xd.data_ptr(), _lib.F32, rows, cols, k.data_ptr(), 50, 8, 128, arr, len(steps), 0, 0.0, vals.data_ptr(),
+        xd.data_ptr(), _lib.F32, rows, cols, k.data_ptr(), 50, 8, 128, arr, len(steps), 0, 0, 0.0, vals.data_ptr(),
         idx.data_ptr(), valid.data_ptr(), depths.data_ptr(), cutoff.data_ptr(), ws.data_ptr(), need,
         _lib.stream_of(xd)), "top_dynamic_k")
     torch.cuda.synchronize()

@@ -207,6 +207,34 @@ def test_topk_config3_spikes(gpu):
     assert np.array_equal(bits(vals.cpu().numpy()), bits(ov))
 
 
+@pytest.mark.parametrize("rows,cols,k,dtype", [(256, 128256, 128, "bf16"), (128, 151936, 50, "f32"),
+                                               (16, 5003, 77, "bf16")])
+def test_topk_replace_per_row_k(gpu, rows, cols, k, dtype):
+    """tallax_topk_replace through the C ABI: the exact top-k whose positions
+    >= k_rows[row] hold replace_val rounded to the input dtype
+    (top_k.py:365-369 on a converged run)."""
+    from tallax_amd import _lib
+    _log(f"topk_replace rows={rows} cols={cols} k={k} dtype={dtype}")
+    rng = np.random.default_rng(rows + cols)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    kr = rng.integers(0, k + 1, rows).astype(np.int32)
+    xd = to_dev(x, dtype, gpu)
+    krd = torch.from_numpy(kr).to(gpu)
+    vals = torch.empty((rows, k), dtype=xd.dtype, device=gpu)
+    idx = torch.empty((rows, k), dtype=torch.int32, device=gpu)
+    dt = _lib.dtype_code(xd)
+    need = _lib.LIB.tallax_topk_workspace_size(rows, cols, k, dt)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=gpu)
+    _lib.check(_lib.LIB.tallax_topk_replace(xd.data_ptr(), dt, rows, cols, k, krd.data_ptr(), -1e12,
+                                            vals.data_ptr(), idx.data_ptr(), ws.data_ptr(), ws.numel(),
+                                            _lib.stream_of(xd)), "topk_replace")
+    torch.cuda.synchronize()
+    ov, oi = O.top_k(host_values(x, dtype), k, dtype)
+    ov = np.where(np.arange(k)[None, :] < kr[:, None], ov, O.round_to_dtype(np.float32(-1e12), dtype))
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(bits(from_dev_vals(vals)), bits(ov))
+
+
 def test_topk_repeated_calls_reuse_workspace(gpu):
     from tallax_amd import tax
     rng = np.random.default_rng(5)

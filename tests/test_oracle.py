@@ -513,7 +513,8 @@ def test_top_dynamic_k_converged_rows_are_exact():
 _GARBAGE = 2 ** 31 - 1
 
 
-def _literal_dynamic_top_k(x, k, max_k, block_token, num_bins, schedule, replace_val=None, dtype="f32"):
+def _literal_dynamic_top_k(x, k, max_k, block_token, num_bins, schedule, replace_val=None, dtype="f32",
+                           guarantee_convergence=False):
     rows, vocab = x.shape
     lo = O.dtype_min(dtype)
     kk = np.broadcast_to(np.asarray(k, np.int64), (rows,))
@@ -561,6 +562,8 @@ def _literal_dynamic_top_k(x, k, max_k, block_token, num_bins, schedule, replace
                 cutoff[r] = pivot[i]
             if flag != block_token:
                 flag = 0
+        if guarantee_convergence and max_m != max_k and flag == 0:    # :317-331
+            _literal_merge(x[ts], sv, si, ts, num_bins, max_m, max_k, dtype)
     gts = sorted(set(2 ** O.log2_ceil(s - 1) if s > 1 else s for s in sched))
     gmax = int(depths.max())
     valid = bool(gmax < sched[-1] or sched[-1] == max_k)
@@ -570,7 +573,7 @@ def _literal_dynamic_top_k(x, k, max_k, block_token, num_bins, schedule, replace
             v = sv[:, :d_up * num_bins].astype(np.float64)
             i = si[:, :d_up * num_bins]
             order = np.lexsort((i, -v), axis=1)[:, :128]
-            ov = np.take_along_axis(sv[:, :d_up * num_bins], order, 1)
+            ov = O.round_to_dtype(np.take_along_axis(sv[:, :d_up * num_bins], order, 1), dtype)
             oi = np.take_along_axis(i, order, 1)
             if replace_val is not None:
                 rv = O.round_to_dtype(np.float32(replace_val), dtype)
@@ -578,6 +581,129 @@ def _literal_dynamic_top_k(x, k, max_k, block_token, num_bins, schedule, replace
             oi = np.where(oi == _GARBAGE, -1, oi).astype(np.int32)
             out = (ov[:, :max_k], oi[:, :max_k])
     return out, valid, depths, cutoff
+
+
+def _literal_merge(logits, sv, si, ts, num_bins, m, max_k, dtype):
+    """_merge_unconverged_bins_top_k (top_k.py:108-200) as written, on the
+    scratch rows ts: tile by tile, with local permutations, range masks and
+    the strided packing of slices into 128-lane tiles.  bitonic_topk_arrays
+    (an undefined name, :141) is read as bitonic_top_k_arrays: counts
+    descending, equal counts in bin order (the network's order is not
+    pinned); the final top-128 orders equal values by index.  Reads past the
+    row's end (the last tile of an offset) give finfo(dtype).min."""
+    vals, idxs = sv[ts].copy(), si[ts].copy()
+    bt, vocab = logits.shape
+    num_packed_bins = 2 ** O.log2_ceil(-(-max_k // (m - 1)))
+    pivot = vals[:, (m - 1) * num_bins:m * num_bins].max(-1, keepdims=True)
+    num_gt_k = np.zeros((bt, num_bins), np.int32)
+    for i in range(m - 1):
+        num_gt_k += (vals[:, i * num_bins:(i + 1) * num_bins] >= pivot).astype(np.int32)
+    bin_indices = np.broadcast_to(np.arange(num_bins, dtype=np.int32), (bt, num_bins))
+    srt = np.lexsort((bin_indices, -num_gt_k), axis=1)[:, :128]
+    sorted_bin_indices = np.take_along_axis(bin_indices, srt, 1)
+    packing_perm = np.take_along_axis(sorted_bin_indices,
+                                      np.broadcast_to(np.arange(128) % num_packed_bins, (bt, 128)), 1)
+    indicator = np.zeros((bt, num_bins), bool)
+    for i in range(num_packed_bins):
+        indicator |= bin_indices == packing_perm[:, i:i + 1]
+    vals = np.concatenate([np.where(indicator, np.finfo(np.float32).min, vals[:, i * num_bins:(i + 1) * num_bins])
+                           for i in range(vals.shape[1] // num_bins)], axis=1)
+    lo = O.dtype_min(dtype)
+    packed = [np.full((bt, 128), lo, np.float32)
+              for _ in range(-(-vocab // (128 * (num_bins // num_packed_bins))))]
+    xpad = np.full((bt, vocab + 128), lo, np.float32)
+    xpad[:, :vocab] = logits
+    lane = np.arange(128)[None, :]
+    for offset in range(0, num_bins, 128):
+        local_perm = (packing_perm - offset) % 128
+        in_range = (packing_perm >= offset) & (packing_perm < offset + 128)
+        tiles = [np.take_along_axis(xpad[:, st:st + 128], local_perm, 1) for st in range(offset, vocab, num_bins)]
+        for i in range(128 // num_packed_bins):
+            pack_mask = (lane >= i * num_packed_bins) & (lane < (i + 1) * num_packed_bins) & in_range
+            for j, v in enumerate(tiles[i::128 // num_packed_bins]):
+                packed[j] = np.where(pack_mask, v, packed[j])
+    packed = np.concatenate(packed, axis=1)
+    n = packed.shape[1]
+    packed_idxs = (np.arange(n)[None, :] // num_packed_bins) * num_bins + np.concatenate((packing_perm,) * (n // 128), 1)
+    val_input = np.concatenate([packed, vals[:, :128]], axis=1)
+    idx_input = np.concatenate([packed_idxs, idxs[:, :128]], axis=1)
+    order = np.lexsort((idx_input, -val_input.astype(np.float64)), axis=1)[:, :128]
+    vals[:, :128] = np.take_along_axis(val_input, order, 1)
+    idxs[:, :128] = np.take_along_axis(idx_input, order, 1)
+    sv[ts], si[ts] = vals, idxs
+
+
+def _merge_cases():
+    rng = np.random.default_rng(91)
+    x = (rng.standard_normal((16, 3000)) * 2).astype(np.float32)
+    for r in (5, 6):                       # block 0 cannot converge: 40 spikes in bin 0, 12 in bin 9
+        x[r, rng.choice(3000 // 128, 20, replace=False) * 128] = 50.0 + rng.random(20).astype(np.float32)
+        x[r, rng.choice(3000 // 128, 12, replace=False) * 128 + 9] = 40.0 + rng.random(12).astype(np.float32)
+    k = rng.integers(1, 33, 16).astype(np.int32)
+    k[5:7] = 32
+    yield "spiked bins, P = 8", "f32", x, k, 32, 8, 128, (3, 6)
+    y = np.full((8, 700), -np.inf, np.float32)
+    for r in range(8):                     # a few finite values; three spikes share bin 3
+        y[r, rng.choice(700, 6 + r, replace=False)] = rng.standard_normal(6 + r).astype(np.float32)
+        y[r, [3, 259, 515]] = [9.0, 8.0, 7.0]
+    y = O.round_to_dtype(y, "bf16")
+    yield "masked bf16 rows past the last slice, P = 16", "bf16", y, np.full(8, 16, np.int32), 16, 4, 256, (2,)
+    z = (rng.standard_normal((16, 2000))).astype(np.float32)
+    yield "P = num_bins", "f32", z, rng.integers(1, 129, 16).astype(np.int32), 128, 8, 128, (2,)
+
+
+@pytest.mark.parametrize("replace", [None, -1e12])
+@pytest.mark.parametrize("case", list(_merge_cases()), ids=lambda c: c[0] if isinstance(c, tuple) else str(c))
+def test_top_dynamic_k_merge_matches_literal_restatement(case, replace):
+    """guarantee_convergence=True: the oracle's closed-form packing (column
+    (e // P) * num_bins + chosen[e % P]) gives what the tile-level literal
+    restatement of _merge_unconverged_bins_top_k gives."""
+    _, dt, x, k, max_k, bt, nb, sched = case
+    (lv, li), _, _, _ = _literal_dynamic_top_k(x, k, max_k, bt, nb, sched, replace, dt, guarantee_convergence=True)
+    ov, oi = O.top_dynamic_k(x, k, max_k, block_token=bt, num_bins=nb, schedule=sched, replace_val=replace,
+                             dtype=dt, guarantee_convergence=True)
+    assert np.array_equal(oi, li)
+    assert np.array_equal(ov.view(np.uint32), lv.view(np.uint32))
+
+
+def test_top_dynamic_k_merge_reaches_its_paths():
+    """The merge cases exercise what they name: unconverged blocks whose
+    result the merge changes; outputs that come from packed slots past the
+    row's end (index >= cols, value finfo.min); and with P == num_bins every row of an unconverged block gets
+    the exact top-k (all bins packed: a closed form)."""
+    cases = {c[0]: c for c in _merge_cases()}
+    _, dt, x, k, max_k, bt, nb, sched = cases["spiked bins, P = 8"]
+    mv, mi = O.top_dynamic_k(x, k, max_k, block_token=bt, num_bins=nb, schedule=sched, guarantee_convergence=True)
+    pv, pi, valid, d, _ = O.top_dynamic_k(x, k, max_k, block_token=bt, num_bins=nb, schedule=sched)
+    assert not valid and d[5] == max_k and d[6] == max_k
+    assert (mi[:8] != pi[:8]).any(axis=1).sum() >= 2 and np.array_equal(mi[8:], pi[8:])
+    for r in (5, 6):   # every spike of bin 0, the bin the counts pick, is found; bin 9 keeps its top 6 (m)
+        spikes0 = set(np.flatnonzero((x[r] >= 50) & (np.arange(x.shape[1]) % nb == 0)))
+        spikes9 = set(np.flatnonzero((x[r] >= 40) & (x[r] < 50)))
+        assert len(spikes0) == 20 and spikes0 <= set(mi[r]) and not spikes0 <= set(pi[r])
+        assert len(spikes9 & set(mi[r])) == sched[-1]
+    _, dt, y, k, max_k, bt, nb, sched = cases["masked bf16 rows past the last slice, P = 16"]
+    mv, mi = O.top_dynamic_k(y, k, max_k, block_token=bt, num_bins=nb, schedule=sched, dtype=dt,
+                             guarantee_convergence=True)
+    past = mi >= y.shape[1]
+    assert past.any() and (mv[past] == O.dtype_min(dt)).all()
+    _, dt, z, k, max_k, bt, nb, sched = cases["P = num_bins"]
+    assert O.packed_bins(max_k, sched[-1]) == nb
+    mv, mi = O.top_dynamic_k(z, k, max_k, block_token=bt, num_bins=nb, schedule=sched, guarantee_convergence=True)
+    _, _, _, d, _ = O.top_dynamic_k(z, k, max_k, block_token=bt, num_bins=nb, schedule=sched)
+    ev, ei = O.top_k(z, max_k)
+    unconv = np.repeat((d.reshape(-1, bt) == max_k).any(axis=1), bt)
+    assert unconv.sum() >= bt
+    assert np.array_equal(mi[unconv], ei[unconv]) and np.array_equal(mv[unconv], ev[unconv])
+
+
+def test_top_dynamic_k_merge_errors():
+    x = np.zeros((8, 300), np.float32)
+    with pytest.raises(ValueError):
+        O.top_dynamic_k(x, 4, 8, schedule=(1,), guarantee_convergence=True)
+    with pytest.raises(NotImplementedError):
+        O.top_dynamic_k(x, 4, 8, num_bins=64, schedule=(2,), guarantee_convergence=True)
+    O.top_dynamic_k(x, 4, 8, num_bins=64, schedule=(2, 8), guarantee_convergence=True)   # last depth = max_k
 
 
 def _dyn_cases():
