@@ -73,6 +73,10 @@ struct PfArgs {
   int32_t* out_cutoff;
 };
 
+// s_barrier after this wave's LDS operations only: unlike __syncthreads it
+// does not wait for the wave's global stores to complete
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // exp(x - m) as 2^(x log2 e - m log2 e), mc = m log2 e (v_exp_f32)
 __device__ __forceinline__ float pf_exp(float x, float mc) {
   return __builtin_amdgcn_exp2f(__builtin_fmaf(x, 1.44269504088896341f, -mc));
@@ -571,7 +575,7 @@ void softmax_topk_kernel(PfArgs a) {
   // bucket's start plus the number of larger composites in its bucket.
   // Buckets larger than kPfRankMax (ties, near-ties) use the bitonic sort.
   bool ranked = false;
-  if (n <= a.cap && n <= a.cap2) {
+  if (n <= a.cap && n + 8 <= a.cap2) {  // + 8: the rank loop's reads run up to 7 records past a bucket
     const uint32_t lo = s_t0 >= 0x007FFFFFu ? s_t0 : 0x007FFFFFu;
     const uint32_t hi = select_key(__float_as_uint(M));
     const uint32_t range = hi > lo ? hi - lo : 0u;
@@ -619,7 +623,13 @@ void softmax_topk_kernel(PfArgs a) {
         const int s0 = b ? (int)bk[b - 1] : 0, e0 = (int)bk[b];
         if (s0 >= k) continue;
         int r = s0;
-        for (int j = s0; j < e0; ++j) r += pool2[j] > cc ? 1 : 0;
+        for (int j0 = s0; j0 < e0; j0 += 8) {  // 8 LDS reads in flight (the region holds n + 8 records)
+          uint64_t x[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) x[u] = pool2[j0 + u];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) r += (j0 + u < e0 && x[u] > cc) ? 1 : 0;
+        }
         if (r < k) pool[r] = cc;
       }
       __syncthreads();
@@ -686,7 +696,7 @@ void softmax_topk_kernel(PfArgs a) {
     a.out_probs[row * k + p] = pr;
     a.out_idx[row * k + p] = idx;
   }
-  __syncthreads();
+  lds_barrier();  // the stores stay in flight
   const int ntiles = (k + 127) / 128;
   float c[2] = {0.0f, 0.0f};
   const bool has_tile = w < ntiles;
@@ -721,7 +731,7 @@ void softmax_topk_kernel(PfArgs a) {
   }
   below = wave_sum_i(below);
   if (l == 0) redi[w] = below;
-  __syncthreads();
+  lds_barrier();
   if (t == 0) {
     int tot = 0;
     for (int i = 0; i < kPfNW; ++i) tot += redi[i];
