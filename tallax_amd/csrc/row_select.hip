@@ -987,6 +987,42 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge_kernel(SelArgs a) {
   finalize_row<DT, SAMPLE>(a, row, tree[0], sg, rp);
 }
 
+// Kernel B for top-k with k <= 64 (no sampler, no lists out): the first 64
+// entries of each segment's sorted list hold the segment's part of the row's
+// top-k, so the lists are merged as 64-entry runs (one entry per lane, half
+// the merge network of the 128-entry runs).
+template <int DT>
+__global__ __launch_bounds__(kMergeNT) void seg_merge64_kernel(SelArgs a) {
+  constexpr int NW = kMergeNT / kWave;
+  constexpr int PER = kMaxSeg / NW;  // lists per wave, at most
+  __shared__ uint64_t tree[NW][kWave];
+  __shared__ float sg[kRun];
+  const int64_t row = blockIdx.x;
+  const int w = threadIdx.x / kWave, l = lane_id();
+  const uint64_t* src = a.ws_lists + (size_t)row * a.nseg * kRun;
+  const RowParams rp = load_row_params<false>(a, row);
+  uint64_t b[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int sgi = w + i * NW;
+    b[i] = sgi < a.nseg ? src[sgi * kRun + l] : 0ull;
+  }
+  uint64_t acc = b[0];
+#pragma unroll
+  for (int i = 1; i < PER; ++i) {
+    if (w + i * NW < a.nseg) acc = wave_merge64_desc(acc, b[i]);
+  }
+#pragma unroll
+  for (int st = 1; st < NW; st <<= 1) {
+    if ((w & (2 * st - 1)) == st) tree[w][l] = acc;
+    __syncthreads();
+    if ((w & (2 * st - 1)) == 0) acc = wave_merge64_desc(acc, tree[w + st][l]);
+  }
+  if (w == 0) tree[0][l] = acc;
+  __syncthreads();
+  finalize_row<DT, false>(a, row, tree[0], sg, rp);  // reads the first k <= 64 entries
+}
+
 // ---------------------------------------------------------------------------
 // Kernel S (stream_select_kernel): a whole row per 1024-thread workgroup (16
 // waves, 4 per SIMD), V 16-byte vectors per thread, vector j of thread t at
@@ -1626,7 +1662,10 @@ static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const c
   }
   int st = launch_status(what);
   if (st || a.nseg == 1) return st;
-  hipLaunchKernelGGL((seg_merge_kernel<DT, SAMPLE>), dim3((unsigned)a.rows), dim3(kMergeNT), 0, s, a);
+  if (!SAMPLE && !a.lists_only && a.k <= kWave)
+    hipLaunchKernelGGL((seg_merge64_kernel<DT>), dim3((unsigned)a.rows), dim3(kMergeNT), 0, s, a);
+  else
+    hipLaunchKernelGGL((seg_merge_kernel<DT, SAMPLE>), dim3((unsigned)a.rows), dim3(kMergeNT), 0, s, a);
   return launch_status(what);
 }
 

@@ -112,4 +112,16 @@ __device__ __forceinline__ void wave_merge128_desc(C a[2], const C b[2]) {
   wave_bitonic_merge128_desc(a);
 }
 
+// The 64 largest of a u b (descending runs of 64, one entry per lane),
+// descending: max(a[i], b[63 - i]) is bitonic and holds them.
+template <typename C>
+__device__ __forceinline__ C wave_merge64_desc(C a, C b) {
+  const int l = lane_id();
+  const C rb = lane_rev_c(b);
+  C v = a > rb ? a : rb;
+#pragma unroll
+  for (int stride = kWave / 2; stride >= 1; stride >>= 1) v = cx(v, lane_xor_c(v, stride), (l & stride) == 0);
+  return v;
+}
+
 }  // namespace tx
