@@ -276,7 +276,7 @@ def _topk(torch, np, _lib, dev, s_handle, gen, nbuf, which):
     else:
         need = _lib.LIB.tallax_topk_workspace_size(rows, cols, k, _lib.F32)
         ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=dev)
-        w.kernel = _lib.select_plan(rows, cols, _lib.F32)["kernel"].replace("SAMPLE", "false")
+        w.kernel = _lib.select_plan(rows, cols, _lib.F32, k=k, sample=False)["kernel"].replace("SAMPLE", "false")
 
         def launch(i):
             x = bufs[i % len(bufs)]

@@ -174,8 +174,10 @@ def require_cuda(*ts: torch.Tensor) -> None:
             raise ValueError(f"operands on different devices: {devs}")
 
 
-def select_plan(rows: int, cols: int, dtype: int) -> dict:
-    """Work split of the selection kernels for a [rows, cols] input (host only)."""
+def select_plan(rows: int, cols: int, dtype: int, k: int = 128, sample: bool = True) -> dict:
+    """Work split of the selection kernels for a [rows, cols] input (host only).
+    Rows of several segments finish in seg_merge64_kernel for top-k with k <= 64
+    (no sampler), else in seg_merge_kernel."""
     out = (ctypes.c_int32 * 4)()
     check(LIB.tallax_testing_select_plan(rows, cols, dtype, out), "select_plan")
     nt, maxv, nseg, vps = list(out)
@@ -183,6 +185,7 @@ def select_plan(rows: int, cols: int, dtype: int) -> dict:
     if nt == 1024:
         name = f"stream_select_kernel<{dt}, {maxv}, SAMPLE>"
     else:
-        name = f"seg_select_kernel<{dt}, {maxv}, {nt}, SAMPLE>" + (" + seg_merge_kernel" if nseg > 1 else "")
+        merge = "seg_merge64_kernel" if (not sample and k <= 64) else "seg_merge_kernel"
+        name = f"seg_select_kernel<{dt}, {maxv}, {nt}, SAMPLE>" + (f" + {merge}" if nseg > 1 else "")
     return {"threads": nt, "vectors_per_thread": maxv, "segments": nseg, "vectors_per_segment": vps,
             "kernel": name}
