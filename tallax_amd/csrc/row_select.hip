@@ -1092,22 +1092,6 @@ __device__ __forceinline__ void wave_kth_and_max(uint32_t v, int k, uint32_t& kt
   top = T;
 }
 
-// Wave-wide exclusive prefix of v and the total: scans of the 16-lane rows
-// with DPP row shifts, then the row totals through readlane.
-__device__ __forceinline__ int wave_exscan_i32(int v, int& total) {
-  const int l = lane_id();
-  int x = v;
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
-  const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31);
-  const int r2 = __builtin_amdgcn_readlane(x, 47), r3 = __builtin_amdgcn_readlane(x, 63);
-  const int row = l >> 4;
-  const int before = (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
-  total = r0 + r1 + r2 + r3;
-  return before + x - v;
-}
 
 // Slots q < lo or q >= hi of a 16-byte vector of VEC elements become all-ones.
 template <int DT>

@@ -38,6 +38,17 @@
 //   the sampler tail with one candidate per thread.
 // The row is read two (bf16) to four (f32) times; the re-reads of a row just
 // streamed are served mostly from the caches.
+//
+// Rows of whole 16-byte vectors that fit 16 vectors per thread (bf16 up to
+// 131072 columns, f32 up to 65536) take a single read first: the vectors stay
+// in registers; each lane keeps its four largest vector maxima (integer max
+// over the raw bits, which orders non-negative values), each wave takes the
+// ceil(K / 16)-th largest of its 256 kept maxima, and L, the smallest of those
+// over the 16 waves, has at least K elements at or above it (each counted
+// maximum is a distinct vector).  When L is a positive value, every element
+// >= L goes to the list; with at most 2048 of them the sort below orders them
+// and its first K are the candidates.  Other rows (non-positive bound, NaN
+// maxima, more than 2048 elements >= L) take the radix select.
 #include <float.h>
 #include <math.h>
 #include <stdint.h>
@@ -57,6 +68,28 @@ constexpr int kSwMaxK = 1024;           // candidates per row, at most (one per 
 constexpr int kSwList = 2048;           // collected records, at most (two per thread in the sort)
 constexpr int kSwBins = 2048;           // 11-bit digits
 constexpr int kSwChunk = kSwNT * 8;     // columns per workgroup step: 8 per thread
+constexpr int kSwV = 16;                // register path: 16-byte vectors per thread
+
+typedef short sw_short2_t __attribute__((ext_vector_type(2)));
+
+// Largest element of a 16-byte vector in the signed integer view of its bits
+// (monotone over non-negative values; positive NaNs above +inf).
+template <int DT>
+__device__ __forceinline__ int32_t sw_vec_smax(uint4 v) {
+  if constexpr (DT == kBF16) {
+    auto mx = [](uint32_t a, uint32_t b) {
+      return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(sw_short2_t, a),
+                                                                    __builtin_bit_cast(sw_short2_t, b)));
+    };
+    const uint32_t m = mx(mx(v.x, v.y), mx(v.z, v.w));
+    const int32_t lo = (int16_t)(m & 0xFFFFu), hi = (int16_t)(m >> 16);
+    return lo > hi ? lo : hi;
+  } else {
+    const int32_t a = (int32_t)v.x > (int32_t)v.y ? (int32_t)v.x : (int32_t)v.y;
+    const int32_t b = (int32_t)v.z > (int32_t)v.w ? (int32_t)v.z : (int32_t)v.w;
+    return a > b ? a : b;
+  }
+}
 
 struct SwArgs {
   const void* x;
@@ -155,6 +188,8 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   constexpr int ES = DT == kBF16 ? 2 : 4;
   __shared__ int s_hist[kSwBins];
   __shared__ uint64_t s_list[kSwList];
+  __shared__ uint64_t s_list2[kSwList + 8];  // register path: the candidates in bucket order (+8: unguarded reads)
+  __shared__ int32_t s_wmax[kSwNW];
   __shared__ float s_v[kSwMaxK];
   __shared__ float s_e[kSwMaxK];
   __shared__ float s_tot[kSwMaxK / 8];
@@ -175,6 +210,190 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   const bool vec = a.vec != 0;
   const int nchunks = (int)((a.cols + kSwChunk - 1) / kSwChunk);
 
+  // --- register path: one read, the elements >= L -----------------------------
+  constexpr int VEC = DT == kBF16 ? 8 : 4;
+  constexpr int32_t kPosInf = DT == kBF16 ? 0x7F80 : 0x7F800000;  // +inf bits in the signed view
+  const int64_t nvec = a.cols / VEC;  // a.vec: the row is whole 16-byte vectors
+  bool fast = vec && nvec <= (int64_t)kSwNT * kSwV;  // block-uniform
+  if (fast) {
+    const uint4* vb = (const uint4*)rowp;
+    uint4 raw[kSwV];
+#pragma unroll
+    for (int j = 0; j < kSwV; ++j) {
+      const int64_t v = (int64_t)j * kSwNT + t;
+      raw[j] = v < nvec ? vb[v] : make_uint4(~0u, ~0u, ~0u, ~0u);  // all-ones: -1, below every bound
+    }
+    if (t == 0) s_cnt = 0;
+    // this lane's four largest vector maxima; a positive NaN maximum sends the row to the radix select
+    int32_t top[4] = {-1, -1, -1, -1};
+    bool nan_max = false;
+#pragma unroll
+    for (int j = 0; j < kSwV; ++j) {
+      int32_t x = sw_vec_smax<DT>(raw[j]);
+      nan_max |= x > kPosInf;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool sw = x > top[r];
+        const int32_t tv = top[r];
+        top[r] = sw ? x : tv;
+        x = sw ? tv : x;
+      }
+    }
+    // the wave's q-th largest kept maximum among the non-negative ones (-1 if fewer)
+    const int q = (K + kSwNW - 1) / kSwNW;
+    auto count_ge = [&](int32_t p) {
+      int c = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) c += (int)__popcll(__ballot(top[r] >= p));
+      return c;
+    };
+    int32_t wl = -1;
+    if (count_ge(1) >= q) {  // wave-uniform; a bound of +0 would need -0 too: positive bounds only
+      wl = 0;
+      constexpr int kBits = DT == kBF16 ? 15 : 31;
+#pragma unroll 1
+      for (int b = kBits - 1; b >= 0; --b) {
+        const int32_t probe = wl | (int32_t)(1u << b);
+        if (count_ge(probe) >= q) wl = probe;
+      }
+    }
+    int32_t wm = top[0];  // the wave's largest vector maximum (signed view)
+#pragma unroll
+    for (int d = kWave / 2; d >= 1; d >>= 1) {
+      const int32_t o = (int32_t)lane_xor((uint32_t)wm, d);
+      wm = o > wm ? o : wm;
+    }
+    if (l == 0) {
+      s_red[w] = wl;
+      s_wmax[w] = wm;
+    }
+    for (int i = t; i < kSwBins; i += kSwNT) s_hist[i] = 0;  // the bucket counts of the rank below
+    fast = !__syncthreads_or(nan_max);
+    int32_t L = s_red[0];
+#pragma unroll
+    for (int i = 1; i < kSwNW; ++i) L = s_red[i] < L ? s_red[i] : L;
+    fast = fast && L >= 1;
+    if (fast) {
+      const uint32_t span = (uint32_t)(kPosInf - L);  // L <= bits <= +inf
+      // pass mask of vector j (bit e: element e is >= L)
+      auto pass_mask = [&](const uint4 x) -> uint32_t {
+        const uint32_t d[4] = {x.x, x.y, x.z, x.w};
+        uint32_t m = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (DT == kBF16) {
+            m |= ((uint32_t)((int32_t)(int16_t)(d[i] & 0xFFFFu) - L) <= span ? 1u : 0u) << (2 * i);
+            m |= ((uint32_t)(((int32_t)d[i] >> 16) - L) <= span ? 1u : 0u) << (2 * i + 1);
+          } else {
+            m |= ((uint32_t)((int32_t)d[i] - L) <= span ? 1u : 0u) << i;
+          }
+        }
+        return m;
+      };
+      // one pool reservation per wave: the lane's count over its vectors, one
+      // wave scan, one atomic; then the writes
+      int c = 0;
+      uint32_t pm[kSwV / 4] = {0u, 0u, 0u, 0u};  // the masks, 8 bits per vector (VEC <= 8)
+#pragma unroll
+      for (int j = 0; j < kSwV; ++j) {
+        const uint32_t m = pass_mask(raw[j]);
+        pm[j >> 2] |= m << (8 * (j & 3));
+        c += __popc(m);
+      }
+      int wtot;
+      const int pre = wave_exscan_i32(c, wtot);
+      int base = 0;
+      if (l == 0 && wtot) base = atomicAdd(&s_cnt, wtot);
+      int pos = __builtin_amdgcn_readfirstlane(base) + pre;
+#pragma unroll
+      for (int j = 0; j < kSwV; ++j) {
+        uint32_t m = (pm[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+        if (!__ballot(m != 0u)) continue;  // wave-uniform
+        const uint4 x = raw[j];
+        const uint32_t d[4] = {x.x, x.y, x.z, x.w};
+        const uint32_t col0 = (uint32_t)(((int64_t)j * kSwNT + t) * VEC);
+        while (m) {
+          const int e = __builtin_ctz(m);
+          m &= m - 1u;
+          const uint32_t bits = DT == kBF16 ? ((e & 1) ? (d[e >> 1] & 0xFFFF0000u) : (d[e >> 1] << 16)) : d[e];
+          // every candidate is a positive finite value: its select key is bits | 2^31
+          if (pos < kSwList) s_list[pos] = make_comp(bits | 0x80000000u, col0 + (uint32_t)e);
+          ++pos;
+        }
+      }
+      __syncthreads();
+      fast = s_cnt <= kSwList;  // block-uniform; s_cnt >= K always
+    }
+    if (fast) {
+      // bucket rank of the n candidates (keys in [select_key(L), kmax]): one
+      // atomic per candidate for its bucket count and slot, a scan, a scatter
+      // in bucket order, then each candidate's place = its bucket's start +
+      // the larger composites in its bucket; places below K go to s_list.
+      const int n = s_cnt;
+      const uint32_t lkey = select_key(DT == kBF16 ? (uint32_t)L << 16 : (uint32_t)L);
+      int32_t kms = s_wmax[0];
+#pragma unroll
+      for (int i = 1; i < kSwNW; ++i) kms = s_wmax[i] > kms ? s_wmax[i] : kms;
+      const uint32_t kmax = select_key(DT == kBF16 ? (uint32_t)kms << 16 : (uint32_t)kms);  // the row's largest key
+      uint64_t c2[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) c2[r] = t + r * kSwNT < n ? s_list[t + r * kSwNT] : 0ull;
+      // buckets: key buckets of width 2^kshift (largest keys first); where a
+      // key bucket holds one key (bf16 keys step by 2^16), nsub column
+      // ranges within it (lowest columns first), so that ties spread out
+      const uint32_t range = kmax - lkey;  // every candidate key lies in [lkey, kmax]
+      int kshift = DT == kBF16 ? 16 : 0;
+      while ((range >> kshift) >= (uint32_t)kSwBins) ++kshift;
+      const int nkb = (int)(range >> kshift) + 1;
+      int nsub = 1;
+      if (kshift == (DT == kBF16 ? 16 : 0))
+        while (nkb * nsub * 2 <= kSwBins) nsub *= 2;
+      int cbits = 0;
+      while (((int64_t)1 << cbits) < a.cols) ++cbits;
+      int lsub = 0;
+      while ((1 << lsub) < nsub) ++lsub;
+      const int csh = cbits > lsub ? cbits - lsub : 0;
+      int bk[2], slot[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int i = t + r * kSwNT;
+        bk[r] = i < n ? (int)((kmax - comp_key(c2[r])) >> kshift) * nsub + (comp_idx(c2[r]) >> csh) : 0;
+        slot[r] = i < n ? atomicAdd(&s_hist[bk[r]], 1) : 0;
+      }
+      __syncthreads();
+      {  // exclusive scan: thread t owns buckets 2t, 2t + 1
+        const int h0 = s_hist[2 * t], h1 = s_hist[2 * t + 1];
+        int total;
+        const int before = block_exscan<kSwNW>(h0 + h1, s_red, total);
+        s_hist[2 * t] = before;
+        s_hist[2 * t + 1] = before + h0;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        if (t + r * kSwNT < n) s_list2[s_hist[bk[r]] + slot[r]] = c2[r];
+      __syncthreads();
+      const int nb = nkb * nsub;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        if (t + r * kSwNT >= n) continue;
+        const int st0 = s_hist[bk[r]];
+        if (st0 >= K) continue;  // buckets that start at or past place K are not needed
+        const int en0 = bk[r] + 1 < nb ? s_hist[bk[r] + 1] : n;
+        int rk = st0;
+        for (int i0 = st0; i0 < en0; i0 += 8) {  // 8 LDS reads in flight (the buffer is padded)
+          uint64_t x[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) x[u] = s_list2[i0 + u];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) rk += (i0 + u < en0 && x[u] > c2[r]) ? 1 : 0;
+        }
+        if (rk < K) s_list[rk] = c2[r];
+      }
+      __syncthreads();
+    }
+  }
+
   // --- radix select of the K-th largest key ---------------------------------
   int need = K;          // elements still to take at or below the prefix
   uint32_t prefix = 0;   // digits found so far
@@ -182,7 +401,7 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   bool take_all = false; // the crossing bin is taken whole
   constexpr int kPasses = DT == kBF16 ? 2 : 3;
 #pragma unroll 1
-  for (int ps = 0; ps < kPasses; ++ps) {
+  for (int ps = 0; ps < (fast ? 0 : kPasses); ++ps) {
     const int bits = ps == 2 ? 10 : 11;
     const int dsh = ps == 0 ? 21 : ps == 1 ? 10 : 0;
     for (int i = t; i < kSwBins; i += kSwNT) s_hist[i] = 0;
@@ -205,11 +424,11 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   }
 
   // --- collect exactly K elements into LDS ------------------------------------
-  if (t == 0) s_cnt = 0;
+  if (!fast && t == 0) s_cnt = 0;
   __syncthreads();
   int tie_base = 0;  // threshold ties met so far in index order
 #pragma unroll 1
-  for (int j = 0; j < nchunks; ++j) {
+  for (int j = 0; j < (fast ? 0 : nchunks); ++j) {
     const int64_t base = ((int64_t)j * kSwNT + t) * 8;
     uint32_t k[8];
     const uint32_t m = sw_load8<DT>(rowp, a.cols, base, vec, k);
@@ -242,16 +461,18 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   }
   __syncthreads();
 
-  // --- sort the K candidates, descending ---------------------------------------
-  const int ncol = min(s_cnt, kSwList);  // K, or more when a tie bin was taken whole
-  uint64_t pair[2];
+  // --- sort the K candidates, descending (the register path ranked them) -----
+  if (!fast) {
+    const int ncol = min(s_cnt, kSwList);  // K, or more when a tie bin was taken whole
+    uint64_t pair[2];
 #pragma unroll
-  for (int r = 0; r < 2; ++r) pair[r] = 2 * t + r < ncol ? s_list[2 * t + r] : 0ull;
-  __syncthreads();
-  block_bitonic_sort_c<uint64_t, 2, kSwList, true>(pair, s_list);
+    for (int r = 0; r < 2; ++r) pair[r] = 2 * t + r < ncol ? s_list[2 * t + r] : 0ull;
+    __syncthreads();
+    block_bitonic_sort_c<uint64_t, 2, kSwList, true>(pair, s_list);
 #pragma unroll
-  for (int r = 0; r < 2; ++r) s_list[2 * t + r] = pair[r];
-  __syncthreads();
+    for (int r = 0; r < 2; ++r) s_list[2 * t + r] = pair[r];
+    __syncthreads();
+  }
   uint64_t rec[1];
   rec[0] = s_list[t];
 
@@ -273,13 +494,22 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   s_e[t] = e;
   int W = 128;
   while (W < K) W <<= 1;
-  for (int h = W / 2; h >= kWave; h >>= 1) {
-    __syncthreads();
-    if (t < h) s_e[t] = s_e[t] + s_e[t + h];
-  }
   __syncthreads();
   if (t < kWave) {
-    float s = s_e[t];
+    // the stride-halving tree over the W slots (slot = slot + slot[+h] for
+    // h = W/2 .. 64), slot t + 64 k held in register k of lane t, then the wave
+    constexpr int KR = kSwMaxK / kWave;
+    float v[KR];
+#pragma unroll
+    for (int k = 0; k < KR; ++k) v[k] = k * kWave < W ? s_e[t + k * kWave] : 0.0f;
+#pragma unroll
+    for (int hk = KR / 2; hk >= 1; hk >>= 1) {
+      if (hk * kWave < W) {  // uniform
+#pragma unroll
+        for (int k = 0; k < hk; ++k) v[k] = v[k] + v[k + hk];
+      }
+    }
+    float s = v[0];
 #pragma unroll
     for (int d = kWave / 2; d >= 1; d >>= 1) s = s + lane_xor_f(s, d);
     if (t == 0) s_sum = s;
@@ -295,12 +525,24 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   const int ntiles = (K + 7) >> 3;
   if ((t & 7) == 7) s_tot[g] = c;
   __syncthreads();
-  if (t == 0) {
-    float run = s_tot[0];
-    for (int i = 1; i < ntiles; ++i) {
-      s_carry[i] = run;
-      run = run + s_tot[i];
+  if (t < kWave) {
+    // the tile totals (two per lane) are read out first, then summed in
+    // tile order: carry_g = t_0 + ... + t_{g-1}, one add after the other
+    float tt[2], cy[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) tt[h] = h * kWave + l < ntiles ? s_tot[h * kWave + l] : 0.0f;
+    float run = readlane_f(tt[0], 0);
+#pragma unroll
+    for (int i = 1; i < kSwMaxK / 8; ++i) {  // constant lanes; only the adds depend on each other
+      if (i < ntiles) {  // uniform
+        const int h = i >> 6, ln = i & (kWave - 1);
+        cy[h] = l == ln ? run : cy[h];
+        run = run + readlane_f(tt[h], ln);
+      }
     }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      if (h * kWave + l < ntiles) s_carry[h * kWave + l] = cy[h];
   }
   __syncthreads();
   if (in && g != 0) c = c + s_carry[g];

@@ -105,9 +105,7 @@ __device__ __forceinline__ int pf_crossing_bin(const uint32_t* h, uint32_t need,
   const int l = lane_id();
   const uint4 hv = ((const uint4*)h)[l];  // bins 4l .. 4l + 3
   const uint32_t hs[4] = {hv.x, hv.y, hv.z, hv.w};
-  uint32_t incl = hv.x + hv.y + hv.z + hv.w;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+  const uint32_t incl = wave_incl_scan(hv.x + hv.y + hv.z + hv.w);
   uint32_t suf = (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1) - incl;  // bins of higher lanes
   int cnt = 0;
 #pragma unroll
@@ -481,9 +479,7 @@ void softmax_topk_kernel(PfArgs a) {
     uint32_t mine = 0;  // bit j: group t + j * kPfNT
     for (int g = t, j = 0; g < ngroups; g += kPfNT, ++j) mine |= (summ[g] >= q0 ? 1u : 0u) << j;
     const int c = __popc(mine);
-    int incl = c;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+    const int incl = wave_incl_scan(c);
     if (l == kWave - 1) redi[w] = incl;
     __syncthreads();
     int off = incl - c, nlist = 0;
@@ -524,9 +520,7 @@ void softmax_topk_kernel(PfArgs a) {
         for (int i = 0; i < 4; ++i) cm |= (((live >> i) & 1u) && __uint_as_float(d[i]) >= t0f ? 1u : 0u) << (4 * j + i);
       }
       const int c = __popc(cm);
-      int incl = c;
-#pragma unroll
-      for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+      const int incl = wave_incl_scan(c);
       const int wtot = __builtin_amdgcn_readlane(incl, kWave - 1);
       if (wtot) {
         int base = 0;
@@ -592,9 +586,8 @@ void softmax_topk_kernel(PfArgs a) {
     __syncthreads();
     // exclusive scan of the bucket counts, and the largest count
     const int c = t < kPfBuckets ? (int)bk[t] : 0;
-    int incl = c, mx = c;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+    const int incl = wave_incl_scan(c);
+    int mx = c;
 #pragma unroll
     for (int d = kWave / 2; d >= 1; d >>= 1) mx = max(mx, (int)lane_xor((uint32_t)mx, d));
     if (l == kWave - 1) {

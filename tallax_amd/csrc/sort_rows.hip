@@ -181,9 +181,7 @@ __global__ __launch_bounds__(kRadixNT) void radix_sort_rows_kernel(SortArgs a) {
       x[j] = run;
       run += c;
     }
-    uint32_t incl = run;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+    const uint32_t incl = wave_incl_scan(run);
     if (l == kWave - 1) wsum[w] = incl;
     __syncthreads();
     uint32_t pre = incl - run, tot = 0u;

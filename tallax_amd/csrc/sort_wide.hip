@@ -160,9 +160,7 @@ __global__ __launch_bounds__(kChunkNT) void sort_chunks_kernel(SortArgs a, int n
       x[j] = run;
       run += cj;
     }
-    uint32_t incl = run;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+    const uint32_t incl = wave_incl_scan(run);
     if (l == kWave - 1) wsum[w] = incl;
     __syncthreads();
     uint32_t pre = incl - run, tot = 0u;

@@ -14,6 +14,30 @@ __device__ __forceinline__ T shfl_up_or_zero(T v, int s, int l) {
   return src < 0 ? (T)0 : __builtin_bit_cast(T, x);
 }
 
+// Inclusive prefix sum of an integer over the wave's 64 lanes: DPP row
+// shifts (1, 2, 4, 8) inside each 16-lane row, then the totals of the rows
+// below added through readlane -- VALU lane exchanges, no LDS crossbar trip.
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  int x = (int)v;
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1 (0 at the row's start)
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(x, 15), r1 = __builtin_amdgcn_readlane(x, 31);
+  const int r2 = __builtin_amdgcn_readlane(x, 47);
+  const int row = lane_id() >> 4;
+  x += (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+  return (T)x;
+}
+
+// Exclusive prefix of v over the wave and the wave's total.
+__device__ __forceinline__ int wave_exscan_i32(int v, int& total) {
+  const int incl = wave_incl_scan(v);
+  total = __builtin_amdgcn_readlane(incl, kWave - 1);
+  return incl - v;
+}
+
 template <typename T>
 __device__ __forceinline__ T add_in_order(T a, T b) {
 #pragma clang fp contract(off)
@@ -29,9 +53,7 @@ __device__ __forceinline__ int32_t add_in_order<int32_t>(int32_t a, int32_t b) {
 template <int NW>
 __device__ __forceinline__ int block_exscan(int v, int* red, int& total) {
   const int l = lane_id(), w = threadIdx.x / kWave;
-  int incl = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) incl += shfl_up_or_zero(incl, d, l);
+  const int incl = wave_incl_scan(v);
   __syncthreads();
   if (l == kWave - 1) red[w] = incl;
   __syncthreads();
