@@ -183,7 +183,9 @@ def select_plan(rows: int, cols: int, dtype: int, k: int = 128, sample: bool = T
     nt, maxv, nseg, vps = list(out)
     dt = {F32: 0, BF16: 1}[dtype]
     if nt == 1024:
-        name = f"stream_select_kernel<{dt}, {maxv}, SAMPLE>"
+        # EDGE: rows not a whole number of 16-byte vectors (a 16-byte aligned base assumed)
+        edge = "true" if (cols * (4 if dtype == F32 else 2)) % 16 else "false"
+        name = f"stream_select_kernel<{dt}, {maxv}, SAMPLE, {edge}>"
     else:
         merge = "seg_merge64_kernel" if (not sample and k <= 64) else "seg_merge_kernel"
         name = f"seg_select_kernel<{dt}, {maxv}, {nt}, SAMPLE>" + (f" + {merge}" if nseg > 1 else "")

@@ -1076,20 +1076,33 @@ __device__ __forceinline__ uint64_t lanes_below() {
 }
 
 // The k-th largest (kth) and the largest (top) of the wave's 64 values
-// (k >= 1), by radix searches over the bits with one ballot per bit and
-// search: the largest K with #(v >= K) >= k.
+// (1 <= k <= 64, values below 2^BITS).  top and the smallest value come from
+// lane-exchange reductions; kth lies between them, so it has the bits above
+// the highest bit in which they differ, and the radix search (one ballot
+// per bit: the largest K with #(v >= K) >= k) runs over the bits below.
 template <int BITS>
 __device__ __forceinline__ void wave_kth_and_max(uint32_t v, int k, uint32_t& kth, uint32_t& top) {
-  uint32_t K = 0, T = 0;
+  uint32_t mx = v, mn = v;
 #pragma unroll
-  for (int b = BITS - 1; b >= 0; --b) {
-    const uint32_t pk = K | (1u << b), pt = T | (1u << b);
-    const uint64_t mk = __ballot(v >= pk), mt = __ballot(v >= pt);
-    K = __popcll(mk) >= k ? pk : K;
-    T = mt ? pt : T;
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t a = lane_xor(mx, d), b = lane_xor(mn, d);
+    mx = a > mx ? a : mx;
+    mn = b < mn ? b : mn;
+  }
+  mx = readlane_u32(mx, 0);
+  mn = readlane_u32(mn, 0);
+  const uint32_t diff = mx ^ mn;
+  uint32_t K = mx;
+  if (diff) {
+    const int hb = 31 - __builtin_clz(diff);
+    K = mx & ~((2u << hb) - 1u);  // every value is >= K
+    for (int b = hb; b >= 0; --b) {
+      const uint32_t pk = K | (1u << b);
+      K = __popcll(__ballot(v >= pk)) >= k ? pk : K;
+    }
   }
   kth = K;
-  top = T;
+  top = mx;
 }
 
 
@@ -1248,7 +1261,7 @@ __device__ __forceinline__ void fill_ineligible(const uint4* row_base, int nv, i
   for (int i = base + tid; i < kMaxK; i += kNTS) list[i] = 0ull;
 }
 
-template <int DT, int V, bool SAMPLE>
+template <int DT, int V, bool SAMPLE, bool EDGE>
 __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   using T = ElemT<DT>;
   constexpr int VEC = T::VEC, ES = T::ES, NW = kNTS / kWave;
@@ -1272,7 +1285,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   const RowParams rp = load_row_params<SAMPLE>(a, row);
 
   // ---- 1. every load up front (global loads: flat loads would also count
-  // against the LDS counter), vector maxima as the data arrives
+  // against the LDS counter)
   uint4 raw[V];
   {
     const GlobalVec gb = (GlobalVec)rv.base;
@@ -1289,16 +1302,20 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     ss.ovf = 0;
   }
   for (int i = tid; i < kBuckets; i += kNTS) ss.hist[i] = 0;
-  {
-    // the row's first vector (misaligned start) and last one (partial end):
-    // dead slots become all-ones, under block-uniform conditions and with
-    // selects of values only (a store guarded per vector would be merged into
-    // a store at a variable index, which would move raw[] to scratch memory)
+  // The row's first vector (misaligned start, thread 0, j = 0) and last one
+  // (partial end) hold slots outside the row, only when EDGE (the host
+  // launches the EDGE = false kernel when every row starts 16-byte aligned
+  // and cols is a multiple of the vector width).  Their outside slots become
+  // all-ones, under block-uniform conditions and with selects of values
+  // only (a store guarded per vector would be merged into a store at a
+  // variable index, which would move raw[] to scratch memory).  One thread
+  // may own both, as different vectors.
+  if (EDGE) {
     const int tail_live = cols + rv.mis - (nv - 1) * VEC;  // live slots of the last vector, 1..VEC
     if (rv.mis > 0 || tail_live < VEC) {
-      int tj = -1, lo = 0, hi = VEC;
+      int hj = -1, tj = -1, lo = 0, hi = VEC;
       if (tid == 0 && rv.mis > 0) {
-        tj = 0;
+        hj = 0;
         lo = rv.mis;
       }
       if (tid == (nv - 1) % kNTS && tail_live < VEC) {
@@ -1306,103 +1323,37 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
         hi = tail_live;
       }
       // the empty asm keeps the masks derived from these values in this block
-      asm volatile("" : "+v"(tj), "+v"(lo), "+v"(hi));
+      asm volatile("" : "+v"(hj), "+v"(tj), "+v"(lo), "+v"(hi));
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         const uint4 x = raw[j];
-        const uint4 y = kill_slots<DT>(x, lo, hi);
-        const bool t = tj == j;
+        const uint4 y = kill_slots<DT>(x, hj == j ? lo : 0, tj == j ? hi : VEC);
+        const bool t = hj == j || tj == j;
         raw[j] = make_uint4(t ? y.x : x.x, t ? y.y : x.y, t ? y.z : x.z, t ? y.w : x.w);
       }
     }
   }
-  int32_t vmax[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) vmax[j] = vec_smax<DT>(raw[j]);
 
-  // ---- 2. the bound L and the row maximum M (canonical keys)
-  int32_t smax = vmax[0];
-#pragma unroll
-  for (int j = 1; j < V; ++j) smax = imax32(smax, vmax[j]);
-  bool ord_view = false;  // some thread's maximum needs the ordered view
-  uint32_t tk;
-  if (smax >= 0 && smax <= kPosInf) {
-    tk = (uint32_t)smax | kZeroKey;
-  } else {
-    int32_t omax = kBF ? -32768 : (int32_t)0x80000000u;
-#pragma unroll
-    for (int j = 0; j < V; ++j) omax = imax32(omax, vec_omax<DT>(raw[j]));
-    if (omax <= kPosInf) {
-      tk = omax < kOrdNegInf ? 0u : (omax == -1 ? kZeroKey : (uint32_t)omax + kZeroKey);
-    } else {  // a positive NaN: canonical maximum element by element
-      tk = 0;
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-#pragma unroll
-        for (int q = 0; q < VEC; ++q) {
-          const uint32_t kk = Sel<DT, true>::canon(elem_bits<DT>(raw[j], q));
-          tk = kk > tk ? kk : tk;
+  // staging: vectors j with flag f go to the wave's own LDS region, one per
+  // slot in lane order; wcnt counts them (past kStageCap: ovf)
+  int wcnt = 0;
+  auto stage_if = [&](int j, bool f) {
+    const uint64_t m = __ballot(f);
+    if (m) {
+      if (f) {
+        const int o = wcnt + (int)__popcll(m & lanes_below());
+        if (o < kStageCap) {
+          ss.vst[w][o] = raw[j];
+          ss.vsi[w][o] = (uint32_t)((j * kNTS + tid) * VEC - rv.mis);
         }
       }
+      wcnt += (int)__popcll(m);
     }
-  }
-  {
-    uint32_t wl, wm;
-    wave_kth_and_max<KB>(tk, kMaxK / NW, wl, wm);
-    if (l == 0) {
-      ss.wl[w] = wl;
-      ss.wm[w] = wm;
-    }
-  }
-  __syncthreads();
-  uint32_t L = ss.wl[0], M = ss.wm[0];
-#pragma unroll
-  for (int i = 1; i < NW; ++i) {
-    L = ss.wl[i] < L ? ss.wl[i] : L;
-    M = ss.wm[i] > M ? ss.wm[i] : M;
-  }
-  const uint32_t thr = L > kFloor ? L : kFloor;
-
-  // ---- 3. stage the vectors that may hold a candidate, then the candidates
-  uint32_t pab = 0, pc = 0;  // rows with thr at the floor: the vectors holding ineligible classes
-  {
-    const bool pos_thr = thr > kZeroKey;
-    const int32_t st = (int32_t)(thr - kZeroKey);                       // bits, positive threshold
-    const int32_t ot = thr == kZeroKey ? -1 : (int32_t)(thr - kZeroKey);  // ordered view otherwise
-    int wcnt = 0;
-    auto stage_if = [&](int j, bool f) {
-      const uint64_t m = __ballot(f);
-      if (m) {
-        if (f) {
-          const int o = wcnt + (int)__popcll(m & lanes_below());
-          if (o < kStageCap) {
-            ss.vst[w][o] = raw[j];
-            ss.vsi[w][o] = (uint32_t)((j * kNTS + tid) * VEC - rv.mis);
-          }
-        }
-        wcnt += (int)__popcll(m);
-      }
-    };
-    if (pos_thr) {  // block-uniform: the signed-view maxima decide
-#pragma unroll
-      for (int j = 0; j < V; ++j) stage_if(j, vmax[j] >= st);
-    } else {
-#pragma unroll
-      for (int j = 0; j < V; ++j) stage_if(j, vec_omax<DT>(raw[j]) >= ot);
-      if (thr == kFloor) {  // block-uniform: the row may hold fewer than 128 eligible elements
-        // vectors that hold finfo.min, and those that may hold -inf (cheap
-        // packed tests; NaNs are not tracked: every vector may hold one)
-#pragma unroll
-        for (int j = 0; j < V; ++j) {
-          const uint32_t o = min_offset_from_min<DT>(raw[j]);
-          pab |= (o == 0u ? 1u : 0u) << j;
-          pab |= (o <= 1u ? 1u : 0u) << (16 + j);
-        }
-        pc = (1u << V) - 1u;
-      }
-    }
+  };
+  // the wave's staged vectors, one per lane: elements with key >= thr are
+  // appended to the candidates
+  auto extract = [&](uint32_t thr) {
     if (l == 0 && wcnt > kStageCap) ss.ovf = 1;
-    // the wave's own region: one staged vector per lane
     const int nst = wcnt < kStageCap ? wcnt : kStageCap;
     for (int r0 = 0; r0 < nst; r0 += kWave) {  // wave-uniform
       const int o = r0 + l;
@@ -1428,6 +1379,81 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
         }
       }
     }
+  };
+
+  uint32_t thr, M;
+  uint32_t pab = 0, pc = 0;  // rows with thr at the floor: the vectors holding ineligible classes
+  {
+    int32_t vmax[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) vmax[j] = vec_smax<DT>(raw[j]);
+
+    // ---- 2. the bound L and the row maximum M (canonical keys)
+    int32_t smax = vmax[0];
+#pragma unroll
+    for (int j = 1; j < V; ++j) smax = imax32(smax, vmax[j]);
+    uint32_t tk;
+    if (smax >= 0 && smax <= kPosInf) {
+      tk = (uint32_t)smax | kZeroKey;
+    } else {
+      int32_t omax = kBF ? -32768 : (int32_t)0x80000000u;
+#pragma unroll
+      for (int j = 0; j < V; ++j) omax = imax32(omax, vec_omax<DT>(raw[j]));
+      if (omax <= kPosInf) {
+        tk = omax < kOrdNegInf ? 0u : (omax == -1 ? kZeroKey : (uint32_t)omax + kZeroKey);
+      } else {  // a positive NaN: canonical maximum element by element
+        tk = 0;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) {
+            const uint32_t kk = Sel<DT, true>::canon(elem_bits<DT>(raw[j], q));
+            tk = kk > tk ? kk : tk;
+          }
+        }
+      }
+    }
+    {
+      uint32_t wl, wm;
+      wave_kth_and_max<KB>(tk, kMaxK / NW, wl, wm);
+      if (l == 0) {
+        ss.wl[w] = wl;
+        ss.wm[w] = wm;
+      }
+    }
+    __syncthreads();
+    uint32_t L = ss.wl[0];
+    M = ss.wm[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) {
+      L = ss.wl[i] < L ? ss.wl[i] : L;
+      M = ss.wm[i] > M ? ss.wm[i] : M;
+    }
+    thr = L > kFloor ? L : kFloor;
+
+    // ---- 3. stage the vectors that may hold a candidate, then the candidates
+    const bool pos_thr = thr > kZeroKey;
+    const int32_t st = (int32_t)(thr - kZeroKey);                       // bits, positive threshold
+    const int32_t ot = thr == kZeroKey ? -1 : (int32_t)(thr - kZeroKey);  // ordered view otherwise
+    if (pos_thr) {  // block-uniform: the signed-view maxima decide
+#pragma unroll
+      for (int j = 0; j < V; ++j) stage_if(j, vmax[j] >= st);
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) stage_if(j, vec_omax<DT>(raw[j]) >= ot);
+      if (thr == kFloor) {  // block-uniform: the row may hold fewer than 128 eligible elements
+        // vectors that hold finfo.min, and those that may hold -inf (cheap
+        // packed tests; NaNs are not tracked: every vector may hold one)
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const uint32_t o = min_offset_from_min<DT>(raw[j]);
+          pab |= (o == 0u ? 1u : 0u) << j;
+          pab |= (o <= 1u ? 1u : 0u) << (16 + j);
+        }
+        pc = (1u << V) - 1u;
+      }
+    }
+    extract(thr);
   }
   __syncthreads();
   const int n = ss.ncand;
@@ -1632,12 +1658,20 @@ static void launch_a(const SelArgs& a, hipStream_t s) {
 template <int DT, bool SAMPLE>
 static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const char* what) {
   if (p.nt == kNTS) {
-    if (p.maxv == 16)
-      hipLaunchKernelGGL((stream_select_kernel<DT, 16, SAMPLE>), dim3((unsigned)a.rows), dim3(kNTS), 0, s, a);
-    else if (p.maxv == 8)
-      hipLaunchKernelGGL((stream_select_kernel<DT, 8, SAMPLE>), dim3((unsigned)a.rows), dim3(kNTS), 0, s, a);
-    else
-      hipLaunchKernelGGL((stream_select_kernel<DT, 4, SAMPLE>), dim3((unsigned)a.rows), dim3(kNTS), 0, s, a);
+    // rows that start 16-byte aligned and fill their last vector have no
+    // slots outside the row: the kernel without the edge handling
+    const bool edge = ((uintptr_t)a.x % 16) != 0 || (a.cols * ElemT<DT>::ES) % 16 != 0;
+    const dim3 g((unsigned)a.rows), b(kNTS);
+    if (p.maxv == 16) {
+      if (edge) hipLaunchKernelGGL((stream_select_kernel<DT, 16, SAMPLE, true>), g, b, 0, s, a);
+      else hipLaunchKernelGGL((stream_select_kernel<DT, 16, SAMPLE, false>), g, b, 0, s, a);
+    } else if (p.maxv == 8) {
+      if (edge) hipLaunchKernelGGL((stream_select_kernel<DT, 8, SAMPLE, true>), g, b, 0, s, a);
+      else hipLaunchKernelGGL((stream_select_kernel<DT, 8, SAMPLE, false>), g, b, 0, s, a);
+    } else {
+      if (edge) hipLaunchKernelGGL((stream_select_kernel<DT, 4, SAMPLE, true>), g, b, 0, s, a);
+      else hipLaunchKernelGGL((stream_select_kernel<DT, 4, SAMPLE, false>), g, b, 0, s, a);
+    }
     return launch_status(what);
   } else {
     if (p.maxv == 16) launch_a<DT, 16, kNT, SAMPLE>(a, s);

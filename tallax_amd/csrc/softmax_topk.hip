@@ -73,10 +73,6 @@ struct PfArgs {
   int32_t* out_cutoff;
 };
 
-// s_barrier after this wave's LDS operations only: unlike __syncthreads it
-// does not wait for the wave's global stores to complete
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // exp(x - m) as 2^(x log2 e - m log2 e), mc = m log2 e (v_exp_f32)
 __device__ __forceinline__ float pf_exp(float x, float mc) {
   return __builtin_amdgcn_exp2f(__builtin_fmaf(x, 1.44269504088896341f, -mc));

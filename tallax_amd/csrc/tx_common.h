@@ -59,6 +59,11 @@ __device__ __forceinline__ int32_t comp_idx(uint64_t c) { return (int32_t)(~(uin
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// s_barrier after this wave's LDS operations only: unlike __syncthreads it
+// does not wait for the wave's global loads and stores to complete, which
+// stay in flight across it
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // v_max_f32 / v_max3_f32 on the operands as they are.  fmaxf makes the
 // compiler quiet every operand first (one v_max_f32 x, x each, since the
 // hardware returns NaN for a signalling NaN); these skip that.  A quiet NaN

@@ -98,6 +98,16 @@ TOPK_CASES = [
     (128, 32768, 100, "f32", "masked_mix"),
     (160, 5003, 128, "bf16", "masked_mix"),
     (128, 100, 64, "f32", "masked_mix"),    # rows shorter than 128
+    # whole-row workgroups: the bound from the first half of every thread's
+    # vectors (positive rows), the whole-row bound (negative rows), overflow
+    # from the first path into the exact tie selection, and misaligned rows
+    # where thread 0 owns both the row's first and its last vector
+    (256, 128256, 128, "bf16", "normal"),
+    (128, 65536, 100, "f32", "normal"),
+    (128, 65536, 100, "bf16", "negative"),
+    (128, 65536, 64, "bf16", "tieblock"),
+    (128, 8195, 128, "bf16", "normal"),
+    (128, 4097, 64, "f32", "normal"),
 ]
 
 
@@ -140,6 +150,8 @@ def _make(rows, cols, kind, seed):
         return x
     if kind == "normal":
         return rng.standard_normal((rows, cols)).astype(np.float32)
+    if kind == "negative":
+        return (rng.standard_normal((rows, cols)) - 20).astype(np.float32)
     if kind == "ints":
         return rng.integers(-6, 7, (rows, cols)).astype(np.float32)
     if kind == "const":
@@ -257,7 +269,8 @@ def _sampler_inputs(rows, vocab, seed, sigma=3.0):
 
 @pytest.mark.parametrize("rows,vocab,dtype,masked", [(256, 128256, "bf16", False), (64, 32000, "f32", False),
                                                      (16, 4096, "bf16", False), (8, 131, "f32", False),
-                                                     (256, 128256, "bf16", True), (128, 32768, "f32", True)])
+                                                     (256, 128256, "bf16", True), (128, 32768, "f32", True),
+                                                     (128, 8195, "bf16", False)])
 def test_fused_sampler_parity(gpu, rows, vocab, dtype, masked):
     from tallax_amd import sampling
     _log(f"sample rows={rows} vocab={vocab} dtype={dtype} masked={masked}")
