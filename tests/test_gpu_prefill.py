@@ -118,3 +118,48 @@ def test_prefill_deterministic(gpu):
         torch.cuda.synchronize()
         for a, b in zip(first, again):
             assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+def test_prefill_full_config5_launch(gpu):
+    """The whole config-5 launch, f32 [1024, 201088] N(0, 2) (both rounds of
+    two workgroups per CU): 128 rows spread over the launch against the
+    float64 oracle, and every row by properties that fix the result --
+    the selected set is exactly the 2048 largest logits with ties to the lowest
+    index (counts against the row), in descending order; probabilities within
+    1e-5 relative of exp(x - max) / sum(exp(x - max)) in float64; the cumsum
+    bit-exact to tax.cumsum's tile order over the kernel's probabilities; the
+    cutoff equal to #(cumsum < p)."""
+    from tallax_amd import prefill
+    rows, cols, k, p = 1024, 201088, 2048, 0.9
+    _log(f"softmax_topk_cumsum full launch [{rows},{cols}] k={k}")
+    g = torch.Generator(device=gpu)
+    g.manual_seed(5)
+    xd = torch.randn((rows, cols), generator=g, device=gpu) * 2
+    probs, idx, cum, cut = prefill.softmax_topk_cumsum(xd, k, p)
+    torch.cuda.synchronize()
+    x = xd.cpu().numpy()
+    gp, gi, gc, gcut = probs.cpu().numpy(), idx.cpu().numpy(), cum.cpu().numpy(), cut.cpu().numpy()
+    del xd
+    sample = np.r_[0:32, 480:544, 992:1024]
+    sidx, sp64, sc64, _ = O.softmax_topk_cumsum_f64(x[sample], k, p)
+    assert np.array_equal(gi[sample], sidx)
+    assert np.all(np.abs(gp[sample] - sp64) <= 1e-5 * np.abs(sp64) + 1e-30)
+    assert np.all(np.abs(gc[sample] - sc64) <= 1e-5 * np.abs(sc64))
+    assert np.all((gi >= 0) & (gi < cols))
+    sel = np.take_along_axis(x, gi, axis=1)
+    assert np.all(sel[:, :-1] >= sel[:, 1:])                          # descending
+    same = sel[:, :-1] == sel[:, 1:]
+    assert np.all(gi[:, :-1][same] < gi[:, 1:][same])                 # equal logits: ascending index
+    vk = sel[:, -1:]
+    above = (x > vk).sum(axis=1)
+    assert np.all(above == (sel > vk).sum(axis=1))                    # every larger logit is selected
+    for r in np.nonzero((x == vk).sum(axis=1) > (sel == vk).sum(axis=1))[0]:
+        tied = np.nonzero(x[r] == vk[r, 0])[0]
+        assert np.array_equal(np.sort(gi[r][sel[r] == vk[r, 0]]), tied[: (sel[r] == vk[r, 0]).sum()])
+    x64 = x.astype(np.float64)
+    m = x64.max(axis=1, keepdims=True)
+    s = np.exp(x64 - m).sum(axis=1, keepdims=True)
+    p64 = np.exp(sel.astype(np.float64) - m) / s
+    assert np.all(np.abs(gp - p64) <= 1e-5 * p64)
+    assert np.array_equal(bits(gc), bits(O.cumsum(gp, 1)))
+    assert np.array_equal(gcut, (gc < p).sum(axis=1))
