@@ -96,8 +96,8 @@ def _read_rates(torch, _lib, dev, stream, steps, warmup):
 
 
 def _measured_traffic(config):
-    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-    (scaled by the copy calibration), as recorded in profiles/*.md lines
+    """HBM bytes per launch measured with rocprofv3 --pmc (128-byte lines of the
+    TCC_EA0 read requests plus WRITE_SIZE), as recorded in profiles/*.md lines
     `traffic_bytes_per_launch[<config>] = <bytes>`; None if absent."""
     import glob
     import re
@@ -120,8 +120,8 @@ def _parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
-                    help="skip the extra measurements: config 3's line in the sampler config, the unmasked "
-                         "comparison in sampler_masked (profiling runs)")
+                    help="skip the extra measurements: the config 3, 5 and 2 lines in the sampler config, the "
+                         "unmasked comparison in sampler_masked (profiling runs)")
     return ap.parse_args()
 
 
@@ -512,10 +512,19 @@ def _cpu_baseline(w, O, seconds):
                       f"{wall:.1f} s wall"}
 
 
-def _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O):
-    """Config 3 (the second north-star target: exact top-k k=50 of f32
-    [128,151936] + spikes), timed the same way as the main line."""
-    w = _topk(torch, np, _lib, dev, s_handle, gen, None, "topk_c3")
+def _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O, which):
+    """Another BASELINE config beside the main line, timed the same way:
+    config 3 (the second north-star target: exact top-k k=50 of f32
+    [128,151936] + spikes), config 5 (the fused prefill pipeline) or config 2
+    (argsort + gather).  Config 5 runs a quarter of the steps (it is ~10x
+    longer per launch)."""
+    if which == "topk_c3":
+        w = _topk(torch, np, _lib, dev, s_handle, gen, None, "topk_c3")
+    elif which == "prefill_c5":
+        w = _prefill_c5(torch, np, _lib, dev, s_handle, gen, None)
+    else:
+        w = _sort_c2(torch, np, _lib, dev, s_handle, gen, None)
+    steps = max(1, args.steps // 4) if which == "prefill_c5" else args.steps
     parity = None if args.no_parity else w.parity(O)
     for i in range(args.warmup):
         w.launch(i)
@@ -523,17 +532,20 @@ def _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         w.launch(i)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    us = e0.elapsed_time(e1) * 1e3 / steps
     achieved = w.alg_bytes / (us * 1e-6) / 1e9
-    return {"metric": w.metric, "value": w.rows * args.steps / max(wall, us * 1e-6 * args.steps), "unit": "rows/s",
-            "kernel": w.kernel, "kernel_avg_us": us, "achieved_GBs": achieved, "roofline_frac": achieved / PEAK_HBM_GBS,
-            "algorithmic_bytes_per_launch": w.alg_bytes, "traffic": _measured_traffic("topk_c3"),
-            "workload": w.workload, "parity_vs_oracle": parity}
+    rec = {"metric": w.metric, "value": w.rows * steps / max(wall, us * 1e-6 * steps), "unit": "rows/s",
+           "steps": steps, "kernel": w.kernel, "kernel_avg_us": us, "achieved_GBs": achieved,
+           "roofline_frac": achieved / PEAK_HBM_GBS, "algorithmic_bytes_per_launch": w.alg_bytes,
+           "traffic": _measured_traffic(which), "workload": w.workload, "parity_vs_oracle": parity}
+    del w
+    torch.cuda.empty_cache()
+    return rec
 
 
 def main() -> int:
@@ -652,7 +664,8 @@ def main() -> int:
         "wall_ms_per_step": wall * 1e3 / args.steps,
     }
     if args.config == "sampler" and not args.no_extra:
-        rec["topk_c3"] = _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O)
+        for which in ("topk_c3", "prefill_c5", "sort_c2"):
+            rec[which] = _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O, which)
     if hasattr(w, "common_us") and not args.no_extra:
         cu = w.common_us(args.steps)
         rec["unmasked_kernel_avg_us"] = cu
