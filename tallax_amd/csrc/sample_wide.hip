@@ -69,6 +69,7 @@ constexpr int kSwList = 2048;           // collected records, at most (two per t
 constexpr int kSwBins = 2048;           // 11-bit digits
 constexpr int kSwChunk = kSwNT * 8;     // columns per workgroup step: 8 per thread
 constexpr int kSwV = 16;                // register path: 16-byte vectors per thread
+constexpr int kSwStage = 128;           // register path: staged vectors per wave
 
 typedef short sw_short2_t __attribute__((ext_vector_type(2)));
 
@@ -199,9 +200,9 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   __shared__ int s_cnt;
   __shared__ float s_sum;
   __shared__ int32_t s_id0;
-  __shared__ float s_bs[kSwNW];
-  __shared__ uint32_t s_bb[kSwNW];
-  __shared__ int32_t s_bi[kSwNW];
+  __shared__ uint64_t s_bk[kSwNW];
+  __shared__ uint4 s_vst[kSwNW][kSwStage];     // register path: the wave's vectors holding a candidate
+  __shared__ uint32_t s_vcol[kSwNW][kSwStage];  // and their first column
 
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x, l = lane_id(), w = t / kWave;
@@ -290,28 +291,29 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
         }
         return m;
       };
-      // one pool reservation per wave: the lane's count over its vectors, one
-      // wave scan, one atomic; then the writes
-      int c = 0;
-      uint32_t pm[kSwV / 4] = {0u, 0u, 0u, 0u};  // the masks, 8 bits per vector (VEC <= 8)
+      // The vectors holding a candidate (maximum >= L; about one in eight for
+      // K = 1024) go to the wave's LDS region in lane order, then each lane
+      // takes one staged vector at a time: the pass masks, the wave's pool
+      // reservation (one scan, one atomic) and the writes then run over the
+      // staged vectors only.  A wave with more than kSwStage of them takes
+      // every vector from its registers instead.
+      int wcnt = 0;
 #pragma unroll
       for (int j = 0; j < kSwV; ++j) {
-        const uint32_t m = pass_mask(raw[j]);
-        pm[j >> 2] |= m << (8 * (j & 3));
-        c += __popc(m);
+        const bool f = sw_vec_smax<DT>(raw[j]) >= L;
+        const uint64_t b = __ballot(f);
+        if (b) {  // wave-uniform
+          const int o = wcnt + (int)__popcll(b & ((1ull << l) - 1ull));
+          if (f && o < kSwStage) {
+            s_vst[w][o] = raw[j];
+            s_vcol[w][o] = (uint32_t)(((int64_t)j * kSwNT + t) * VEC);
+          }
+          wcnt += (int)__popcll(b);
+        }
       }
-      int wtot;
-      const int pre = wave_exscan_i32(c, wtot);
-      int base = 0;
-      if (l == 0 && wtot) base = atomicAdd(&s_cnt, wtot);
-      int pos = __builtin_amdgcn_readfirstlane(base) + pre;
-#pragma unroll
-      for (int j = 0; j < kSwV; ++j) {
-        uint32_t m = (pm[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-        if (!__ballot(m != 0u)) continue;  // wave-uniform
-        const uint4 x = raw[j];
+      // elements of x (first column col0) in pass mask m go to the pool from slot pos on
+      auto put = [&](const uint4 x, uint32_t m, uint32_t col0, int pos) {
         const uint32_t d[4] = {x.x, x.y, x.z, x.w};
-        const uint32_t col0 = (uint32_t)(((int64_t)j * kSwNT + t) * VEC);
         while (m) {
           const int e = __builtin_ctz(m);
           m &= m - 1u;
@@ -319,6 +321,46 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
           // every candidate is a positive finite value: its select key is bits | 2^31
           if (pos < kSwList) s_list[pos] = make_comp(bits | 0x80000000u, col0 + (uint32_t)e);
           ++pos;
+        }
+      };
+      if (wcnt <= kSwStage) {  // wave-uniform
+        for (int r0 = 0; r0 < wcnt; r0 += kWave) {
+          const int o = r0 + l;
+          uint4 x = make_uint4(0u, 0u, 0u, 0u);
+          uint32_t col0 = 0u, m = 0u;
+          if (o < wcnt) {
+            x = s_vst[w][o];
+            col0 = s_vcol[w][o];
+            m = pass_mask(x);
+          }
+          int wtot;
+          const int pre = wave_exscan_i32(__popc(m), wtot);
+          int base = 0;
+          if (l == 0 && wtot) base = atomicAdd(&s_cnt, wtot);
+          put(x, m, col0, __builtin_amdgcn_readfirstlane(base) + pre);
+        }
+      } else {
+        // one pool reservation per wave: the lane's count over its vectors, one
+        // wave scan, one atomic; then the writes
+        int c = 0;
+        uint32_t pm[kSwV / 4] = {0u, 0u, 0u, 0u};  // the masks, 8 bits per vector (VEC <= 8)
+#pragma unroll
+        for (int j = 0; j < kSwV; ++j) {
+          const uint32_t m = pass_mask(raw[j]);
+          pm[j >> 2] |= m << (8 * (j & 3));
+          c += __popc(m);
+        }
+        int wtot;
+        const int pre = wave_exscan_i32(c, wtot);
+        int base = 0;
+        if (l == 0 && wtot) base = atomicAdd(&s_cnt, wtot);
+        int pos = __builtin_amdgcn_readfirstlane(base) + pre;
+#pragma unroll
+        for (int j = 0; j < kSwV; ++j) {
+          const uint32_t m = (pm[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+          if (!__ballot(m != 0u)) continue;  // wave-uniform
+          put(raw[j], m, (uint32_t)(((int64_t)j * kSwNT + t) * VEC), pos);
+          pos += __popc(m);
         }
       }
       __syncthreads();
@@ -554,46 +596,40 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   int pbits = 0;
   while ((1 << pbits) < P) ++pbits;
   const float temp = a.temperature[row];
-  float sc = -INFINITY;
-  uint32_t br = 0u;
-  int32_t tok = 0;
-  if (in) {
-    const float masked = vv >= thr ? vv : a.replace_f32;
-    const float scaled = masked / temp;
-    sc = scaled + candidate_noise(a.rng_key[0], a.rng_key[1], (uint32_t)(row + a.dim0_offset),
-                                  (uint32_t)a.cols, id);
-    tok = id;
-    br = bitrev((uint32_t)t, pbits);
-  } else if (t < P) {
-    sc = -FLT_MAX;
-    tok = INT32_MIN;
-    br = bitrev((uint32_t)t, pbits);
+  // One u64 key per slot, as max_arrays orders them: the score as an
+  // order-preserving integer (-0 as +0) above the bit-reversed position, so
+  // the largest key is the largest score with ties to the largest
+  // bit-reversed position; padding slots (K <= t < P) score -FLT_MAX and
+  // give INT32_MIN, slots past P get key 0 and never win.
+  uint64_t key = 0ull;
+  if (t < P) {
+    float sc = -FLT_MAX;
+    if (in) {
+      const float masked = vv >= thr ? vv : a.replace_f32;
+      const float scaled = masked / temp;
+      sc = scaled + candidate_noise(a.rng_key[0], a.rng_key[1], (uint32_t)(row + a.dim0_offset),
+                                    (uint32_t)a.cols, id);
+    }
+    uint32_t sb = __float_as_uint(sc);
+    sb = sb == 0x80000000u ? 0u : sb;
+    const uint32_t ord = sb ^ ((uint32_t)((int32_t)sb >> 31) | 0x80000000u);
+    key = ((uint64_t)ord << 32) | bitrev((uint32_t)t, pbits);
   }
   auto reduce = [&]() {
 #pragma unroll
     for (int d = kWave / 2; d >= 1; d >>= 1) {
-      const float os = lane_xor_f(sc, d);
-      const uint32_t ob = lane_xor(br, d);
-      const int32_t oi = (int32_t)lane_xor((uint32_t)tok, d);
-      if (os > sc || (os == sc && ob > br)) {
-        sc = os;
-        br = ob;
-        tok = oi;
-      }
+      const uint64_t o = shfl_xor_u64(key, d);
+      key = o > key ? o : key;
     }
   };
   reduce();
-  if (l == 0) {
-    s_bs[w] = sc;
-    s_bb[w] = br;
-    s_bi[w] = tok;
-  }
+  if (l == 0) s_bk[w] = key;
   __syncthreads();
   if (t < kWave) {
-    sc = l < kSwNW ? s_bs[l] : -INFINITY;
-    br = l < kSwNW ? s_bb[l] : 0u;
-    tok = l < kSwNW ? s_bi[l] : 0;
+    key = l < kSwNW ? s_bk[l] : 0ull;
     reduce();
+    const int pw = (int)bitrev((uint32_t)key, pbits);  // the winning slot (uniform)
+    const int32_t tok = pw < K ? comp_idx(s_list[pw]) : INT32_MIN;
     if (t == 0) a.out_tokens[row] = temp < 1e-5f ? s_id0 : tok;
   }
 }
