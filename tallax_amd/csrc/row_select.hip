@@ -1076,11 +1076,10 @@ __device__ __forceinline__ uint64_t lanes_below() {
 }
 
 // The k-th largest (kth) and the largest (top) of the wave's 64 values
-// (1 <= k <= 64, values below 2^BITS).  top and the smallest value come from
+// (1 <= k <= 64).  top and the smallest value come from
 // lane-exchange reductions; kth lies between them, so it has the bits above
 // the highest bit in which they differ, and the radix search (one ballot
 // per bit: the largest K with #(v >= K) >= k) runs over the bits below.
-template <int BITS>
 __device__ __forceinline__ void wave_kth_and_max(uint32_t v, int k, uint32_t& kth, uint32_t& top) {
   uint32_t mx = v, mn = v;
 #pragma unroll
@@ -1266,7 +1265,6 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   using T = ElemT<DT>;
   constexpr int VEC = T::VEC, ES = T::ES, NW = kNTS / kWave;
   constexpr bool kBF = DT == kBF16;
-  constexpr int KB = kBF ? 16 : 32;  // canonical key bits
   using ST = Sel<DT, (kNTS * V * VEC > 65535)>;  // the tie path's composites (tie_select's choice)
   using CT = typename ST::Comp;
   constexpr uint32_t kZeroKey = kBF ? 0x8000u : 0x80000000u;
@@ -1415,7 +1413,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     }
     {
       uint32_t wl, wm;
-      wave_kth_and_max<KB>(tk, kMaxK / NW, wl, wm);
+      wave_kth_and_max(tk, kMaxK / NW, wl, wm);
       if (l == 0) {
         ss.wl[w] = wl;
         ss.wm[w] = wm;
