@@ -1076,32 +1076,20 @@ __device__ __forceinline__ uint64_t lanes_below() {
 }
 
 // The k-th largest (kth) and the largest (top) of the wave's 64 values
-// (1 <= k <= 64).  top and the smallest value come from
-// lane-exchange reductions; kth lies between them, so it has the bits above
-// the highest bit in which they differ, and the radix search (one ballot
-// per bit: the largest K with #(v >= K) >= k) runs over the bits below.
+// (k >= 1), by radix searches over the bits with one ballot per bit and
+// search: the largest K with #(v >= K) >= k.
+template <int BITS>
 __device__ __forceinline__ void wave_kth_and_max(uint32_t v, int k, uint32_t& kth, uint32_t& top) {
-  uint32_t mx = v, mn = v;
+  uint32_t K = 0, T = 0;
 #pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint32_t a = lane_xor(mx, d), b = lane_xor(mn, d);
-    mx = a > mx ? a : mx;
-    mn = b < mn ? b : mn;
-  }
-  mx = readlane_u32(mx, 0);
-  mn = readlane_u32(mn, 0);
-  const uint32_t diff = mx ^ mn;
-  uint32_t K = mx;
-  if (diff) {
-    const int hb = 31 - __builtin_clz(diff);
-    K = mx & ~((2u << hb) - 1u);  // every value is >= K
-    for (int b = hb; b >= 0; --b) {
-      const uint32_t pk = K | (1u << b);
-      K = __popcll(__ballot(v >= pk)) >= k ? pk : K;
-    }
+  for (int b = BITS - 1; b >= 0; --b) {
+    const uint32_t pk = K | (1u << b), pt = T | (1u << b);
+    const uint64_t mk = __ballot(v >= pk), mt = __ballot(v >= pt);
+    K = __popcll(mk) >= k ? pk : K;
+    T = mt ? pt : T;
   }
   kth = K;
-  top = mx;
+  top = T;
 }
 
 
@@ -1265,6 +1253,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   using T = ElemT<DT>;
   constexpr int VEC = T::VEC, ES = T::ES, NW = kNTS / kWave;
   constexpr bool kBF = DT == kBF16;
+  constexpr int KB = kBF ? 16 : 32;  // canonical key bits
   using ST = Sel<DT, (kNTS * V * VEC > 65535)>;  // the tie path's composites (tie_select's choice)
   using CT = typename ST::Comp;
   constexpr uint32_t kZeroKey = kBF ? 0x8000u : 0x80000000u;
@@ -1413,7 +1402,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     }
     {
       uint32_t wl, wm;
-      wave_kth_and_max(tk, kMaxK / NW, wl, wm);
+      wave_kth_and_max<KB>(tk, kMaxK / NW, wl, wm);
       if (l == 0) {
         ss.wl[w] = wl;
         ss.wm[w] = wm;
