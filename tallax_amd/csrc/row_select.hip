@@ -728,7 +728,7 @@ void seg_select_kernel(SelArgs a) {
 #pragma unroll
   for (int j = 0; j < MAXV; ++j) {
     const int64_t v = s0 + (int64_t)j * NT + tid;
-    raw[j] = v < s1 ? rv.base[v] : make_uint4(~0u, ~0u, ~0u, ~0u);
+    raw[j] = v < s1 ? load_once(rv.base + v) : make_uint4(~0u, ~0u, ~0u, ~0u);
   }
   // Segment-local slot index of (j, q): lbase + j * NT * VEC + q.  Live slots
   // (inside the row and the segment) are those in [live_lo, live_hi).
@@ -1280,7 +1280,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       const int v = j * kNTS + tid;
-      const u32x4_t x = *(v < nv ? gb + v : dead);
+      const u32x4_t x = __builtin_nontemporal_load(v < nv ? gb + v : dead);
       raw[j] = make_uint4(x.x, x.y, x.z, x.w);
     }
   }

@@ -222,7 +222,7 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
 #pragma unroll
     for (int j = 0; j < kSwV; ++j) {
       const int64_t v = (int64_t)j * kSwNT + t;
-      raw[j] = v < nvec ? vb[v] : make_uint4(~0u, ~0u, ~0u, ~0u);  // all-ones: -1, below every bound
+      raw[j] = v < nvec ? load_once(vb + v) : make_uint4(~0u, ~0u, ~0u, ~0u);  // all-ones: -1, below every bound
     }
     if (t == 0) s_cnt = 0;
     // this lane's four largest vector maxima; a positive NaN maximum sends the row to the radix select

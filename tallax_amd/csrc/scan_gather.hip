@@ -58,14 +58,14 @@ __global__ __launch_bounds__(kGatherNT) void gather_row_lds_kernel(const T* __re
 #pragma unroll
     for (int u = 0; u < kGatherBatch; ++u) {
       const int64_t b = (int64_t)u * kGatherNT + t;
-      if (b < ni) iv[u] = i4[b];
+      if (b < ni) iv[u] = load_once(i4 + b);
     }
     for (int64_t b0 = 0; b0 < nv; b0 += (int64_t)kGatherBatch * kGatherNT) {
       uint4 sv[kGatherBatch];
 #pragma unroll
       for (int u = 0; u < kGatherBatch; ++u) {
         const int64_t b = b0 + (int64_t)u * kGatherNT + t;
-        if (b < nv) sv[u] = v4[b];
+        if (b < nv) sv[u] = load_once(v4 + b);
       }
 #pragma unroll
       for (int u = 0; u < kGatherBatch; ++u) {
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(kGatherNT) void gather_row_lds_kernel(const T* __re
 #pragma unroll
         for (int u = 0; u < kGatherBatch; ++u) {
           const int64_t b = ib + (int64_t)u * kGatherNT + t;
-          if (b < ni) iv[u] = i4[b];
+          if (b < ni) iv[u] = load_once(i4 + b);
         }
       }
 #pragma unroll

@@ -219,7 +219,7 @@ void softmax_topk_kernel(PfArgs a) {
   // any vector (row edges, tail); every thread of the workgroup calls it together
   auto step1 = [&](int64_t v) {
     const uint32_t live = v < nv ? live_mask(v) : 0u;
-    const uint4 q = v < nv ? rv.base[v] : make_uint4(0u, 0u, 0u, 0u);
+    const uint4 q = v < nv ? load_once(rv.base + v) : make_uint4(0u, 0u, 0u, 0u);
     float xs[4];
     vec_vals(q, live, xs);
     const float vm = fmaxf(fmaxf(xs[0], xs[1]), fmaxf(xs[2], xs[3]));
@@ -243,7 +243,7 @@ void softmax_topk_kernel(PfArgs a) {
     constexpr int U = decltype(u_const)::value;
     uint4 q[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) q[u] = rv.base[i0 + t + u * kPfNT];
+    for (int u = 0; u < U; ++u) q[u] = load_once(rv.base + i0 + t + u * kPfNT);
     float vm[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -294,7 +294,7 @@ void softmax_topk_kernel(PfArgs a) {
     const int32_t base = c * (6 * kWave);
     uint4 q[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) q[u] = rv.base[base + l + kWave * u];
+    for (int u = 0; u < U; ++u) q[u] = load_once(rv.base + base + l + kWave * u);
     float vm[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)

@@ -133,7 +133,7 @@ __global__ __launch_bounds__(kRadixNT) void radix_sort_rows_kernel(SortArgs a) {
   const bool vec = E == 4 && (n & 3) == 0 && (((uintptr_t)a.key + (uintptr_t)base * 2) & 7) == 0;
   if (vec && t * E < n) {
     const int i0 = a.ties_desc ? n - 4 - t * E : t * E;
-    const uint2 q = *(const uint2*)((const uint16_t*)a.key + base + i0);
+    const uint2 q = load_once((const uint2*)((const uint16_t*)a.key + base + i0));
     const uint32_t h[4] = {q.x << 16, q.x & 0xFFFF0000u, q.y << 16, q.y & 0xFFFF0000u};
 #pragma unroll
     for (int r = 0; r < E; ++r) {

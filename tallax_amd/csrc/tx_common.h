@@ -59,6 +59,21 @@ __device__ __forceinline__ int32_t comp_idx(uint64_t c) { return (int32_t)(~(uin
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
+// 16-byte load of data that is read once: the nontemporal hint streams it
+// past the caches instead of evicting what stays resident there (the
+// kernel's code, the small arrays every workgroup reads).
+__device__ __forceinline__ uint4 load_once(const uint4* p) {
+  typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+  const u32x4_nt x = __builtin_nontemporal_load((const u32x4_nt*)p);
+  return make_uint4(x.x, x.y, x.z, x.w);
+}
+
+__device__ __forceinline__ uint2 load_once(const uint2* p) {
+  typedef unsigned int u32x2_nt __attribute__((ext_vector_type(2)));
+  const u32x2_nt x = __builtin_nontemporal_load((const u32x2_nt*)p);
+  return make_uint2(x.x, x.y);
+}
+
 // s_barrier after this wave's LDS operations only: unlike __syncthreads it
 // does not wait for the wave's global loads and stores to complete, which
 // stay in flight across it
