@@ -207,6 +207,14 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x, l = lane_id(), w = t / kWave;
   const int K = a.k;
+  // the row's sampling parameters, loaded while the row streams in
+  int row_k = 0;
+  float row_p = 0.0f, row_temp = 1.0f;
+  if (a.out_tokens) {
+    row_k = a.top_k[row];
+    row_p = a.top_p[row];
+    row_temp = a.temperature[row];
+  }
   const char* rowp = (const char*)a.x + (size_t)(row * a.cols) * ES;
   const bool vec = a.vec != 0;
   const int nchunks = (int)((a.cols + kSwChunk - 1) / kSwChunk);
@@ -528,11 +536,14 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   if (!a.out_tokens) return;  // uniform
 
   // --- top-p mask, temperature, Gumbel-max (no contraction: built with -ffp-contract=off)
-  const float vv = t < a.top_k[row] ? val : a.replace_in_dtype;
+  const float vv = t < row_k ? val : a.replace_in_dtype;
   s_v[t] = vv;
   if (t == 0) s_id0 = id;
-  __syncthreads();
-  const float e = in ? candidate_exp(vv, s_v[0]) : 0.0f;
+  // the first candidate's value, as thread 0 has it (s_list is complete)
+  const uint32_t kk0 = comp_key(s_list[0]);
+  const float val0 = __uint_as_float(kk0 > ineligible_key_max(DT) ? key_to_bits(kk0) : min_bits);
+  const float v0 = 0 < row_k ? val0 : a.replace_in_dtype;
+  const float e = in ? candidate_exp(vv, v0) : 0.0f;
   s_e[t] = e;
   int W = 128;
   while (W < K) W <<= 1;
@@ -588,14 +599,14 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   }
   __syncthreads();
   if (in && g != 0) c = c + s_carry[g];
-  const int tcount = __syncthreads_count(in && c < a.top_p[row]);
+  const int tcount = __syncthreads_count(in && c < row_p);
   const float thr = tcount < K ? s_v[tcount] : 0.0f;
 
   int P = 8;
   while (P < K) P <<= 1;
   int pbits = 0;
   while ((1 << pbits) < P) ++pbits;
-  const float temp = a.temperature[row];
+  const float temp = row_temp;
   // One u64 key per slot, as max_arrays orders them: the score as an
   // order-preserving integer (-0 as +0) above the bit-reversed position, so
   // the largest key is the largest score with ties to the largest
