@@ -130,7 +130,7 @@ void softmax_topk_kernel(PfArgs a) {
   __shared__ float redf[kPfNW];
   __shared__ int redi[kPfNW];
   __shared__ uint32_t s_t0, s_above;
-  __shared__ int s_cnt, s_bin, s_next;
+  __shared__ int s_cnt, s_bin, s_next, s_mx;
   __shared__ float s_bmc[kPfMaxBatches], s_bsum[kPfMaxBatches];  // per wave-batch: reference mc, exp-sum
   __shared__ float s_cum_carry[kPfMaxK / 128];
   __shared__ float s_tile_sum[kPfMaxK / 128];
@@ -430,6 +430,9 @@ void softmax_topk_kernel(PfArgs a) {
   }
   // candidates: key >= T0, i.e. x >= t0f as floats (NaN never passes)
   const float t0f = s_t0 >= 0x007FFFFFu ? __uint_as_float(key_to_bits(s_t0)) : -INFINITY;
+  // the threshold histograms are done: their words become the sort's bucket
+  // counts (pass 2's barriers order this before the counting)
+  if (t < kPfBuckets) hist_all[t] = 0u;
 
   // ---- pass 2: candidates ---------------------------------------------------------
   auto pass2_vec = [&](uint4 q, int64_t v) {
@@ -575,29 +578,33 @@ void softmax_topk_kernel(PfArgs a) {
       const uint32_t o = key > lo ? (key - lo) >> shift : 0u;
       return kPfBuckets - 1 - (int)(o < (uint32_t)kPfBuckets ? o : (uint32_t)(kPfBuckets - 1));
     };
-    uint32_t* bk = hist_all;
-    if (t < kPfBuckets) bk[t] = 0u;
-    __syncthreads();
+    uint32_t* bk = hist_all;  // zeroed after the threshold
     for (int i = t; i < n; i += kPfNT) atomicAdd(&bk[bucket(pool[i])], 1u);
     __syncthreads();
-    // exclusive scan of the bucket counts, and the largest count
-    const int c = t < kPfBuckets ? (int)bk[t] : 0;
-    const int incl = wave_incl_scan(c);
-    int mx = c;
+    // exclusive scan of the bucket counts and the largest count, by wave 0
+    if (w == 0) {
+      constexpr int PER = kPfBuckets / kWave;
+      uint32_t cnt[PER];
+      int loc = 0, mxl = 0;
 #pragma unroll
-    for (int d = kWave / 2; d >= 1; d >>= 1) mx = max(mx, (int)lane_xor((uint32_t)mx, d));
-    if (l == kWave - 1) {
-      redi[w] = incl;
-      redf[w] = __int_as_float(mx);
+      for (int i = 0; i < PER; ++i) {
+        cnt[i] = bk[l * PER + i];
+        loc += (int)cnt[i];
+        mxl = max(mxl, (int)cnt[i]);
+      }
+      int tot;
+      uint32_t run = (uint32_t)wave_exscan_i32(loc, tot);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        bk[l * PER + i] = run;
+        run += cnt[i];
+      }
+#pragma unroll
+      for (int d = kWave / 2; d >= 1; d >>= 1) mxl = max(mxl, (int)lane_xor((uint32_t)mxl, d));
+      if (l == 0) s_mx = mxl;
     }
     __syncthreads();
-    int off = incl - c, mxall = 0;
-    for (int i = 0; i < kPfNW; ++i) {
-      off += i < w ? redi[i] : 0;
-      mxall = max(mxall, __float_as_int(redf[i]));
-    }
-    if (t < kPfBuckets) bk[t] = (uint32_t)off;
-    __syncthreads();
+    const int mxall = s_mx;
     if (mxall <= kPfRankMax) {
       ranked = true;
       uint64_t* pool2 = (uint64_t*)summ;  // n <= a.cap2 records
@@ -698,12 +705,20 @@ void softmax_topk_kernel(PfArgs a) {
     if (l == kWave - 1) s_tile_sum[w] = c[1];
   }
   __syncthreads();
-  if (t == 0) {
-    float acc = 0.0f;
-    for (int i = 0; i < ntiles; ++i) {
-      s_cum_carry[i] = acc;
-      acc = i == 0 ? s_tile_sum[0] : add_in_order(acc, s_tile_sum[i]);
+  if (w == 0) {
+    // the carries in tile order: the totals are read out first (one LDS read
+    // per lane), then added one after the other
+    const float ts = l < ntiles ? s_tile_sum[l] : 0.0f;
+    float acc = 0.0f, mine = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPfMaxK / 128; ++i) {
+      if (i < ntiles) {  // uniform
+        mine = l == i ? acc : mine;
+        const float ti = readlane_f(ts, i);
+        acc = i == 0 ? ti : add_in_order(acc, ti);
+      }
     }
+    if (l < ntiles) s_cum_carry[l] = mine;
   }
   __syncthreads();
   int below = 0;
