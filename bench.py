@@ -552,7 +552,7 @@ def main() -> int:
     args = _parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the sort/select/sample path is single-GPU here -- see DESIGN.md for how it shards.",
+              "rows are independent, so a multi-GPU run shards them by rows with no communication.",
               file=sys.stderr)
         return 2
 
