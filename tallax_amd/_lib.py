@@ -8,7 +8,6 @@ on torch's current HIP stream of the tensor's device.
 from __future__ import annotations
 
 import ctypes
-import os
 import pathlib
 import threading
 
@@ -168,10 +167,9 @@ def require_cuda(*ts: torch.Tensor) -> None:
     for t in ts:
         if not isinstance(t, torch.Tensor) or not t.is_cuda:
             raise ValueError("tallax_amd operands must be torch tensors on a ROCm (cuda) device")
-    if os.environ.get("TALLAX_AMD_STRICT_DEVICE", "1") == "1":
-        devs = {t.device for t in ts}
-        if len(devs) > 1:
-            raise ValueError(f"operands on different devices: {devs}")
+    devs = {t.device for t in ts}
+    if len(devs) > 1:
+        raise ValueError(f"operands on different devices: {devs}")
 
 
 def select_plan(rows: int, cols: int, dtype: int, k: int = 128, sample: bool = True) -> dict:

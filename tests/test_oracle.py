@@ -453,6 +453,103 @@ def test_depth_probs_closed_forms_and_monte_carlo():
         assert S.topm_schedule(kk, nn, 8) == O.topm_schedule(kk, nn, 8)[1:]
 
 
+def _exact_max_occupancy_cdf(k: int, n: int, m_max: int | None = None) -> list:
+    """P(max bin occupancy <= m) for m = 1..k, k labelled balls thrown into n
+    bins, as exact fractions: N_m / n^k, where N_m counts the maps
+    [k] -> [n] with every bin holding <= m balls.  N_m = k! [x^k]
+    (sum_{i<=m} x^i / i!)^n; with integer coefficients c_j = j! [x^j] the
+    product of two such series is the binomial convolution
+    c_j = sum_i C(j, i) a_i b_{j-i}, so the power is taken by repeated
+    squaring over Python integers, truncated at degree k.  Independent of
+    the log-space float routine it checks."""
+    from fractions import Fraction
+
+    def bconv(a, b):
+        return [sum(math.comb(j, i) * a[i] * b[j - i] for i in range(j + 1)) for j in range(k + 1)]
+
+    out = []
+    for m in range(1, (m_max or k) + 1):
+        base = [1 if j <= m else 0 for j in range(k + 1)]
+        acc = [1] + [0] * k
+        p = n
+        while p:
+            if p & 1:
+                acc = bconv(acc, base)
+            base = bconv(base, base)
+            p >>= 1
+        out.append(Fraction(acc[k], n ** k))
+    return out
+
+
+def _exact_schedule(k: int, n: int, block: int, yields=(0.8, 0.98, 0.9999)) -> tuple:
+    """top_dynamic_k's automatic schedule (top_k.py:444-450) from the exact
+    cdf: for each yield, the first depth m with cdf(m)^block >= yield
+    (top_k_convergence_theory.py:115-125, 1-based), then + 1, deduplicated
+    and sorted.  The yields are compared as the float64 values the reference
+    passes, converted exactly."""
+    from fractions import Fraction
+    cdf = _exact_max_occupancy_cdf(k, n, min(k, 12))   # every yield here is met by depth 12
+    depths = set()
+    for y in yields:
+        for m, c in enumerate(cdf, start=1):
+            if c ** block >= Fraction(y):
+                depths.add(m)
+                break
+        else:
+            raise AssertionError(f"yield {y} not met by depth {len(cdf)}")
+    return tuple(sorted(d + 1 for d in depths))
+
+
+def test_depth_schedule_exact_rational():
+    """calculate_depth_thresholds + the +1 of top_dynamic_k
+    (top_k_convergence_theory.py:103-128, top_k.py:444-450), pinned by exact
+    rational arithmetic rather than a second log-space restatement.
+
+    Hand-checkable cases first, each exercising one step:
+      * k = 1: one ball, max occupancy is always 1, so every yield is met at
+        depth 1 and the schedule is (2,) -- the "+1";
+      * k = 3, n = 3: 27 maps; max <= 1 for the 3! = 6 permutations (2/9),
+        max <= 2 for all but the 3 maps into one bin (8/9), max <= 3 always.
+        block 1: yield 0.8 first met at depth 2, 0.98 and 0.9999 at depth 3
+        -> thresholds (2, 3), schedule (3, 4) -- the "first index" and the
+        deduplication; block 8: (8/9)^8 = 0.39 < 0.8, so only depth 3 ->
+        schedule (4,) -- the "cdf ** block" power;
+      * k = 2, n = 2: max <= 1 with probability 1/2, so a yield of 0.4 is met
+        at depth 1 with block 1 but at depth 2 with block 2 (1/4 < 0.4).
+    Then realistic cases against the exact counts, both restatements (the
+    oracle's and the product's tallax_amd/schedule.py) checked against them.
+    """
+    from fractions import Fraction
+    from tallax_amd import schedule as S
+    assert _exact_max_occupancy_cdf(3, 3) == [Fraction(2, 9), Fraction(8, 9), Fraction(1)]
+    assert _exact_max_occupancy_cdf(2, 2) == [Fraction(1, 2), Fraction(1)]
+    assert _exact_max_occupancy_cdf(1, 128) == [Fraction(1)]
+    hand = {(1, 128, 8): (2,), (3, 3, 1): (3, 4), (3, 3, 8): (4,)}
+    for (k, n, b), want in hand.items():
+        assert _exact_schedule(k, n, b) == want
+        assert O.topm_schedule(k, n, b)[1:] == want, (k, n, b)
+        assert S.topm_schedule(k, n, b) == want, (k, n, b)
+    assert _exact_schedule(2, 2, 1, yields=(0.4,)) == (2,)
+    assert _exact_schedule(2, 2, 2, yields=(0.4,)) == (3,)
+    assert O.calculate_depth_thresholds(2, 2, 1, (0.4,)) == (1,)
+    assert O.calculate_depth_thresholds(2, 2, 2, (0.4,)) == (2,)
+    assert S.calculate_depth_thresholds(2, 2, 1, (0.4,)) == (1,)
+    assert S.calculate_depth_thresholds(2, 2, 2, (0.4,)) == (2,)
+    realistic = {(50, 128, 8): (5, 6, 8), (128, 256, 8): (6, 7, 9), (64, 128, 8): (5, 6, 8),
+                 (8, 16, 8): (4, 5, 7), (16, 32, 8): (5, 6, 7), (32, 64, 8): (5, 6, 8)}
+    for (k, n, b), want in realistic.items():
+        assert _exact_schedule(k, n, b) == want, (k, n, b)
+        assert O.topm_schedule(k, n, b)[1:] == want, (k, n, b)
+        assert S.topm_schedule(k, n, b) == want, (k, n, b)
+    # the cdf itself: float restatements within 1e-9 of the exact fractions
+    for k, n in [(50, 128), (16, 32)]:
+        exact = np.array([float(c) for c in _exact_max_occupancy_cdf(k, n, 12)])
+        for pdf in (O.depth_probs(k, n), S.max_occupancy_pdf(k, n)):
+            got = np.cumsum(pdf)
+            m = min(len(got), len(exact))
+            assert np.abs(got[:m] - exact[:m]).max() < 1e-9
+
+
 def test_binned_topm_brute_force():
     """binned_top_k (top_k.py:13-106) simulated literally (strict-> sinking
     insert in index order; NaN / -inf / finfo.min never admitted): the values at
