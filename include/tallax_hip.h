@@ -52,12 +52,16 @@ int tallax_abi_version(void);
  * Replaces tax.top_k(logits, k)  -- tallax/_src/top_k.py:516-567
  * (= top_dynamic_k(max_k=k, guarantee_convergence=True), top_k.py:372-514,
  * kernel dynamic_top_k_refs top_k.py:203-370).
- * x: [rows, cols] f32 or bf16.  Outputs: out_vals [rows, k] (same dtype,
- * descending), out_idx [rows, k] int32; ties broken to the lowest index.
- * 1 <= k <= 128 (the reference raises NotImplementedError above 128,
+ * x: [rows, cols] f32, bf16 or int32.  Outputs: out_vals [rows, k] (same
+ * dtype, descending), out_idx [rows, k] int32; ties broken to the lowest
+ * index.  1 <= k <= 128 (the reference raises NotImplementedError above 128,
  * top_k.py:438-439), k <= cols.  NaN, -inf and finfo(dtype).min are never
  * preferred over other values; slots that can only be filled by them hold
- * finfo(dtype).min, as the reference's bins do (top_k.py:241-243).
+ * finfo(dtype).min, as the reference's bins do (top_k.py:241-243).  int32
+ * rows (the reference's dtype-generic path, utils.py:48-56) are the first k
+ * of the row's stable descending sort, iinfo.min entries last; their
+ * workspace holds that sort's permutation (rows * cols * 4 bytes plus the
+ * row sort's own workspace).
  * ---------------------------------------------------------------------- */
 size_t tallax_topk_workspace_size(int64_t rows, int64_t cols, int64_t k, int dtype);
 int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k, void* out_vals,
@@ -69,7 +73,8 @@ int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k,
  * The exact counterpart of top_dynamic_k(logits, k, max_k, replace_val)
  * -- tallax/_src/top_k.py:385-514 (replacement :365-369) -- for a run that
  * converges, under the lowest-index tie rule of tax.top_k.  Workspace as tallax_topk
- * (tallax_topk_workspace_size).
+ * (tallax_topk_workspace_size).  For int32 x, replace_val is converted toward
+ * zero and saturated at the int32 range.
  * ---------------------------------------------------------------------- */
 int tallax_topk_replace(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k, const int32_t* k_rows,
                         double replace_val, void* out_vals, int32_t* out_idx, void* workspace,
@@ -81,7 +86,7 @@ int tallax_topk_replace(const void* x, int dtype, int64_t rows, int64_t cols, in
  * dynamic_top_k_refs :203-370, binned_top_k :13-106, and with
  * guarantee_convergence the bin-packing merge of unconverged blocks,
  * _merge_unconverged_bins_top_k :108-200, invoked at :317-331).
- * x [rows, cols] f32/bf16; k_rows [rows] int32 (per-row k <= max_k <= 128);
+ * x [rows, cols] f32/bf16/int32; k_rows [rows] int32 (per-row k <= max_k <= 128);
  * rows % block_token == 0; num_bins divides 1024; schedule: the strictly
  * increasing depths m (the reference's bins_topm_schedule without its
  * leading 0; the caller computes the automatic one), deepest <= 16 after
@@ -91,7 +96,11 @@ int tallax_topk_replace(const void* x, int dtype, int64_t rows, int64_t cols, in
  * out_vals [rows, max_k] (x's dtype), out_idx [rows, max_k] int32 (-1 where
  * fewer admissible elements exist; the merge can also return columns past
  * the row's end, with finfo.min, where the reference reads past it),
- * out_valid [1] int32 (0/1), out_depths [rows] int32, out_cutoff [rows] f32.
+ * out_valid [1] int32 (0/1), out_depths [rows] int32, out_cutoff [rows] f32
+ * (int32 for int32 x: the reference's cutoff is to_32bit_dtype(x.dtype),
+ * top_k.py:465; the buffer is 4 bytes per row either way).  int32 x: bins
+ * start at iinfo.min, the merge fills chosen bins with iinfo.min, and
+ * replace_val is converted toward zero and saturated at the int32 range.
  * Workspace: tallax_top_dynamic_k_workspace_size bytes.
  * ---------------------------------------------------------------------- */
 size_t tallax_top_dynamic_k_workspace_size(int64_t rows, int num_bins, const int32_t* schedule, int num_steps);

@@ -59,8 +59,29 @@ def round_to_dtype(x, dtype: str) -> np.ndarray:
     return bf16_bits_to_f32(f32_to_bf16_bits(x)) if dtype == "bf16" else x
 
 
-def dtype_min(dtype: str) -> np.float32:
+I32_MIN = np.int32(np.iinfo(np.int32).min)
+
+
+def dtype_min(dtype: str):
+    """get_dtype_info(x).min (utils.py:48-56): finfo for floats, iinfo for int32."""
+    if dtype == "i32":
+        return I32_MIN
     return BF16_MIN if dtype == "bf16" else F32_MIN
+
+
+def _as_values(x, dtype: str) -> np.ndarray:
+    """Values as the oracle carries them: float32 (bf16 as its exact f32
+    values) or int32."""
+    return np.asarray(x, dtype=np.int32 if dtype == "i32" else np.float32)
+
+
+def value_key(v: np.ndarray) -> np.ndarray:
+    """Monotone int64 key of list values: select_key for floats (NaN lowest,
+    -0 == +0), the value itself for int32."""
+    v = np.asarray(v)
+    if np.issubdtype(v.dtype, np.integer):
+        return v.astype(np.int64)
+    return select_key(v.astype(np.float32)).astype(np.int64)
 
 
 # ---------------------------------------------------------------------------
@@ -107,7 +128,17 @@ def top_k(x: np.ndarray, k: int, dtype: str = "f32"):
     xla_equivalent_sort(descending=True, is_stable=True) (sort.py:932-970).
     Elements the binned reference can never admit (<= finfo.min or NaN,
     top_k.py:64,241-243) are reported as finfo(dtype).min.
-    x: float32 values (bf16 inputs as their exact f32 values)."""
+    x: float32 values (bf16 inputs as their exact f32 values), or int32 with
+    dtype "i32": values descending, ties by lowest index, and iinfo.min (never
+    admitted, the dtype's min) last in index order."""
+    if dtype == "i32":
+        xi = np.asarray(x, dtype=np.int32)
+        key = (xi.astype(np.int64) + 2 ** 31).astype(np.uint64)
+        comp = (key << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - np.arange(xi.shape[-1], dtype=np.uint64))
+        part = np.argpartition(comp, comp.shape[-1] - k, axis=-1)[..., -k:]
+        order = np.argsort(np.take_along_axis(comp, part, -1), axis=-1)[..., ::-1]
+        idx = np.take_along_axis(part, order, -1).astype(np.int32)
+        return np.take_along_axis(xi, idx, -1).copy(), idx
     x = np.asarray(x, dtype=np.float32)
     comp = topk_composite(x)
     part = np.argpartition(comp, comp.shape[-1] - k, axis=-1)[..., -k:]
@@ -197,26 +228,27 @@ def binned_topm(x: np.ndarray, m: int, num_bins: int, dtype: str = "f32"):
     simulation in tests/test_oracle.py); among tied values the reference's
     kept indices depend on the insertion path, and this restatement keeps the
     lowest indices (the BASELINE tie contract).  Returns (vals [R, m, num_bins] f32, idxs
-    [R, m, num_bins] int32), rank-major; unfilled slots hold (finfo.min, -1)."""
-    x = np.asarray(x, dtype=np.float32)
+    [R, m, num_bins] int32), rank-major; unfilled slots hold (finfo.min, -1).
+    int32 (dtype "i32"): bins start at iinfo.min, values and results int32."""
+    x = _as_values(x, dtype)
     rows, cols = x.shape
     lo = dtype_min(dtype)
     nb = -(-cols // num_bins)
-    pad = np.full((rows, nb * num_bins), np.nan, np.float32)
+    pad = np.full((rows, nb * num_bins), lo if dtype == "i32" else np.nan, x.dtype)
     pad[:, :cols] = x
     vb = pad.reshape(rows, nb, num_bins)                        # [R, slice, bin]
     jb = (np.arange(nb)[:, None] * num_bins + np.arange(num_bins)[None, :]).astype(np.int64)
-    admitted = vb > lo                                          # False for NaN, -inf, finfo.min, padding
-    key = np.where(admitted, vb, -np.inf).astype(np.float64)
+    admitted = vb > lo                                          # False for NaN, -inf, the dtype min, padding
+    key = np.where(admitted, vb.astype(np.float64), -np.inf)    # exact for int32 too
     # order inside each bin: value descending, index ascending
     order = np.lexsort((np.broadcast_to(jb, vb.shape), -key), axis=1)[:, :m, :]
     vals = np.take_along_axis(key, order, axis=1)
     idxs = np.take_along_axis(np.broadcast_to(jb, vb.shape), order, axis=1)
     ok = vals > -np.inf
-    out_v = np.full((rows, m, num_bins), lo, np.float32)
+    out_v = np.full((rows, m, num_bins), lo, x.dtype)
     out_i = np.full((rows, m, num_bins), -1, np.int32)
     take = min(m, nb)
-    out_v[:, :take][ok[:, :take]] = vals[:, :take][ok[:, :take]].astype(np.float32)
+    out_v[:, :take][ok[:, :take]] = vals[:, :take][ok[:, :take]].astype(x.dtype)
     out_i[:, :take][ok[:, :take]] = idxs[:, :take][ok[:, :take]].astype(np.int32)
     return out_v, out_i
 
@@ -226,8 +258,8 @@ def list_order(v: np.ndarray, i: np.ndarray) -> np.ndarray:
     then index ascending as an unsigned 32-bit number, so that the scratch
     fillers (finfo.min, index -1) follow every entry of a value >= finfo.min
     with a real index (the reference orders them by value; their indices are
-    uninitialised there)."""
-    key = select_key(np.asarray(v, np.float32)).astype(np.int64)
+    uninitialised there).  int32 values order by value."""
+    key = value_key(v)
     iu = np.asarray(i).astype(np.int64) & 0xFFFFFFFF
     return np.lexsort((iu, -key), axis=-1)
 
@@ -249,7 +281,7 @@ def merge_unconverged_bins(x, bv, bi, num_bins, m, max_k, dtype="f32"):
         the reference's bitonic network leaves the order among equal counts
         open, and this restatement takes the lowest bin first);
       * every rank of a chosen bin becomes float32's finfo.min (:147-151,
-        the scratch is 32-bit) with its index kept;
+        the scratch is 32-bit; iinfo(int32).min for int32) with its index kept;
       * packed position e of ceil(V / (128 num_bins / P)) * 128 holds column
         (e // P) * num_bins + chosen[e % P] (:153-183: lane L of packed tile
         j is slice j * 128 / P + L // P of bin chosen[L % P]); columns past
@@ -262,7 +294,7 @@ def merge_unconverged_bins(x, bv, bi, num_bins, m, max_k, dtype="f32"):
     bins, and 128 bins are ranked at :139)."""
     if num_bins % NUM_LANES:
         raise NotImplementedError(f"the bin-packing merge needs num_bins % {NUM_LANES} == 0, got {num_bins}")
-    x = np.asarray(x, np.float32)
+    x = _as_values(x, dtype)
     rows, V = x.shape
     P = packed_bins(max_k, m)
     lo = dtype_min(dtype)
@@ -271,11 +303,11 @@ def merge_unconverged_bins(x, bv, bi, num_bins, m, max_k, dtype="f32"):
     bins = np.broadcast_to(np.arange(num_bins), cnt.shape)
     chosen = np.lexsort((bins, -cnt), axis=1)[:, :P]
     for r in range(rows):
-        bv[r][:, chosen[r]] = F32_MIN
+        bv[r][:, chosen[r]] = I32_MIN if dtype == "i32" else F32_MIN
     n = -(-V // (NUM_LANES * (num_bins // P))) * NUM_LANES
     e = np.arange(n)
     col = (e // P)[None, :] * num_bins + chosen[:, e % P]
-    pv = np.where(col < V, np.take_along_axis(x, np.minimum(col, V - 1), 1), lo).astype(np.float32)
+    pv = np.where(col < V, np.take_along_axis(x, np.minimum(col, V - 1), 1), lo).astype(x.dtype)
     cv = np.concatenate([pv, bv[:, 0, :NUM_LANES]], axis=1)
     ci = np.concatenate([col.astype(np.int64), bi[:, 0, :NUM_LANES].astype(np.int64)], axis=1)
     top = list_order(cv, ci)[:, :NUM_LANES]
@@ -310,8 +342,11 @@ def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, repla
     for that block's rows: they keep the finfo.min the scratch starts with
     (top_k.py:241-243, 250-281), so they reach the output only as
     (finfo.min, -1) fillers (the reference leaves those indices
-    uninitialised)."""
-    x = np.asarray(x, dtype=np.float32)
+    uninitialised).
+    int32 logits (dtype "i32"): int32 values and cutoff_vals (to_32bit_dtype,
+    top_k.py:465); replace_val converted toward zero, saturated at the int32
+    range."""
+    x = _as_values(x, dtype)
     rows, cols = x.shape
     if rows % block_token:
         raise ValueError("num_tokens must be divisible by block_token")
@@ -329,7 +364,7 @@ def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, repla
     bv, bi = binned_topm(x, buf, num_bins, dtype)
     lo = dtype_min(dtype)
     depths = np.full(rows, max_k, np.int32)
-    cutoff = np.zeros(rows, np.float32)
+    cutoff = np.zeros(rows, np.int32 if dtype == "i32" else np.float32)
     for b0 in range(0, rows, block_token):
         blk = slice(b0, b0 + block_token)
         for m in sched[1:]:
@@ -357,12 +392,17 @@ def top_dynamic_k(x, k, max_k, block_token=8, num_bins=128, schedule=None, repla
     sv = bv[:, :upper, :].reshape(rows, -1)
     si = bi[:, :upper, :].reshape(rows, -1)
     order = list_order(sv, si)[:, :NUM_LANES]
-    vals = round_to_dtype(np.take_along_axis(sv, order, 1)[:, :max_k], dtype).astype(np.float32)
+    vals = np.take_along_axis(sv, order, 1)[:, :max_k]
+    vals = vals.copy() if dtype == "i32" else round_to_dtype(vals, dtype).astype(np.float32)
     idxs = np.take_along_axis(si, order, 1)[:, :max_k].copy()
     if replace_val is not None:
         pos = np.arange(vals.shape[1])[None, :]
-        rv = round_to_dtype(np.float32(replace_val), dtype)
-        vals = np.where(pos < kk[:, None], vals, rv).astype(np.float32)
+        if dtype == "i32":
+            r = 0.0 if math.isnan(replace_val) else min(max(float(replace_val), -2.0 ** 31), 2.0 ** 31 - 1)
+            rv = np.int32(math.trunc(r))
+        else:
+            rv = round_to_dtype(np.float32(replace_val), dtype)
+        vals = np.where(pos < kk[:, None], vals, rv).astype(vals.dtype)
     if guarantee_convergence:
         return vals, idxs
     return vals, idxs, valid, depths, cutoff

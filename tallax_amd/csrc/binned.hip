@@ -66,7 +66,8 @@ struct BinArgs {
   int gsched[kMaxSteps + 1];  // power-of-two depth buckets, ascending
   int ngs;
   int has_replace;
-  float replace_val;       // in the input dtype
+  float replace_val;       // in the input dtype (float inputs)
+  int32_t replace_i;       // int32 inputs: replace_val converted with saturation
   int merge;               // bin-packing merge of unconverged blocks
   int num_packed;          // bins packed by the merge (a power of two <= 128)
   void* out_vals;
@@ -95,25 +96,69 @@ __device__ __forceinline__ float load_val(const void* x, int dt, int64_t i) {
 __device__ __forceinline__ float dtype_min_f(int dt) {
   return dt == kBF16 ? __uint_as_float(0xFF7F0000u) : -FLT_MAX;
 }
+
+// The 32-bit values the per-bin lists hold: float for float32 and bfloat16
+// inputs (bfloat16 widened), int32 for int32 inputs.  The lists only compare,
+// take maxima of and move values, so one template covers both; the workspace
+// arrays are 32-bit either way.
+//   lowest    the dtype's min, where bins start (finfo.min / iinfo.min,
+//             top_k.py:241-243 via utils.py:48-56); only strictly greater
+//             values are admitted (top_k.py:64)
+//   pad       value of a slot past the row: never admitted
+//   key       the unsigned select key (monotone, 0 = nothing below it)
+//   fill      what the bin-packing merge writes into a chosen bin: the min of
+//             the 32-bit scratch dtype (top_k.py:147-151)
+template <typename VT>
+struct BinVal;
+template <>
+struct BinVal<float> {
+  static constexpr bool kInt = false;
+  static __device__ __forceinline__ float load(const void* x, int dt, int64_t i) { return load_val(x, dt, i); }
+  static __device__ __forceinline__ float lowest(int dt) { return dtype_min_f(dt); }
+  static __device__ __forceinline__ float pad() { return -INFINITY; }
+  static __device__ __forceinline__ float vmax(float a, float b) { return fmaxf(a, b); }
+  static __device__ __forceinline__ uint32_t key(float v) { return select_key(__float_as_uint(v)); }
+  static __device__ __forceinline__ float from_key(uint32_t k) { return __uint_as_float(key_to_bits(k)); }
+  static __device__ __forceinline__ float fill() { return -FLT_MAX; }
+  static __device__ __forceinline__ uint32_t bits(float v) { return __float_as_uint(v); }
+  static __device__ __forceinline__ float from_bits(uint32_t u) { return __uint_as_float(u); }
+};
+template <>
+struct BinVal<int32_t> {
+  static constexpr bool kInt = true;
+  static __device__ __forceinline__ int32_t load(const void* x, int, int64_t i) { return ((const int32_t*)x)[i]; }
+  static __device__ __forceinline__ int32_t lowest(int) { return INT32_MIN; }
+  static __device__ __forceinline__ int32_t pad() { return INT32_MIN; }
+  static __device__ __forceinline__ int32_t vmax(int32_t a, int32_t b) { return a > b ? a : b; }
+  static __device__ __forceinline__ uint32_t key(int32_t v) { return (uint32_t)v ^ 0x80000000u; }
+  static __device__ __forceinline__ int32_t from_key(uint32_t k) { return (int32_t)(k ^ 0x80000000u); }
+  static __device__ __forceinline__ int32_t fill() { return INT32_MIN; }
+  static __device__ __forceinline__ uint32_t bits(int32_t v) { return (uint32_t)v; }
+  static __device__ __forceinline__ int32_t from_bits(uint32_t u) { return (int32_t)u; }
+};
+
 // (value desc, index asc) order: a before b
-__device__ __forceinline__ bool ahead(float va, int32_t ia, float vb, int32_t ib) {
+template <typename VT>
+__device__ __forceinline__ bool ahead(VT va, int32_t ia, VT vb, int32_t ib) {
   return va > vb || (va == vb && (uint32_t)ia < (uint32_t)ib);
 }
 
 // Full scan of one row by a kBinNT-thread workgroup; smem holds
 // kBinNT * MC * 8 bytes.
-template <int MC>
+template <int MC, typename VT>
 __device__ __forceinline__ void scan_row(const BinArgs& a, int64_t row, unsigned char* smem) {
+  using B = BinVal<VT>;
   const int NB = a.num_bins;
   const int S = kBinNT / NB;  // slices per bin
-  float* sv = (float*)smem;                         // [S][MC][NB]
+  VT* sv = (VT*)smem;                               // [S][MC][NB]
   int32_t* si = (int32_t*)(sv + (size_t)S * MC * NB);
-  __shared__ float red_f[kBinNT / kWave];
+  VT* lv = (VT*)a.lv;
+  __shared__ VT red_f[kBinNT / kWave];
   __shared__ int red_i[kBinNT / kWave];
   const int t = threadIdx.x;
   const int b = t % NB, s = t / NB;
-  const float lo = dtype_min_f(a.dtype);
-  float v[MC];
+  const VT lo = B::lowest(a.dtype);
+  VT v[MC];
   int32_t id[MC];
 #pragma unroll
   for (int r = 0; r < MC; ++r) {
@@ -128,21 +173,21 @@ __device__ __forceinline__ void scan_row(const BinArgs& a, int64_t row, unsigned
   constexpr int U = MC <= 8 ? 16 : 8;
   const int j0 = s * NB + b;
   for (int64_t jb = j0; jb < a.cols; jb += (int64_t)U * step) {
-    float xs[U];
+    VT xs[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t j = jb + (int64_t)u * step;
-      xs[u] = j < a.cols ? load_val(a.x, a.dtype, base + j) : -INFINITY;
+      xs[u] = j < a.cols ? B::load(a.x, a.dtype, base + j) : B::pad();
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      float x = xs[u];
+      VT x = xs[u];
       if (x > v[MC - 1]) {  // strict: ties keep the earlier (lower) index; NaN never enters
         int32_t xi = (int32_t)(jb + (int64_t)u * step);
 #pragma unroll
         for (int r = 0; r < MC; ++r) {
           const bool sw = x > v[r];
-          const float tv = v[r];
+          const VT tv = v[r];
           const int32_t ti = id[r];
           v[r] = sw ? x : tv;
           id[r] = sw ? xi : ti;
@@ -159,7 +204,7 @@ __device__ __forceinline__ void scan_row(const BinArgs& a, int64_t row, unsigned
   }
   // fillers for every rank of this bin's output list (real entries overwrite them)
   for (int r = s; r < a.buf; r += S) {
-    a.lv[((size_t)row * a.buf + r) * NB + b] = lo;
+    lv[((size_t)row * a.buf + r) * NB + b] = lo;
     a.li[((size_t)row * a.buf + r) * NB + b] = -1;
   }
   __syncthreads();
@@ -173,7 +218,7 @@ __device__ __forceinline__ void scan_row(const BinArgs& a, int64_t row, unsigned
     for (int h = 0; h < MC; ++h) {
       const int32_t ci = si[((size_t)q * MC + h) * NB + b];
       if (ci < 0) continue;
-      const float cv = sv[((size_t)q * MC + h) * NB + b];
+      const VT cv = sv[((size_t)q * MC + h) * NB + b];
       ++nreal;
 #pragma unroll
       for (int r = 0; r < MC; ++r) rank[r] += ahead(cv, ci, v[r], id[r]) ? 1 : 0;
@@ -183,7 +228,7 @@ __device__ __forceinline__ void scan_row(const BinArgs& a, int64_t row, unsigned
 #pragma unroll
   for (int r = 0; r < MC; ++r) {
     if (id[r] >= 0 && rank[r] < a.buf) {
-      a.lv[((size_t)row * a.buf + rank[r]) * NB + b] = v[r];
+      lv[((size_t)row * a.buf + rank[r]) * NB + b] = v[r];
       a.li[((size_t)row * a.buf + rank[r]) * NB + b] = id[r];
     }
   }
@@ -193,17 +238,21 @@ __device__ __forceinline__ void scan_row(const BinArgs& a, int64_t row, unsigned
   const int kept = nreal < MC ? nreal : MC;  // real entries in the bin's merged list
   for (int q = 0; q < a.nsteps; ++q) {
     const int m = a.steps[q];
-    float pv = -INFINITY;
+    VT pv = B::pad();
 #pragma unroll
     for (int r = 0; r < MC; ++r)
-      if (id[r] >= 0 && rank[r] == m - 1) pv = fmaxf(pv, v[r]);
-    if (s == 0 && kept < m) pv = fmaxf(pv, lo);  // the bin's m-th entry is a filler
-#pragma unroll
-    for (int d = kWave / 2; d >= 1; d >>= 1) pv = fmaxf(pv, lane_xor_f(pv, d));
+      if (id[r] >= 0 && rank[r] == m - 1) pv = B::vmax(pv, v[r]);
+    if (s == 0 && kept < m) pv = B::vmax(pv, lo);  // the bin's m-th entry is a filler
+    pv = B::vmax(pv, B::from_bits(lane_xor(B::bits(pv), 32)));
+    pv = B::vmax(pv, B::from_bits(lane_xor(B::bits(pv), 16)));
+    pv = B::vmax(pv, B::from_bits(lane_xor(B::bits(pv), 8)));
+    pv = B::vmax(pv, B::from_bits(lane_xor(B::bits(pv), 4)));
+    pv = B::vmax(pv, B::from_bits(lane_xor(B::bits(pv), 2)));
+    pv = B::vmax(pv, B::from_bits(lane_xor(B::bits(pv), 1)));
     if (l == 0) red_f[w] = pv;
     __syncthreads();
-    float pivot = red_f[0];
-    for (int i = 1; i < NW; ++i) pivot = fmaxf(pivot, red_f[i]);
+    VT pivot = red_f[0];
+    for (int i = 1; i < NW; ++i) pivot = B::vmax(pivot, red_f[i]);
     int c = 0;
 #pragma unroll
     for (int r = 0; r < MC; ++r) c += (id[r] >= 0 && rank[r] < m - 1 && v[r] >= pivot) ? 1 : 0;
@@ -214,17 +263,17 @@ __device__ __forceinline__ void scan_row(const BinArgs& a, int64_t row, unsigned
     if (t == 0) {
       int tot = 0;
       for (int i = 0; i < NW; ++i) tot += red_i[i];
-      a.st_pivot[row * a.nsteps + q] = pivot;
+      ((VT*)a.st_pivot)[row * a.nsteps + q] = pivot;
       a.st_count[row * a.nsteps + q] = tot;
     }
     __syncthreads();
   }
 }
 
-template <int MC>
+template <int MC, typename VT>
 __global__ __launch_bounds__(kBinNT) void binned_lists_kernel(BinArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  scan_row<MC>(a, blockIdx.x, smem);
+  scan_row<MC, VT>(a, blockIdx.x, smem);
 }
 
 // Depths, cutoffs, valid, depth_upper and each row's last evaluated m from
@@ -275,12 +324,11 @@ __device__ __forceinline__ void finish_rows(const BinArgs& a) {
   __syncthreads();
   for (int64_t r = t; r < a.rows; r += kFinishNT) {
     const int last = a.blk_last[r / a.block_token];
-    a.out_cutoff[r] = a.st_pivot[r * a.nsteps + last];
+    ((uint32_t*)a.out_cutoff)[r] = ((const uint32_t*)a.st_pivot)[r * a.nsteps + last];  // float or int32 bits
     a.row_mlast[r] = a.steps[last];
   }
   const int l = lane_id();
-#pragma unroll
-  for (int d = kWave / 2; d >= 1; d >>= 1) gmax = max(gmax, (int)lane_xor((uint32_t)gmax, d));
+  gmax = wave_max_i(gmax);
   if (l == 0) red[t / kWave] = gmax;
   __syncthreads();
   if (t == 0) {
@@ -507,7 +555,7 @@ __global__ __launch_bounds__(kCandNT) void binned_cand_kernel(BinArgs a) {
     }
   } else {
     __syncthreads();  // the scan reuses the LDS
-    scan_row<MC>(a, row, smem);
+    scan_row<MC, float>(a, row, smem);
   }
 }
 
@@ -516,8 +564,9 @@ __host__ __device__ inline size_t cand_lds_bytes(int nb) { return (size_t)nb * c
 // composite of a list entry: value descending then index ascending as an
 // unsigned number, so that a scratch filler (finfo.min, index -1) follows
 // every entry of its value or above with a real index; 0 stays "no entry"
-__device__ __forceinline__ uint64_t entry_comp(float v, int32_t i) {
-  return make_comp(select_key(__float_as_uint(v)), (uint32_t)i);
+template <typename VT>
+__device__ __forceinline__ uint64_t entry_comp(VT v, int32_t i) {
+  return make_comp(BinVal<VT>::key(v), (uint32_t)i);
 }
 
 // float -> bfloat16 bits, nearest even (NaN kept quiet): list values are
@@ -557,8 +606,9 @@ __device__ __forceinline__ void tree_merge128(uint64_t acc[2], int nwr, uint64_t
 // saves a kernel launch; otherwise binned_finish_kernel ran before.
 constexpr int kSelNT = 1024;
 static_assert(kSelNT == kFinishNT, "the inline finish step uses one thread per row");
-template <bool INLINE>
+template <bool INLINE, typename VT>
 __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
+  using B = BinVal<VT>;
   constexpr int NW = kSelNT / kWave;
   __shared__ uint64_t tree[NW][128];
   __shared__ int fcs[kSelNT];
@@ -570,16 +620,16 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
   // this wave's 128-entry runs of all buf ranks are loaded before depth_upper is known
   constexpr int kPre = 2;  // runs per wave prefetched
   const int nall = a.buf * NB;
-  const float* lv = a.lv + (size_t)row * a.buf * NB;  // rank-major: entry e = rank * NB + bin
+  const VT* lv = (const VT*)a.lv + (size_t)row * a.buf * NB;  // rank-major: entry e = rank * NB + bin
   const int32_t* li = a.li + (size_t)row * a.buf * NB;
-  float pv[kPre][2];
+  VT pv[kPre][2];
   int32_t pi[kPre][2];
 #pragma unroll
   for (int k = 0; k < kPre; ++k) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int e = (w + k * NW) * 128 + h * kWave + l;
-      pv[k][h] = e < nall ? lv[e] : 0.0f;
+      pv[k][h] = e < nall ? lv[e] : (VT)0;
       pi[k][h] = e < nall ? li[e] : -1;
     }
   }
@@ -589,8 +639,7 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
     const int fc = live ? first_converged(a, t) : a.nsteps;
     fcs[t] = fc;
     int g = live ? (fc < a.nsteps ? a.steps[fc] - 1 : a.max_k) : 0;
-#pragma unroll
-    for (int d = kWave / 2; d >= 1; d >>= 1) g = max(g, (int)lane_xor((uint32_t)g, d));
+    g = wave_max_i(g);
     if (l == 0) red[w] = g;
     __syncthreads();
     g = 0;
@@ -605,7 +654,7 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
       const int last = qb < a.nsteps - 1 ? qb : a.nsteps - 1;
       const int fr = fcs[r];
       a.out_depths[row] = fr < a.nsteps ? a.steps[fr] - 1 : a.max_k;
-      a.out_cutoff[row] = a.st_pivot[row * a.nsteps + last];
+      ((uint32_t*)a.out_cutoff)[row] = ((const uint32_t*)a.st_pivot)[row * a.nsteps + last];
       if (row == 0) a.out_valid[0] = (g < a.steps[a.nsteps - 1] || a.steps[a.nsteps - 1] == a.max_k) ? 1 : 0;
       s_mlast = a.steps[last];
     }
@@ -643,25 +692,29 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
   }
   tree_merge128<NW>(acc, nr < NW ? nr : NW, tree);  // waves holding a list
   if (w != 0) return;
-  const float lo = dtype_min_f(a.dtype);
+  const VT lo = B::lowest(a.dtype);
   const int kr = a.k_rows[row];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int p = h * kWave + l;
     if (p >= a.max_k) continue;
     const uint64_t c = acc[h];
-    float v = lo;
+    VT v = lo;
     int32_t id = -1;
     if (c != 0ull) {
-      v = __uint_as_float(key_to_bits(comp_key(c)));
+      v = B::from_key(comp_key(c));
       id = comp_idx(c);
     }
-    if (a.has_replace && p >= kr) v = a.replace_val;
     const int64_t o = row * a.max_k + p;
-    if (a.dtype == kBF16)
-      ((uint16_t*)a.out_vals)[o] = bf16_bits_rne(v);
-    else
-      ((float*)a.out_vals)[o] = v;
+    if constexpr (B::kInt) {
+      ((int32_t*)a.out_vals)[o] = (a.has_replace && p >= kr) ? a.replace_i : (int32_t)v;
+    } else {
+      if (a.has_replace && p >= kr) v = a.replace_val;
+      if (a.dtype == kBF16)
+        ((uint16_t*)a.out_vals)[o] = bf16_bits_rne(v);
+      else
+        ((float*)a.out_vals)[o] = v;
+    }
     a.out_idx[o] = id;
   }
 }
@@ -686,7 +739,9 @@ __global__ __launch_bounds__(kSelNT) void binned_select_kernel(BinArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kMergeNT = 1024;
 static_assert(kMergeNT >= kBinNT, "one thread per bin");
+template <typename VT>
 __global__ __launch_bounds__(kMergeNT) void binned_merge_kernel(BinArgs a) {
+  using B = BinVal<VT>;
   constexpr int NW = kMergeNT / kWave;
   __shared__ uint64_t tree[NW][128];
   __shared__ int s_chosen[128];
@@ -700,9 +755,9 @@ __global__ __launch_bounds__(kMergeNT) void binned_merge_kernel(BinArgs a) {
   int open = 0;
   for (int64_t i = t; i < a.block_token; i += kMergeNT) open |= a.row_fc[b0 + i] >= a.nsteps ? 1 : 0;
   if (!__syncthreads_or(open)) return;  // the block converged
-  float* lv = a.lv + (size_t)row * a.buf * NB;  // rank-major: entry rank * NB + bin
+  VT* lv = (VT*)a.lv + (size_t)row * a.buf * NB;  // rank-major: entry rank * NB + bin
   int32_t* li = a.li + (size_t)row * a.buf * NB;
-  const float pivot = a.st_pivot[row * a.nsteps + last];
+  const VT pivot = ((const VT*)a.st_pivot)[row * a.nsteps + last];
   // 1. counts, as (count, bin) composites in LDS, then the top 128 of them
   uint64_t* cb = &tree[0][0];  // NB <= NW * 128 entries
   if (t < NB) {
@@ -740,17 +795,17 @@ __global__ __launch_bounds__(kMergeNT) void binned_merge_kernel(BinArgs a) {
   const int64_t V = a.cols;
   const int64_t npk = (V + (int64_t)128 * (NB / P) - 1) / ((int64_t)128 * (NB / P)) * 128;
   const int64_t nr = npk / 128 + 1;  // runs; the last one is rank 0 of bins 0..127
-  const float lo = dtype_min_f(a.dtype);
-  const uint32_t lo_key = select_key(__float_as_uint(lo));
+  const VT lo = B::lowest(a.dtype);
+  const uint32_t lo_key = B::key(lo);
   const int64_t xrow = row * V;
   auto entry = [&](int64_t e) -> uint64_t {
     if (e < npk) {
       const int64_t col = (e / P) * NB + s_chosen[e % P];
-      const uint32_t key = col < V ? select_key(__float_as_uint(load_val(a.x, a.dtype, xrow + col))) : lo_key;
+      const uint32_t key = col < V ? B::key(B::load(a.x, a.dtype, xrow + col)) : lo_key;
       return make_comp(key, (uint32_t)col);
     }
     const int c = (int)(e - npk);
-    return entry_comp(s_isch[c] ? -FLT_MAX : lv[c], li[c]);
+    return entry_comp<VT>(s_isch[c] ? B::fill() : lv[c], li[c]);
   };
   constexpr int U = 4;  // runs loaded per batch
   acc[0] = acc[1] = 0ull;
@@ -789,14 +844,14 @@ __global__ __launch_bounds__(kMergeNT) void binned_merge_kernel(BinArgs a) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int p = h * kWave + l;
-      lv[p] = __uint_as_float(key_to_bits(comp_key(acc[h])));
+      lv[p] = B::from_key(comp_key(acc[h]));
       li[p] = comp_idx(acc[h]);
     }
   }
   for (int e = t; e < a.buf * P; e += kMergeNT) {
     const int r = e / P, b = s_chosen[e % P];
     if (r == 0 && b < 128) continue;  // written above
-    lv[(size_t)r * NB + b] = -FLT_MAX;
+    lv[(size_t)r * NB + b] = B::fill();
   }
 }
 
@@ -881,7 +936,10 @@ static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t co
     set_error("null pointer argument");
     return kInvalidArgument;
   }
-  if (dtype != kF32 && dtype != kBF16) { set_error("dtype %d not supported (f32=0, bf16=1)", dtype); return kUnsupported; }
+  if (dtype != kF32 && dtype != kBF16 && dtype != kI32) {
+    set_error("dtype %d not supported (f32=0, bf16=1, i32=2)", dtype);
+    return kUnsupported;
+  }
   if (rows < 0 || cols <= 0) { set_error("bad shape [%lld, %lld]", (long long)rows, (long long)cols); return kInvalidArgument; }
   if (max_k < 1 || max_k > 128) { set_error("max_k=%d outside [1, 128]", max_k); return max_k > 128 ? kUnsupported : kInvalidArgument; }
   if (block_token < 1 || rows % block_token) { set_error("num_tokens must be divisible by block_token"); return kInvalidArgument; }
@@ -953,6 +1011,11 @@ static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t co
     memcpy(&rv, &u, 4);
   }
   a.replace_val = rv;
+  // int32 logits: the replacement is stored into the int32 output, so it is
+  // converted toward zero and saturated at the int32 range (NaN -> 0)
+  double ri = replace_val != replace_val ? 0.0 : replace_val;
+  ri = ri < -2147483648.0 ? -2147483648.0 : (ri > 2147483647.0 ? 2147483647.0 : ri);
+  a.replace_i = (int32_t)ri;
   a.merge = merge ? 1 : 0;
   a.num_packed = packed;
   a.out_vals = out_vals; a.out_idx = out_idx; a.out_valid = out_valid; a.out_depths = out_depths;
@@ -985,7 +1048,8 @@ static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t co
   int nseg = 0, maxv = 0;
   int64_t vps = 0;
   const int min_seg = (num_bins * max_m + 127) / 128;
-  const bool cand = mode == 0 && max_m <= kCandRank &&
+  // the candidate path starts from the float segment kernel: float inputs only
+  const bool cand = mode == 0 && dtype != kI32 && max_m <= kCandRank &&
                     segment_lists_plan(cols, dtype, min_seg < 2 ? 2 : min_seg, &nseg, &maxv, &vps) == kOk &&
                     nseg <= kMaxSegLists;
   const int mc = buf <= 8 ? 8 : 16;
@@ -1013,13 +1077,25 @@ static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t co
       if (st) return st;
     }
   } else {
-    const hipError_t attr8 = set_dynamic_lds_limit((const void*)binned_lists_kernel<8>, 128 * 1024, stream);
-    const hipError_t attr16 = set_dynamic_lds_limit((const void*)binned_lists_kernel<16>, 128 * 1024, stream);
-    if (attr8 != hipSuccess || attr16 != hipSuccess) { set_error("hipFuncSetAttribute failed"); return kHipError; }
-    if (mc == 8)
-      hipLaunchKernelGGL(binned_lists_kernel<8>, dim3((unsigned)rows), dim3(kBinNT), lds_scan, stream, a);
-    else
-      hipLaunchKernelGGL(binned_lists_kernel<16>, dim3((unsigned)rows), dim3(kBinNT), lds_scan, stream, a);
+    const void* kern = dtype == kI32 ? (mc == 8 ? (const void*)binned_lists_kernel<8, int32_t>
+                                                : (const void*)binned_lists_kernel<16, int32_t>)
+                                     : (mc == 8 ? (const void*)binned_lists_kernel<8, float>
+                                                : (const void*)binned_lists_kernel<16, float>);
+    if (set_dynamic_lds_limit(kern, 128 * 1024, stream) != hipSuccess) {
+      set_error("hipFuncSetAttribute failed");
+      return kHipError;
+    }
+    if (dtype == kI32) {
+      if (mc == 8)
+        hipLaunchKernelGGL((binned_lists_kernel<8, int32_t>), dim3((unsigned)rows), dim3(kBinNT), lds_scan, stream, a);
+      else
+        hipLaunchKernelGGL((binned_lists_kernel<16, int32_t>), dim3((unsigned)rows), dim3(kBinNT), lds_scan, stream, a);
+    } else {
+      if (mc == 8)
+        hipLaunchKernelGGL((binned_lists_kernel<8, float>), dim3((unsigned)rows), dim3(kBinNT), lds_scan, stream, a);
+      else
+        hipLaunchKernelGGL((binned_lists_kernel<16, float>), dim3((unsigned)rows), dim3(kBinNT), lds_scan, stream, a);
+    }
     st = launch_status("tallax_top_dynamic_k");
     if (st) return st;
     hipLaunchKernelGGL(binned_finish_kernel, dim3(1), dim3(kFinishNT), 0, stream, a);
@@ -1032,13 +1108,18 @@ static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t co
       st = launch_status("tallax_top_dynamic_k");
       if (st) return st;
     }
-    hipLaunchKernelGGL(binned_merge_kernel, dim3((unsigned)rows), dim3(kMergeNT), 0, stream, a);
+    if (dtype == kI32)
+      hipLaunchKernelGGL(binned_merge_kernel<int32_t>, dim3((unsigned)rows), dim3(kMergeNT), 0, stream, a);
+    else
+      hipLaunchKernelGGL(binned_merge_kernel<float>, dim3((unsigned)rows), dim3(kMergeNT), 0, stream, a);
     st = launch_status("tallax_top_dynamic_k");
     if (st) return st;
   }
-  if (cand && rows <= kFinishNT && !merge)
-    hipLaunchKernelGGL(binned_select_kernel<true>, dim3((unsigned)rows), dim3(kSelNT), 0, stream, a);
+  if (dtype == kI32)
+    hipLaunchKernelGGL((binned_select_kernel<false, int32_t>), dim3((unsigned)rows), dim3(kSelNT), 0, stream, a);
+  else if (cand && rows <= kFinishNT && !merge)
+    hipLaunchKernelGGL((binned_select_kernel<true, float>), dim3((unsigned)rows), dim3(kSelNT), 0, stream, a);
   else
-    hipLaunchKernelGGL(binned_select_kernel<false>, dim3((unsigned)rows), dim3(kSelNT), 0, stream, a);
+    hipLaunchKernelGGL((binned_select_kernel<false, float>), dim3((unsigned)rows), dim3(kSelNT), 0, stream, a);
   return launch_status("tallax_top_dynamic_k");
 }

@@ -1730,6 +1730,59 @@ static int check_common(const void* x, int dt, int64_t rows, int64_t cols) {
   return kOk;
 }
 
+// ---------------------------------------------------------------------------
+// int32 logits (the reference's top-k is dtype-generic: bins start at
+// iinfo.min and admit only strictly greater values, utils.py:48-56,
+// top_k.py:64,241-243).  The exact answer under the lowest-index tie rule is
+// the first k of the row's stable descending sort: values descending, equal
+// values by ascending index, and iinfo.min elements (never admitted, so they
+// fill the tail with the dtype's min) last in index order.  The int32 row sort
+// (sort_rows.hip) writes that permutation into the workspace; this kernel
+// gathers the first k columns.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void topk_from_perm_kernel(const int32_t* __restrict__ x,
+                                                             const int32_t* __restrict__ perm, int64_t cols, int k,
+                                                             int32_t* __restrict__ out_vals,
+                                                             int32_t* __restrict__ out_idx,
+                                                             const int32_t* __restrict__ k_rows, int has_replace,
+                                                             int32_t replace_val, int64_t n) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+    const int64_t r = e / k;
+    const int j = (int)(e - r * k);
+    const int32_t p = perm[r * cols + j];  // in [0, cols): a permutation of the row
+    out_idx[e] = p;
+    out_vals[e] = (has_replace && j >= k_rows[r]) ? replace_val : x[r * cols + p];
+  }
+}
+
+static size_t topk_i32_ws(int64_t rows, int64_t cols) {
+  return align_up((size_t)rows * (size_t)cols * 4, 256) + sort_wide_workspace_bytes(rows, cols);
+}
+
+static int topk_i32(const void* x, int64_t rows, int64_t cols, int64_t k, const int32_t* k_rows, double replace_val,
+                    void* out_vals, int32_t* out_idx, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                    const char* what) {
+  const size_t need = topk_i32_ws(rows, cols);
+  if (!workspace || workspace_bytes < need) {
+    set_error("workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
+    return kWorkspaceTooSmall;
+  }
+  int32_t* perm = (int32_t*)workspace;
+  const size_t perm_bytes = align_up((size_t)rows * (size_t)cols * 4, 256);
+  int st = tallax_sort_rows_ws(x, kI32, rows, cols, /*descending=*/1, /*ties_descending=*/0, nullptr, perm, nullptr,
+                               0, nullptr, 0, nullptr, 0, (char*)workspace + perm_bytes, workspace_bytes - perm_bytes,
+                               stream);
+  if (st) return st;
+  // int32 outputs take replace_val converted toward zero, saturated at the int32 range (NaN -> 0)
+  double rv = replace_val != replace_val ? 0.0 : replace_val;
+  rv = rv < -2147483648.0 ? -2147483648.0 : (rv > 2147483647.0 ? 2147483647.0 : rv);
+  const int64_t n = rows * k;
+  const int64_t blocks = (n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536;
+  hipLaunchKernelGGL(topk_from_perm_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (const int32_t*)x, perm,
+                     cols, (int)k, (int32_t*)out_vals, out_idx, k_rows, k_rows ? 1 : 0, (int32_t)rv, n);
+  return launch_status(what);
+}
+
 }  // namespace tx
 
 using namespace tx;
@@ -1738,19 +1791,23 @@ extern "C" {
 
 size_t tallax_topk_workspace_size(int64_t rows, int64_t cols, int64_t k, int dtype) {
   Plan p;
-  if (k < 1 || k > kMaxK || (dtype != kF32 && dtype != kBF16) || rows < 0 || cols <= 0) return 0;
+  if (k < 1 || k > kMaxK || rows < 0 || cols <= 0) return 0;
+  if (dtype == kI32) return topk_i32_ws(rows, cols);
+  if (dtype != kF32 && dtype != kBF16) return 0;
   if (plan_rows(rows, cols, dtype, &p) != kOk) return 0;
   return ws_bytes_for(rows, p);
 }
 
 int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k, void* out_vals,
                 int32_t* out_idx, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  int st = check_common(x, dtype, rows, cols);
+  int st = check_common(x, dtype == kI32 ? kF32 : dtype, rows, cols);
   if (st) return st;
   if (k < 1 || k > kMaxK) { set_error("k=%lld outside [1, %d]", (long long)k, kMaxK); return k > kMaxK ? kUnsupported : kInvalidArgument; }
   if (k > cols) { set_error("k=%lld exceeds row length %lld", (long long)k, (long long)cols); return kInvalidArgument; }
   if (!out_vals || !out_idx) { set_error("null output pointer"); return kInvalidArgument; }
   if (rows == 0) return kOk;
+  if (dtype == kI32)
+    return topk_i32(x, rows, cols, k, nullptr, 0.0, out_vals, out_idx, workspace, workspace_bytes, stream, "tallax_topk");
   Plan p;
   st = plan_rows(rows, cols, dtype, &p);
   if (st) return st;
@@ -1771,12 +1828,15 @@ int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k,
 int tallax_topk_replace(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k, const int32_t* k_rows,
                         double replace_val, void* out_vals, int32_t* out_idx, void* workspace,
                         size_t workspace_bytes, hipStream_t stream) {
-  int st = check_common(x, dtype, rows, cols);
+  int st = check_common(x, dtype == kI32 ? kF32 : dtype, rows, cols);
   if (st) return st;
   if (k < 1 || k > kMaxK) { set_error("k=%lld outside [1, %d]", (long long)k, kMaxK); return k > kMaxK ? kUnsupported : kInvalidArgument; }
   if (k > cols) { set_error("k=%lld exceeds row length %lld", (long long)k, (long long)cols); return kInvalidArgument; }
   if (!out_vals || !out_idx || !k_rows) { set_error("null pointer argument"); return kInvalidArgument; }
   if (rows == 0) return kOk;
+  if (dtype == kI32)
+    return topk_i32(x, rows, cols, k, k_rows, replace_val, out_vals, out_idx, workspace, workspace_bytes, stream,
+                    "tallax_topk_replace");
   Plan p;
   st = plan_rows(rows, cols, dtype, &p);
   if (st) return st;

@@ -169,6 +169,17 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
+// Wave maximum, written out step by step: a loop over the distances is not
+// always unrolled, and lane_xor needs constant distances.
+__device__ __forceinline__ int wave_max_i(int v) {
+  v = max(v, (int)lane_xor((uint32_t)v, 32));
+  v = max(v, (int)lane_xor((uint32_t)v, 16));
+  v = max(v, (int)lane_xor((uint32_t)v, 8));
+  v = max(v, (int)lane_xor((uint32_t)v, 4));
+  v = max(v, (int)lane_xor((uint32_t)v, 2));
+  return max(v, (int)lane_xor((uint32_t)v, 1));
+}
+
 __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
   for (int d = kWave / 2; d >= 1; d >>= 1) v += lane_xor_f(v, d);

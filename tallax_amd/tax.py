@@ -29,7 +29,9 @@ def top_k(logits: torch.Tensor, k: int, block_token: int = 8, num_bins: int = NU
 
     Reference: top_k (tallax/_src/top_k.py:516-567).  Ties are broken to the
     lowest index.  k > 128 raises NotImplementedError as in the reference
-    (top_k.py:438-439).
+    (top_k.py:438-439).  float32, bfloat16 and int32 logits (the reference is
+    dtype-generic, utils.py:48-56): slots only the dtype's min (or NaN, -inf)
+    could fill hold the dtype's min.
     """
     del block_token, num_bins, bins_topm_unroll, bins_topm_schedule, interpret
     _lib.require_cuda(logits)
@@ -42,8 +44,6 @@ def top_k(logits: torch.Tensor, k: int, block_token: int = 8, num_bins: int = NU
         raise ValueError(f"k={k} must be in [1, {cols}]")
     x = logits.contiguous()
     dt = _lib.dtype_code(x)
-    if dt == _lib.I32:
-        raise NotImplementedError("top_k on int32 logits is not supported")
     vals = torch.empty((rows, k), dtype=x.dtype, device=x.device)
     idx = torch.empty((rows, k), dtype=torch.int32, device=x.device)
     need = _lib.LIB.tallax_topk_workspace_size(rows, cols, k, dt)
@@ -75,7 +75,8 @@ def top_dynamic_k(logits: torch.Tensor, k, max_k: int, block_token: int = 8, num
     Reference: top_dynamic_k (tallax/_src/top_k.py:385-514).
       * guarantee_convergence=False: the binned algorithm, returning
         (vals [R, max_k], idxs [R, max_k] int32, valid (bool scalar tensor),
-        depths [R] int32, cutoff_vals [R] float32).  Bins are columns mod
+        depths [R] int32, cutoff_vals [R] float32 -- int32 for int32 logits,
+        the reference's to_32bit_dtype, top_k.py:465).  Bins are columns mod
         num_bins; the schedule (auto from the convergence theory if None)
         decides depths/cutoffs; the result is the top-128 of the first
         depth_upper ranks of every bin, ordered by value then lowest index.
@@ -88,7 +89,8 @@ def top_dynamic_k(logits: torch.Tensor, k, max_k: int, block_token: int = 8, num
         0 of bins 0..127.  Like the reference, no max_k step is added to the
         schedule; this needs m >= 2 and num_bins % 128 == 0 (ValueError /
         NotImplementedError otherwise).  For the exact answer use tax.top_k.
-    Positions >= k[row] hold replace_val (in the logits dtype) when given.
+    Positions >= k[row] hold replace_val (in the logits dtype; int32 logits
+    take it converted toward zero, saturated at the int32 range) when given.
     Raises ValueError if rows % block_token != 0 and NotImplementedError for
     max_k > 128, like the reference.  `workspace` (keyword only): a uint8
     device tensor of at least the entry point's workspace size, used instead
@@ -115,8 +117,6 @@ def _top_dynamic_k(logits, k, max_k, block_token, num_bins, bins_topm_unroll, bi
         raise NotImplementedError(f"max_k={max_k} > {NUM_LANES}")
     x = logits.contiguous()
     dt = _lib.dtype_code(x)
-    if dt == _lib.I32:
-        raise NotImplementedError("top_dynamic_k on int32 logits is not supported")
     kr = _k_rows(k, rows, x.device)
     dev = x.device
     stream = _lib.stream_of(x)
@@ -134,7 +134,7 @@ def _top_dynamic_k(logits, k, max_k, block_token, num_bins, bins_topm_unroll, bi
     ws = _lib.workspace_arg(workspace, dev, max(need, 1))
     valid = torch.empty(1, dtype=torch.int32, device=dev)
     depths = torch.empty(rows, dtype=torch.int32, device=dev)
-    cutoff = torch.empty(rows, dtype=torch.float32, device=dev)
+    cutoff = torch.empty(rows, dtype=torch.int32 if dt == _lib.I32 else torch.float32, device=dev)
     args = (x.data_ptr(), dt, rows, cols, kr.data_ptr(), max_k, block_token, num_bins, arr, len(steps),
             int(bool(guarantee_convergence)), int(replace_val is not None), float(replace_val) if replace_val is not None else 0.0, vals.data_ptr(),
             idx.data_ptr(), valid.data_ptr(), depths.data_ptr(), cutoff.data_ptr(), ws.data_ptr(), ws.numel(),

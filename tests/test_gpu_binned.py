@@ -241,6 +241,87 @@ def test_top_dynamic_k_sampler_call_on_config4_is_exact(gpu):
     assert np.array_equal(np.where(inside, wi, -2), np.where(inside, ei, -2))
 
 
+def test_top_dynamic_k_sampler_call_unclipped_k_on_config4(gpu):
+    """The reference sampler's own top-k call (sampling.py:283-290, 333-336)
+    with the per-row k it really passes: tpu_sampling_metadata.top_k is not
+    clipped, so k[row] in [1, 1024] enters the convergence test
+    (top_k.py:298) and most blocks cannot converge, reaching the bin-packing
+    merge (top_k.py:317-331).  Bit-exact against the oracle on the same call;
+    the merged result equals the exact top-128 inside min(k, 128); and the
+    reference route (this top-k, then top_p_and_sample) gives the fused
+    sampler's tokens."""
+    from tallax_amd import sampling, tax
+    _log("config 4 sampler top-k call, unclipped k in [1, 1024]")
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((256, 128256)) * 3).astype(np.float32)
+    k = rng.integers(1, 1025, 256).astype(np.int32)
+    temp = rng.uniform(0.5, 1.5, 256).astype(np.float32)
+    topp = rng.uniform(0.7, 1.0, 256).astype(np.float32)
+    xd = to_dev(x, "bf16", gpu)
+    vals, idx = tax.top_dynamic_k(xd, torch.from_numpy(k).to(gpu), 128, num_bins=256, bins_topm_schedule=(5, 9),
+                                  guarantee_convergence=True, replace_val=-1e12)
+    torch.cuda.synchronize()
+    hv = O.round_to_dtype(x, "bf16")
+    wv, wi = O.top_dynamic_k(hv, k, 128, num_bins=256, schedule=(5, 9), replace_val=-1e12, dtype="bf16",
+                             guarantee_convergence=True)
+    assert np.array_equal(idx.cpu().numpy(), wi)
+    assert np.array_equal(bits(from_dev_vals(vals)), bits(wv))
+    _, _, valid, depths, _ = O.top_dynamic_k(hv, k, 128, num_bins=256, schedule=(5, 9), dtype="bf16")
+    unconv = (depths.reshape(-1, 8) == 128).any(axis=1)
+    _log(f"blocks through the merge: {int(unconv.sum())} of 32; rows at depth 128: {int((depths == 128).sum())}")
+    assert not valid and unconv.any()
+    ev, ei = O.top_k(hv, 128, dtype="bf16")
+    inside = np.arange(128)[None, :] < np.minimum(k, 128)[:, None]
+    assert np.array_equal(np.where(inside, wi, -2), np.where(inside, ei, -2))
+    key = (0, 1234)
+    route = O.top_p_and_sample(wv, wi, key, topp, temp, 128256, -1e12)
+    meta = sampling.SamplingMetadata(torch.from_numpy(k), torch.from_numpy(topp), torch.from_numpy(temp))
+    tok = sampling.sample(key, xd, meta)
+    torch.cuda.synchronize()
+    assert np.array_equal(tok.cpu().numpy(), route)
+
+
+def _int32_cases():
+    imin = np.iinfo(np.int32).min
+    rng = np.random.default_rng(31)
+    a = rng.integers(0, 1000, (16, 20000)).astype(np.int32)           # heavy ties
+    a[3, ::7] = imin
+    yield "ties", a, rng.integers(1, 65, 16).astype(np.int32), 64, 128, 8, None, False
+    b = rng.integers(-2 ** 31 + 1, 2 ** 31 - 1, (16, 3000), dtype=np.int64).astype(np.int32)
+    for r in (5, 6):                                                    # unconverged block 0
+        b[r, rng.choice(3000 // 128, 20, replace=False) * 128] = 2 ** 31 - 1 - rng.permutation(20)
+    yield "unconverged, merge", b, np.full(16, 32, np.int32), 32, 128, 8, (3, 6), True
+    yield "unconverged, no merge", b, np.full(16, 32, np.int32), 32, 128, 8, (3, 6), False
+    c = np.full((8, 700), imin, np.int32)
+    for r in range(8):
+        c[r, rng.choice(700, 6 + r, replace=False)] = rng.integers(-1000, 1000, 6 + r)
+    yield "mostly iinfo.min", c, rng.integers(1, 17, 8).astype(np.int32), 16, 32, 4, (2, 5), False
+
+
+@pytest.mark.parametrize("replace", [None, -1e12, 7.9], ids=["no_replace", "replace_min", "replace_7"])
+@pytest.mark.parametrize("case", list(_int32_cases()), ids=lambda c: c[0] if isinstance(c, tuple) else str(c))
+def test_top_dynamic_k_int32(gpu, binned_mode, case, replace):
+    """int32 logits (the reference's dtype-generic path: iinfo.min bins,
+    utils.py:48-56): values, indices, valid, depths and int32 cutoff_vals
+    bit-exact against the oracle, which the literal block restatement pins
+    for int32 in test_oracle.py.  int32 always takes the full scan."""
+    from tallax_amd import tax
+    name, x, k, max_k, nb, bt, sched, gc = case
+    _log(f"top_dynamic_k int32 {name} [{x.shape[0]},{x.shape[1]}] replace={replace} path={binned_mode}")
+    out = tax._top_dynamic_k(torch.from_numpy(x).to(gpu), torch.from_numpy(k).to(gpu), max_k, bt, nb, 32, sched,
+                             gc, replace, False, None, binned_mode)
+    torch.cuda.synchronize()
+    want = O.top_dynamic_k(x, k, max_k, block_token=bt, num_bins=nb, schedule=sched, replace_val=replace,
+                           dtype="i32", guarantee_convergence=gc)
+    assert out[0].dtype == torch.int32
+    assert np.array_equal(out[1].cpu().numpy(), want[1])
+    assert np.array_equal(out[0].cpu().numpy(), want[0])
+    if not gc:
+        assert bool(out[2].item()) == want[2]
+        assert np.array_equal(out[3].cpu().numpy(), want[3])
+        assert out[4].dtype == torch.int32 and np.array_equal(out[4].cpu().numpy(), want[4])
+
+
 def test_top_dynamic_k_errors(gpu):
     from tallax_amd import tax
     x = torch.zeros((12, 100), device=gpu)

@@ -581,6 +581,92 @@ def test_binned_topm_brute_force():
                     assert i[r, q, b] == li[q]
 
 
+def test_int32_topk_brute_force():
+    """int32 top-k (dtype-generic reference: iinfo bins, utils.py:48-56): the
+    oracle equals a brute-force sort by (value descending, index ascending),
+    with iinfo.min -- never admitted, the dtype's min -- last in index order;
+    also on heavy ties (randint(0, 1000), bitonic_topk_test.py:20-23)."""
+    rng = np.random.default_rng(21)
+    imin, imax = np.iinfo(np.int32).min, np.iinfo(np.int32).max
+    for trial in range(60):
+        n = int(rng.integers(1, 60)); k = int(rng.integers(1, n + 1))
+        row = rng.integers(-4, 5, n).astype(np.int32)
+        sp = rng.random(n)
+        row[sp < 0.15] = imin
+        row[(sp >= 0.15) & (sp < 0.25)] = imax
+        order = sorted(range(n), key=lambda j: (-int(row[j]), j))[:k]
+        v, i = O.top_k(row[None], k, "i32")
+        assert v.dtype == np.int32 and np.array_equal(i[0], np.array(order, np.int32))
+        assert np.array_equal(v[0], row[order])
+    x = rng.integers(0, 1000, (13, 167)).astype(np.int32)
+    v, i = O.top_k(x, 128, "i32")
+    for r in range(13):
+        order = sorted(range(167), key=lambda j: (-int(x[r, j]), j))[:128]
+        assert np.array_equal(i[r], order) and np.array_equal(v[r], x[r, order])
+
+
+def test_int32_binned_topm_literal():
+    """binned_top_k on int32 simulated literally (strict-> sinking insert from
+    iinfo.min): values at every rank equal the oracle's, and indices where the
+    value is untied in its bin."""
+    rng = np.random.default_rng(22)
+    imin = np.iinfo(np.int32).min
+    x = rng.integers(-6, 7, (3, 90)).astype(np.int32)
+    x[0, ::7] = imin
+    x[1, 60:] = rng.integers(-2 ** 31 + 1, 2 ** 31 - 1, 30).astype(np.int32)   # untied values
+    v, i = O.binned_topm(x, 5, 8, "i32")
+    assert v.dtype == np.int32
+    for r in range(3):
+        for b in range(8):
+            lv, li = [imin] * 5, [-1] * 5
+            for j in range(b, 90, 8):
+                bv, bi = int(x[r, j]), j
+                for q in range(5):
+                    if bv > lv[q]:
+                        lv[q], bv = bv, lv[q]
+                        li[q], bi = bi, li[q]
+            assert np.array_equal(v[r, :, b], np.array(lv, np.int32))
+            col = x[r, b::8]
+            for q in range(5):
+                if li[q] >= 0 and np.sum(col == lv[q]) == 1:
+                    assert i[r, q, b] == li[q]
+
+
+def _int32_dyn_cases():
+    rng = np.random.default_rng(78)
+    imin = np.iinfo(np.int32).min
+    x = rng.integers(-2 ** 31 + 1, 2 ** 31 - 1, (16, 3000), dtype=np.int64).astype(np.int32)  # untied
+    for r in (5, 6):                       # block 0 cannot converge: 40 spikes in bin 0
+        x[r, rng.choice(3000 // 64, 40, replace=False) * 64] = 2 ** 31 - 1 - rng.permutation(40)
+    x[9, ::3] = imin
+    yield "int32 unconverged block", x, rng.integers(1, 33, 16).astype(np.int32), 32, 8, 64, (3, 6, 12), False
+    yield "int32 merge, P = 8", x, rng.integers(1, 33, 16).astype(np.int32), 32, 8, 128, (3, 6), True
+    y = np.full((8, 700), imin, np.int32)
+    for r in range(8):                     # a few admissible values per row
+        y[r, rng.choice(700, 6 + r, replace=False)] = rng.integers(-1000, 1000, 6 + r)
+    yield "int32 mostly iinfo.min rows", y, rng.integers(1, 17, 8).astype(np.int32), 16, 4, 32, (2, 5), False
+
+
+@pytest.mark.parametrize("replace", [None, -1e12, 7.9])
+@pytest.mark.parametrize("case", list(_int32_dyn_cases()), ids=lambda c: c[0] if isinstance(c, tuple) else str(c))
+def test_int32_top_dynamic_k_matches_literal_restatement(case, replace):
+    """int32 logits: every output of O.top_dynamic_k(dtype="i32") equals the
+    literal block restatement run on the int32 scratch (iinfo.min bins and
+    merge fill, int32 cutoff_vals, replace_val stored into int32)."""
+    _, x, k, max_k, bt, nb, sched, gc = case
+    (lv, li), lvalid, ld, lc = _literal_dynamic_top_k(x, k, max_k, bt, nb, sched, replace, "i32",
+                                                      guarantee_convergence=gc)
+    out = O.top_dynamic_k(x, k, max_k, block_token=bt, num_bins=nb, schedule=sched, replace_val=replace,
+                          dtype="i32", guarantee_convergence=gc)
+    ov, oi = out[:2]
+    assert ov.dtype == np.int32
+    assert np.array_equal(oi, li) and np.array_equal(ov, lv)
+    if not gc:
+        _, _, ovalid, od, oc = out
+        assert oc.dtype == np.int32
+        assert ovalid == lvalid and np.array_equal(od, ld) and np.array_equal(oc, lc)
+
+
 def test_top_dynamic_k_converged_rows_are_exact():
     rng = np.random.default_rng(2)
     x = rng.standard_normal((16, 20000)).astype(np.float32)
@@ -614,16 +700,17 @@ def _literal_dynamic_top_k(x, k, max_k, block_token, num_bins, schedule, replace
                            guarantee_convergence=False):
     rows, vocab = x.shape
     lo = O.dtype_min(dtype)
+    vt = np.int32 if dtype == "i32" else np.float32              # to_32bit_dtype of the scratch (:476-478)
     kk = np.broadcast_to(np.asarray(k, np.int64), (rows,))
     sched = (0,) + tuple(sorted(set(schedule)))
     max_m = sched[-1]
     buf = max(max_m, 2 ** O.log2_ceil(max_m - 1)) * num_bins
-    sv = np.full((rows, buf), np.nan, np.float32)
+    sv = np.full((rows, buf), 0 if dtype == "i32" else np.nan, vt)
     si = np.full((rows, buf), _GARBAGE, np.int64)
     depths = np.zeros(rows, np.int32)
-    cutoff = np.zeros(rows, np.float32)
+    cutoff = np.zeros(rows, vt)
     nslices = -(-vocab // num_bins)
-    xp = np.full((rows, nslices * num_bins), lo, np.float32)   # pad(val='min'), :96-105
+    xp = np.full((rows, nslices * num_bins), lo, vt)            # pad(val='min'), :96-105
     xp[:, :vocab] = x
     for pid in range(rows // block_token):
         ts = slice(pid * block_token, (pid + 1) * block_token)
@@ -670,11 +757,16 @@ def _literal_dynamic_top_k(x, k, max_k, block_token, num_bins, schedule, replace
             v = sv[:, :d_up * num_bins].astype(np.float64)
             i = si[:, :d_up * num_bins]
             order = np.lexsort((i, -v), axis=1)[:, :128]
-            ov = O.round_to_dtype(np.take_along_axis(sv[:, :d_up * num_bins], order, 1), dtype)
+            ov = np.take_along_axis(sv[:, :d_up * num_bins], order, 1)
+            if dtype != "i32":
+                ov = O.round_to_dtype(ov, dtype)
             oi = np.take_along_axis(i, order, 1)
             if replace_val is not None:
-                rv = O.round_to_dtype(np.float32(replace_val), dtype)
-                ov = np.where(np.arange(ov.shape[1])[None, :] < kk[:, None], ov, rv).astype(np.float32)
+                if dtype == "i32":     # stored into int32: toward zero, saturated
+                    rv = np.int32(math.trunc(min(max(float(replace_val), -2.0 ** 31), 2.0 ** 31 - 1)))
+                else:
+                    rv = O.round_to_dtype(np.float32(replace_val), dtype)
+                ov = np.where(np.arange(ov.shape[1])[None, :] < kk[:, None], ov, rv).astype(vt)
             oi = np.where(oi == _GARBAGE, -1, oi).astype(np.int32)
             out = (ov[:, :max_k], oi[:, :max_k])
     return out, valid, depths, cutoff
@@ -703,12 +795,14 @@ def _literal_merge(logits, sv, si, ts, num_bins, m, max_k, dtype):
     indicator = np.zeros((bt, num_bins), bool)
     for i in range(num_packed_bins):
         indicator |= bin_indices == packing_perm[:, i:i + 1]
-    vals = np.concatenate([np.where(indicator, np.finfo(np.float32).min, vals[:, i * num_bins:(i + 1) * num_bins])
-                           for i in range(vals.shape[1] // num_bins)], axis=1)
+    vt = np.int32 if dtype == "i32" else np.float32
+    scratch_min = np.iinfo(np.int32).min if dtype == "i32" else np.finfo(np.float32).min   # get_dtype_info(scratch)
+    vals = np.concatenate([np.where(indicator, scratch_min, vals[:, i * num_bins:(i + 1) * num_bins])
+                           for i in range(vals.shape[1] // num_bins)], axis=1).astype(vt)
     lo = O.dtype_min(dtype)
-    packed = [np.full((bt, 128), lo, np.float32)
+    packed = [np.full((bt, 128), lo, vt)
               for _ in range(-(-vocab // (128 * (num_bins // num_packed_bins))))]
-    xpad = np.full((bt, vocab + 128), lo, np.float32)
+    xpad = np.full((bt, vocab + 128), lo, vt)
     xpad[:, :vocab] = logits
     lane = np.arange(128)[None, :]
     for offset in range(0, num_bins, 128):
