@@ -143,6 +143,10 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
  * lists need more (rows x segments x 1 KiB; e.g. f32 rows of 151936 columns
  * beyond about 1600 rows) return TALLAX_UNSUPPORTED before any launch.  All
  * calls on one GPU share the array: calls that overlap on one GPU race.
+ * The first call on a device looks up the array's device address; made
+ * while `stream` is capturing, that call returns TALLAX_UNSUPPORTED and
+ * leaves the capture untouched, so a capturing caller makes one call per
+ * device first.  Later calls capture and replay like the other entry points.
  * ---------------------------------------------------------------------- */
 int tallax_fused_topk_topp_sample_noalloc(const void* logits, int dtype, int64_t rows, int64_t vocab,
                                           const int32_t* top_k, const float* top_p, const float* temperature,

@@ -1885,6 +1885,11 @@ constexpr int kMaxDevices = 64;
 
 // Device address of `scratch` on the device of `stream` (the current device
 // for the null stream), looked up once per device with that device current.
+// The lookup (hipSetDevice, hipGetSymbolAddress) is not made while `stream`
+// is capturing: a device's first call under capture returns
+// TALLAX_UNSUPPORTED and leaves the capture untouched, so a capturing caller
+// makes one call per device before it captures.  Later calls only read the
+// cached address and are capturable.
 static int scratch_address(hipStream_t stream, void** out) {
   static std::mutex mu;
   static void* addr[kMaxDevices] = {};
@@ -1904,6 +1909,16 @@ static int scratch_address(hipStream_t stream, void** out) {
   }
   std::lock_guard<std::mutex> lock(mu);
   if (!addr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+      set_error("hipStreamIsCapturing failed");
+      return kHipError;
+    }
+    if (cs != hipStreamCaptureStatusNone) {
+      set_error("the first no-allocation call on device %d is under stream capture; make one call on that device "
+                "before capturing (it looks up the device address of the scratch array)", dev);
+      return kUnsupported;
+    }
     if (dev != cur && hipSetDevice(dev) != hipSuccess) {
       set_error("hipSetDevice(%d) failed", dev);
       return kHipError;
