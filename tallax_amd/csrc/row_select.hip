@@ -1029,9 +1029,14 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge64_kernel(SelArgs a) {
 // row vector j * 1024 + t.
 //   1. Every load is issued up front; as the vectors arrive each thread keeps
 //      their maxima (signed view) -- the only work during the stream.
-//   2. The bound L: the minimum over waves of each wave's 8th largest thread
-//      maximum (a radix search with one ballot per key bit), so at least 128
-//      elements reach L; also the row's largest key M.
+//   2. The bound L: the minimum over waves 0..7 of each one's 16th largest
+//      thread maximum (a radix search with one ballot per key bit), so at
+//      least 128 elements reach L.  Those waves' loads are issued first and
+//      arrive first, so L is known before waves 8..15 have their data, and
+//      they stage as soon as it is in (measured at config 4: 16.86 -> 16.15
+//      us against the bound over all 16 waves; waves 0..11 gave 17.0 us,
+//      waves 0..3 overflow the candidate array).  Also the row's largest key
+//      M.
 //   3. Vectors whose maximum reaches L are staged in their wave's LDS region
 //      (one ballot per vector index), then each wave takes its staged vectors
 //      one per lane and appends the elements >= L as composites
@@ -1058,6 +1063,7 @@ struct StreamShared {
   int hist[kBuckets];                      // bucket counts, then bucket starts
   uint32_t wl[kNTS / kWave];
   uint32_t wm[kNTS / kWave];
+  uint32_t posted;  // bit w: wave w (< 8) has its bound term in wl
   int ncand;
   int ovf;                                 // a wave's staged vectors overflowed its region
 };
@@ -1271,6 +1277,9 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   const int cols = (int)a.cols;
   const RowParams rp = load_row_params<SAMPLE>(a, row);
 
+  if (tid == 0) ss.posted = 0;
+  lds_barrier();  // posted is clear before any wave posts; no load is in flight yet
+
   // ---- 1. every load up front (global loads: flat loads would also count
   // against the LDS counter)
   uint4 raw[V];
@@ -1284,6 +1293,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
       raw[j] = make_uint4(x.x, x.y, x.z, x.w);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);  // every load issues before any use of one
   if (tid == 0) {
     ss.ncand = 0;
     ss.ovf = 0;
@@ -1400,22 +1410,35 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
         }
       }
     }
-    {
+    // The bound L comes from waves 0..7 alone: the minimum over them of each
+    // one's 16th largest thread maximum, so at least 128 elements of the row
+    // reach it.  Their loads are issued first and arrive first, so L is
+    // posted before waves 8..15 have their data, and those stage as soon as
+    // it is in.
+    constexpr int NE = NW / 2;
+    if (w < NE) {
       uint32_t wl, wm;
-      wave_kth_and_max<KB>(tk, kMaxK / NW, wl, wm);
+      wave_kth_and_max<KB>(tk, kMaxK / NE, wl, wm);
       if (l == 0) {
         ss.wl[w] = wl;
         ss.wm[w] = wm;
+        __hip_atomic_fetch_or(&ss.posted, 1u << w, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
-    }
-    __syncthreads();
-    uint32_t L = ss.wl[0];
-    M = ss.wm[0];
+    } else {
+      uint32_t mx = tk;
 #pragma unroll
-    for (int i = 1; i < NW; ++i) {
-      L = ss.wl[i] < L ? ss.wl[i] : L;
-      M = ss.wm[i] > M ? ss.wm[i] : M;
+      for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t o = lane_xor(mx, d);
+        mx = o > mx ? o : mx;
+      }
+      if (l == 0) ss.wm[w] = mx;
     }
+    while ((__hip_atomic_load(&ss.posted, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) & ((1u << NE) - 1u)) !=
+           ((1u << NE) - 1u))
+      __builtin_amdgcn_s_sleep(1);
+    uint32_t L = ss.wl[0];
+#pragma unroll
+    for (int i = 1; i < NE; ++i) L = ss.wl[i] < L ? ss.wl[i] : L;
     thr = L > kFloor ? L : kFloor;
 
     // ---- 3. stage the vectors that may hold a candidate, then the candidates
@@ -1443,6 +1466,9 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     extract(thr);
   }
   __syncthreads();
+  M = ss.wm[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) M = ss.wm[i] > M ? ss.wm[i] : M;
   const int n = ss.ncand;
   // fewer than 128 with thr at the eligibility floor: every eligible element
   // of the row is a candidate, the rest of the list is ineligible elements
