@@ -30,6 +30,14 @@ streams its input from HBM.  K back-to-back steps are bracketed by
 torch.cuda.synchronize(); HIP events recorded on the launch stream around
 them give the average launch duration used for the roofline.  One JSON line
 is printed.
+
+Traffic: before it touches the GPU, the run profiles a short copy of itself
+twice, `rocprofv3 --pmc FETCH_SIZE` then `--pmc WRITE_SIZE` (child processes;
+about 10-30 s each), and reports roofline.traffic = HBM bytes per launch of
+the dominant kernels, each counter scaled by what it reads for the runtime's
+256 MiB copy kernel in the same pass.  Under a profiler already, or if a pass
+fails, the figure recorded in profiles/*.md is reported instead and
+roofline.traffic_source says which.
 """
 from __future__ import annotations
 
@@ -95,10 +103,11 @@ def _read_rates(torch, _lib, dev, stream, steps, warmup):
     return res
 
 
-def _measured_traffic(config):
+def _recorded_traffic(config):
     """HBM bytes per launch measured with rocprofv3 --pmc (128-byte lines of the
     TCC_EA0 read requests plus WRITE_SIZE), as recorded in profiles/*.md lines
-    `traffic_bytes_per_launch[<config>] = <bytes>`; None if absent."""
+    `traffic_bytes_per_launch[<config>] = <bytes>`; None if absent.  Used only
+    when the live passes (_live_traffic) cannot run."""
     import glob
     import re
     pat = re.compile(r"traffic_bytes_per_launch\[" + re.escape(config) + r"\]\s*=\s*([0-9]+)")
@@ -107,6 +116,122 @@ def _measured_traffic(config):
         if m:
             return int(m.group(1))
     return None
+
+
+# Kernel-name fragments of the dispatches one launch of each config makes
+# (every other kernel in a run is input generation, torch copies or the copy
+# calibration).
+TRAFFIC_KERNELS = {
+    "sampler": ("tx::stream_select_kernel",),
+    "sampler_masked": ("tx::stream_select_kernel",),
+    "sampler_wide": ("tx::sample_wide_kernel",),
+    "topk_c3": ("tx::seg_select_kernel", "tx::seg_merge"),
+    "topk_c1": ("tx::seg_select_kernel", "tx::seg_merge"),
+    "topk_c3_approx": ("tx::binned_",),
+    "sort_c2": ("tx::radix_sort_rows_kernel", "tx::gather_row_lds_kernel"),
+    "prefill_c5": ("tx::softmax_topk_kernel",),
+    "sort_wide": ("tx::sort_chunks_kernel", "tx::merge_runs_kernel"),
+}
+EXTRA_CONFIGS = ("topk_c3", "prefill_c5", "sort_c2")
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+PMC_STEPS, PMC_WARMUP = 10, 2
+
+
+def _extra_steps(which, steps):
+    """Timed launches of an extra line: config 5 runs a quarter of the steps."""
+    return max(1, steps // 4) if which == "prefill_c5" else steps
+
+
+def _under_profiler():
+    """True when this process already runs under rocprofv3 (its tool library
+    is preloaded): no nested profiler passes then."""
+    return "ROCP_TOOL_LIBRARIES" in os.environ or "ROCPROF_OUTPUT_PATH" in os.environ
+
+
+def _pmc_pass(counter, config, extras, outdir, timeout):
+    """One `rocprofv3 --pmc <counter>` pass over a short run of this script
+    (PMC_STEPS timed + PMC_WARMUP warmup launches, no parity, no CPU baseline,
+    no passes of its own), started as a child process in its own process
+    group before this process touches the GPU.  Returns the counter values of
+    every dispatch, {kernel name: [KiB, ...]}."""
+    import csv
+    import glob
+    import shutil
+    import signal
+    import subprocess
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    d = os.path.join(outdir, counter)
+    cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "run", "--",
+           sys.executable, os.path.join(ROOT, "bench.py"), "--config", config, "--steps", str(PMC_STEPS),
+           "--warmup", str(PMC_WARMUP), "--no-cpu-baseline", "--no-parity", "--traffic", "off"]
+    if not extras:
+        cmd.append("--no-extra")
+    log_path = os.path.join(outdir, counter + ".log")
+    with open(log_path, "w") as log:
+        p = subprocess.Popen(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), stdout=log,
+                             stderr=subprocess.STDOUT, start_new_session=True)
+        try:
+            rc = p.wait(timeout=timeout)
+        except subprocess.TimeoutExpired:
+            os.killpg(p.pid, signal.SIGKILL)
+            p.wait()
+            raise RuntimeError(f"rocprofv3 --pmc {counter} pass exceeded {timeout} s")
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    finished = '"metric"' in open(log_path, errors="replace").read()
+    # rocprofv3 may end with SIGSEGV after the program has finished and its
+    # results are written: accepted when the run printed its line.
+    if not files or not finished or rc not in (0, 139, -11):
+        raise RuntimeError(f"rocprofv3 --pmc {counter} pass failed (exit {rc}, csv {bool(files)}, "
+                           f"line printed {finished})")
+    vals = {}
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return vals
+
+
+def _median(xs):
+    s = sorted(xs)
+    n = len(s)
+    return s[n // 2] if n % 2 else 0.5 * (s[n // 2 - 1] + s[n // 2])
+
+
+def _live_traffic(config, extras, timeout=300):
+    """HBM bytes per launch of `config` (and of the extra configs when
+    `extras`), measured now by two rocprofv3 --pmc passes of this script:
+    FETCH_SIZE, then WRITE_SIZE.  Each counter is scaled by the factor that
+    makes it read the bytes the runtime's 256 MiB copy kernel in the same pass
+    moves (COPY_BYTES read and COPY_BYTES written per dispatch).  A kernel's
+    bytes per launch are its median per-dispatch value x its dispatches per
+    launch; a config's are the sum over its kernels (TRAFFIC_KERNELS).
+    Returns ({config: bytes}, {counter: scale factor})."""
+    import shutil
+    import tempfile
+    outdir = tempfile.mkdtemp(prefix="tallax_pmc_", dir="/tmp")
+    try:
+        per = {}
+        factors = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            print(f"bench: rocprofv3 --pmc {counter} pass over --config {config}", file=sys.stderr, flush=True)
+            vals = _pmc_pass(counter, config, extras, outdir, timeout)
+            cp = vals.get(COPY_KERNEL, [])
+            big = [v for v in cp if cp and v >= 0.5 * max(cp)]
+            if not big or _median(big) <= 0:
+                raise RuntimeError(f"no {COPY_KERNEL} dispatch in the {counter} pass")
+            factors[counter] = COPY_BYTES / (_median(big) * 1024.0)
+            for which in (config,) + (EXTRA_CONFIGS if extras else ()):
+                launches = PMC_WARMUP + (_extra_steps(which, PMC_STEPS) if which != config else PMC_STEPS)
+                tot = 0.0
+                for name, xs in vals.items():
+                    if any(frag in name for frag in TRAFFIC_KERNELS[which]):
+                        tot += _median(xs) * len(xs) / launches * 1024.0 * factors[counter]
+                if tot <= 0:
+                    raise RuntimeError(f"no dispatch of {which}'s kernels in the {counter} pass; kernels seen: "
+                                       f"{sorted(vals)[:12]}")
+                per[which] = per.get(which, 0.0) + tot
+        return {k: int(round(v)) for k, v in per.items()}, factors
+    finally:
+        shutil.rmtree(outdir, ignore_errors=True)
 
 
 def _parse():
@@ -122,6 +247,10 @@ def _parse():
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the extra measurements: the config 3, 5 and 2 lines in the sampler config, the "
                          "unmasked comparison in sampler_masked (profiling runs)")
+    ap.add_argument("--traffic", default="live", choices=["live", "recorded", "off"],
+                    help="roofline.traffic: live = two rocprofv3 --pmc passes of this script run first (the "
+                         "default; 'recorded' is taken when already under a profiler), recorded = the figure "
+                         "in profiles/*.md, off = null")
     return ap.parse_args()
 
 
@@ -512,7 +641,7 @@ def _cpu_baseline(w, O, seconds):
                       f"{wall:.1f} s wall"}
 
 
-def _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O, which):
+def _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O, which, traffic):
     """Another BASELINE config beside the main line, timed the same way:
     config 3 (the second north-star target: exact top-k k=50 of f32
     [128,151936] + spikes), config 5 (the fused prefill pipeline) or config 2
@@ -524,7 +653,7 @@ def _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O, which):
         w = _prefill_c5(torch, np, _lib, dev, s_handle, gen, None)
     else:
         w = _sort_c2(torch, np, _lib, dev, s_handle, gen, None)
-    steps = max(1, args.steps // 4) if which == "prefill_c5" else args.steps
+    steps = _extra_steps(which, args.steps)
     parity = None if args.no_parity else w.parity(O)
     for i in range(args.warmup):
         w.launch(i)
@@ -542,7 +671,9 @@ def _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O, which):
     rec = {"metric": w.metric, "value": w.rows * steps / max(wall, us * 1e-6 * steps), "unit": "rows/s",
            "steps": steps, "kernel": w.kernel, "kernel_avg_us": us, "achieved_GBs": achieved,
            "roofline_frac": achieved / PEAK_HBM_GBS, "algorithmic_bytes_per_launch": w.alg_bytes,
-           "traffic": _measured_traffic(which), "workload": w.workload, "parity_vs_oracle": parity}
+           "traffic": traffic.get(which),
+           "traffic_over_algorithmic": traffic[which] / w.alg_bytes if traffic.get(which) else None,
+           "workload": w.workload, "parity_vs_oracle": parity}
     del w
     torch.cuda.empty_cache()
     return rec
@@ -555,6 +686,30 @@ def main() -> int:
               "rows are independent, so a multi-GPU run shards them by rows with no communication.",
               file=sys.stderr)
         return 2
+
+    # HBM traffic per launch: two rocprofv3 --pmc passes of this script, run
+    # as child processes before this process touches the GPU
+    traffic, traffic_src, traffic_cal = {}, None, None
+    mode = args.traffic
+    if mode == "live" and _under_profiler():
+        mode = "recorded"
+    if args.config not in TRAFFIC_KERNELS:
+        mode = "off"
+    extras = args.config == "sampler" and not args.no_extra
+    if mode == "live":
+        try:
+            traffic, traffic_cal = _live_traffic(args.config, extras)
+            traffic_src = (f"live: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes of this script "
+                           f"({PMC_STEPS} steps + {PMC_WARMUP} warmup), each scaled by the copy calibration "
+                           f"measured in the same pass")
+        except Exception as e:  # the profiler is a measurement aid: the bench line still runs
+            print(f"bench: live traffic passes failed ({e}); using the recorded figures", file=sys.stderr,
+                  flush=True)
+            mode = "recorded"
+    if mode == "recorded":
+        for which in (args.config,) + (EXTRA_CONFIGS if extras else ()):
+            traffic[which] = _recorded_traffic(which)
+        traffic_src = "recorded: traffic_bytes_per_launch lines of profiles/*.md"
 
     import numpy as np
     import torch
@@ -655,7 +810,10 @@ def main() -> int:
         "data": "synthetic (torch.randn on device, seed 4; rotating input buffers)",
         "config": {"workload": w.workload, "rows": w.shape[0], "cols": w.shape[1], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": _measured_traffic(args.config),
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic.get(args.config),
+                     "traffic_over_algorithmic": (traffic[args.config] / w.alg_bytes
+                                                  if traffic.get(args.config) else None),
+                     "traffic_source": traffic_src, "traffic_counter_scale": traffic_cal,
                      "measured_copy_GBs": copy_gbs, "frac_of_copy": achieved / copy_gbs,
                      "kernel": w.kernel, "kernel_avg_us": kern_us,
                      "algorithmic_bytes_per_launch": w.alg_bytes},
@@ -664,8 +822,8 @@ def main() -> int:
         "wall_ms_per_step": wall * 1e3 / args.steps,
     }
     if args.config == "sampler" and not args.no_extra:
-        for which in ("topk_c3", "prefill_c5", "sort_c2"):
-            rec[which] = _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O, which)
+        for which in EXTRA_CONFIGS:
+            rec[which] = _extra_line(torch, np, _lib, dev, s_handle, gen, stream, args, O, which, traffic)
     if hasattr(w, "common_us") and not args.no_extra:
         cu = w.common_us(args.steps)
         rec["unmasked_kernel_avg_us"] = cu
