@@ -1027,20 +1027,21 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge64_kernel(SelArgs a) {
 // Kernel S (stream_select_kernel): a whole row per 1024-thread workgroup (16
 // waves, 4 per SIMD), V 16-byte vectors per thread, vector j of thread t at
 // row vector j * 1024 + t.
-//   1. Every load is issued up front; as the vectors arrive each thread keeps
-//      their maxima (signed view) -- the only work during the stream.
+//   1. Every load is issued up front.
 //   2. The bound L: the minimum over waves 0..7 of each one's 16th largest
 //      thread maximum (a radix search with one ballot per key bit), so at
 //      least 128 elements reach L.  Those waves' loads are issued first and
-//      arrive first, so L is known before waves 8..15 have their data, and
-//      they stage as soon as it is in (measured at config 4: 16.86 -> 16.15
-//      us against the bound over all 16 waves; waves 0..11 gave 17.0 us,
-//      waves 0..3 overflow the candidate array).  Also the row's largest key
-//      M.
+//      arrive first, so L is known before waves 8..15 have their first
+//      vector (measured at config 4: 16.86 -> 16.15 us against the bound over
+//      all 16 waves; waves 0..11 gave 17.0 us, waves 0..3 overflow the
+//      candidate array).
 //   3. Vectors whose maximum reaches L are staged in their wave's LDS region
-//      (one ballot per vector index), then each wave takes its staged vectors
-//      one per lane and appends the elements >= L as composites
-//      (canonical key << 32 | ~index).
+//      (one ballot per vector index; waves 8..15 stage each vector as it
+//      arrives), then each wave takes its staged vectors one per lane and
+//      appends the elements >= L as composites (canonical key << 32 |
+//      ~index).  The row maximum M the rank needs is at least the largest
+//      candidate key: waves 0..7 post their largest element, waves 8..15
+//      their largest candidate.
 //   4. The candidates are put in order by an LDS bucket rank: buckets of
 //      (M - key) >> shift (at most kBuckets), one atomic per candidate for the
 //      histogram and its slot, an exclusive scan, a scatter, and each
@@ -1049,7 +1050,9 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge64_kernel(SelArgs a) {
 // Rows with fewer than 128 eligible elements rank them and take the rest of
 // the list by class (fill_ineligible).  Rows whose staged vectors or
 // candidates overflow (heavy ties: constant rows, long tie blocks) take
-// tie_select over the whole row instead.
+// tie_select over the whole row instead (stream_tie_path).  Both rare paths
+// are out of line: the kernel's hot code is 31 KB instead of 50 KB (measured
+// at config 4 together with step 3's per-vector staging: 16.2 -> 15.8 us).
 // ---------------------------------------------------------------------------
 constexpr int kNTS = 1024;
 constexpr int kStageCap = 128;   // staged vectors per wave
@@ -1191,18 +1194,18 @@ __device__ __forceinline__ uint32_t min_offset_from_min(const uint4 v) {
 // hold a class anywhere in the row are read again one at a time (vector j of
 // thread t at row vector j * kNTS + t of the aligned base, nv vectors, the
 // row's first element at slot mis), in order, until the list is full.
-// tmp: 2 * 16 words of LDS.
+// tmp: 2 * 16 words of LDS.  Out of line: a rare path kept out of the
+// kernel's hot code (the kernel's code size sets its instruction-cache
+// footprint).
 template <int DT, int V>
-__device__ __forceinline__ void fill_ineligible(const uint4* row_base, int nv, int mis, int cols, int n, uint32_t pab,
-                                                uint32_t pc, uint64_t* list, int* red, uint32_t* tmp) {
+__device__ __attribute__((noinline)) void fill_ineligible(const uint4* row_base, int nv, int mis, int cols, int n,
+                                                          uint32_t pab, uint32_t pc, uint64_t* list, int* red,
+                                                          uint32_t* tmp) {
   constexpr bool kBF = DT == kBF16;
   constexpr int VEC = ElemT<DT>::VEC, NW = kNTS / kWave;
   constexpr uint32_t kMinKey = kBF ? 0x0080FFFFu : 0x00800000u;  // global keys of the three classes
   constexpr uint32_t kNegInfKey = 0x007FFFFFu, kNaNKey = 1u;
-  // the empty asm hides that these addresses equal the first read's: shared,
-  // those would stay live (in registers or spilled) from the kernel's start
-  int tid = threadIdx.x;
-  asm volatile("" : "+v"(tid), "+s"(row_base));
+  const int tid = threadIdx.x;
   const int w = tid / kWave, l = lane_id();
   const GlobalVec gb = (GlobalVec)row_base;
   const GlobalVec dead = (GlobalVec)(uintptr_t)&g_dead_vec;
@@ -1252,6 +1255,28 @@ __device__ __forceinline__ void fill_ineligible(const uint4* row_base, int nv, i
     }
   }
   for (int i = base + tid; i < kMaxK; i += kNTS) list[i] = 0ull;
+}
+
+// Rows whose staged vectors or candidates overflow (heavy ties): tie_select
+// over the whole row, then the block's merge, into the sorted 128-entry list.
+// Out of line, like fill_ineligible.
+template <int DT, int V>
+__device__ __attribute__((noinline)) void stream_tie_path(
+    const uint4* base, int nv, int mis, int cols,
+    SegShared<typename Sel<DT, (kNTS * V * ElemT<DT>::VEC > 65535)>::Comp, kNTS>& sh, uint4* stage) {
+  using ST = Sel<DT, (kNTS * V * ElemT<DT>::VEC > 65535)>;
+  constexpr int VEC = ElemT<DT>::VEC;
+  const int tid = threadIdx.x, w = tid / kWave, l = lane_id();
+  const int lbase = tid * VEC;
+  const int64_t seg_e0 = -(int64_t)mis;
+  const int live_lo = mis;
+  const int live_hi = cols + mis < nv * VEC ? cols + mis : nv * VEC;
+  const int wcnt = tie_select<DT, V, kNTS, 2>(base, 0, nv, lbase, live_lo, live_hi, (uint32_t)seg_e0, kMaxK,
+                                              sh.cand + w * Geo<kNTS>::WCAP, sh.red, stage);
+  if (l == 0) sh.wc[w] = wcnt;
+  __syncthreads();
+  block_select(sh, (const int*)sh.wc);
+  for (int i = tid; i < kRun; i += kNTS) sh.list64[i] = ST::to_global(sh.list[i], seg_e0);
 }
 
 template <int DT, int V, bool SAMPLE, bool EDGE>
@@ -1348,10 +1373,12 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     }
   };
   // the wave's staged vectors, one per lane: elements with key >= thr are
-  // appended to the candidates
-  auto extract = [&](uint32_t thr) {
+  // appended to the candidates; post_top: the wave's M term is the largest
+  // key it appended
+  auto extract = [&](uint32_t thr, bool post_top) {
     if (l == 0 && wcnt > kStageCap) ss.ovf = 1;
     const int nst = wcnt < kStageCap ? wcnt : kStageCap;
+    uint32_t top = 0;  // the largest key appended by this lane
     for (int r0 = 0; r0 < nst; r0 += kWave) {  // wave-uniform
       const int o = r0 + l;
       uint32_t pm = 0;
@@ -1371,52 +1398,61 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
         while (pm) {
           const int q = __builtin_ctz(pm);
           pm &= pm - 1u;
-          if (oc < kCandCap) ss.cand[oc] = make_comp(Sel<DT, true>::canon(elem_bits<DT>(vv, q)), e0 + (uint32_t)q);
+          const uint32_t kk = Sel<DT, true>::canon(elem_bits<DT>(vv, q));
+          top = kk > top ? kk : top;
+          if (oc < kCandCap) ss.cand[oc] = make_comp(kk, e0 + (uint32_t)q);
           ++oc;
         }
       }
+    }
+    if (post_top) {
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const uint32_t o = lane_xor(top, d);
+        top = o > top ? o : top;
+      }
+      if (l == 0) ss.wm[w] = top;
     }
   };
 
   uint32_t thr, M;
   uint32_t pab = 0, pc = 0;  // rows with thr at the floor: the vectors holding ineligible classes
+  // ---- 2. the bound L from waves 0..7 alone: the minimum over them of each
+  // one's 16th largest thread maximum, so at least 128 elements of the row
+  // reach it.  Their loads are issued first and arrive first, so L is posted
+  // before waves 8..15 have their first vector, and those stage each vector
+  // as it arrives.
+  constexpr int NE = NW / 2;
+  const bool early = w < NE;
   {
-    int32_t vmax[V];
+    if (early) {
+      int32_t vmax[V];
 #pragma unroll
-    for (int j = 0; j < V; ++j) vmax[j] = vec_smax<DT>(raw[j]);
-
-    // ---- 2. the bound L and the row maximum M (canonical keys)
-    int32_t smax = vmax[0];
+      for (int j = 0; j < V; ++j) vmax[j] = vec_smax<DT>(raw[j]);
+      int32_t smax = vmax[0];
 #pragma unroll
-    for (int j = 1; j < V; ++j) smax = imax32(smax, vmax[j]);
-    uint32_t tk;
-    if (smax >= 0 && smax <= kPosInf) {
-      tk = (uint32_t)smax | kZeroKey;
-    } else {
-      int32_t omax = kBF ? -32768 : (int32_t)0x80000000u;
+      for (int j = 1; j < V; ++j) smax = imax32(smax, vmax[j]);
+      uint32_t tk;  // canonical key of the thread's largest element
+      if (smax >= 0 && smax <= kPosInf) {
+        tk = (uint32_t)smax | kZeroKey;
+      } else {
+        int32_t omax = kBF ? -32768 : (int32_t)0x80000000u;
 #pragma unroll
-      for (int j = 0; j < V; ++j) omax = imax32(omax, vec_omax<DT>(raw[j]));
-      if (omax <= kPosInf) {
-        tk = omax < kOrdNegInf ? 0u : (omax == -1 ? kZeroKey : (uint32_t)omax + kZeroKey);
-      } else {  // a positive NaN: canonical maximum element by element
-        tk = 0;
+        for (int j = 0; j < V; ++j) omax = imax32(omax, vec_omax<DT>(raw[j]));
+        if (omax <= kPosInf) {
+          tk = omax < kOrdNegInf ? 0u : (omax == -1 ? kZeroKey : (uint32_t)omax + kZeroKey);
+        } else {  // a positive NaN: canonical maximum element by element
+          tk = 0;
 #pragma unroll
-        for (int j = 0; j < V; ++j) {
+          for (int j = 0; j < V; ++j) {
 #pragma unroll
-          for (int q = 0; q < VEC; ++q) {
-            const uint32_t kk = Sel<DT, true>::canon(elem_bits<DT>(raw[j], q));
-            tk = kk > tk ? kk : tk;
+            for (int q = 0; q < VEC; ++q) {
+              const uint32_t kk = Sel<DT, true>::canon(elem_bits<DT>(raw[j], q));
+              tk = kk > tk ? kk : tk;
+            }
           }
         }
       }
-    }
-    // The bound L comes from waves 0..7 alone: the minimum over them of each
-    // one's 16th largest thread maximum, so at least 128 elements of the row
-    // reach it.  Their loads are issued first and arrive first, so L is
-    // posted before waves 8..15 have their data, and those stage as soon as
-    // it is in.
-    constexpr int NE = NW / 2;
-    if (w < NE) {
       uint32_t wl, wm;
       wave_kth_and_max<KB>(tk, kMaxK / NE, wl, wm);
       if (l == 0) {
@@ -1424,14 +1460,6 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
         ss.wm[w] = wm;
         __hip_atomic_fetch_or(&ss.posted, 1u << w, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
-    } else {
-      uint32_t mx = tk;
-#pragma unroll
-      for (int d = 1; d < kWave; d <<= 1) {
-        const uint32_t o = lane_xor(mx, d);
-        mx = o > mx ? o : mx;
-      }
-      if (l == 0) ss.wm[w] = mx;
     }
     while ((__hip_atomic_load(&ss.posted, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) & ((1u << NE) - 1u)) !=
            ((1u << NE) - 1u))
@@ -1441,14 +1469,23 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     for (int i = 1; i < NE; ++i) L = ss.wl[i] < L ? ss.wl[i] : L;
     thr = L > kFloor ? L : kFloor;
 
-    // ---- 3. stage the vectors that may hold a candidate, then the candidates
+    // ---- 3. stage the vectors that may hold a candidate (each as soon as it
+    // is in: the wait for vector j sits before its maximum), then the
+    // candidates
     const bool pos_thr = thr > kZeroKey;
     const int32_t st = (int32_t)(thr - kZeroKey);                       // bits, positive threshold
     const int32_t ot = thr == kZeroKey ? -1 : (int32_t)(thr - kZeroKey);  // ordered view otherwise
+    // Two ifs, not if/else (the empty asm keeps the compiler from merging
+    // them): the join of an if/else leaves the other side's values undefined,
+    // and the code generator reads such an undefined register with a wait for
+    // every load in flight.
     if (pos_thr) {  // block-uniform: the signed-view maxima decide
 #pragma unroll
-      for (int j = 0; j < V; ++j) stage_if(j, vmax[j] >= st);
-    } else {
+      for (int j = 0; j < V; ++j) stage_if(j, vec_smax<DT>(raw[j]) >= st);
+    }
+    uint32_t thr_b = __builtin_amdgcn_readfirstlane(thr);
+    asm volatile("" : "+s"(thr_b));
+    if (thr_b <= kZeroKey) {
 #pragma unroll
       for (int j = 0; j < V; ++j) stage_if(j, vec_omax<DT>(raw[j]) >= ot);
       if (thr == kFloor) {  // block-uniform: the row may hold fewer than 128 eligible elements
@@ -1463,9 +1500,11 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
         pc = (1u << V) - 1u;
       }
     }
-    extract(thr);
+    extract(thr, !early);
   }
   __syncthreads();
+  // M: at least the largest candidate key (waves 0..7 post their largest
+  // element, waves 8..15 their largest candidate), all the rank needs
   M = ss.wm[0];
 #pragma unroll
   for (int i = 1; i < NW; ++i) M = ss.wm[i] > M ? ss.wm[i] : M;
@@ -1477,18 +1516,9 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   const bool tie = !fill && (ss.ovf != 0 || n < kMaxK || n > kCandCap);
   if (fill) fill_ineligible<DT, V>(rv.base, nv, rv.mis, cols, n, pab, pc, sh.list64, sh.red, &ss.vsi[0][0]);
   if (tie) {
-    const int lbase = tid * VEC;
-    const int64_t seg_e0 = -(int64_t)rv.mis;
-    const int live_lo = rv.mis;
-    const int live_hi = cols + rv.mis < nv * VEC ? cols + rv.mis : nv * VEC;
-    const int wcnt = tie_select<DT, V, kNTS, 2>(rv.base, 0, nv, lbase, live_lo, live_hi, (uint32_t)seg_e0, kMaxK,
-                                                sh.cand + w * Geo<kNTS>::WCAP, sh.red, stage);
-    if (l == 0) sh.wc[w] = wcnt;
-    __syncthreads();
-    block_select(sh, (const int*)sh.wc);
-    for (int i = tid; i < kRun; i += kNTS) sh.list64[i] = ST::to_global(sh.list[i], seg_e0);
+    stream_tie_path<DT, V>(rv.base, nv, rv.mis, cols, sh, stage);
   } else if (n > 0) {
-    // ---- 4. bucket rank (and the candidates' noise meanwhile)
+    // ---- 4. bucket rank
     const uint32_t range = M - thr;  // the candidates' keys lie in [thr, M]
     int shift = 0;
     while ((range >> shift) >= (uint32_t)kBuckets) ++shift;
