@@ -1050,7 +1050,7 @@ static int top_dynamic_k_impl(const void* x, int dtype, int64_t rows, int64_t co
   const int min_seg = (num_bins * max_m + 127) / 128;
   // the candidate path starts from the float segment kernel: float inputs only
   const bool cand = mode == 0 && dtype != kI32 && max_m <= kCandRank &&
-                    segment_lists_plan(cols, dtype, min_seg < 2 ? 2 : min_seg, &nseg, &maxv, &vps) == kOk &&
+                    segment_lists_plan(rows, cols, dtype, min_seg < 2 ? 2 : min_seg, &nseg, &maxv, &vps) == kOk &&
                     nseg <= kMaxSegLists;
   const int mc = buf <= 8 ? 8 : 16;
   const size_t lds_scan = (size_t)kBinNT * mc * 8;  // <= 128 KiB

@@ -1424,9 +1424,9 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   // as it arrives.
   constexpr int NE = NW / 2;
   const bool early = w < NE;
+  int32_t vmax[V];  // early waves: their vectors' maxima, kept for the staging
   {
     if (early) {
-      int32_t vmax[V];
 #pragma unroll
       for (int j = 0; j < V; ++j) vmax[j] = vec_smax<DT>(raw[j]);
       int32_t smax = vmax[0];
@@ -1480,8 +1480,13 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     // and the code generator reads such an undefined register with a wait for
     // every load in flight.
     if (pos_thr) {  // block-uniform: the signed-view maxima decide
+      if (early) {
 #pragma unroll
-      for (int j = 0; j < V; ++j) stage_if(j, vec_smax<DT>(raw[j]) >= st);
+        for (int j = 0; j < V; ++j) stage_if(j, vmax[j] >= st);
+      } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) stage_if(j, vec_smax<DT>(raw[j]) >= st);
+      }
     }
     uint32_t thr_b = __builtin_amdgcn_readfirstlane(thr);
     asm volatile("" : "+s"(thr_b));
@@ -1752,9 +1757,24 @@ static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const c
 // vectors, maxv in {4, 8, 16}; a row is cut into at least min_seg segments
 // when its length allows, at most kMaxSeg.  Returns kUnsupported when the row
 // needs more segments than that.
-int segment_lists_plan(int64_t cols, int dt, int min_seg, int* nseg_out, int* maxv_out, int64_t* vps_out) {
+int segment_lists_plan(int64_t rows, int64_t cols, int dt, int min_seg, int* nseg_out, int* maxv_out,
+                       int64_t* vps_out) {
   const int vec = dt == kF32 ? 4 : 8;
   const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
+  // 19 vectors per thread when that puts every segment in one residency
+  // round (rows * nseg <= kTargetBlocks) where 16 would not, as plan_rows does
+  {
+    const int64_t n16 = (nv + (int64_t)kNT * 16 - 1) / ((int64_t)kNT * 16);
+    const int64_t per19 = (int64_t)kNT * 19;
+    const int64_t n19 = (nv + per19 - 1) / per19;
+    if (rows * n16 > kTargetBlocks && rows * n19 <= kTargetBlocks && n19 >= min_seg && n19 >= 2 &&
+        n19 <= kMaxSeg) {
+      *nseg_out = (int)n19;
+      *maxv_out = 19;
+      *vps_out = per19;
+      return kOk;
+    }
+  }
   int64_t nseg = (nv + (int64_t)kNT * 16 - 1) / ((int64_t)kNT * 16);
   if (nseg < min_seg) nseg = min_seg;
   if (nseg > nv) nseg = nv;
@@ -1782,11 +1802,13 @@ int launch_segment_lists(const void* x, int dt, int64_t rows, int64_t cols, int 
   a.ws_lists = lists;
   a.lists_only = 1;
   if (dt == kF32) {
-    if (maxv == 16) launch_a<kF32, 16, kNT, false>(a, s);
+    if (maxv == 19) launch_a<kF32, 19, kNT, false>(a, s);
+    else if (maxv == 16) launch_a<kF32, 16, kNT, false>(a, s);
     else if (maxv == 8) launch_a<kF32, 8, kNT, false>(a, s);
     else launch_a<kF32, 4, kNT, false>(a, s);
   } else {
-    if (maxv == 16) launch_a<kBF16, 16, kNT, false>(a, s);
+    if (maxv == 19) launch_a<kBF16, 19, kNT, false>(a, s);
+    else if (maxv == 16) launch_a<kBF16, 16, kNT, false>(a, s);
     else if (maxv == 8) launch_a<kBF16, 8, kNT, false>(a, s);
     else launch_a<kBF16, 4, kNT, false>(a, s);
   }

@@ -52,7 +52,8 @@ hipError_t set_dynamic_lds_limit(const void* kernel, int bytes, hipStream_t stre
 // Per-segment sorted top-128 composites of every row (row_select.hip):
 // plan the segments (at least min_seg per row), then launch the segment kernel
 // writing lists[rows][nseg][128].
-int segment_lists_plan(int64_t cols, int dt, int min_seg, int* nseg_out, int* maxv_out, int64_t* vps_out);
+int segment_lists_plan(int64_t rows, int64_t cols, int dt, int min_seg, int* nseg_out, int* maxv_out,
+                       int64_t* vps_out);
 int launch_segment_lists(const void* x, int dt, int64_t rows, int64_t cols, int nseg, int maxv, int64_t vps,
                          uint64_t* lists, hipStream_t s);
 
