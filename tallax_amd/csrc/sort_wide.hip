@@ -219,14 +219,25 @@ __device__ int merge_split_wave(const uint64_t* A, int la, const uint64_t* B, in
 // One merge pass over runs of length `run`: the pair of runs starting at
 // column s = 2 run j merges into columns [s, s + 2 run) of dst.  A run with
 // no partner (the row's last) is copied.  FINAL writes the outputs instead.
+// LDS slot of merge-tile record j: one spare slot per 16 records, so that
+// the 64 lanes of a wave, each merging its own run of 16 outputs (records 16
+// apart), spread over the banks instead of all hitting one.
+__device__ __forceinline__ int ms(int j) { return j + (j >> 4); }
+
 template <bool FINAL>
 __global__ __launch_bounds__(kMergeNT) void merge_runs_kernel(SortArgs a, const uint64_t* src, uint64_t* dst,
                                                               int64_t run, int tiles) {
-  __shared__ uint64_t lds[kMergeTile];
+  __shared__ uint64_t lds[kMergeTile + kMergeTile / 16];  // record j at ms(j)
   __shared__ int split[2];
   const int t = threadIdx.x, w = t / kWave;
-  const int64_t row = blockIdx.x / (unsigned)tiles;
-  const int ti = (int)(blockIdx.x - row * tiles);
+  // Workgroups go to the 8 XCDs round-robin, each with its own L2: the tile
+  // order is remapped so that every XCD takes a contiguous range of tiles, and
+  // neighbouring tiles, whose merge-path searches probe the same lines of the
+  // same runs, share an L2.
+  const unsigned nwg = gridDim.x;
+  const unsigned vb = nwg % 8u == 0u ? (blockIdx.x % 8u) * (nwg / 8u) + blockIdx.x / 8u : blockIdx.x;
+  const int64_t row = vb / (unsigned)tiles;
+  const int ti = (int)(vb - row * tiles);
   const int64_t base = row * a.cols;
   const int64_t o0 = (int64_t)ti * kMergeTile;  // first output column of the tile
   const int64_t s = o0 / (2 * run) * (2 * run);
@@ -255,7 +266,7 @@ __global__ __launch_bounds__(kMergeNT) void merge_runs_kernel(SortArgs a, const 
 #pragma unroll
     for (int k = 0; k < kMergeItems; ++k) {
       const int j = k * kMergeNT + t;
-      if (j < count) lds[j] = st[k];
+      if (j < count) lds[ms(j)] = st[k];
     }
   }
   __syncthreads();
@@ -265,22 +276,22 @@ __global__ __launch_bounds__(kMergeNT) void merge_runs_kernel(SortArgs a, const 
     int lo = max(0, dt - nb), hi = min(dt, na);
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      if (lds[mid] > lds[na + dt - 1 - mid]) hi = mid;
+      if (lds[ms(mid)] > lds[ms(na + dt - 1 - mid)]) hi = mid;
       else lo = mid + 1;
     }
     int ia = lo, ib = dt - lo;
-    uint64_t x = ia < na ? lds[ia] : ~0ull;
-    uint64_t y = ib < nb ? lds[na + ib] : ~0ull;
+    uint64_t x = ia < na ? lds[ms(ia)] : ~0ull;
+    uint64_t y = ib < nb ? lds[ms(na + ib)] : ~0ull;
 #pragma unroll
     for (int r = 0; r < kMergeItems; ++r) {
       const bool take_a = x < y;
       out[r] = take_a ? x : y;
       if (take_a) {
         ++ia;
-        x = ia < na ? lds[ia] : ~0ull;
+        x = ia < na ? lds[ms(ia)] : ~0ull;
       } else {
         ++ib;
-        y = ib < nb ? lds[na + ib] : ~0ull;
+        y = ib < nb ? lds[ms(na + ib)] : ~0ull;
       }
     }
   }
@@ -288,11 +299,11 @@ __global__ __launch_bounds__(kMergeNT) void merge_runs_kernel(SortArgs a, const 
   if (dt < count) {
 #pragma unroll
     for (int r = 0; r < kMergeItems; ++r)
-      if (dt + r < count) lds[dt + r] = out[r];
+      if (dt + r < count) lds[ms(dt + r)] = out[r];
   }
   __syncthreads();
   if (!FINAL) {
-    for (int j = t; j < count; j += kMergeNT) dst[base + o0 + j] = lds[j];
+    for (int j = t; j < count; j += kMergeNT) dst[base + o0 + j] = lds[ms(j)];
     return;
   }
   // outputs: source columns, then the gathered second key, each batch of
@@ -303,7 +314,7 @@ __global__ __launch_bounds__(kMergeNT) void merge_runs_kernel(SortArgs a, const 
     const int j = k * kMergeNT + t;
     col[k] = 0;
     if (j < count) {
-      const uint32_t tie = (uint32_t)lds[j];
+      const uint32_t tie = (uint32_t)lds[ms(j)];
       const int32_t pos = (int32_t)(a.ties_desc ? kTieMask - tie : tie);
       col[k] = a.perm_in ? a.perm_in[base + pos] : pos;
     }
@@ -314,7 +325,7 @@ __global__ __launch_bounds__(kMergeNT) void merge_runs_kernel(SortArgs a, const 
     if (j >= count) continue;
     a.perm_out[base + o0 + j] = col[k];
     if (a.key_out) {
-      uint32_t key = (uint32_t)(lds[j] >> 32);
+      uint32_t key = (uint32_t)(lds[ms(j)] >> 32);
       if (a.descending) key = ~key;
       store_sorted(a.key_out, a.key_out_dtype, a.key_dtype, base + o0 + j, key);
     }
