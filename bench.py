@@ -453,7 +453,7 @@ def _sort_c2(torch, np, _lib, dev, s_handle, gen, nbuf):
     w.alg_bytes = 20971520  # sort: 2 MiB keys in, 2 MiB keys + 4 MiB indices out; gather: 3 x 4 MiB
     w.workload = ("tumpy.argsort (stable, packed bf16 path) of bf16 keys [256,4096] = round(16 z)/16, then "
                   "tumpy.take_along_axis of an f32 [256,4096] array by the indices")
-    w.kernel = "radix_sort_rows_kernel<4> + gather_row_lds_kernel<u32>"
+    w.kernel = "radix_sort_rows_kernel<8> + gather_row_lds_kernel<u32>"
     w.cpu_batch = 16
 
     def launch(i):

@@ -55,6 +55,13 @@ int tallax_testing_top_dynamic_k_path(const void* x, int dtype, int64_t rows, in
  * words): the calibration launch for the FETCH_SIZE counter. */
 int tallax_testing_read_bytes(const void* src, int64_t nbytes, int width, uint32_t* out, tallax_stream_t stream);
 
+/* One LDS atomic add per lane of each wave on the counter of its digit
+ * (digits[i] mod ndig, 1 <= ndig <= 256), 256 lanes per workgroup, nblocks
+ * workgroups: out[i] = the counter's value before lane i's add.  The bf16
+ * radix sort relies on these adds returning in ascending lane order. */
+int tallax_testing_lds_atomic_order(const uint32_t* digits, int64_t nblocks, int ndig, uint32_t* out,
+                                    tallax_stream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

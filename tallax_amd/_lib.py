@@ -62,6 +62,7 @@ _SIGNATURES = {
     "tallax_testing_gumbel": ([ctypes.c_uint32, ctypes.c_uint32, _c_p, _c_p, _c_p, _c_i64, _c_p], _c_int),
     "tallax_testing_lane_ops": ([_c_p, _c_p], _c_int),
     "tallax_testing_read_bytes": ([_c_p, _c_i64, _c_int, _c_p, _c_p], _c_int),
+    "tallax_testing_lds_atomic_order": ([_c_p, _c_i64, _c_int, _c_p, _c_p], _c_int),
     "tallax_testing_select_plan": ([_c_i64, _c_i64, _c_int, _c_p], _c_int),
     "tallax_testing_top_dynamic_k_path": ([_c_p, _c_int, _c_i64, _c_i64, _c_p, _c_int, _c_int, _c_int, _c_p, _c_int,
                                            _c_int, _c_int, _c_d, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_sz, _c_p, _c_int],

@@ -20,7 +20,7 @@
 // strides < E are exchanged within the thread, strides < 64 E across lanes
 // with DPP / v_permlane*_swap, larger strides through LDS.  bf16 rows of up
 // to 4096 elements use a stable LSD radix sort instead (see
-// radix_sort_rows_kernel).
+// radix_sort_rows_kernel: two passes of 8-bit digits).
 #include <stdint.h>
 
 #include "tallax_hip.h"
@@ -102,146 +102,7 @@ __global__ __launch_bounds__(P / E) void sort_rows_kernel(SortArgs a) {
   }
 }
 
-// bf16 keys (records of a 16-bit key and a 16-bit tie): a stable LSD radix
-// sort on the key, four passes of 4-bit digits.  The records start in
-// ascending tie order (position p holds tie p), so sorting by key alone,
-// stably, is the ascending record order the bitonic network gives.
-//   * each thread holds E consecutive records; per pass it counts its digits
-//     in its own packed LDS counters (word j * NT + t: digit j in the low
-//     half, digit j + 8 in the high half); the value before its increment is
-//     the record's rank among the thread's earlier records of that digit;
-//   * a raking exclusive scan over the words in (j, t) order gives, per
-//     half, the count of earlier (digit, thread) pairs; the high halves then
-//     add the number of records with digit < 8;
-//   * records move to their ranks through LDS and are read back in order.
 constexpr int kRadixNT = 1024;
-
-template <int E>
-__global__ __launch_bounds__(kRadixNT) void radix_sort_rows_kernel(SortArgs a) {
-  using RT = RecT<uint32_t>;
-  extern __shared__ __align__(16) unsigned char smem[];
-  uint32_t* cnt = (uint32_t*)smem;       // 8 * kRadixNT counter words
-  uint32_t* buf = cnt + 8 * kRadixNT;    // cols records
-  __shared__ uint32_t wsum[kRadixNT / kWave];
-  const int t = threadIdx.x, l = lane_id(), w = t / kWave;
-  const int n = (int)a.cols;
-  const int64_t row = blockIdx.x;
-  const int64_t base = row * a.cols;
-  uint32_t v[E];
-  // the E keys of positions t E .. t E + E - 1 (ties descending: original
-  // indices n - 1 - p, read in one piece when the row allows)
-  const bool vec = E == 4 && (n & 3) == 0 && (((uintptr_t)a.key + (uintptr_t)base * 2) & 7) == 0;
-  if (vec && t * E < n) {
-    const int i0 = a.ties_desc ? n - 4 - t * E : t * E;
-    const uint2 q = load_once((const uint2*)((const uint16_t*)a.key + base + i0));
-    const uint32_t h[4] = {q.x << 16, q.x & 0xFFFF0000u, q.y << 16, q.y & 0xFFFF0000u};
-#pragma unroll
-    for (int r = 0; r < E; ++r) {
-      const int i = a.ties_desc ? n - 1 - (t * E + r) : t * E + r;
-      uint32_t k = sort_order_bits(&h[a.ties_desc ? 3 - r : r], kF32, 0);
-      if (a.descending) k = ~k;
-      v[r] = RT::make(k, a.ties_desc ? 0xFFFFu - (uint32_t)i : (uint32_t)i);
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < E; ++r) {
-      const int p = t * E + r;
-      v[r] = 0u;
-      if (p < n) {
-        const int i = a.ties_desc ? n - 1 - p : p;  // ascending ties either way
-        uint32_t k = sort_order_bits(a.key, a.key_dtype, base + i);
-        if (a.descending) k = ~k;
-        v[r] = RT::make(k, a.ties_desc ? 0xFFFFu - (uint32_t)i : (uint32_t)i);
-      }
-    }
-  }
-#pragma unroll 1
-  for (int sh = 16; sh < 32; sh += 4) {
-    // this thread's own counters (nobody else reads them before the barrier below)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) cnt[j * kRadixNT + t] = 0u;
-    uint32_t lr[E];
-#pragma unroll
-    for (int r = 0; r < E; ++r) {
-      lr[r] = 0u;
-      if (t * E + r < n) {
-        const uint32_t d = (v[r] >> sh) & 15u;
-        const uint32_t hs = (d >> 3) * 16u;
-        lr[r] = (atomicAdd(&cnt[(d & 7u) * kRadixNT + t], 1u << hs) >> hs) & 0xFFFFu;
-      }
-    }
-    __syncthreads();  // every thread's counts are in
-    // raking exclusive scan: thread t takes words 8t .. 8t + 7
-    const uint4 wa = ((const uint4*)cnt)[2 * t], wb = ((const uint4*)cnt)[2 * t + 1];
-    uint32_t x[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-    uint32_t run = 0u;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t c = x[j];
-      x[j] = run;
-      run += c;
-    }
-    const uint32_t incl = wave_incl_scan(run);
-    if (l == kWave - 1) wsum[w] = incl;
-    __syncthreads();
-    uint32_t pre = incl - run, tot = 0u;
-#pragma unroll
-    for (int i = 0; i < kRadixNT / kWave; ++i) {
-      const uint32_t s = wsum[i];
-      pre += i < w ? s : 0u;
-      tot += s;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] += pre;
-    ((uint4*)cnt)[2 * t] = make_uint4(x[0], x[1], x[2], x[3]);
-    ((uint4*)cnt)[2 * t + 1] = make_uint4(x[4], x[5], x[6], x[7]);
-    __syncthreads();
-    const uint32_t below8 = tot & 0xFFFFu;  // records with digit < 8
-#pragma unroll
-    for (int r = 0; r < E; ++r) {
-      if (t * E + r < n) {
-        const uint32_t d = (v[r] >> sh) & 15u;
-        const uint32_t word = cnt[(d & 7u) * kRadixNT + t];
-        const uint32_t dest = (d >> 3) ? (word >> 16) + below8 : (word & 0xFFFFu);
-        buf[dest + lr[r]] = v[r];
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < E; ++r)
-      if (t * E + r < n) v[r] = buf[t * E + r];
-  }
-  const uint32_t tie_mask = 0xFFFFu;
-  if (vec && ((uintptr_t)(a.perm_out + base) & 15) == 0 && t * E < n) {
-    int32_t pp[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const uint32_t tie = RT::tie(v[r]);
-      pp[r] = a.ties_desc ? (int)(tie_mask - tie) : (int)tie;
-    }
-    *(int4*)(a.perm_out + base + t * E) = make_int4(pp[0], pp[1], pp[2], pp[3]);
-  }
-#pragma unroll
-  for (int r = 0; r < E; ++r) {
-    const int i = t * E + r;
-    if (i >= n) continue;
-    const uint32_t tie = RT::tie(v[r]);
-    const int pos = a.ties_desc ? (int)(tie_mask - tie) : (int)tie;
-    if (!(vec && ((uintptr_t)(a.perm_out + base) & 15) == 0)) a.perm_out[base + i] = pos;
-    if (a.key_out) {
-      uint32_t k = RT::key(v[r]);
-      if (a.descending) k = ~k;
-      k &= 0xFFFF0000u;  // rebuild the full order bits of a bf16 key from its high half
-      if (k < 0x80000000u) k |= 0xFFFFu;
-      else if (k > 0xFF800000u) k = 0xFFFFFFFEu;
-      store_sorted(a.key_out, a.key_out_dtype, a.key_dtype, base + i, k);
-    }
-    if (a.aux_out) {
-      const uint32_t u = sort_order_bits(a.aux, a.aux_dtype, base + pos);
-      store_sorted(a.aux_out, a.aux_out_dtype, a.aux_dtype, base + i, u);
-    }
-  }
-}
 
 // out[i] = the key at column perm[i] of the same row, standardised and
 // decoded like the sorted key outputs (store_sorted): the third and later
@@ -262,15 +123,110 @@ __global__ __launch_bounds__(256) void gather_sort_key_kernel(const void* key, i
   }
 }
 
-template <int E>
-static int launch_radix(const SortArgs& a, int64_t rows, hipStream_t s) {
-  const size_t lds = (size_t)8 * kRadixNT * 4 + (size_t)a.cols * 4;
-  const hipError_t attr = set_dynamic_lds_limit((const void*)radix_sort_rows_kernel<E>, 8 * kRadixNT * 4 + 4 * kRadixNT * 4, s);
-  if (attr != hipSuccess) {
-    set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr));
-    return kHipError;
+// bf16 keys (records of a 16-bit key and a 16-bit tie): a stable LSD radix
+// sort on the key, two passes of 8-bit digits.  The records start in
+// ascending tie order (slot p holds tie p), so sorting by key alone, stably,
+// is the ascending record order the bitonic network gives.  The 4096 record
+// slots of a row sit record-major inside each wave: slot p = 256 w + 64 r + l
+// is record r of lane l of wave w, so the wave's slots in ascending order are
+// (r, l).  Per pass:
+//   * each wave counts its digits in its own 256 counters (digit-major, 17
+//     words apart, so that random digits spread over the banks) with one LDS
+//     atomic per record, record r = 0..3 in turn.  The atomics of one
+//     instruction on one address return in ascending lane order (gfx950), so
+//     the value before a record's increment is its rank among the wave's
+//     earlier slots of that digit: a stable rank;
+//   * an exclusive scan over (digit, wave) in digit-major order gives each
+//     pair its start, and records move to start + rank through LDS;
+//   * slots past the row hold all-ones records, which every pass keeps after
+//     the row's own (their slots are the highest, their digits the largest).
+// (Four passes of 4-bit digits with per-thread packed counters took 13.0 us at
+// config 2; these two passes, with the same three barriers each, 1.6 us less.)
+template <int BITS>
+__global__ __launch_bounds__(kRadixNT) void radix_sort_rows_kernel(SortArgs a) {
+  static_assert(BITS == 8, "8-bit digits: 256 counters per wave");
+  using RT = RecT<uint32_t>;
+  constexpr int NW = kRadixNT / kWave;  // 16 waves, 256 slots each
+  constexpr int HS = NW + 1;            // counter stride per digit
+  __shared__ uint32_t hist[256 * HS];
+  __shared__ uint32_t buf[4 * kRadixNT];
+  __shared__ uint32_t wsum[NW];
+  const int t = threadIdx.x, l = lane_id(), w = t / kWave;
+  const int n = (int)a.cols;
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * a.cols;
+  uint32_t v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int p = w * 256 + r * kWave + l;
+    v[r] = ~0u;
+    if (p < n) {
+      const int i = a.ties_desc ? n - 1 - p : p;  // ascending ties either way
+      uint32_t k = sort_order_bits(a.key, a.key_dtype, base + i);
+      if (a.descending) k = ~k;
+      v[r] = RT::make(k, a.ties_desc ? 0xFFFFu - (uint32_t)i : (uint32_t)i);
+    }
   }
-  hipLaunchKernelGGL((radix_sort_rows_kernel<E>), dim3((unsigned)rows), dim3(kRadixNT), lds, s, a);
+#pragma unroll 1
+  for (int sh = 16; sh < 32; sh += 8) {
+#pragma unroll
+    for (int d = l; d < 256; d += kWave) hist[d * HS + w] = 0u;  // this wave's counters
+    uint32_t dg[4], rk[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      dg[r] = (v[r] >> sh) & 0xFFu;
+      rk[r] = atomicAdd(&hist[dg[r] * HS + w], 1u);
+    }
+    __syncthreads();  // every count is in
+    // exclusive scan over i = digit * NW + wave: thread t takes i = 4t .. 4t + 3
+    const int d0 = t >> 2, w0 = 4 * (t & 3);
+    uint32_t c[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c[q] = hist[d0 * HS + w0 + q];
+    const uint32_t run = c[0] + c[1] + c[2] + c[3];
+    const uint32_t incl = wave_incl_scan(run);
+    if (l == kWave - 1) wsum[w] = incl;
+    __syncthreads();
+    uint32_t pre = incl - run;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) pre += i < w ? wsum[i] : 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      hist[d0 * HS + w0 + q] = pre;
+      pre += c[q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) buf[hist[dg[r] * HS + w] + rk[r]] = v[r];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = buf[w * 256 + r * kWave + l];
+  }
+  const uint32_t tie_mask = 0xFFFFu;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = w * 256 + r * kWave + l;
+    if (i >= n) continue;
+    const uint32_t tie = RT::tie(v[r]);
+    const int pos = a.ties_desc ? (int)(tie_mask - tie) : (int)tie;
+    a.perm_out[base + i] = pos;
+    if (a.key_out) {
+      uint32_t k = RT::key(v[r]);
+      if (a.descending) k = ~k;
+      k &= 0xFFFF0000u;  // rebuild the full order bits of a bf16 key from its high half
+      if (k < 0x80000000u) k |= 0xFFFFu;
+      else if (k > 0xFF800000u) k = 0xFFFFFFFEu;
+      store_sorted(a.key_out, a.key_out_dtype, a.key_dtype, base + i, k);
+    }
+    if (a.aux_out) {
+      const uint32_t u = sort_order_bits(a.aux, a.aux_dtype, base + pos);
+      store_sorted(a.aux_out, a.aux_out_dtype, a.aux_dtype, base + i, u);
+    }
+  }
+}
+
+static int launch_radix8(const SortArgs& a, int64_t rows, hipStream_t s) {
+  hipLaunchKernelGGL((radix_sort_rows_kernel<8>), dim3((unsigned)rows), dim3(kRadixNT), 0, s, a);
   return kOk;
 }
 
@@ -345,7 +301,7 @@ int tallax_sort_rows_ws(const void* key, int key_dtype, int64_t rows, int64_t co
   // bf16 keys on the packed path fit (16-bit key | 16-bit tie) in one u32
   const bool narrow = key_dtype == kBF16 && !perm_in && cols <= 65536;
   // bf16 rows up to 4096: radix sort; longer ones: the bitonic network
-  const int st = narrow ? (cols <= 4 * kRadixNT ? launch_radix<4>(a, rows, stream) : launch_sort_p<uint32_t>(a, rows, stream))
+  const int st = narrow ? (cols <= 4 * kRadixNT ? launch_radix8(a, rows, stream) : launch_sort_p<uint32_t>(a, rows, stream))
                         : launch_sort_p<uint64_t>(a, rows, stream);
   if (st) return st;
   return launch_status("tallax_sort_rows");

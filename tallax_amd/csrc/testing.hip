@@ -72,6 +72,18 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const void* src, int64_
 
 }  // namespace tx
 
+// Every lane of a wave adds 1 to the LDS counter of its digit (digits[] mod
+// ndig) in one atomic instruction; out[] gets the value before each add.
+// Lane-ordered atomics give each lane the count of lower lanes with its digit.
+__global__ __launch_bounds__(256) void lds_atomic_order_kernel(const uint32_t* digits, int ndig, uint32_t* out) {
+  __shared__ uint32_t cnt[4][256];
+  const int w = threadIdx.x / 64;
+  for (int i = threadIdx.x; i < 4 * 256; i += 256) cnt[i / 256][i % 256] = 0u;
+  __syncthreads();
+  const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  out[e] = atomicAdd(&cnt[w][digits[e] % (uint32_t)ndig], 1u);
+}
+
 extern "C" {
 
 int tallax_testing_lane_ops(uint32_t* out, hipStream_t stream) {
@@ -119,6 +131,17 @@ int tallax_testing_read_bytes(const void* src, int64_t nbytes, int width, uint32
   else if (width == 8) hipLaunchKernelGGL(tx::read_probe_kernel<8>, grid, block, 0, stream, src, nbytes, out);
   else hipLaunchKernelGGL(tx::read_probe_kernel<4>, grid, block, 0, stream, src, nbytes, out);
   return tx::launch_status("tallax_testing_read_bytes");
+}
+
+
+int tallax_testing_lds_atomic_order(const uint32_t* digits, int64_t nblocks, int ndig, uint32_t* out,
+                                    hipStream_t stream) {
+  if (!digits || !out || nblocks <= 0 || nblocks > 65535 || ndig < 1 || ndig > 256) {
+    tx::set_error("lds_atomic_order: bad arguments");
+    return tx::kInvalidArgument;
+  }
+  hipLaunchKernelGGL(lds_atomic_order_kernel, dim3((unsigned)nblocks), dim3(256), 0, stream, digits, ndig, out);
+  return tx::launch_status("tallax_testing_lds_atomic_order");
 }
 
 }  // extern "C"

@@ -22,7 +22,7 @@ def _fake_pass(counter, config, extras, outdir, timeout):
             "tx::seg_select_kernel<0, 19, 256, false>": [38000.0] * launches,
             "tx::seg_merge64_kernel<0>": [300.0] * launches,
             "tx::softmax_topk_kernel<true>": [500000.0] * c5,
-            "tx::radix_sort_rows_kernel<4>": [1000.0] * launches,
+            "tx::radix_sort_rows_kernel<8>": [1000.0] * launches,
             "tx::gather_row_lds_kernel<unsigned int>": [4000.0] * launches,
             "at::native::normal_kernel": [99999.0] * 7,               # input generation: not counted
         }
@@ -32,7 +32,7 @@ def _fake_pass(counter, config, extras, outdir, timeout):
         "tx::seg_select_kernel<0, 19, 256, false>": [1024.0] * launches,
         "tx::seg_merge64_kernel<0>": [56.0] * launches,
         "tx::softmax_topk_kernel<true>": [24000.0] * c5,
-        "tx::radix_sort_rows_kernel<4>": [6144.0] * launches,
+        "tx::radix_sort_rows_kernel<8>": [6144.0] * launches,
         "tx::gather_row_lds_kernel<unsigned int>": [4096.0] * launches,
     }
 

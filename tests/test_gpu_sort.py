@@ -35,6 +35,24 @@ def _special_row(rng, cols):
     return x
 
 
+def test_lds_atomics_return_in_lane_order(gpu):
+    """The bf16 radix sort's stable ranks come from per-wave LDS counters: one
+    atomic add per lane, whose returns must follow ascending lane order."""
+    from tallax_amd import _lib
+    nblocks = 512
+    for ndig in (1, 3, 16, 256):
+        _log(f"lds atomic order, {ndig} digits")
+        d = torch.randint(0, 1 << 30, (nblocks * 256,), dtype=torch.int32, device=gpu)
+        out = torch.empty_like(d)
+        _lib.check(_lib.LIB.tallax_testing_lds_atomic_order(d.data_ptr(), nblocks, ndig, out.data_ptr(),
+                                                            _lib.stream_of(d)), "lds_atomic_order")
+        dig = (d.cpu().numpy().astype(np.int64) % ndig).reshape(-1, 64)
+        want = np.zeros_like(dig)
+        for lane in range(64):
+            want[:, lane] = (dig[:, :lane] == dig[:, lane:lane + 1]).sum(axis=1)
+        assert np.array_equal(out.cpu().numpy().reshape(-1, 64), want)
+
+
 def test_config2_argsort_then_gather(gpu):
     from tallax_amd import tumpy
     _log("config 2: bf16 [256,4096] stable argsort + take_along_axis")
