@@ -14,7 +14,7 @@
 // unique, so any correct sort of them gives exactly that order, and two
 // sorted runs merge without a stability rule.
 //   1. sort_chunks_kernel: one 512-thread workgroup sorts each 16384-record
-//      chunk of a row in LDS (a stable LSD radix sort on the key, 4-bit
+//      chunk of a row in LDS (a stable LSD radix sort on the key, 8-bit
 //      digits) and writes the sorted run to the workspace.
 //   2. merge_runs_kernel, ceil(log2(chunks)) passes: runs of length L are
 //      merged pairwise into runs of 2L, ping-ponging between two workspace
@@ -41,41 +41,41 @@ namespace tx {
 constexpr int kWideChunk = 16384;  // records per chunk sorted in LDS
 constexpr int kChunkNT = 512;
 constexpr int kChunkE = kWideChunk / kChunkNT;
-constexpr int kChunkSlots = kWideChunk + kWideChunk / 32;
-constexpr int kChunkLds = 8 * kChunkNT * 4 + kChunkSlots * 8;  // counters + records
+constexpr int kChunkLds = kWideChunk * 8 + 256 * (kChunkNT / kWave + 1) * 4;  // records + digit counters
 constexpr int kMergeNT = 256;
 constexpr int kMergeItems = 16;                      // outputs per thread
 constexpr int kMergeTile = kMergeNT * kMergeItems;   // outputs per workgroup
 constexpr uint32_t kTieMask = 0x7FFFFFFFu;
 static_assert((2 * kWideChunk) % kMergeTile == 0, "a merge tile never straddles two pairs of runs");
-static_assert(kChunkE * kChunkNT == kWideChunk && kWideChunk < 65536, "16-bit packed digit counts");
-
-// LDS slot of chunk record L: one spare slot per 32 records, so that the
-// thread-major reads (thread t reads records 32 t .. 32 t + 31) of a wave
-// spread over the banks.
-__device__ __forceinline__ int chunk_slot(int L) { return L + (L >> 5); }
+static_assert(kChunkE * kChunkNT == kWideChunk, "whole chunks per workgroup");
 
 // Pass 1: sorted runs of kWideChunk records, by a stable LSD radix sort on
-// the 32-bit key in 4-bit digits (at most eight passes; a digit that every
-// key of the chunk shares is skipped).  Records start in LDS in tie order
-// (linear index L = column - c0, or its reverse for descending ties), so the
-// stable sort by key alone is the order of the full records.
-//   * thread t owns records L = 32 t .. 32 t + 31 of the current order; per
-//     pass it counts their digits in its own packed LDS counters (word
-//     j * NT + t: digit j in the low half, digit j + 8 in the high half), the
-//     value before each increment being the record's rank among the thread's
-//     earlier records of that digit;
-//   * a raking exclusive scan over the words in (j, t) order gives, per half,
-//     the number of records of earlier (digit, thread) pairs; the high halves
-//     then add the count of digits < 8;
-//   * records are scattered to their new slots; the next pass reads them back
-//     thread-major.
+// the 32-bit key in 8-bit digits (at most four passes; a digit that every key
+// of the chunk shares is skipped).  Slot p of the chunk holds record
+// (order bits << 32 | tie) of linear index p (column c0 + p, or its reverse
+// for descending ties), so the stable sort by key alone is the order of the
+// full records; slots past the row hold all-ones records, which stay last.
+// The 16384 slots sit record-major inside each wave: slot p = 2048 w + 64 r + l
+// is record r (0..31) of lane l of wave w, so a wave's slots in ascending order
+// are (r, l).  Per pass:
+//   * each wave counts its digits in its own 256 LDS counters (digit-major,
+//     NW + 1 words apart) with one atomic per record, r = 0..31 in turn; the
+//     atomics of one instruction on one address return in ascending lane order
+//     (gfx950; tallax_testing_lds_atomic_order checks it), so the value before
+//     a record's increment is its stable rank among the wave's earlier slots
+//     of that digit;
+//   * an exclusive scan over (digit, wave) in digit-major order gives each
+//     pair its start, records move to start + rank through LDS, and the next
+//     pass reads them back in slot order.
+// (Eight passes of 4-bit digits with per-thread packed counters took 2.93 ms
+// at [1024, 201088].)
 template <int DT, bool PERM>
 __global__ __launch_bounds__(kChunkNT) void sort_chunks_kernel(SortArgs a, int nchunks, uint64_t* out) {
   constexpr int NW = kChunkNT / kWave;
+  constexpr int HS = NW + 1;  // counter stride per digit
   extern __shared__ __align__(16) unsigned char smem[];
-  uint32_t* cnt = (uint32_t*)smem;
-  uint64_t* buf = (uint64_t*)(cnt + 8 * kChunkNT);
+  uint64_t* buf = (uint64_t*)smem;                     // kWideChunk records
+  uint32_t* hist = (uint32_t*)(buf + kWideChunk);      // 256 * HS counters
   __shared__ uint32_t wsum[NW];
   __shared__ uint32_t red[2][NW];
   const int t = threadIdx.x, l = lane_id(), w = t / kWave;
@@ -84,32 +84,34 @@ __global__ __launch_bounds__(kChunkNT) void sort_chunks_kernel(SortArgs a, int n
   const int64_t base = row * a.cols;
   const int64_t c0 = (int64_t)c * kWideChunk;
   const int n = (int)min((int64_t)kWideChunk, a.cols - c0);
-  // records in tie order (coalesced reads, each batch of loads in flight at
-  // once), and which key bits vary
+  // records in slot order (coalesced reads, every load of the chunk in
+  // flight at once), and which key bits vary
   uint32_t kand = ~0u, kor = 0u;
+  uint64_t v[kChunkE];
   {
     uint32_t raw[kChunkE];
     int32_t src[kChunkE];
 #pragma unroll
     for (int r = 0; r < kChunkE; ++r) {
-      const int L = r * kChunkNT + t;
+      const int L = w * (kChunkE * kWave) + r * kWave + l;
       src[r] = (int32_t)(c0 + (a.ties_desc ? n - 1 - L : L));
       if (PERM && L < n) src[r] = a.perm_in[base + src[r]];
     }
 #pragma unroll
     for (int r = 0; r < kChunkE; ++r) {
-      const int L = r * kChunkNT + t;
+      const int L = w * (kChunkE * kWave) + r * kWave + l;
       raw[r] = L < n ? key_bits_at<DT>(a.key, base + src[r]) : 0u;
     }
 #pragma unroll
     for (int r = 0; r < kChunkE; ++r) {
-      const int L = r * kChunkNT + t;
+      const int L = w * (kChunkE * kWave) + r * kWave + l;
+      v[r] = ~0ull;
       if (L < n) {
         uint32_t k = order_from_bits(raw[r], DT);
         if (a.descending) k = ~k;
         const uint32_t p = (uint32_t)(c0 + (a.ties_desc ? n - 1 - L : L));
         const uint32_t tie = a.ties_desc ? kTieMask - p : p;
-        buf[chunk_slot(L)] = ((uint64_t)k << 32) | tie;
+        v[r] = ((uint64_t)k << 32) | tie;
         kand &= k;
         kor |= k;
       }
@@ -132,63 +134,51 @@ __global__ __launch_bounds__(kChunkNT) void sort_chunks_kernel(SortArgs a, int n
   }
   const uint32_t varying = kand ^ kor;
 #pragma unroll 1
-  for (int sh = 0; sh < 32; sh += 4) {
-    if (((varying >> sh) & 15u) == 0u) continue;  // every key has this digit: the pass is the identity
+  for (int sh = 0; sh < 32; sh += 8) {
+    if (((varying >> sh) & 0xFFu) == 0u) continue;  // every key has this digit: the pass is the identity
 #pragma unroll
-    for (int j = 0; j < 8; ++j) cnt[j * kChunkNT + t] = 0u;  // own words: no one else reads them yet
-    uint64_t v[kChunkE];
-    uint32_t lr[kChunkE];
+    for (int d = l; d < 256; d += kWave) hist[d * HS + w] = 0u;  // this wave's counters
+    uint32_t rk[kChunkE];
 #pragma unroll
     for (int r = 0; r < kChunkE; ++r) {
-      const int L = t * kChunkE + r;
-      v[r] = 0ull;
-      lr[r] = 0u;
-      if (L < n) {
-        v[r] = buf[chunk_slot(L)];
-        const uint32_t d = (uint32_t)(v[r] >> (32 + sh)) & 15u;
-        const uint32_t hs = (d >> 3) * 16u;
-        lr[r] = (atomicAdd(&cnt[(d & 7u) * kChunkNT + t], 1u << hs) >> hs) & 0xFFFFu;
-      }
+      const uint32_t d = (uint32_t)(v[r] >> (32 + sh)) & 0xFFu;
+      rk[r] = atomicAdd(&hist[d * HS + w], 1u);
     }
-    __syncthreads();  // every count is in, every record read
-    const uint4 wa = ((const uint4*)cnt)[2 * t], wb = ((const uint4*)cnt)[2 * t + 1];
-    uint32_t x[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-    uint32_t run = 0u;
+    __syncthreads();  // every count is in
+    // exclusive scan over i = digit * NW + wave: thread t takes i = 4t .. 4t + 3
+    static_assert(256 * NW == 4 * kChunkNT, "four counters per thread in the scan");
+    const int d0 = (4 * t) / NW, w0 = (4 * t) % NW;
+    uint32_t cq[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t cj = x[j];
-      x[j] = run;
-      run += cj;
-    }
+    for (int q = 0; q < 4; ++q) cq[q] = hist[d0 * HS + w0 + q];
+    const uint32_t run = cq[0] + cq[1] + cq[2] + cq[3];
     const uint32_t incl = wave_incl_scan(run);
     if (l == kWave - 1) wsum[w] = incl;
     __syncthreads();
-    uint32_t pre = incl - run, tot = 0u;
+    uint32_t pre = incl - run;
 #pragma unroll
-    for (int i = 0; i < NW; ++i) {
-      const uint32_t sw = wsum[i];
-      pre += i < w ? sw : 0u;
-      tot += sw;
+    for (int i = 0; i < NW; ++i) pre += i < w ? wsum[i] : 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      hist[d0 * HS + w0 + q] = pre;
+      pre += cq[q];
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] += pre;
-    ((uint4*)cnt)[2 * t] = make_uint4(x[0], x[1], x[2], x[3]);
-    ((uint4*)cnt)[2 * t + 1] = make_uint4(x[4], x[5], x[6], x[7]);
     __syncthreads();
-    const uint32_t below8 = tot & 0xFFFFu;  // records whose digit is < 8
 #pragma unroll
     for (int r = 0; r < kChunkE; ++r) {
-      if (t * kChunkE + r < n) {
-        const uint32_t d = (uint32_t)(v[r] >> (32 + sh)) & 15u;
-        const uint32_t word = cnt[(d & 7u) * kChunkNT + t];
-        const uint32_t dest = (d >> 3) ? (word >> 16) + below8 : (word & 0xFFFFu);
-        buf[chunk_slot((int)(dest + lr[r]))] = v[r];
-      }
+      const uint32_t d = (uint32_t)(v[r] >> (32 + sh)) & 0xFFu;
+      buf[hist[d * HS + w] + rk[r]] = v[r];
     }
     __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kChunkE; ++r) v[r] = buf[w * (kChunkE * kWave) + r * kWave + l];
   }
   uint64_t* dst = out + base + c0;
-  for (int j = t; j < n; j += kChunkNT) dst[j] = buf[chunk_slot(j)];
+#pragma unroll
+  for (int r = 0; r < kChunkE; ++r) {
+    const int L = w * (kChunkE * kWave) + r * kWave + l;
+    if (L < n) dst[L] = v[r];
+  }
 }
 
 // Merge path: the number of A records among the first d records of the
