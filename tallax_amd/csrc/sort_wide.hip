@@ -31,6 +31,7 @@
 #include <stdint.h>
 
 #include "tallax_hip.h"
+#include "tx_block_sort.h"
 #include "tx_common.h"
 #include "tx_host.h"
 #include "tx_scan.h"
@@ -49,17 +50,15 @@ constexpr uint32_t kTieMask = 0x7FFFFFFFu;
 static_assert((2 * kWideChunk) % kMergeTile == 0, "a merge tile never straddles two pairs of runs");
 static_assert(kChunkE * kChunkNT == kWideChunk, "whole chunks per workgroup");
 
-// Pass 1: sorted runs of kWideChunk records, by a stable LSD radix sort on
-// the 32-bit key in 8-bit digits (at most four passes; a digit that every key
-// of the chunk shares is skipped).  Slot p of the chunk holds record
-// (order bits << 32 | tie) of linear index p (column c0 + p, or its reverse
-// for descending ties), so the stable sort by key alone is the order of the
-// full records; slots past the row hold all-ones records, which stay last.
-// The 16384 slots sit record-major inside each wave: slot p = 2048 w + 64 r + l
-// is record r (0..31) of lane l of wave w, so a wave's slots in ascending order
-// are (r, l).  Per pass:
+// Stable LSD radix sort by the key (the records' high 32 bits) of the E x NT
+// records a workgroup holds in registers in slot order, slot
+// (E * 64) w + 64 r + l being record r of lane l of wave w; 8-bit digits, the
+// digits in which no key varies skipped.  Slots n and above hold all-ones
+// records, which stay last: waves wholly past n neither count nor move theirs.
+// buf holds E * NT records, hist 256 * (NT / 64 + 1) counters.  Every thread
+// of the workgroup calls it.
 //   * each wave counts its digits in its own 256 LDS counters (digit-major,
-//     NW + 1 words apart) with one atomic per record, r = 0..31 in turn; the
+//     NW + 1 words apart) with one atomic per record, r = 0..E-1 in turn; the
 //     atomics of one instruction on one address return in ascending lane order
 //     (gfx950; tallax_testing_lds_atomic_order checks it), so the value before
 //     a record's increment is its stable rank among the wave's earlier slots
@@ -67,12 +66,73 @@ static_assert(kChunkE * kChunkNT == kWideChunk, "whole chunks per workgroup");
 //   * an exclusive scan over (digit, wave) in digit-major order gives each
 //     pair its start, records move to start + rank through LDS, and the next
 //     pass reads them back in slot order.
-// (Eight passes of 4-bit digits with per-thread packed counters took 2.93 ms
-// at [1024, 201088].)
+template <int E, int NT>
+__device__ __forceinline__ void radix_sort_slots(uint64_t (&v)[E], uint64_t* buf, uint32_t* hist, uint32_t* wsum,
+                                                 uint32_t varying, int n) {
+  constexpr int NW = NT / kWave;
+  constexpr int HS = NW + 1;  // counter stride per digit
+  static_assert(256 * NW == 4 * NT, "four counters per thread in the scan");
+  const int t = threadIdx.x, l = lane_id(), w = t / kWave;
+  const bool live = w * (E * kWave) < n;  // wave-uniform: the wave holds a slot below n
+#pragma unroll 1
+  for (int sh = 0; sh < 32; sh += 8) {
+    if (((varying >> sh) & 0xFFu) == 0u) continue;  // every key has this digit: the pass is the identity
+#pragma unroll
+    for (int d = l; d < 256; d += kWave) hist[d * HS + w] = 0u;  // this wave's counters
+    uint32_t rk[E];
+    if (live) {
+#pragma unroll
+      for (int r = 0; r < E; ++r) {
+        const uint32_t d = (uint32_t)(v[r] >> (32 + sh)) & 0xFFu;
+        rk[r] = atomicAdd(&hist[d * HS + w], 1u);
+      }
+    }
+    __syncthreads();  // every count is in
+    // exclusive scan over i = digit * NW + wave: thread t takes i = 4t .. 4t + 3
+    const int d0 = (4 * t) / NW, w0 = (4 * t) % NW;
+    uint32_t cq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cq[q] = hist[d0 * HS + w0 + q];
+    const uint32_t run = cq[0] + cq[1] + cq[2] + cq[3];
+    const uint32_t incl = wave_incl_scan(run);
+    if (l == kWave - 1) wsum[w] = incl;
+    __syncthreads();
+    uint32_t pre = incl - run;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) pre += i < w ? wsum[i] : 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      hist[d0 * HS + w0 + q] = pre;
+      pre += cq[q];
+    }
+    __syncthreads();
+    if (live) {
+#pragma unroll
+      for (int r = 0; r < E; ++r) {
+        const uint32_t d = (uint32_t)(v[r] >> (32 + sh)) & 0xFFu;
+        buf[hist[d * HS + w] + rk[r]] = v[r];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const int L = w * (E * kWave) + r * kWave + l;
+      v[r] = L < n ? buf[L] : ~0ull;
+    }
+  }
+}
+
+// Pass 1: sorted runs of kWideChunk records, by a stable LSD radix sort on
+// the 32-bit key in 8-bit digits (radix_sort_slots: at most four passes; a
+// digit that every key of the chunk shares is skipped).  Slot p of the chunk
+// holds record (order bits << 32 | tie) of linear index p (column c0 + p, or
+// its reverse for descending ties), so the stable sort by key alone is the
+// order of the full records; slots past the row hold all-ones records, which
+// stay last.  (Eight passes of 4-bit digits with per-thread packed counters
+// took 2.93 ms at [1024, 201088]; these four, 1.60 ms.)
 template <int DT, bool PERM>
 __global__ __launch_bounds__(kChunkNT) void sort_chunks_kernel(SortArgs a, int nchunks, uint64_t* out) {
   constexpr int NW = kChunkNT / kWave;
-  constexpr int HS = NW + 1;  // counter stride per digit
   extern __shared__ __align__(16) unsigned char smem[];
   uint64_t* buf = (uint64_t*)smem;                     // kWideChunk records
   uint32_t* hist = (uint32_t*)(buf + kWideChunk);      // 256 * HS counters
@@ -133,46 +193,7 @@ __global__ __launch_bounds__(kChunkNT) void sort_chunks_kernel(SortArgs a, int n
     kor |= red[1][i];
   }
   const uint32_t varying = kand ^ kor;
-#pragma unroll 1
-  for (int sh = 0; sh < 32; sh += 8) {
-    if (((varying >> sh) & 0xFFu) == 0u) continue;  // every key has this digit: the pass is the identity
-#pragma unroll
-    for (int d = l; d < 256; d += kWave) hist[d * HS + w] = 0u;  // this wave's counters
-    uint32_t rk[kChunkE];
-#pragma unroll
-    for (int r = 0; r < kChunkE; ++r) {
-      const uint32_t d = (uint32_t)(v[r] >> (32 + sh)) & 0xFFu;
-      rk[r] = atomicAdd(&hist[d * HS + w], 1u);
-    }
-    __syncthreads();  // every count is in
-    // exclusive scan over i = digit * NW + wave: thread t takes i = 4t .. 4t + 3
-    static_assert(256 * NW == 4 * kChunkNT, "four counters per thread in the scan");
-    const int d0 = (4 * t) / NW, w0 = (4 * t) % NW;
-    uint32_t cq[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) cq[q] = hist[d0 * HS + w0 + q];
-    const uint32_t run = cq[0] + cq[1] + cq[2] + cq[3];
-    const uint32_t incl = wave_incl_scan(run);
-    if (l == kWave - 1) wsum[w] = incl;
-    __syncthreads();
-    uint32_t pre = incl - run;
-#pragma unroll
-    for (int i = 0; i < NW; ++i) pre += i < w ? wsum[i] : 0u;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      hist[d0 * HS + w0 + q] = pre;
-      pre += cq[q];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kChunkE; ++r) {
-      const uint32_t d = (uint32_t)(v[r] >> (32 + sh)) & 0xFFu;
-      buf[hist[d * HS + w] + rk[r]] = v[r];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kChunkE; ++r) v[r] = buf[w * (kChunkE * kWave) + r * kWave + l];
-  }
+  radix_sort_slots<kChunkE, kChunkNT>(v, buf, hist, wsum, varying, n);
   uint64_t* dst = out + base + c0;
 #pragma unroll
   for (int r = 0; r < kChunkE; ++r) {
@@ -340,6 +361,252 @@ __global__ __launch_bounds__(kMergeNT) void merge_runs_kernel(SortArgs a, const 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Multiway merge by splitters (rows of 3 to kBucketMaxRuns chunks): one pass
+// instead of ceil(log2 chunks) pairwise merge passes.
+//   * bucket_split_kernel, one workgroup per row: every kBucketStride-th record
+//     of every sorted run is a sample (record (a + 1) G - 1 of a run, G the
+//     stride); the samples (at most 4096) are sorted by a block bitonic
+//     network, and every m-th one of them in that order is a splitter s_k.
+//     For every splitter and run, the run's first position p_kj with a record
+//     >= s_k: the run's samples below s_k, c, put it in [c G, (c + 1) G), so a
+//     binary search of G records finds it.  Bucket k holds the records in
+//     [s_k, s_k+1).  From run j it takes at most (q_j + 1) G records, q_j its
+//     samples in the bucket, and the bucket's samples number at most m, so a
+//     bucket never exceeds (m + runs) G records: m is chosen so that this is
+//     the bucket kernel's capacity.  The table holds every p_kj and each
+//     bucket's first output rank, sum_j p_kj.
+//   * bucket_sort_kernel, one workgroup per (row, bucket): the bucket's part of
+//     every run is loaded, run after run in tie order (chunk j holds columns
+//     [j, j + 1) kWideChunk: ascending ties take the runs in order, descending
+//     ones in reverse).  Inside one run the records are sorted, and between
+//     runs records of equal keys then come in tie order.  So the stable radix sort by the key
+//     alone (radix_sort_slots) gives the records' order, and the outputs
+//     (permutation, keys, gathered second key) are written at the bucket's
+//     first output rank.
+// Traffic: the chunk pass (4 bytes in, 8 out per element), then 8 in and the
+// outputs out: 28 bytes per element with keys and indices out, against 76 for
+// four pairwise merge passes at [1024, 201088].
+// ---------------------------------------------------------------------------
+constexpr int kBucketStride = 256;       // G: records between samples
+constexpr int kBucketMaxRuns = 56;       // (m >= 8) + runs <= 64: buckets of at most 64 G = 16384 records
+constexpr int kSplitNT = 1024;
+constexpr int kSplitSamples = 4096;      // >= kBucketMaxRuns * kWideChunk / kBucketStride
+constexpr int kBucketNT = 512;
+static_assert(kBucketMaxRuns * (kWideChunk / kBucketStride) <= kSplitSamples, "every sample fits the sort");
+
+struct BucketPlan {
+  int runs;     // chunks of a row
+  int samples;  // S: samples of a row
+  int m;        // samples per bucket
+  int K;        // buckets of a row
+  int E;        // records per thread of the bucket kernel (capacity E * kBucketNT)
+};
+
+__host__ __device__ inline int run_len(int64_t cols, int j) {
+  const int64_t left = cols - (int64_t)j * kWideChunk;
+  return (int)(left < kWideChunk ? left : kWideChunk);
+}
+
+__global__ __launch_bounds__(kSplitNT) void bucket_split_kernel(SortArgs a, BucketPlan bp, const uint64_t* runs,
+                                                                int32_t* table) {
+  __shared__ uint64_t srt[kSplitSamples];   // samples, sorted
+  __shared__ uint64_t per[kSplitSamples];   // samples in run order (each run's ascending)
+  __shared__ int sp[kBucketMaxRuns + 1];    // first sample of each run
+  __shared__ int soff[kSplitSamples / 8 + 2];
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * a.cols;
+  const int R = bp.runs, G = kBucketStride;
+  if (t == 0) {
+    int acc = 0;
+    for (int j = 0; j < R; ++j) {
+      sp[j] = acc;
+      acc += run_len(a.cols, j) / G;
+    }
+    sp[R] = acc;
+  }
+  for (int k = t; k <= bp.K; k += kSplitNT) soff[k] = 0;
+  __syncthreads();
+  // sample i = 4t + r: run j with sp[j] <= i < sp[j + 1], record (i - sp[j] + 1) G - 1 of it
+  uint64_t v[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = 4 * t + r;
+    v[r] = ~0ull;
+    if (i < bp.samples) {
+      int j = 0;
+      while (sp[j + 1] <= i) ++j;
+      v[r] = runs[base + (int64_t)j * kWideChunk + (int64_t)(i - sp[j] + 1) * G - 1];
+      per[i] = v[r];
+    }
+  }
+  block_bitonic_sort_c<uint64_t, 4, kSplitSamples, false>(v, srt);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) srt[4 * t + r] = v[r];
+  __syncthreads();
+  // p_kj for k = 0..K (k = 0: 0; k = K: the run's length), one (k, j) per thread in turn
+  int32_t* tp = table + row * (int64_t)(bp.K + 1) * (R + 1);  // [(K + 1) R] positions, then [K + 1] offsets
+  for (int q = t; q < (bp.K + 1) * R; q += kSplitNT) {
+    const int k = q / R, j = q - k * R;
+    const int len = run_len(a.cols, j);
+    int pos;
+    if (k == 0) {
+      pos = 0;
+    } else if (k == bp.K) {
+      pos = len;
+    } else {
+      const uint64_t sk = srt[k * bp.m];
+      // samples of run j below sk (each run's samples ascend)
+      int lo = sp[j], hi = sp[j + 1];
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (per[mid] < sk) lo = mid + 1;
+        else hi = mid;
+      }
+      const int c = lo - sp[j];
+      // first record >= sk in [c G, min((c + 1) G - 1, len)]
+      int l0 = c * G, h0 = c < sp[j + 1] - sp[j] ? (c + 1) * G - 1 : len;
+      const uint64_t* rj = runs + base + (int64_t)j * kWideChunk;
+      while (l0 < h0) {
+        const int mid = (l0 + h0) >> 1;
+        if (rj[mid] < sk) l0 = mid + 1;
+        else h0 = mid;
+      }
+      pos = l0;
+    }
+    tp[q] = pos;
+    atomicAdd(&soff[k], pos);
+  }
+  __syncthreads();
+  for (int k = t; k <= bp.K; k += kSplitNT) tp[(bp.K + 1) * R + k] = soff[k];
+}
+
+template <int E>
+__global__ __launch_bounds__(kBucketNT) void bucket_sort_kernel(SortArgs a, BucketPlan bp, const uint64_t* runs,
+                                                                const int32_t* table) {
+  constexpr int NW = kBucketNT / kWave;
+  constexpr int CAP = E * kBucketNT;
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint64_t* buf = (uint64_t*)smem;                 // CAP records
+  uint32_t* hist = (uint32_t*)(buf + CAP);         // 256 * (NW + 1) counters
+  __shared__ uint32_t wsum[NW];
+  __shared__ uint32_t red[2][NW];
+  __shared__ int s_lo[kBucketMaxRuns], s_off[kBucketMaxRuns + 1];
+  const int t = threadIdx.x, l = lane_id(), w = t / kWave;
+  const int R = bp.runs;
+  const int64_t row = blockIdx.x / (unsigned)bp.K;
+  const int k = (int)(blockIdx.x - row * bp.K);
+  const int64_t base = row * a.cols;
+  const int32_t* tp = table + row * (int64_t)(bp.K + 1) * (R + 1);
+  if (w == 0) {  // the bucket's range in each run and its slots, by a wave scan
+    // runs in tie order: chunk j holds columns [j, j + 1) * kWideChunk, so
+    // with descending ties (tie = kTieMask - column) the last run comes first
+    int lo = 0, sz = 0;
+    if (l < R) {
+      const int j = a.ties_desc ? R - 1 - l : l;
+      lo = tp[k * R + j];
+      sz = tp[(k + 1) * R + j] - lo;
+    }
+    int tot;
+    const int pre = wave_exscan_i32(sz, tot);
+    if (l < R) {
+      s_lo[l] = lo;
+      s_off[l] = pre;
+    }
+    if (l == 0) s_off[R] = tot;
+  }
+  __syncthreads();
+  const int n = s_off[R];  // at most CAP (the split's bound)
+  if (n > CAP) return;     // never taken; keeps a broken table from writing past the LDS buffer
+  const int64_t o0 = tp[(bp.K + 1) * R + k];
+  // slot L is record L - s_off[i] of the bucket's part of the i-th run (in tie
+  // order); the slots of a thread ascend, so its run index only moves up
+  uint32_t kand = ~0u, kor = 0u;
+  uint64_t v[E];
+  {
+    const uint64_t* src[E];
+    int i = 0;
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const int L = w * (E * kWave) + r * kWave + l;
+      src[r] = nullptr;
+      if (L < n) {
+        while (s_off[i + 1] <= L) ++i;
+        const int j = a.ties_desc ? R - 1 - i : i;
+        src[r] = runs + base + (int64_t)j * kWideChunk + s_lo[i] + (L - s_off[i]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < E; ++r) v[r] = src[r] ? *src[r] : ~0ull;
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      if (src[r]) {
+        kand &= (uint32_t)(v[r] >> 32);
+        kor |= (uint32_t)(v[r] >> 32);
+      }
+    }
+  }
+#pragma unroll
+  for (int d = kWave / 2; d >= 1; d >>= 1) {
+    kand &= lane_xor(kand, d);
+    kor |= lane_xor(kor, d);
+  }
+  if (l == 0) {
+    red[0][w] = kand;
+    red[1][w] = kor;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    kand &= red[0][i];
+    kor |= red[1][i];
+  }
+  radix_sort_slots<E, kBucketNT>(v, buf, hist, wsum, kand ^ kor, n);
+  // outputs at ranks o0 + slot: the source column, then the sorted key and
+  // the gathered second key, each batch of dependent loads in flight at once
+  int32_t col[E];
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int L = w * (E * kWave) + r * kWave + l;
+    col[r] = 0;
+    if (L < n) {
+      const uint32_t tie = (uint32_t)v[r];
+      const int32_t pos = (int32_t)(a.ties_desc ? kTieMask - tie : tie);
+      col[r] = a.perm_in ? a.perm_in[base + pos] : pos;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int L = w * (E * kWave) + r * kWave + l;
+    if (L >= n) continue;
+    a.perm_out[base + o0 + L] = col[r];
+    if (a.key_out) {
+      uint32_t key = (uint32_t)(v[r] >> 32);
+      if (a.descending) key = ~key;
+      store_sorted(a.key_out, a.key_out_dtype, a.key_dtype, base + o0 + L, key);
+    }
+  }
+  if (a.aux_out) {
+    uint32_t u[E];
+    if (a.aux_dtype == kBF16) {
+#pragma unroll
+      for (int r = 0; r < E; ++r)
+        u[r] = w * (E * kWave) + r * kWave + l < n ? key_bits_at<kBF16>(a.aux, base + col[r]) : 0u;
+    } else {
+#pragma unroll
+      for (int r = 0; r < E; ++r)
+        u[r] = w * (E * kWave) + r * kWave + l < n ? key_bits_at<kF32>(a.aux, base + col[r]) : 0u;
+    }
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const int L = w * (E * kWave) + r * kWave + l;
+      if (L < n)
+        store_sorted(a.aux_out, a.aux_out_dtype, a.aux_dtype, base + o0 + L, order_from_bits(u[r], a.aux_dtype));
+    }
+  }
+}
+
 template <int DT, bool PERM>
 static int launch_chunks(const SortArgs& a, int64_t rows, int64_t nchunks, uint64_t* out, hipStream_t s) {
   const hipError_t attr = set_dynamic_lds_limit((const void*)sort_chunks_kernel<DT, PERM>, kChunkLds, s);
@@ -390,6 +657,41 @@ int launch_sort_wide(const SortArgs& a, int64_t rows, void* ws, size_t ws_bytes,
                                 : (a.perm_in ? launch_chunks<kF32, true>(a, rows, nchunks, buf[0], s)
                                               : launch_chunks<kF32, false>(a, rows, nchunks, buf[0], s));
   if (!st) st = launch_status("tallax_sort_rows (chunks)");
+  if (st) return st;
+  // rows of 3 .. kBucketMaxRuns chunks: the multiway merge by splitters
+  // (the table lives in the second workspace buffer, which exists whenever
+  // there are two or more pairwise passes)
+  if (nchunks >= 3 && nchunks <= kBucketMaxRuns) {
+    BucketPlan bp;
+    bp.runs = (int)nchunks;
+    bp.samples = 0;
+    for (int j = 0; j < bp.runs; ++j) bp.samples += run_len(cols, j) / kBucketStride;
+    bp.E = bp.runs <= 24 ? 16 : 32;                    // capacity 8192 or 16384 records
+    bp.m = (bp.E * kBucketNT) / kBucketStride - bp.runs;  // (m + runs) G = capacity
+    bp.K = (bp.samples + bp.m - 1) / bp.m;
+    if (bp.K < 1) bp.K = 1;
+    if (rows * bp.K > 2147483647) {
+      set_error("sort of %lld rows needs more than 2^31 - 1 workgroups", (long long)rows);
+      return kUnsupported;
+    }
+    int32_t* table = (int32_t*)buf[1];
+    hipLaunchKernelGGL(bucket_split_kernel, dim3((unsigned)rows), dim3(kSplitNT), 0, s, a, bp, buf[0], table);
+    st = launch_status("tallax_sort_rows (splitters)");
+    if (st) return st;
+    const int lds = bp.E * kBucketNT * 8 + 256 * (kBucketNT / kWave + 1) * 4;
+    const void* kfn = bp.E == 16 ? (const void*)bucket_sort_kernel<16> : (const void*)bucket_sort_kernel<32>;
+    const hipError_t attr = set_dynamic_lds_limit(kfn, lds, s);
+    if (attr != hipSuccess) {
+      set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr));
+      return kHipError;
+    }
+    const dim3 grid((unsigned)(rows * bp.K));
+    if (bp.E == 16)
+      hipLaunchKernelGGL(bucket_sort_kernel<16>, grid, dim3(kBucketNT), lds, s, a, bp, (const uint64_t*)buf[0], table);
+    else
+      hipLaunchKernelGGL(bucket_sort_kernel<32>, grid, dim3(kBucketNT), lds, s, a, bp, (const uint64_t*)buf[0], table);
+    return launch_status("tallax_sort_rows (buckets)");
+  }
   const int passes = wide_passes(cols);
   for (int p = 0; p < passes && !st; ++p) {
     const int64_t run = (int64_t)kWideChunk << p;

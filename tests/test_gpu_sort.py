@@ -184,6 +184,24 @@ def test_sort_wide_rows(gpu, cols, dtype, descending, stable, argsort):
         assert _same(_host(g), w)
 
 
+# Rows of 25 to 56 chunks take the splitter merge with 16384-record buckets,
+# longer ones the pairwise merge passes.
+@pytest.mark.parametrize("cols", [500001, 1000003])
+@pytest.mark.parametrize("descending,stable", [(True, True), (False, False)])
+def test_sort_wide_long_rows(gpu, cols, descending, stable):
+    from tallax_amd import tax
+    _log(f"wide sort f32 cols={cols} desc={descending} stable={stable}")
+    rng = np.random.default_rng(cols + descending)
+    x = np.round(rng.standard_normal((2, cols)) * 8).astype(np.float32) / 8
+    x[1, cols // 3: 2 * cols // 3] = -1.5  # ties across many chunks
+    got = tax.sort(torch.from_numpy(x).to(gpu), num_keys=1, is_stable=stable, return_argsort=True,
+                   descending=descending)
+    torch.cuda.synchronize()
+    want, _ = O.sort([x], 1, is_stable=stable, return_argsort=True, descending=descending)
+    for g, w in zip(got, want):
+        assert _same(_host(g), w)
+
+
 def test_sort_wide_constant_and_nan_rows(gpu):
     from tallax_amd import tax
     cols = 40000
