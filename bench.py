@@ -130,7 +130,7 @@ TRAFFIC_KERNELS = {
     "topk_c3_approx": ("tx::binned_",),
     "sort_c2": ("tx::radix_sort_rows_kernel", "tx::gather_row_lds_kernel"),
     "prefill_c5": ("tx::softmax_topk_kernel",),
-    "sort_wide": ("tx::sort_chunks_kernel", "tx::merge_runs_kernel"),
+    "sort_wide": ("tx::sort_chunks_kernel", "tx::bucket_", "tx::merge_runs_kernel"),
 }
 EXTRA_CONFIGS = ("topk_c3", "prefill_c5", "sort_c2")
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
@@ -548,8 +548,8 @@ def _sort_wide(torch, np, _lib, dev, s_handle, gen, nbuf):
     w.alg_bytes = rows * cols * 12  # keys in; sorted keys and int32 indices out
     w.workload = ("tax.sort(p, num_keys=1, is_stable=True, return_argsort=True, descending=True) of f32 "
                   "[1024,201088] softmax(N(0, sigma=2)) rows: the reference's sort route for config 5 "
-                  "(rows > 16384: chunk radix sorts + merge passes through the workspace)")
-    w.kernel = "sort_chunks_kernel<f32> + 4 merge_runs_kernel passes"
+                  "(rows > 16384: chunk radix sorts, then a multiway merge by splitters through the workspace)")
+    w.kernel = "sort_chunks_kernel<f32> + bucket_split_kernel + bucket_sort_kernel<16>"
     w.cpu_batch = 1
     sample = 4  # rows checked against the oracle
 
