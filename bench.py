@@ -19,7 +19,7 @@ samples one token for each of the 256 rows.
   prefill_c5     f32 [1024,201088] softmax -> top-2048 -> cumsum -> cutoff p=0.9
   sort_wide      tax.sort of f32 [1024,201088] probabilities, descending stable
                  argsort with keys: the reference's own route for config 5's
-                 sort (rows > 16384: chunk radix sorts + merge passes)
+                 sort (rows > 16384: chunk radix sorts + a splitter merge)
   copy           torch's device copy of 256 MiB (the counter calibration)
   read_calib     read-only kernels over 256 MiB with 16-, 8- and 4-byte loads
                  (FETCH_SIZE calibration per load width)
