@@ -578,25 +578,34 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
   const int ntiles = (K + 7) >> 3;
   if ((t & 7) == 7) s_tot[g] = c;
   __syncthreads();
-  if (t < kWave) {
-    // the tile totals (two per lane) are read out first, then summed in
-    // tile order: carry_g = t_0 + ... + t_{g-1}, one add after the other
-    float tt[2], cy[2] = {0.0f, 0.0f};
+  // the candidate's Gumbel noise: waves 1-15 draw it while thread 0 sums the
+  // tile totals, wave 0 after that
+  const uint32_t row_ctr = (uint32_t)(row + a.dim0_offset);
+  float gn = 0.0f;
+  if (t >= kWave && in) gn = candidate_noise(a.rng_key[0], a.rng_key[1], row_ctr, (uint32_t)a.cols, id);
+  if (t == 0) {
+    // carry_g = t_0 + ... + t_{g-1}, one add after the other in tile order,
+    // by one lane (-0 + x == x, so the chain starts exactly at t_0), the
+    // totals read from LDS 16 at a time
+    float run = -0.0f;
+    float cur[16];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) tt[h] = h * kWave + l < ntiles ? s_tot[h * kWave + l] : 0.0f;
-    float run = readlane_f(tt[0], 0);
+    for (int u = 0; u < 16; ++u) cur[u] = s_tot[u];
+    for (int i0 = 0; i0 < ntiles; i0 += 16) {
+      float nxt[16];
+      const int n0 = i0 + 16 < kSwMaxK / 8 ? i0 + 16 : i0;  // in bounds; unused past the last batch
 #pragma unroll
-    for (int i = 1; i < kSwMaxK / 8; ++i) {  // constant lanes; only the adds depend on each other
-      if (i < ntiles) {  // uniform
-        const int h = i >> 6, ln = i & (kWave - 1);
-        cy[h] = l == ln ? run : cy[h];
-        run = run + readlane_f(tt[h], ln);
+      for (int u = 0; u < 16; ++u) nxt[u] = s_tot[n0 + u];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        s_carry[i0 + u] = run;
+        run = run + cur[u];
       }
-    }
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      if (h * kWave + l < ntiles) s_carry[h * kWave + l] = cy[h];
+      for (int u = 0; u < 16; ++u) cur[u] = nxt[u];
+    }
   }
+  if (t < kWave && in) gn = candidate_noise(a.rng_key[0], a.rng_key[1], row_ctr, (uint32_t)a.cols, id);
   __syncthreads();
   if (in && g != 0) c = c + s_carry[g];
   const int tcount = __syncthreads_count(in && c < row_p);
@@ -618,8 +627,7 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
     if (in) {
       const float masked = vv >= thr ? vv : a.replace_f32;
       const float scaled = masked / temp;
-      sc = scaled + candidate_noise(a.rng_key[0], a.rng_key[1], (uint32_t)(row + a.dim0_offset),
-                                    (uint32_t)a.cols, id);
+      sc = scaled + gn;
     }
     uint32_t sb = __float_as_uint(sc);
     sb = sb == 0x80000000u ? 0u : sb;
