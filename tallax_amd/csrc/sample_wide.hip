@@ -258,20 +258,17 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
     };
     int32_t wl = -1;
     if (count_ge(1) >= q) {  // wave-uniform; a bound of +0 would need -0 too: positive bounds only
-      wl = 0;
-      constexpr int kBits = DT == kBF16 ? 15 : 31;
+      // two bits per step: the three probes of a step are independent
+      constexpr int kBits = DT == kBF16 ? 15 : 31;  // odd: the top bit alone first
+      wl = count_ge(1 << (kBits - 1)) >= q ? (1 << (kBits - 1)) : 0;
 #pragma unroll 1
-      for (int b = kBits - 1; b >= 0; --b) {
-        const int32_t probe = wl | (int32_t)(1u << b);
-        if (count_ge(probe) >= q) wl = probe;
+      for (int b = kBits - 3; b >= 0; b -= 2) {
+        const int32_t p1 = wl | (1 << b), p2 = wl | (2 << b), p3 = wl | (3 << b);
+        const int c1 = count_ge(p1), c2 = count_ge(p2), c3 = count_ge(p3);
+        wl = c3 >= q ? p3 : (c2 >= q ? p2 : (c1 >= q ? p1 : wl));
       }
     }
-    int32_t wm = top[0];  // the wave's largest vector maximum (signed view)
-#pragma unroll
-    for (int d = kWave / 2; d >= 1; d >>= 1) {
-      const int32_t o = (int32_t)lane_xor((uint32_t)wm, d);
-      wm = o > wm ? o : wm;
-    }
+    const int32_t wm = wave_max_i(top[0]);  // the wave's largest vector maximum (signed view)
     if (l == 0) {
       s_red[w] = wl;
       s_wmax[w] = wm;

@@ -599,8 +599,7 @@ void softmax_topk_kernel(PfArgs a) {
         bk[l * PER + i] = run;
         run += cnt[i];
       }
-#pragma unroll
-      for (int d = kWave / 2; d >= 1; d >>= 1) mxl = max(mxl, (int)lane_xor((uint32_t)mxl, d));
+      mxl = wave_max_i(mxl);
       if (l == 0) s_mx = mxl;
     }
     __syncthreads();

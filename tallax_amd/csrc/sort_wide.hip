@@ -177,11 +177,8 @@ __global__ __launch_bounds__(kChunkNT) void sort_chunks_kernel(SortArgs a, int n
       }
     }
   }
-#pragma unroll
-  for (int d = kWave / 2; d >= 1; d >>= 1) {
-    kand &= lane_xor(kand, d);
-    kor |= lane_xor(kor, d);
-  }
+  kand = wave_and_u32(kand);
+  kor = wave_or_u32(kor);
   if (l == 0) {
     red[0][w] = kand;
     red[1][w] = kor;
@@ -547,11 +544,8 @@ __global__ __launch_bounds__(kBucketNT) void bucket_sort_kernel(SortArgs a, Buck
       }
     }
   }
-#pragma unroll
-  for (int d = kWave / 2; d >= 1; d >>= 1) {
-    kand &= lane_xor(kand, d);
-    kor |= lane_xor(kor, d);
-  }
+  kand = wave_and_u32(kand);
+  kor = wave_or_u32(kor);
   if (l == 0) {
     red[0][w] = kand;
     red[1][w] = kor;

@@ -180,6 +180,23 @@ __device__ __forceinline__ int wave_max_i(int v) {
   return max(v, (int)lane_xor((uint32_t)v, 1));
 }
 
+__device__ __forceinline__ uint32_t wave_and_u32(uint32_t v) {
+  v &= lane_xor(v, 32);
+  v &= lane_xor(v, 16);
+  v &= lane_xor(v, 8);
+  v &= lane_xor(v, 4);
+  v &= lane_xor(v, 2);
+  return v & lane_xor(v, 1);
+}
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+  v |= lane_xor(v, 32);
+  v |= lane_xor(v, 16);
+  v |= lane_xor(v, 8);
+  v |= lane_xor(v, 4);
+  v |= lane_xor(v, 2);
+  return v | lane_xor(v, 1);
+}
+
 __device__ __forceinline__ float wave_sum_f(float v) {
 #pragma unroll
   for (int d = kWave / 2; d >= 1; d >>= 1) v += lane_xor_f(v, d);
