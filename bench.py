@@ -126,7 +126,7 @@ TRAFFIC_KERNELS = {
     "sampler_masked": ("tx::stream_select_kernel",),
     "sampler_wide": ("tx::sample_wide_kernel",),
     "topk_c3": ("tx::seg_select_kernel", "tx::seg_merge"),
-    "topk_c1": ("tx::seg_select_kernel", "tx::seg_merge"),
+    "topk_c1": ("tx::stream_select_kernel", "tx::seg_select_kernel", "tx::seg_merge"),
     "topk_c3_approx": ("tx::binned_",),
     "sort_c2": ("tx::radix_sort_rows_kernel", "tx::gather_row_lds_kernel"),
     "prefill_c5": ("tx::softmax_topk_kernel",),

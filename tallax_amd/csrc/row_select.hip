@@ -1651,8 +1651,11 @@ struct Plan {
 
 // Work split.  A row of nv 16-byte vectors is handled either
 //   * whole by one 1024-thread workgroup of stream_select_kernel (up to 16
-//     vectors per thread) when that gives enough workgroups (>= 128 rows):
-//     no merge kernel at all; or
+//     vectors per thread) when that gives enough workgroups (>= 128 rows),
+//     or when a row is at most 128 KiB: one workgroup reads that in ~3 us
+//     (it streams at most ~40 GB/s), less than the segment path's second
+//     launch costs (config 1, [8, 32768] f32: 9.90 -> 8.05 us); no merge
+//     kernel at all; or
 //   * in segments of 256 x MAXV vectors, MAXV in {4, 8, 16}: the largest that
 //     still gives ~4 workgroups per CU over the launch, then a per-row merge;
 //     where 16 gives more than one residency round (4 workgroups per CU,
@@ -1663,7 +1666,7 @@ static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
   const int vec = dt == kF32 ? 4 : 8;
   const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
   static const int kOpts[3] = {16, 8, 4};
-  if (rows >= 128 && nv <= (int64_t)kNTS * 16) {
+  if ((rows >= 128 || cols * (dt == kF32 ? 4 : 2) <= 131072) && nv <= (int64_t)kNTS * 16) {
     int maxv = 16;
     while (maxv > 4 && (int64_t)kNTS * (maxv / 2) >= nv) maxv /= 2;
     p->nt = kNTS;
