@@ -1651,11 +1651,13 @@ struct Plan {
 
 // Work split.  A row of nv 16-byte vectors is handled either
 //   * whole by one 1024-thread workgroup of stream_select_kernel (up to 16
-//     vectors per thread) when that gives enough workgroups (>= 128 rows),
-//     or when a row is at most 128 KiB: one workgroup reads that in ~3 us
-//     (it streams at most ~40 GB/s), less than the segment path's second
-//     launch costs (config 1, [8, 32768] f32: 9.90 -> 8.05 us); no merge
-//     kernel at all; or
+//     vectors per thread) whenever the row fits: no merge kernel at all.  At
+//     small row counts one workgroup per row leaves most CUs idle, but a
+//     256 KiB row streams into one workgroup in ~6 us (at most ~40 GB/s),
+//     less than the segment path's bound-after-loads plus second launch
+//     (measured, A/B: sampler [1, 128256] bf16 13.0 -> 9.0 us, [64, 128256]
+//     16.6 -> 11.7; top-k [8, 32768] f32 9.90 -> 8.05, [100, 65472] f32
+//     16.7 -> 11.8; no shape slower); or
 //   * in segments of 256 x MAXV vectors, MAXV in {4, 8, 16}: the largest that
 //     still gives ~4 workgroups per CU over the launch, then a per-row merge;
 //     where 16 gives more than one residency round (4 workgroups per CU,
@@ -1666,7 +1668,7 @@ static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
   const int vec = dt == kF32 ? 4 : 8;
   const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
   static const int kOpts[3] = {16, 8, 4};
-  if ((rows >= 128 || cols * (dt == kF32 ? 4 : 2) <= 131072) && nv <= (int64_t)kNTS * 16) {
+  if (nv <= (int64_t)kNTS * 16) {
     int maxv = 16;
     while (maxv > 4 && (int64_t)kNTS * (maxv / 2) >= nv) maxv /= 2;
     p->nt = kNTS;

@@ -41,6 +41,23 @@ def test_error_path_without_gpu():
     assert _lib.LIB.tallax_topk_workspace_size(8, 200000, 64, 0) > 0
 
 
+def test_work_split_without_gpu():
+    """Every row that fits 1024 threads x 16 vectors goes to the whole-row
+    kernel, at any row count; longer rows are cut into segments."""
+    from tallax_amd import _lib
+    for rows, cols, dt in [(1, 128256, _lib.BF16), (64, 128256, _lib.BF16), (8, 32768, _lib.F32),
+                           (100, 65472, _lib.F32), (13, 167, _lib.F32), (256, 131058, _lib.BF16)]:
+        p = _lib.select_plan(rows, cols, dt)
+        assert p["threads"] == 1024 and p["segments"] == 1, (rows, cols, p)
+        assert _lib.LIB.tallax_topk_workspace_size(rows, cols, 64, dt) == 0
+    for rows, cols, dt in [(1, 151936, _lib.BF16), (8, 65536, _lib.F32), (128, 151936, _lib.F32)]:
+        p = _lib.select_plan(rows, cols, dt)
+        assert p["threads"] == 256 and p["segments"] > 1, (rows, cols, p)
+    assert _lib.select_plan(128, 151936, _lib.F32) == {"threads": 256, "vectors_per_thread": 19, "segments": 8,
+                                                        "vectors_per_segment": 256 * 19,
+                                                        "kernel": "seg_select_kernel<0, 19, 256, SAMPLE> + seg_merge_kernel"}
+
+
 def test_sort_workspace_contract_without_gpu():
     from tallax_amd import _lib
     L = _lib.LIB

@@ -92,6 +92,13 @@ TOPK_CASES = [
     (4, 40000, 100, "bf16", "tieblock"),    # 60 large values, then a 10000-wide tie block
     (4, 40000, 100, "f32", "tieblock"),
     (4, 40000, 100, "f32", "nan_heavy"),    # NaN rows with a few finite, -inf and finfo.min values
+    # the same inputs on rows too long for one workgroup (segments, then the merge)
+    (2, 140000, 17, "f32", "const"),
+    (3, 140000, 64, "f32", "ints"),
+    (6, 140000, 50, "f32", "special"),
+    (4, 140000, 100, "bf16", "tieblock"),
+    (4, 140000, 100, "f32", "tieblock"),
+    (4, 140000, 100, "f32", "nan_heavy"),
     # whole-row workgroups on masked rows: fewer than 128 eligible values take
     # the rest of the list by class (finfo.min, -inf, NaN, each in index order)
     (256, 128256, 128, "bf16", "masked_mix"),
