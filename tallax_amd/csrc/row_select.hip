@@ -1188,9 +1188,9 @@ __device__ __forceinline__ uint32_t min_offset_from_min(const uint4 v) {
 // Rows with fewer than 128 eligible elements, all n of them candidates:
 // list[n..127] <- the first 128 - n ineligible elements in composite order --
 // the finfo.min elements, then -inf, then NaN, each class in index order --
-// and zeros where the row has fewer than 128 elements.  pab / pc: this
-// thread's vectors j (bit j) that may hold finfo.min (pab bits 0-15), -inf
-// (pab bits 16-31) or NaN (pc), from the first read; the vectors that
+// and zeros where the row has fewer than 128 elements.  pmin / pinf: this
+// thread's vectors j (bit j) that may hold finfo.min or -inf, from the first
+// read (NaNs are not tracked: every vector may hold one); the vectors that
 // hold a class anywhere in the row are read again one at a time (vector j of
 // thread t at row vector j * kNTS + t of the aligned base, nv vectors, the
 // row's first element at slot mis), in order, until the list is full.
@@ -1199,7 +1199,7 @@ __device__ __forceinline__ uint32_t min_offset_from_min(const uint4 v) {
 // footprint).
 template <int DT, int V>
 __device__ __attribute__((noinline)) void fill_ineligible(const uint4* row_base, int nv, int mis, int cols, int n,
-                                                          uint32_t pab, uint32_t pc, uint64_t* list, int* red,
+                                                          uint32_t pmin, uint32_t pinf, uint64_t* list, int* red,
                                                           uint32_t* tmp) {
   constexpr bool kBF = DT == kBF16;
   constexpr int VEC = ElemT<DT>::VEC, NW = kNTS / kWave;
@@ -1209,27 +1209,25 @@ __device__ __attribute__((noinline)) void fill_ineligible(const uint4* row_base,
   const int w = tid / kWave, l = lane_id();
   const GlobalVec gb = (GlobalVec)row_base;
   const GlobalVec dead = (GlobalVec)(uintptr_t)&g_dead_vec;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    pab |= lane_xor(pab, d);
-    pc |= lane_xor(pc, d);
-  }
+  pmin = wave_or_u32(pmin);
+  pinf = wave_or_u32(pinf);
   if (l == 0) {
-    tmp[w] = pab;
-    tmp[NW + w] = pc;
+    tmp[w] = pmin;
+    tmp[NW + w] = pinf;
   }
   __syncthreads();
-  pab = 0;
-  pc = 0;
+  pmin = 0;
+  pinf = 0;
 #pragma unroll
   for (int i = 0; i < NW; ++i) {
-    pab |= tmp[i];
-    pc |= tmp[NW + i];
+    pmin |= tmp[i];
+    pinf |= tmp[NW + i];
   }
+  constexpr uint32_t kAll = (1u << V) - 1u;
   int r = kMaxK - n, base = n;
 #pragma unroll 1
   for (int c = 0; c < 3 && r > 0; ++c) {  // block-uniform
-    uint32_t pres = c == 0 ? (pab & 0xFFFFu) : (c == 1 ? pab >> 16 : pc);
+    uint32_t pres = c == 0 ? pmin : (c == 1 ? pinf : kAll);
     const uint32_t key = c == 0 ? kMinKey : (c == 1 ? kNegInfKey : kNaNKey);
     while (pres && r > 0) {  // block-uniform: the vectors that may hold the class, in order
       const int j = __builtin_ctz(pres);
@@ -1283,6 +1281,7 @@ template <int DT, int V, bool SAMPLE, bool EDGE>
 __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   using T = ElemT<DT>;
   constexpr int VEC = T::VEC, ES = T::ES, NW = kNTS / kWave;
+  static_assert(V <= 31, "one bit per vector in 32-bit masks");
   constexpr bool kBF = DT == kBF16;
   constexpr int KB = kBF ? 16 : 32;  // canonical key bits
   using ST = Sel<DT, (kNTS * V * VEC > 65535)>;  // the tie path's composites (tie_select's choice)
@@ -1416,7 +1415,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   };
 
   uint32_t thr, M;
-  uint32_t pab = 0, pc = 0;  // rows with thr at the floor: the vectors holding ineligible classes
+  uint32_t pmin = 0, pinf = 0;  // rows with thr at the floor: the vectors that may hold finfo.min / -inf
   // ---- 2. the bound L from waves 0..7 alone: the minimum over them of each
   // one's 16th largest thread maximum, so at least 128 elements of the row
   // reach it.  Their loads are issued first and arrive first, so L is posted
@@ -1499,10 +1498,9 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
 #pragma unroll
         for (int j = 0; j < V; ++j) {
           const uint32_t o = min_offset_from_min<DT>(raw[j]);
-          pab |= (o == 0u ? 1u : 0u) << j;
-          pab |= (o <= 1u ? 1u : 0u) << (16 + j);
+          pmin |= (o == 0u ? 1u : 0u) << j;
+          pinf |= (o <= 1u ? 1u : 0u) << j;
         }
-        pc = (1u << V) - 1u;
       }
     }
     extract(thr, !early);
@@ -1519,7 +1517,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   const bool fill = ss.ovf == 0 && n < kMaxK && thr == kFloor;  // block-uniform
   // an overflowing staging region or more than kCandCap candidates: heavy ties
   const bool tie = !fill && (ss.ovf != 0 || n < kMaxK || n > kCandCap);
-  if (fill) fill_ineligible<DT, V>(rv.base, nv, rv.mis, cols, n, pab, pc, sh.list64, sh.red, &ss.vsi[0][0]);
+  if (fill) fill_ineligible<DT, V>(rv.base, nv, rv.mis, cols, n, pmin, pinf, sh.list64, sh.red, &ss.vsi[0][0]);
   if (tie) {
     stream_tie_path<DT, V>(rv.base, nv, rv.mis, cols, sh, stage);
   } else if (n > 0) {
@@ -1650,14 +1648,16 @@ struct Plan {
 };
 
 // Work split.  A row of nv 16-byte vectors is handled either
-//   * whole by one 1024-thread workgroup of stream_select_kernel (up to 16
+//   * whole by one 1024-thread workgroup of stream_select_kernel (up to 19
 //     vectors per thread) whenever the row fits: no merge kernel at all.  At
 //     small row counts one workgroup per row leaves most CUs idle, but a
 //     256 KiB row streams into one workgroup in ~6 us (at most ~40 GB/s),
 //     less than the segment path's bound-after-loads plus second launch
 //     (measured, A/B: sampler [1, 128256] bf16 13.0 -> 9.0 us, [64, 128256]
 //     16.6 -> 11.7; top-k [8, 32768] f32 9.90 -> 8.05, [100, 65472] f32
-//     16.7 -> 11.8; no shape slower); or
+//     16.7 -> 11.8; 19 vectors per thread for the 151936-wide bf16
+//     vocabulary: sampler [64, 151936] 20.5 -> 12.7, [256, 151936] 25.2 ->
+//     17.8; no shape slower); or
 //   * in segments of 256 x MAXV vectors, MAXV in {4, 8, 16}: the largest that
 //     still gives ~4 workgroups per CU over the launch, then a per-row merge;
 //     where 16 gives more than one residency round (4 workgroups per CU,
@@ -1668,8 +1668,8 @@ static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
   const int vec = dt == kF32 ? 4 : 8;
   const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
   static const int kOpts[3] = {16, 8, 4};
-  if (nv <= (int64_t)kNTS * 16) {
-    int maxv = 16;
+  if (nv <= (int64_t)kNTS * 19) {
+    int maxv = nv > (int64_t)kNTS * 16 ? 19 : 16;
     while (maxv > 4 && (int64_t)kNTS * (maxv / 2) >= nv) maxv /= 2;
     p->nt = kNTS;
     p->maxv = maxv;
@@ -1730,7 +1730,10 @@ static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const c
     // slots outside the row: the kernel without the edge handling
     const bool edge = ((uintptr_t)a.x % 16) != 0 || (a.cols * ElemT<DT>::ES) % 16 != 0;
     const dim3 g((unsigned)a.rows), b(kNTS);
-    if (p.maxv == 16) {
+    if (p.maxv == 19) {
+      if (edge) hipLaunchKernelGGL((stream_select_kernel<DT, 19, SAMPLE, true>), g, b, 0, s, a);
+      else hipLaunchKernelGGL((stream_select_kernel<DT, 19, SAMPLE, false>), g, b, 0, s, a);
+    } else if (p.maxv == 16) {
       if (edge) hipLaunchKernelGGL((stream_select_kernel<DT, 16, SAMPLE, true>), g, b, 0, s, a);
       else hipLaunchKernelGGL((stream_select_kernel<DT, 16, SAMPLE, false>), g, b, 0, s, a);
     } else if (p.maxv == 8) {

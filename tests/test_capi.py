@@ -42,15 +42,18 @@ def test_error_path_without_gpu():
 
 
 def test_work_split_without_gpu():
-    """Every row that fits 1024 threads x 16 vectors goes to the whole-row
+    """Every row that fits 1024 threads x 19 vectors goes to the whole-row
     kernel, at any row count; longer rows are cut into segments."""
     from tallax_amd import _lib
     for rows, cols, dt in [(1, 128256, _lib.BF16), (64, 128256, _lib.BF16), (8, 32768, _lib.F32),
-                           (100, 65472, _lib.F32), (13, 167, _lib.F32), (256, 131058, _lib.BF16)]:
+                           (100, 65472, _lib.F32), (13, 167, _lib.F32), (256, 131058, _lib.BF16),
+                           (1, 151936, _lib.BF16), (8, 65536, _lib.F32), (64, 77810, _lib.F32)]:
         p = _lib.select_plan(rows, cols, dt)
         assert p["threads"] == 1024 and p["segments"] == 1, (rows, cols, p)
         assert _lib.LIB.tallax_topk_workspace_size(rows, cols, 64, dt) == 0
-    for rows, cols, dt in [(1, 151936, _lib.BF16), (8, 65536, _lib.F32), (128, 151936, _lib.F32)]:
+    assert _lib.select_plan(1, 151936, _lib.BF16)["vectors_per_thread"] == 19
+    assert _lib.select_plan(1, 128256, _lib.BF16)["vectors_per_thread"] == 16
+    for rows, cols, dt in [(1, 160000, _lib.BF16), (8, 80000, _lib.F32), (128, 151936, _lib.F32)]:
         p = _lib.select_plan(rows, cols, dt)
         assert p["threads"] == 256 and p["segments"] > 1, (rows, cols, p)
     assert _lib.select_plan(128, 151936, _lib.F32) == {"threads": 256, "vectors_per_thread": 19, "segments": 8,

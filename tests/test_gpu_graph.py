@@ -56,7 +56,7 @@ def _run_all(b):
     out["gather"] = tumpy.take_along_axis(b["sort_x"], out["sort_p"], 1)
     out["pf"] = prefill.softmax_topk_cumsum(b["pf_x"], k=256, p=0.9)
     out["cumsum"] = tax.cumsum(b["cs_x"], axis=1)
-    st, out["noalloc"] = _noalloc(b, b["na_x"])   # [64, 151936] bf16: segmented, uses the static scratch
+    st, out["noalloc"] = _noalloc(b, b["na_x"])   # [64, 200000] bf16: segmented, uses the static scratch
     assert st == 0
     return out
 
@@ -96,7 +96,7 @@ def _buffers(gpu, rng):
         "top_p": torch.from_numpy(rng.uniform(0.7, 1.0, rows).astype(np.float32)).to(gpu),
         "temp": torch.from_numpy(rng.uniform(0.5, 1.5, rows).astype(np.float32)).to(gpu),
         "key": torch.tensor([0, 1234], dtype=torch.int32, device=gpu),
-        "na_x": torch.empty((na_rows, 151936), dtype=torch.bfloat16, device=gpu),
+        "na_x": torch.empty((na_rows, 200000), dtype=torch.bfloat16, device=gpu),
         "na_k": torch.from_numpy(rng.integers(1, 1025, na_rows).astype(np.int32)).to(gpu),
         "na_p": torch.from_numpy(rng.uniform(0.7, 1.0, na_rows).astype(np.float32)).to(gpu),
         "na_t": torch.from_numpy(rng.uniform(0.5, 1.5, na_rows).astype(np.float32)).to(gpu),

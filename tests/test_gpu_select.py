@@ -93,12 +93,22 @@ TOPK_CASES = [
     (4, 40000, 100, "f32", "tieblock"),
     (4, 40000, 100, "f32", "nan_heavy"),    # NaN rows with a few finite, -inf and finfo.min values
     # the same inputs on rows too long for one workgroup (segments, then the merge)
-    (2, 140000, 17, "f32", "const"),
-    (3, 140000, 64, "f32", "ints"),
-    (6, 140000, 50, "f32", "special"),
-    (4, 140000, 100, "bf16", "tieblock"),
-    (4, 140000, 100, "f32", "tieblock"),
-    (4, 140000, 100, "f32", "nan_heavy"),
+    (2, 200000, 17, "f32", "const"),
+    (3, 200000, 64, "f32", "ints"),
+    (6, 200000, 50, "f32", "special"),
+    (4, 200000, 100, "bf16", "tieblock"),
+    (4, 200000, 100, "f32", "tieblock"),
+    (4, 200000, 100, "f32", "nan_heavy"),
+    # whole rows at 19 vectors per thread (bf16 rows up to 155648 elements,
+    # f32 up to 77824), aligned and misaligned, with the rare paths
+    (128, 151936, 50, "bf16", "normal"),
+    (6, 151931, 50, "bf16", "special"),
+    (16, 151936, 128, "bf16", "const"),
+    (8, 151936, 100, "bf16", "tieblock"),
+    (64, 151936, 128, "bf16", "masked5"),
+    (96, 151936, 128, "bf16", "masked_mix"),
+    (8, 70001, 64, "f32", "normal"),
+    (4, 77000, 100, "f32", "nan_heavy"),
     # whole-row workgroups on masked rows: fewer than 128 eligible values take
     # the rest of the list by class (finfo.min, -inf, NaN, each in index order)
     (256, 128256, 128, "bf16", "masked_mix"),
@@ -277,7 +287,9 @@ def _sampler_inputs(rows, vocab, seed, sigma=3.0):
 @pytest.mark.parametrize("rows,vocab,dtype,masked", [(256, 128256, "bf16", False), (64, 32000, "f32", False),
                                                      (16, 4096, "bf16", False), (8, 131, "f32", False),
                                                      (256, 128256, "bf16", True), (128, 32768, "f32", True),
-                                                     (128, 8195, "bf16", False)])
+                                                     (128, 8195, "bf16", False), (64, 151936, "bf16", False),
+                                                     (32, 151936, "bf16", True), (8, 70001, "f32", False),
+                                                     (16, 200000, "bf16", False)])
 def test_fused_sampler_parity(gpu, rows, vocab, dtype, masked):
     from tallax_amd import sampling
     _log(f"sample rows={rows} vocab={vocab} dtype={dtype} masked={masked}")
