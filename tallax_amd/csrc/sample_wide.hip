@@ -68,7 +68,7 @@ constexpr int kSwMaxK = 1024;           // candidates per row, at most (one per 
 constexpr int kSwList = 2048;           // collected records, at most (two per thread in the sort)
 constexpr int kSwBins = 2048;           // 11-bit digits
 constexpr int kSwChunk = kSwNT * 8;     // columns per workgroup step: 8 per thread
-constexpr int kSwV = 16;                // register path: 16-byte vectors per thread
+constexpr int kSwV = 19;                // register path: 16-byte vectors per thread
 constexpr int kSwStage = 128;           // register path: staged vectors per wave
 
 typedef short sw_short2_t __attribute__((ext_vector_type(2)));
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(kSwNT) void sample_wide_kernel(SwArgs a) {
         // one pool reservation per wave: the lane's count over its vectors, one
         // wave scan, one atomic; then the writes
         int c = 0;
-        uint32_t pm[kSwV / 4] = {0u, 0u, 0u, 0u};  // the masks, 8 bits per vector (VEC <= 8)
+        uint32_t pm[(kSwV + 3) / 4] = {};  // the masks, 8 bits per vector (VEC <= 8)
 #pragma unroll
         for (int j = 0; j < kSwV; ++j) {
           const uint32_t m = pass_mask(raw[j]);

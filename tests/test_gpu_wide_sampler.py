@@ -35,6 +35,9 @@ WIDE_TOPK_CASES = [
     (3, 40000, 1024, "f32", "outlier"),    # K-th value far below the maximum: the whole-row digit passes
     (3, 40000, 1024, "bf16", "outlier"),
     (2, 6000, 1024, "bf16", "normal"),     # fewer than K threads hold an element
+    (4, 151936, 1024, "bf16", "normal"),   # one read at 19 vectors per thread
+    (3, 76000, 1024, "f32", "outlier"),
+    (2, 200000, 1024, "bf16", "normal"),   # too long for the registers: the radix select path
 ]
 
 
@@ -61,7 +64,8 @@ def test_wide_top_k_parity(gpu, rows, cols, k, dtype, kind):
 
 
 @pytest.mark.parametrize("rows,vocab,dtype,max_k", [(256, 128256, "bf16", 1024), (64, 32000, "f32", 1024),
-                                                    (32, 32001, "bf16", 300), (16, 4096, "f32", 777)])
+                                                    (32, 32001, "bf16", 300), (16, 4096, "f32", 777),
+                                                    (64, 151936, "bf16", 1024)])
 def test_wide_sampler_parity(gpu, rows, vocab, dtype, max_k):
     from tallax_amd import sampling
     _log(f"sample max_k={max_k} rows={rows} vocab={vocab} dtype={dtype}")
