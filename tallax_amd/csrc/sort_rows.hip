@@ -14,13 +14,24 @@
 //     non-stable descending argsort orders ties by descending index (the
 //     packed key makes the order unique, utils.py:205-216).
 //
-// One workgroup sorts one row: records (transformed key, tie value) are
-// padded to P = 2^m >= cols with the largest record and sorted ascending by a
-// bitonic network.  Each thread holds E consecutive records in registers;
-// strides < E are exchanged within the thread, strides < 64 E across lanes
-// with DPP / v_permlane*_swap, larger strides through LDS.  bf16 rows of up
-// to 4096 elements use a stable LSD radix sort instead (see
-// radix_sort_rows_kernel: two passes of 8-bit digits).
+// One workgroup sorts one row.  Three kernels, by row length:
+//   * rows of at most 512 elements: records (transformed key, tie value) are
+//     padded to P = 2^m >= cols with the largest record and sorted ascending
+//     by a bitonic network (sort_rows_kernel, P / 4 threads).  Each thread
+//     holds E consecutive records in registers; strides < E are exchanged
+//     within the thread, strides < 64 E across lanes with DPP /
+//     v_permlane*_swap, larger strides through LDS;
+//   * packed bf16 rows of 2049-4096 elements, at most 256 rows: a stable LSD
+//     radix sort of 32-bit records (radix_sort_rows_kernel, two passes of
+//     8-bit digits, 1024 threads);
+//   * everything else up to 16384 elements: the wide sort's chunk radix sort
+//     run on the whole row (sort_row_radix_kernel, sort_wide.hip).  The
+//     bitonic network's LDS traffic grows as n log^2 n: at [256, 16384] f32
+//     it took 190.8 us against 32.4 us for the radix sort, at [256, 2048]
+//     12.1 against 7.5, at [1024, 1024] 14.6 against 12.4; at [1024, 256]
+//     the network is faster (6.2 against 9.1 us), and the 1024-thread
+//     packed radix sort wins only at config 2's shape (7.8 against 9.0 us at
+//     [256, 4096] bf16; 23.9 against 19.6 at [1024, 3000]).
 #include <stdint.h>
 
 #include "tallax_hip.h"
@@ -245,16 +256,8 @@ static int launch_sort(const SortArgs& a, int64_t rows, hipStream_t s) {
 }
 
 template <typename R>
-static int launch_sort_p(const SortArgs& a, int64_t rows, hipStream_t s) {
-  switch (a.P) {
-    case 256: return launch_sort<R, 4, 256>(a, rows, s);
-    case 512: return launch_sort<R, 4, 512>(a, rows, s);
-    case 1024: return launch_sort<R, 4, 1024>(a, rows, s);
-    case 2048: return launch_sort<R, 4, 2048>(a, rows, s);
-    case 4096: return launch_sort<R, 4, 4096>(a, rows, s);
-    case 8192: return launch_sort<R, 8, 8192>(a, rows, s);
-    default: return launch_sort<R, 16, 16384>(a, rows, s);
-  }
+static int launch_sort_p(const SortArgs& a, int64_t rows, hipStream_t s) {  // rows of at most 512 elements
+  return a.P == 256 ? launch_sort<R, 4, 256>(a, rows, s) : launch_sort<R, 4, 512>(a, rows, s);
 }
 
 }  // namespace tx
@@ -300,9 +303,13 @@ int tallax_sort_rows_ws(const void* key, int key_dtype, int64_t rows, int64_t co
   }
   // bf16 keys on the packed path fit (16-bit key | 16-bit tie) in one u32
   const bool narrow = key_dtype == kBF16 && !perm_in && cols <= 65536;
-  // bf16 rows up to 4096: radix sort; longer ones: the bitonic network
-  const int st = narrow ? (cols <= 4 * kRadixNT ? launch_radix8(a, rows, stream) : launch_sort_p<uint32_t>(a, rows, stream))
-                        : launch_sort_p<uint64_t>(a, rows, stream);
+  int st;
+  if (narrow && rows <= 256 && cols > 2048 && cols <= 4 * kRadixNT)
+    st = launch_radix8(a, rows, stream);
+  else if (cols <= 512)
+    st = narrow ? launch_sort_p<uint32_t>(a, rows, stream) : launch_sort_p<uint64_t>(a, rows, stream);
+  else
+    st = launch_sort_row_radix(a, rows, stream);
   if (st) return st;
   return launch_status("tallax_sort_rows");
 }

@@ -79,5 +79,8 @@ struct SortArgs {
 // merge passes through a workspace of sort_wide_workspace_bytes bytes.
 size_t sort_wide_workspace_bytes(int64_t rows, int64_t cols);
 int launch_sort_wide(const SortArgs& a, int64_t rows, void* ws, size_t ws_bytes, hipStream_t s);
+// Rows of at most 16384 elements sorted whole by one workgroup each with the
+// chunk pass's LSD radix sort (sort_wide.hip).
+int launch_sort_row_radix(const SortArgs& a, int64_t rows, hipStream_t s);
 
 }  // namespace tx
