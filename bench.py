@@ -122,11 +122,13 @@ def _recorded_traffic(config):
 # (every other kernel in a run is input generation, torch copies or the copy
 # calibration).
 TRAFFIC_KERNELS = {
-    "sampler": ("tx::stream_select_kernel",),
-    "sampler_masked": ("tx::stream_select_kernel",),
+    "sampler": ("tx::stream_select_kernel<1, 16, true",),
+    "sampler_masked": ("tx::stream_select_kernel<1, 16, true",),
     "sampler_wide": ("tx::sample_wide_kernel",),
-    "topk_c3": ("tx::seg_select_kernel", "tx::seg_merge"),
-    "topk_c1": ("tx::stream_select_kernel", "tx::seg_select_kernel", "tx::seg_merge"),
+    # config 3: two whole-row parts per row, then the merge (the default line
+    # runs it in the sampler's process, so the fragments name the f32 instances)
+    "topk_c3": ("tx::stream_select_kernel<0, 19, false", "tx::seg_select_kernel", "tx::seg_merge"),
+    "topk_c1": ("tx::stream_select_kernel<0, 16, false", "tx::seg_select_kernel", "tx::seg_merge"),
     "topk_c3_approx": ("tx::binned_",),
     "sort_c2": ("tx::radix_sort_rows_kernel", "tx::gather_row_lds_kernel"),
     "prefill_c5": ("tx::softmax_topk_kernel",),

@@ -175,18 +175,23 @@ def require_cuda(*ts: torch.Tensor) -> None:
 
 def select_plan(rows: int, cols: int, dtype: int, k: int = 128, sample: bool = True) -> dict:
     """Work split of the selection kernels for a [rows, cols] input (host only).
-    Rows of several segments finish in seg_merge64_kernel for top-k with k <= 64
-    (no sampler), else in seg_merge_kernel."""
+    A row is one whole-row workgroup (1024 threads, one segment), 2-4 equal
+    whole-row parts (1024 threads, `segments` = parts) or 256-thread segments.
+    Rows of several segments or parts finish in seg_merge64_kernel for top-k
+    with k <= 64 (no sampler), else in seg_merge_kernel."""
     out = (ctypes.c_int32 * 4)()
     check(LIB.tallax_testing_select_plan(rows, cols, dtype, out), "select_plan")
     nt, maxv, nseg, vps = list(out)
     dt = {F32: 0, BF16: 1}[dtype]
+    merge = "seg_merge64_kernel" if (not sample and k <= 64) else "seg_merge_kernel"
     if nt == 1024:
-        # EDGE: rows not a whole number of 16-byte vectors (a 16-byte aligned base assumed)
-        edge = "true" if (cols * (4 if dtype == F32 else 2)) % 16 else "false"
-        name = f"stream_select_kernel<{dt}, {maxv}, SAMPLE, {edge}>"
+        # EDGE: rows (or parts) not a whole number of 16-byte vectors (a 16-byte aligned base assumed)
+        edge = "true" if (cols // nseg * (4 if dtype == F32 else 2)) % 16 else "false"
+        if nseg == 1:
+            name = f"stream_select_kernel<{dt}, {maxv}, SAMPLE, {edge}>"
+        else:
+            name = f"stream_select_kernel<{dt}, {maxv}, false, {edge}> (parts) + {merge}"
     else:
-        merge = "seg_merge64_kernel" if (not sample and k <= 64) else "seg_merge_kernel"
         name = f"seg_select_kernel<{dt}, {maxv}, {nt}, SAMPLE>" + (f" + {merge}" if nseg > 1 else "")
     return {"threads": nt, "vectors_per_thread": maxv, "segments": nseg, "vectors_per_segment": vps,
             "kernel": name}

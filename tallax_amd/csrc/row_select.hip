@@ -61,6 +61,7 @@ constexpr int kMaxK = 128;                 // the reference's limit (top_k.py:43
 constexpr int kRun = 128;                  // list length handed between kernels
 constexpr int kMaxSeg = 32;
 constexpr int kTargetBlocks = 1024;        // ~4 workgroups per CU on 256 CUs
+constexpr int kPartsMaxBlocks = 512;       // whole-row parts: two rounds of one workgroup per CU at most
 
 struct SelArgs {
   const void* x;
@@ -76,6 +77,8 @@ struct SelArgs {
   uint64_t* ws_lists;
   int lists_only;  // write the segment list even when a row is one segment
   int64_t col_offset;   // added to every column index of a written list (a vocabulary shard's first column)
+  int64_t part_cols;    // whole-row kernel on row parts: row r of the [np rows, cols / np] view adds (r % np) * part_cols
+  int nparts;
   uint64_t* out_lists;  // merge kernel, lists_only: the merged list of each row, [rows][128]
   // sampler
   const int32_t* top_k;
@@ -1580,7 +1583,8 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     finalize_row<DT, SAMPLE>(a, row, sh.list64, sh.samp_g, rp);
   } else {
     uint64_t* dst = a.ws_lists + (size_t)row * kRun;
-    for (int i = tid; i < kRun; i += kNTS) dst[i] = sh.list64[i] ? sh.list64[i] - (uint64_t)a.col_offset : 0ull;
+    const uint64_t off = (uint64_t)(a.col_offset + (a.nparts > 1 ? (row % a.nparts) * a.part_cols : 0));
+    for (int i = tid; i < kRun; i += kNTS) dst[i] = sh.list64[i] ? sh.list64[i] - off : 0ull;
   }
 }
 
@@ -1645,6 +1649,7 @@ struct Plan {
   int maxv;
   int nseg;
   int64_t vps;
+  int parts;  // > 1: whole-row kernel on that many equal parts of each row, then the merge
 };
 
 // Work split.  A row of nv 16-byte vectors is handled either
@@ -1658,6 +1663,14 @@ struct Plan {
 //     16.7 -> 11.8; 19 vectors per thread for the 151936-wide bf16
 //     vocabulary: sampler [64, 151936] 20.5 -> 12.7, [256, 151936] 25.2 ->
 //     17.8; no shape slower); or
+//   * as 2-4 equal parts of at most 19 vectors per thread when the row
+//     divides and rows x parts <= kPartsMaxBlocks: the whole-row kernel
+//     writes each part's top-128 list (rows of the [parts x rows, cols /
+//     parts] view, column offsets added back), then the per-row merge
+//     (config 3, [128, 151936] f32: 21.50 -> 20.05 us; f32 sampler
+//     [64, 128256] 19.5 -> 15.7, [64, 201088] 26.9 -> 17.2; at more blocks
+//     the segments win: [256, 201088] 46.5 against 50.4, [512, 151936]
+//     top-k 55.1 against 62.6); or
 //   * in segments of 256 x MAXV vectors, MAXV in {4, 8, 16}: the largest that
 //     still gives ~4 workgroups per CU over the launch, then a per-row merge;
 //     where 16 gives more than one residency round (4 workgroups per CU,
@@ -1668,6 +1681,7 @@ static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
   const int vec = dt == kF32 ? 4 : 8;
   const int64_t nv = (cols + 2 * (vec - 1)) / vec;  // covers any row misalignment
   static const int kOpts[3] = {16, 8, 4};
+  p->parts = 0;
   if (nv <= (int64_t)kNTS * 19) {
     int maxv = nv > (int64_t)kNTS * 16 ? 19 : 16;
     while (maxv > 4 && (int64_t)kNTS * (maxv / 2) >= nv) maxv /= 2;
@@ -1676,6 +1690,18 @@ static int plan_rows(int64_t rows, int64_t cols, int dt, Plan* p) {
     p->nseg = 1;
     p->vps = (int64_t)kNTS * maxv;
     return kOk;
+  }
+  for (int np = 2; np <= 4 && rows * np <= kPartsMaxBlocks; ++np) {  // equal whole-row parts
+    if (cols % np) continue;
+    const int64_t nvh = (cols / np + 2 * (vec - 1)) / vec;
+    if (nvh <= (int64_t)kNTS * 19) {
+      p->nt = kNTS;
+      p->maxv = nvh > (int64_t)kNTS * 16 ? 19 : 16;
+      p->nseg = np;
+      p->vps = (int64_t)kNTS * p->maxv;
+      p->parts = np;
+      return kOk;
+    }
   }
   int maxv = 4;
   for (int o = 0; o < 3; ++o) {
@@ -1724,8 +1750,30 @@ static void launch_a(const SelArgs& a, hipStream_t s) {
 }
 
 template <int DT, bool SAMPLE>
-static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const char* what) {
-  if (p.nt == kNTS) {
+static int launch_select(const SelArgs& a0, const Plan& p, hipStream_t s, const char* what) {
+  // parts: the whole-row kernel writes each part's list (no sampling; its
+  // rows are the [np rows, cols / np] view), the merge kernel finishes the row
+  SelArgs h = a0;
+  if (p.parts > 1) {
+    h.rows = a0.rows * p.parts;
+    h.cols = a0.cols / p.parts;
+    h.nseg = 1;
+    h.lists_only = 1;
+    h.part_cols = h.cols;
+    h.nparts = p.parts;
+  }
+  const SelArgs& a = h;
+  if (p.nt == kNTS && p.parts > 1) {
+    const bool edge = ((uintptr_t)a.x % 16) != 0 || (a.cols * ElemT<DT>::ES) % 16 != 0;
+    const dim3 g((unsigned)a.rows), b(kNTS);
+    if (p.maxv == 19) {
+      if (edge) hipLaunchKernelGGL((stream_select_kernel<DT, 19, false, true>), g, b, 0, s, a);
+      else hipLaunchKernelGGL((stream_select_kernel<DT, 19, false, false>), g, b, 0, s, a);
+    } else {
+      if (edge) hipLaunchKernelGGL((stream_select_kernel<DT, 16, false, true>), g, b, 0, s, a);
+      else hipLaunchKernelGGL((stream_select_kernel<DT, 16, false, false>), g, b, 0, s, a);
+    }
+  } else if (p.nt == kNTS) {
     // rows that start 16-byte aligned and fill their last vector have no
     // slots outside the row: the kernel without the edge handling
     const bool edge = ((uintptr_t)a.x % 16) != 0 || (a.cols * ElemT<DT>::ES) % 16 != 0;
@@ -1751,11 +1799,11 @@ static int launch_select(const SelArgs& a, const Plan& p, hipStream_t s, const c
     else launch_a<DT, 4, kNT, SAMPLE>(a, s);
   }
   int st = launch_status(what);
-  if (st || a.nseg == 1) return st;
-  if (!SAMPLE && !a.lists_only && a.k <= kWave)
-    hipLaunchKernelGGL((seg_merge64_kernel<DT>), dim3((unsigned)a.rows), dim3(kMergeNT), 0, s, a);
+  if (st || a0.nseg == 1) return st;
+  if (!SAMPLE && !a0.lists_only && a0.k <= kWave)
+    hipLaunchKernelGGL((seg_merge64_kernel<DT>), dim3((unsigned)a0.rows), dim3(kMergeNT), 0, s, a0);
   else
-    hipLaunchKernelGGL((seg_merge_kernel<DT, SAMPLE>), dim3((unsigned)a.rows), dim3(kMergeNT), 0, s, a);
+    hipLaunchKernelGGL((seg_merge_kernel<DT, SAMPLE>), dim3((unsigned)a0.rows), dim3(kMergeNT), 0, s, a0);
   return launch_status(what);
 }
 

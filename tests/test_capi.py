@@ -43,7 +43,8 @@ def test_error_path_without_gpu():
 
 def test_work_split_without_gpu():
     """Every row that fits 1024 threads x 19 vectors goes to the whole-row
-    kernel, at any row count; longer rows are cut into segments."""
+    kernel, at any row count; longer rows into 2-4 whole-row parts or into
+    segments."""
     from tallax_amd import _lib
     for rows, cols, dt in [(1, 128256, _lib.BF16), (64, 128256, _lib.BF16), (8, 32768, _lib.F32),
                            (100, 65472, _lib.F32), (13, 167, _lib.F32), (256, 131058, _lib.BF16),
@@ -53,12 +54,18 @@ def test_work_split_without_gpu():
         assert _lib.LIB.tallax_topk_workspace_size(rows, cols, 64, dt) == 0
     assert _lib.select_plan(1, 151936, _lib.BF16)["vectors_per_thread"] == 19
     assert _lib.select_plan(1, 128256, _lib.BF16)["vectors_per_thread"] == 16
-    for rows, cols, dt in [(1, 160000, _lib.BF16), (8, 80000, _lib.F32), (128, 151936, _lib.F32)]:
+    # rows that divide into 2-4 whole-row parts, at most 512 part workgroups
+    for rows, cols, dt, np_ in [(1, 160000, _lib.BF16, 2), (8, 80000, _lib.F32, 2), (128, 151936, _lib.F32, 2),
+                                (64, 201088, _lib.F32, 4), (128, 256000, _lib.F32, 4), (256, 256000, _lib.BF16, 2)]:
+        p = _lib.select_plan(rows, cols, dt)
+        assert p["threads"] == 1024 and p["segments"] == np_, (rows, cols, p)
+    assert _lib.select_plan(128, 151936, _lib.F32, k=50, sample=False)["kernel"] == \
+        "stream_select_kernel<0, 19, false, false> (parts) + seg_merge64_kernel"
+    # otherwise segments: too many part workgroups, or a row that does not divide
+    for rows, cols, dt in [(256, 201088, _lib.F32), (512, 151936, _lib.F32), (4, 200003, _lib.F32),
+                           (2048, 151936, _lib.F32)]:
         p = _lib.select_plan(rows, cols, dt)
         assert p["threads"] == 256 and p["segments"] > 1, (rows, cols, p)
-    assert _lib.select_plan(128, 151936, _lib.F32) == {"threads": 256, "vectors_per_thread": 19, "segments": 8,
-                                                        "vectors_per_segment": 256 * 19,
-                                                        "kernel": "seg_select_kernel<0, 19, 256, SAMPLE> + seg_merge_kernel"}
 
 
 def test_sort_workspace_contract_without_gpu():

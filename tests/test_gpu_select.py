@@ -92,13 +92,22 @@ TOPK_CASES = [
     (4, 40000, 100, "bf16", "tieblock"),    # 60 large values, then a 10000-wide tie block
     (4, 40000, 100, "f32", "tieblock"),
     (4, 40000, 100, "f32", "nan_heavy"),    # NaN rows with a few finite, -inf and finfo.min values
-    # the same inputs on rows too long for one workgroup (segments, then the merge)
-    (2, 200000, 17, "f32", "const"),
-    (3, 200000, 64, "f32", "ints"),
-    (6, 200000, 50, "f32", "special"),
+    # the same inputs on rows too long for one workgroup that do not divide
+    # into whole-row parts (segments, then the merge)
+    (2, 200003, 17, "f32", "const"),
+    (3, 200003, 64, "f32", "ints"),
+    (6, 200003, 50, "f32", "special"),
+    (4, 200003, 100, "bf16", "tieblock"),
+    (4, 200003, 100, "f32", "tieblock"),
+    (4, 200003, 100, "f32", "nan_heavy"),
+    # ... and rows that do: 2-4 whole-row parts, then the merge (misaligned
+    # parts when a part is not a whole number of vectors)
+    (8, 200000, 64, "f32", "normal"),
+    (4, 151938, 100, "f32", "special"),
     (4, 200000, 100, "bf16", "tieblock"),
-    (4, 200000, 100, "f32", "tieblock"),
-    (4, 200000, 100, "f32", "nan_heavy"),
+    (2, 200000, 17, "f32", "const"),
+    (16, 151936, 128, "f32", "masked5"),
+    (32, 151936, 128, "f32", "masked_mix"),
     # whole rows at 19 vectors per thread (bf16 rows up to 155648 elements,
     # f32 up to 77824), aligned and misaligned, with the rare paths
     (128, 151936, 50, "bf16", "normal"),
@@ -289,7 +298,8 @@ def _sampler_inputs(rows, vocab, seed, sigma=3.0):
                                                      (256, 128256, "bf16", True), (128, 32768, "f32", True),
                                                      (128, 8195, "bf16", False), (64, 151936, "bf16", False),
                                                      (32, 151936, "bf16", True), (8, 70001, "f32", False),
-                                                     (16, 200000, "bf16", False)])
+                                                     (16, 200003, "bf16", False), (32, 151936, "f32", False),
+                                                     (16, 201088, "f32", True)])
 def test_fused_sampler_parity(gpu, rows, vocab, dtype, masked):
     from tallax_amd import sampling
     _log(f"sample rows={rows} vocab={vocab} dtype={dtype} masked={masked}")
