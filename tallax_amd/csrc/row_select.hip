@@ -79,6 +79,7 @@ struct SelArgs {
   int64_t col_offset;   // added to every column index of a written list (a vocabulary shard's first column)
   int64_t part_cols;    // whole-row kernel on row parts: row r of the [np rows, cols / np] view adds (r % np) * part_cols
   int nparts;
+  int list_k;           // whole-row kernel: places of the row's (or part's) list that are read (64; 0: all 128)
   uint64_t* out_lists;  // merge kernel, lists_only: the merged list of each row, [rows][128]
   // sampler
   const int32_t* top_k;
@@ -1301,6 +1302,9 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   const char* rowp = (const char*)a.x + (size_t)(row * a.cols) * ES;
   const RowVec<ES> rv(rowp);
   const int nv = (int)((a.cols + rv.mis + VEC - 1) / VEC);  // 1 <= nv <= kNTS * V (host plan)
+  // list places the consumer reads: the bound guarantees kq elements, the
+  // rank writes places below kq (the rest of the list is not read)
+  const int kq = a.list_k == 64 ? 64 : kMaxK;
   const int cols = (int)a.cols;
   const RowParams rp = load_row_params<SAMPLE>(a, row);
 
@@ -1456,7 +1460,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
         }
       }
       uint32_t wl, wm;
-      wave_kth_and_max<KB>(tk, kMaxK / NE, wl, wm);
+      wave_kth_and_max<KB>(tk, kq / NE, wl, wm);
       if (l == 0) {
         ss.wl[w] = wl;
         ss.wm[w] = wm;
@@ -1517,9 +1521,9 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   const int n = ss.ncand;
   // fewer than 128 with thr at the eligibility floor: every eligible element
   // of the row is a candidate, the rest of the list is ineligible elements
-  const bool fill = ss.ovf == 0 && n < kMaxK && thr == kFloor;  // block-uniform
+  const bool fill = ss.ovf == 0 && n < kq && thr == kFloor;  // block-uniform
   // an overflowing staging region or more than kCandCap candidates: heavy ties
-  const bool tie = !fill && (ss.ovf != 0 || n < kMaxK || n > kCandCap);
+  const bool tie = !fill && (ss.ovf != 0 || n < kq || n > kCandCap);
   if (fill) fill_ineligible<DT, V>(rv.base, nv, rv.mis, cols, n, pmin, pinf, sh.list64, sh.red, &ss.vsi[0][0]);
   if (tie) {
     stream_tie_path<DT, V>(rv.base, nv, rv.mis, cols, sh, stage);
@@ -1555,7 +1559,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
     __syncthreads();
     // buckets that start at rank >= 128 are not needed any further
     int start = 0, end = 0;
-    const bool need = mine && (start = ss.hist[b]) < kMaxK;
+    const bool need = mine && (start = ss.hist[b]) < kq;
     if (need) {
       end = b + 1 < nb ? ss.hist[b + 1] : n;
       ss.cand[start + slot] = c;  // every thread read its own entry before the barriers above
@@ -1570,7 +1574,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) r += (i0 + u < end && x[u] > c) ? 1 : 0;
       }
-      if (r < kMaxK) {
+      if (r < kq) {
         const uint32_t k = comp_key(c);
         uint32_t key = k;
         if (kBF) key = k >= 0x8000u ? (k << 16) : ((k << 16) | 0xFFFFu);
@@ -1584,7 +1588,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
   } else {
     uint64_t* dst = a.ws_lists + (size_t)row * kRun;
     const uint64_t off = (uint64_t)(a.col_offset + (a.nparts > 1 ? (row % a.nparts) * a.part_cols : 0));
-    for (int i = tid; i < kRun; i += kNTS) dst[i] = sh.list64[i] ? sh.list64[i] - off : 0ull;
+    for (int i = tid; i < kq; i += kNTS) dst[i] = sh.list64[i] ? sh.list64[i] - off : 0ull;
   }
 }
 
@@ -1754,6 +1758,8 @@ static int launch_select(const SelArgs& a0, const Plan& p, hipStream_t s, const 
   // parts: the whole-row kernel writes each part's list (no sampling; its
   // rows are the [np rows, cols / np] view), the merge kernel finishes the row
   SelArgs h = a0;
+  // top-k with k <= 64 reads the first 64 places of a row's (or a part's) list
+  if (!SAMPLE && !a0.lists_only && a0.k <= kWave) h.list_k = kWave;
   if (p.parts > 1) {
     h.rows = a0.rows * p.parts;
     h.cols = a0.cols / p.parts;
@@ -1761,6 +1767,7 @@ static int launch_select(const SelArgs& a0, const Plan& p, hipStream_t s, const 
     h.lists_only = 1;
     h.part_cols = h.cols;
     h.nparts = p.parts;
+
   }
   const SelArgs& a = h;
   if (p.nt == kNTS && p.parts > 1) {
