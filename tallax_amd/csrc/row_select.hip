@@ -974,7 +974,7 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge_kernel(SelArgs a) {
       tree[w][kWave + l] = acc[1];
     }
     __syncthreads();
-    if ((w & (2 * st - 1)) == 0) {
+    if ((w & (2 * st - 1)) == 0 && w + st < a.nseg) {  // waves from nseg on hold no list
       const uint64_t c[2] = {tree[w + st][l], tree[w + st][kWave + l]};
       wave_merge128_desc(acc, c);
     }
@@ -1020,11 +1020,29 @@ __global__ __launch_bounds__(kMergeNT) void seg_merge64_kernel(SelArgs a) {
   for (int st = 1; st < NW; st <<= 1) {
     if ((w & (2 * st - 1)) == st) tree[w][l] = acc;
     __syncthreads();
-    if ((w & (2 * st - 1)) == 0) acc = wave_merge64_desc(acc, tree[w + st][l]);
+    if ((w & (2 * st - 1)) == 0 && w + st < a.nseg) acc = wave_merge64_desc(acc, tree[w + st][l]);
   }
   if (w == 0) tree[0][l] = acc;
   __syncthreads();
   finalize_row<DT, false>(a, row, tree[0], sg, rp);  // reads the first k <= 64 entries
+}
+
+// Kernel B for top-k with k <= 64 over at most two lists per row (the
+// whole-row kernel's two parts): one wave per row merges the two 64-entry
+// runs in registers and writes the outputs, no LDS tree and no barrier.
+template <int DT>
+__global__ __launch_bounds__(kWave) void seg_merge64_pair_kernel(SelArgs a) {
+  __shared__ uint64_t list[kWave];
+  __shared__ float sg[kRun];
+  const int64_t row = blockIdx.x;
+  const int l = lane_id();
+  const uint64_t* src = a.ws_lists + (size_t)row * a.nseg * kRun;
+  const RowParams rp = load_row_params<false>(a, row);
+  uint64_t acc = src[l];
+  if (a.nseg > 1) acc = wave_merge64_desc(acc, src[kRun + l]);
+  list[l] = acc;
+  __syncthreads();
+  finalize_row<DT, false>(a, row, list, sg, rp);  // reads the first k <= 64 entries
 }
 
 // ---------------------------------------------------------------------------
@@ -1807,7 +1825,9 @@ static int launch_select(const SelArgs& a0, const Plan& p, hipStream_t s, const 
   }
   int st = launch_status(what);
   if (st || a0.nseg == 1) return st;
-  if (!SAMPLE && !a0.lists_only && a0.k <= kWave)
+  if (!SAMPLE && !a0.lists_only && a0.k <= kWave && a0.nseg <= 2)
+    hipLaunchKernelGGL((seg_merge64_pair_kernel<DT>), dim3((unsigned)a0.rows), dim3(kWave), 0, s, a0);
+  else if (!SAMPLE && !a0.lists_only && a0.k <= kWave)
     hipLaunchKernelGGL((seg_merge64_kernel<DT>), dim3((unsigned)a0.rows), dim3(kMergeNT), 0, s, a0);
   else
     hipLaunchKernelGGL((seg_merge_kernel<DT, SAMPLE>), dim3((unsigned)a0.rows), dim3(kMergeNT), 0, s, a0);
