@@ -177,13 +177,15 @@ def select_plan(rows: int, cols: int, dtype: int, k: int = 128, sample: bool = T
     """Work split of the selection kernels for a [rows, cols] input (host only).
     A row is one whole-row workgroup (1024 threads, one segment), 2-4 equal
     whole-row parts (1024 threads, `segments` = parts) or 256-thread segments.
-    Rows of several segments or parts finish in seg_merge64_kernel for top-k
-    with k <= 64 (no sampler), else in seg_merge_kernel."""
+    Rows of several segments or parts finish in seg_merge64_pair_kernel (two
+    lists) or seg_merge64_kernel for top-k with k <= 64 (no sampler), else in
+    seg_merge_kernel."""
     out = (ctypes.c_int32 * 4)()
     check(LIB.tallax_testing_select_plan(rows, cols, dtype, out), "select_plan")
     nt, maxv, nseg, vps = list(out)
     dt = {F32: 0, BF16: 1}[dtype]
-    merge = "seg_merge64_kernel" if (not sample and k <= 64) else "seg_merge_kernel"
+    merge = ("seg_merge64_pair_kernel" if nseg <= 2 else "seg_merge64_kernel") if (not sample and k <= 64) \
+        else "seg_merge_kernel"
     if nt == 1024:
         # EDGE: rows (or parts) not a whole number of 16-byte vectors (a 16-byte aligned base assumed)
         edge = "true" if (cols // nseg * (4 if dtype == F32 else 2)) % 16 else "false"

@@ -60,7 +60,7 @@ def test_work_split_without_gpu():
         p = _lib.select_plan(rows, cols, dt)
         assert p["threads"] == 1024 and p["segments"] == np_, (rows, cols, p)
     assert _lib.select_plan(128, 151936, _lib.F32, k=50, sample=False)["kernel"] == \
-        "stream_select_kernel<0, 19, false, false> (parts) + seg_merge64_kernel"
+        "stream_select_kernel<0, 19, false, false> (parts) + seg_merge64_pair_kernel"
     # otherwise segments: too many part workgroups, or a row that does not divide
     for rows, cols, dt in [(256, 201088, _lib.F32), (512, 151936, _lib.F32), (4, 200003, _lib.F32),
                            (2048, 151936, _lib.F32)]:
