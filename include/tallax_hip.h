@@ -137,11 +137,12 @@ int tallax_fused_topk_topp_sample(const void* logits, int dtype, int64_t rows, i
  * NO COUNTERPART IN THE REFERENCE: for callers that cannot allocate device
  * memory or pass a workspace (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  Same arguments and results as
- * tallax_fused_topk_topp_sample; the per-segment candidate lists of
- * segmented rows go to a static device array of 16 MiB that each GPU holds
- * until the process ends (it calls no hipMalloc/hipFree).  Inputs whose
- * lists need more (rows x segments x 1 KiB; e.g. f32 rows of 151936 columns
- * beyond about 1600 rows) return TALLAX_UNSUPPORTED before any launch.  All
+ * tallax_fused_topk_topp_sample; the candidate lists of rows split into
+ * segments or whole-row parts go to a static device array of 16 MiB that
+ * each GPU holds until the process ends (it calls no hipMalloc/hipFree).
+ * Inputs whose lists need more (rows x lists x 1 KiB; e.g. f32 rows of 151936
+ * columns beyond about 1600 rows) return TALLAX_UNSUPPORTED before any
+ * launch.  All
  * calls on one GPU share the array: calls that overlap on one GPU race.
  * The first call on a device looks up the array's device address; made
  * while `stream` is capturing, that call returns TALLAX_UNSUPPORTED and
