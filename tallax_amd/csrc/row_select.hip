@@ -1508,6 +1508,11 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
 #pragma unroll
         for (int j = 0; j < V; ++j) stage_if(j, vmax[j] >= st);
       } else {
+        // the late waves' staging and extraction are the critical path: they
+        // issue ahead of the early waves' extraction on the shared SIMDs
+        // (config 4: 15.78 -> 15.44 us; priority 3, or also raising the
+        // early waves for their bound, no better)
+        __builtin_amdgcn_s_setprio(2);
 #pragma unroll
         for (int j = 0; j < V; ++j) stage_if(j, vec_smax<DT>(raw[j]) >= st);
       }
@@ -1529,6 +1534,7 @@ __global__ __launch_bounds__(kNTS) void stream_select_kernel(SelArgs a) {
       }
     }
     extract(thr, !early);
+    __builtin_amdgcn_s_setprio(0);
   }
   __syncthreads();
   // M: at least the largest candidate key (waves 0..7 post their largest
