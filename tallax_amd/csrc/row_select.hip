@@ -1046,20 +1046,22 @@ __global__ __launch_bounds__(kWave) void seg_merge64_pair_kernel(SelArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel S (stream_select_kernel): a whole row per 1024-thread workgroup (16
-// waves, 4 per SIMD), V 16-byte vectors per thread, vector j of thread t at
-// row vector j * 1024 + t.
+// Kernel S (stream_select_kernel): a whole row (or one equal part of it) per
+// 1024-thread workgroup (16 waves, 4 per SIMD), V 16-byte vectors per thread
+// (V <= 19), vector j of thread t at row vector j * 1024 + t.
 //   1. Every load is issued up front.
 //   2. The bound L: the minimum over waves 0..7 of each one's 16th largest
-//      thread maximum (a radix search with one ballot per key bit), so at
-//      least 128 elements reach L.  Those waves' loads are issued first and
+//      thread maximum (8th when only 64 list places are read), a radix search
+//      with one ballot per key bit, so at least 128 (64) elements reach L.
+//      Those waves' loads are issued first and
 //      arrive first, so L is known before waves 8..15 have their first
 //      vector (measured at config 4: 16.86 -> 16.15 us against the bound over
 //      all 16 waves; waves 0..11 gave 17.0 us, waves 0..3 overflow the
 //      candidate array).
 //   3. Vectors whose maximum reaches L are staged in their wave's LDS region
 //      (one ballot per vector index; waves 8..15 stage each vector as it
-//      arrives), then each wave takes its staged vectors one per lane and
+//      arrives, at raised wave priority), then each wave takes its staged
+//      vectors one per lane and
 //      appends the elements >= L as composites (canonical key << 32 |
 //      ~index).  The row maximum M the rank needs is at least the largest
 //      candidate key: waves 0..7 post their largest element, waves 8..15
@@ -1068,7 +1070,7 @@ __global__ __launch_bounds__(kWave) void seg_merge64_pair_kernel(SelArgs a) {
 //      (M - key) >> shift (at most kBuckets), one atomic per candidate for the
 //      histogram and its slot, an exclusive scan, a scatter, and each
 //      candidate's rank = its bucket's start + the larger composites in its
-//      bucket.  The first 128 ranks are the row's top-128 in order.
+//      bucket.  The first 128 (64) ranks are the row's top-128 (64) in order.
 // Rows with fewer than 128 eligible elements rank them and take the rest of
 // the list by class (fill_ineligible).  Rows whose staged vectors or
 // candidates overflow (heavy ties: constant rows, long tie blocks) take
@@ -1699,7 +1701,7 @@ struct Plan {
 //     [64, 128256] 19.5 -> 15.7, [64, 201088] 26.9 -> 17.2; at more blocks
 //     the segments win: [256, 201088] 46.5 against 50.4, [512, 151936]
 //     top-k 55.1 against 62.6); or
-//   * in segments of 256 x MAXV vectors, MAXV in {4, 8, 16}: the largest that
+//   * in segments of 256 x MAXV vectors, MAXV in {4, 8, 16, 19}: the largest that
 //     still gives ~4 workgroups per CU over the launch, then a per-row merge;
 //     where 16 gives more than one residency round (4 workgroups per CU,
 //     kTargetBlocks) and 19 gives exactly one, MAXV = 19 (config 3: 8
