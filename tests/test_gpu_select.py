@@ -390,6 +390,8 @@ def test_top_p_mask_errors(gpu):
     (256, 128256, "bf16", [64128, 64128]),
     (64, 50000, "f32", [20000, 129, 29871]),            # uneven, a shard barely over 128 columns
     (32, 32000, "bf16", [32000]),
+    (16, 400000, "f32", [200000, 200000]),              # shards of 4 whole-row parts each (offsets composed)
+    (8, 400006, "f32", [200003, 200003]),               # shards of segments
 ])
 def test_sample_sharded_equals_sample(gpu, rows, vocab, dtype, widths):
     """The vocabulary-sharded composition (per-shard top-128, global indices,
