@@ -299,7 +299,7 @@ def _sampler_inputs(rows, vocab, seed, sigma=3.0):
                                                      (128, 8195, "bf16", False), (64, 151936, "bf16", False),
                                                      (32, 151936, "bf16", True), (8, 70001, "f32", False),
                                                      (16, 200003, "bf16", False), (32, 151936, "f32", False),
-                                                     (16, 201088, "f32", True)])
+                                                     (16, 201088, "f32", True), (32, 256000, "bf16", False)])
 def test_fused_sampler_parity(gpu, rows, vocab, dtype, masked):
     from tallax_amd import sampling
     _log(f"sample rows={rows} vocab={vocab} dtype={dtype} masked={masked}")
