@@ -243,7 +243,8 @@ int tallax_take_along_axis(const void* values, int dtype, int64_t vrows, int64_t
  * running total of earlier tiles added sequentially.
  * Replaces tax.cumsum(arr, axis, reverse) -- tallax/_src/cumsum.py:75-101
  *   (kernel cumsum_arrays, cumsum.py:32-63).
- * x, out [rows, cols] f32 or int32 (int32 adds wrap).
+ * x, out [rows, cols] f32 or int32 (int32 adds wrap); out must not overlap x
+ * (tile totals are staged in out; overlap returns TALLAX_INVALID_ARGUMENT).
  * ---------------------------------------------------------------------- */
 int tallax_cumsum(const void* x, int dtype, int64_t rows, int64_t cols, int axis, int reverse, void* out,
                   tallax_stream_t stream);

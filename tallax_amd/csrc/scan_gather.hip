@@ -134,14 +134,47 @@ __global__ __launch_bounds__(256) void gather_col_kernel(const T* __restrict__ v
 }
 
 // ---------------------------------------------------------------------------
-// cumsum along axis 1: one workgroup per row, 16 waves; wave w scans tiles
-// w, w + 16, ... of a chunk of up to 16 * kTPW tiles held in registers (two
-// elements per lane per tile: tile position p = h * 64 + lane).
+// cumsum.  Tile t of a scan line (a row for axis 1, a column for axis 0) holds
+// scan positions [t * TS, (t + 1) * TS) of the zero-padded line of length
+// plen = ntiles * TS (TS = 128 for axis 1, 8 for axis 0); position q is
+// element q, or element plen - 1 - q when reversed.  The tile's total is its
+// scanned last position; for every tile but the last that position is a real
+// element (forward: TS t + TS - 1 < cols; reversed: plen - TS (t + 1) >= 0),
+// and its final value, scan + carry, is the carry of the next tile:
+// carry[t + 1] = add(total[t], carry[t]) in the reference's sequential order.
+// Last positions sit at element index = TS - 1 (mod TS) forward and 0
+// (mod TS) reversed (plen is a multiple of TS).
 // ---------------------------------------------------------------------------
+
+// element index of tile t's last scan position
+__device__ __forceinline__ int64_t tile_last_pos(int64_t t, int ts, int64_t plen, int reverse) {
+  return reverse ? plen - (int64_t)ts * (t + 1) : (int64_t)ts * t + ts - 1;
+}
+
+// element index where the three-launch path stages tile t's total: the line's
+// leading elements with the last positions skipped (TS - 1 totals per TS
+// elements), so that the totals of a line are nearly contiguous and never
+// share an element with a final value.  Staged indices stay below
+// TS * (ntiles - 1) <= len for t <= ntiles - 2.
+__device__ __forceinline__ int64_t tile_stage_pos(int64_t t, int ts, int reverse) {
+  return (int64_t)ts * (t / (ts - 1)) + (reverse ? 1 : 0) + t % (ts - 1);
+}
+
+template <typename T>
+__device__ __forceinline__ T readlane_t(T v, int src) {
+  return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+}
+
+// Axis 1, one workgroup per row, 16 waves; wave w scans tiles w, w + 16, ...
+// of a chunk of 64 tiles held in registers (two elements per lane per tile:
+// tile position p = h * 64 + lane).  The next chunk's loads are issued before
+// this chunk's carries are chained, and wave 0 chains the 64 tile totals with
+// readlanes (one dependent add per tile).
 constexpr int kScanNT = 1024;
 constexpr int kScanNW = kScanNT / kWave;
 constexpr int kTPW = 4;                        // tiles per wave per chunk
 constexpr int kChunkTiles = kScanNW * kTPW;    // 64 tiles = 8192 elements
+static_assert(kChunkTiles == kWave, "one tile total per lane of wave 0");
 
 template <typename T>
 __global__ __launch_bounds__(kScanNT) void cumsum_rows_kernel(const T* __restrict__ x, int64_t cols, int reverse,
@@ -155,35 +188,44 @@ __global__ __launch_bounds__(kScanNT) void cumsum_rows_kernel(const T* __restric
   const int64_t ntiles = pcols / 128;
   const T* xr = x + r * cols;
   T* orow = out + r * cols;
-  // element at scan position q (of the possibly flipped padded row)
-  auto src_index = [&](int64_t q) -> int64_t { return reverse ? pcols - 1 - q : q; };
-  T run = (T)0;
-  for (int64_t t0 = 0; t0 < ntiles; t0 += kChunkTiles) {
-    T c[kTPW][2];
+  auto load_chunk = [&](int64_t t0, T (&c)[kTPW][2]) {
 #pragma unroll
     for (int i = 0; i < kTPW; ++i) {
       const int64_t t = t0 + w + (int64_t)i * kScanNW;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int64_t q = t * 128 + h * kWave + l;
-        const int64_t e = src_index(q);
+        const int64_t e = reverse ? pcols - 1 - q : q;
         c[i][h] = (t < ntiles && e < cols) ? xr[e] : (T)0;
       }
+    }
+  };
+  T c[kTPW][2];
+  load_chunk(0, c);
+  T run = (T)0;
+  for (int64_t t0 = 0; t0 < ntiles; t0 += kChunkTiles) {
+#pragma unroll
+    for (int i = 0; i < kTPW; ++i) {
       hs_scan128(c[i], l);
       if (l == kWave - 1) tsum[w + i * kScanNW] = c[i][1];
     }
-    __syncthreads();
+    T nx[kTPW][2];
+    load_chunk(t0 + kChunkTiles, nx);
+    lds_barrier();
     // sequential running total over the chunk's tiles (reference order)
-    if (threadIdx.x == 0) {
-      T acc = run;
-      const int64_t n = ntiles - t0 < kChunkTiles ? ntiles - t0 : kChunkTiles;
-      for (int i = 0; i < n; ++i) {
-        carry[i] = acc;
-        acc = (t0 + i == 0) ? tsum[i] : add_in_order(acc, tsum[i]);
+    if (w == 0) {
+      const T mine = t0 + l < ntiles ? tsum[l] : (T)0;
+      T acc = t0 == 0 ? readlane_t(mine, 0) : add_in_order(run, readlane_t(mine, 0));
+      T cy = run;
+#pragma unroll
+      for (int i = 1; i < kChunkTiles; ++i) {
+        cy = l == i ? acc : cy;
+        acc = add_in_order(acc, readlane_t(mine, i));
       }
-      run_sh = acc;
+      carry[l] = cy;
+      if (l == 0) run_sh = acc;
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int i = 0; i < kTPW; ++i) {
       const int64_t t = t0 + w + (int64_t)i * kScanNW;
@@ -192,25 +234,90 @@ __global__ __launch_bounds__(kScanNT) void cumsum_rows_kernel(const T* __restric
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int64_t q = t * 128 + h * kWave + l;
-        const int64_t e = src_index(q);
+        const int64_t e = reverse ? pcols - 1 - q : q;
         const T v = t == 0 ? c[i][h] : add_in_order(c[i][h], cy);
         if (e < cols) orow[e] = v;
       }
     }
     run = run_sh;
-    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kTPW; ++i) {
+      c[i][0] = nx[i][0];
+      c[i][1] = nx[i][1];
+    }
+    // no third barrier: the next writes of tsum, carry and run_sh follow the
+    // next chunk's first barrier, which every wave reaches after its reads
   }
 }
 
-// cumsum along axis 0: one thread per column, tiles of 8 rows.
-template <typename T>
-__global__ __launch_bounds__(256) void cumsum_cols_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
-                                                          int reverse, T* __restrict__ out) {
-  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
-  const int64_t prows = (rows + 7) / 8 * 8;
-  T run = (T)0;
-  for (int64_t t = 0; t < prows / 8; ++t) {
+// Axis 1, any number of rows, in three launches (each tile scanned by one
+// wave, so the chip fills whatever the row count):
+//   FINAL = false: scan tiles 0 .. ntiles - 2 of every row and stage each
+//                  tile's total in `out` (tile_stage_pos);
+//   cumsum_chain_kernel: chain the staged totals and store the final values
+//                  at the tiles' last positions;
+//   FINAL = true:  scan every tile again and add the carry (the previous
+//                  tile's final last position); positions already final are
+//                  not written, staged totals are overwritten.
+constexpr int kTileWaves = 4;      // waves per workgroup
+constexpr int kTilesPerWave = 4;   // tiles per wave, loads issued together
+template <typename T, bool FINAL>
+__global__ __launch_bounds__(kTileWaves * kWave) void cumsum_row_tiles_kernel(const T* __restrict__ x, int64_t rows,
+                                                                              int64_t cols, int64_t ntiles,
+                                                                              int reverse, T* __restrict__ out) {
+  const int l = lane_id();
+  const int64_t per_row = FINAL ? ntiles : ntiles - 1;
+  const int64_t ntask = rows * per_row;
+  const int64_t pcols = ntiles * 128;
+  const int64_t g0 = ((int64_t)blockIdx.x * kTileWaves + threadIdx.x / kWave) * kTilesPerWave;
+  T c[kTilesPerWave][2];
+  T cy[kTilesPerWave];
+  int64_t rr[kTilesPerWave], tt[kTilesPerWave];
+#pragma unroll
+  for (int i = 0; i < kTilesPerWave; ++i) {
+    const int64_t g = g0 + i;
+    rr[i] = g < ntask ? g / per_row : -1;
+    tt[i] = g < ntask ? g - rr[i] * per_row : 0;
+    const T* xr = x + rr[i] * cols;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t q = tt[i] * 128 + h * kWave + l;
+      const int64_t e = reverse ? pcols - 1 - q : q;
+      c[i][h] = (rr[i] >= 0 && e < cols) ? xr[e] : (T)0;
+    }
+    cy[i] = (FINAL && rr[i] >= 0 && tt[i] > 0) ? out[rr[i] * cols + tile_last_pos(tt[i] - 1, 128, pcols, reverse)]
+                                               : (T)0;
+  }
+#pragma unroll
+  for (int i = 0; i < kTilesPerWave; ++i) {
+    hs_scan128(c[i], l);
+    if (rr[i] < 0) continue;
+    T* orow = out + rr[i] * cols;
+    if (!FINAL) {
+      if (l == kWave - 1) orow[tile_stage_pos(tt[i], 128, reverse)] = c[i][1];
+      continue;
+    }
+    const bool last_final = tt[i] < ntiles - 1;  // the last position already holds its final value
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t q = tt[i] * 128 + h * kWave + l;
+      const int64_t e = reverse ? pcols - 1 - q : q;
+      const T v = tt[i] == 0 ? c[i][h] : add_in_order(c[i][h], cy[i]);
+      if (e < cols && !(last_final && h == 1 && l == kWave - 1)) orow[e] = v;
+    }
+  }
+}
+
+// Axis 0, in the same three launches: one thread per (tile of 8 rows,
+// column), consecutive threads on consecutive columns.
+template <typename T, bool FINAL>
+__global__ __launch_bounds__(256) void cumsum_col_tiles_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
+                                                               int64_t ntiles, int reverse, T* __restrict__ out) {
+  const int64_t per_col = FINAL ? ntiles : ntiles - 1;
+  const int64_t ntask = per_col * cols;
+  const int64_t prows = ntiles * 8;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < ntask; g += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = g / cols, c = g - t * cols;
     T v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -218,6 +325,7 @@ __global__ __launch_bounds__(256) void cumsum_cols_kernel(const T* __restrict__ 
       const int64_t rr = reverse ? prows - 1 - q : q;
       v[i] = rr < rows ? x[rr * cols + c] : (T)0;
     }
+    const T cy = (FINAL && t > 0) ? out[tile_last_pos(t - 1, 8, prows, reverse) * cols + c] : (T)0;
 #pragma unroll
     for (int s = 1; s < 8; s <<= 1) {
       T n[8];
@@ -226,13 +334,105 @@ __global__ __launch_bounds__(256) void cumsum_cols_kernel(const T* __restrict__ 
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = n[i];
     }
+    if (!FINAL) {
+      out[tile_stage_pos(t, 8, reverse) * cols + c] = v[7];
+      continue;
+    }
+    const int last = t < ntiles - 1 ? 7 : 8;  // row 7 of a tile with a successor is already final
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int64_t q = t * 8 + i;
       const int64_t rr = reverse ? prows - 1 - q : q;
-      if (rr < rows) out[rr * cols + c] = t == 0 ? v[i] : add_in_order(v[i], run);
+      if (rr < rows && i < last) out[rr * cols + c] = t == 0 ? v[i] : add_in_order(v[i], cy);
     }
-    run = t == 0 ? v[7] : add_in_order(run, v[7]);
+  }
+}
+
+// Sequential carries over staged tile totals: for tiles t = 1 .. ntot - 1 of
+// each line, F[t] = add(total[t], F[t - 1]) (F[0] = total[0]), total[t] read
+// from out[line * lstride + tile_stage_pos(t) * step] and F[t] stored at
+// out[line * lstride + tile_last_pos(t) * step].  A workgroup takes `gl`
+// lines (a power of two <= 64); all its threads stage a block of totals into
+// LDS (16 loads in flight per thread; line_major: consecutive threads on
+// consecutive tiles of a line, else on consecutive lines), lane j of wave 0
+// chains line j from LDS (line-major rows, 16-byte reads and writes, 32 adds
+// per stretch with no branch: one dependent add per tile), and all threads
+// store the block's final values.
+constexpr int kChainNT = 256;
+constexpr int kChainBuf = 16384;  // LDS words (64 KiB for 4-byte T)
+constexpr int kChainRun = 32;     // tiles per branch-free stretch of the chain
+
+// add(v, chain_identity) == v bit for bit (-0.0 + -0.0 = -0.0, +0.0 + -0.0 = +0.0)
+template <typename T>
+__device__ __forceinline__ T chain_identity() { return (T)0; }
+template <>
+__device__ __forceinline__ float chain_identity<float>() { return -0.0f; }
+
+template <typename T>
+__global__ __launch_bounds__(kChainNT) void cumsum_chain_kernel(T* __restrict__ out, int64_t nlines, int64_t lstride,
+                                                                int64_t step, int ts, int64_t plen, int reverse,
+                                                                int64_t ntot, int gl, int line_major) {
+  static_assert(sizeof(T) == 4, "4-byte totals");
+  __shared__ __align__(16) T buf[kChainBuf];  // buf[line * rs + t]
+  const int64_t L0 = (int64_t)blockIdx.x * gl;
+  const int tb = kChainBuf / gl - kChainRun;  // tiles per block, a multiple of kChainRun
+  const int rs = tb + 4;                       // LDS row stride (16-byte aligned, staggered banks)
+  const int j0 = threadIdx.x;
+  constexpr int kLoadBatch = 16;  // loads in flight per thread
+  T acc = chain_identity<T>();
+  for (int64_t t0 = 0; t0 < ntot; t0 += tb) {
+    const int nb = (int)(ntot - t0 < tb ? ntot - t0 : tb);
+    const int n = nb * gl;
+    for (int jb = 0; jb < n; jb += kChainNT * kLoadBatch) {
+      T v[kLoadBatch];
+#pragma unroll
+      for (int u = 0; u < kLoadBatch; ++u) {
+        const int j = jb + u * kChainNT + j0;
+        const int ll = line_major ? j / nb : (j & (gl - 1));
+        const int ti = line_major ? j - ll * nb : j / gl;
+        const int64_t line = L0 + ll;
+        v[u] = (j < n && line < nlines) ? out[line * lstride + tile_stage_pos(t0 + ti, ts, reverse) * step] : (T)0;
+      }
+#pragma unroll
+      for (int u = 0; u < kLoadBatch; ++u) {
+        const int j = jb + u * kChainNT + j0;
+        const int ll = line_major ? j / nb : (j & (gl - 1));
+        const int ti = line_major ? j - ll * nb : j / gl;
+        if (j < n) buf[ll * rs + ti] = v[u];
+      }
+    }
+    __syncthreads();
+    if (j0 < gl) {
+      // stretches past nb read and rewrite LDS words that are never stored
+      // to memory; acc is then spent (only the last block is partial)
+      uint4* row = (uint4*)(buf + j0 * rs);
+      for (int i0 = 0; i0 < nb; i0 += kChainRun) {
+        uint4 q[kChainRun / 4];
+#pragma unroll
+        for (int u = 0; u < kChainRun / 4; ++u) q[u] = row[i0 / 4 + u];
+#pragma unroll
+        for (int u = 0; u < kChainRun / 4; ++u) {
+          acc = add_in_order(__builtin_bit_cast(T, q[u].x), acc);
+          q[u].x = __builtin_bit_cast(uint32_t, acc);
+          acc = add_in_order(__builtin_bit_cast(T, q[u].y), acc);
+          q[u].y = __builtin_bit_cast(uint32_t, acc);
+          acc = add_in_order(__builtin_bit_cast(T, q[u].z), acc);
+          q[u].z = __builtin_bit_cast(uint32_t, acc);
+          acc = add_in_order(__builtin_bit_cast(T, q[u].w), acc);
+          q[u].w = __builtin_bit_cast(uint32_t, acc);
+        }
+#pragma unroll
+        for (int u = 0; u < kChainRun / 4; ++u) row[i0 / 4 + u] = q[u];
+      }
+    }
+    __syncthreads();
+    for (int j = j0; j < n; j += kChainNT) {
+      const int ll = line_major ? j / nb : (j & (gl - 1));
+      const int ti = line_major ? j - ll * nb : j / gl;
+      const int64_t line = L0 + ll;
+      if (line < nlines) out[line * lstride + tile_last_pos(t0 + ti, ts, plen, reverse) * step] = buf[ll * rs + ti];
+    }
+    __syncthreads();
   }
 }
 
@@ -245,6 +445,55 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(uint8_t* out, int64_t n)
 static unsigned grid_for(int64_t total) {
   int64_t b = (total + 255) / 256;
   return (unsigned)(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+
+// One workgroup per row pays off for >= 256 rows of >= 64 tiles (measured on
+// f32: [256, 128256] 84 us against 114 us in three launches, [512, 32768]
+// 46 against 63, [2048, 8192] 50 against 62); fewer rows leave CUs idle and
+// shorter rows leave its waves idle ([4096, 4096] 83 against 63 us,
+// [1024, 2048] 21.3 against 18.8), so those take the three launches.
+constexpr int64_t kRowKernelMinRows = 256;
+constexpr int64_t kRowKernelMinTiles = 64;
+
+// cumsum as tile totals -> sequential chain over them -> rescan plus carry
+// (one launch when every line is a single tile).
+template <typename T>
+static void cumsum_three_launch(const T* x, int64_t rows, int64_t cols, int axis, int reverse, T* out,
+                                hipStream_t stream) {
+  const int ts = axis == 1 ? 128 : 8;
+  const int64_t len = axis == 1 ? cols : rows;
+  const int64_t nlines = axis == 1 ? rows : cols;
+  const int64_t ntiles = (len + ts - 1) / ts;
+  auto tile_grid = [&](int64_t per_line) -> unsigned {
+    const int64_t tasks = per_line * nlines;
+    const int64_t per_block = axis == 1 ? (int64_t)kTileWaves * kTilesPerWave : 256;
+    const int64_t b = (tasks + per_block - 1) / per_block;
+    return (unsigned)(b > 2147483647 ? 2147483647 : b);
+  };
+  const unsigned tile_nt = axis == 1 ? kTileWaves * kWave : 256;
+  if (ntiles > 1) {
+    if (axis == 1)
+      hipLaunchKernelGGL((cumsum_row_tiles_kernel<T, false>), dim3(tile_grid(ntiles - 1)), dim3(tile_nt), 0, stream,
+                         x, rows, cols, ntiles, reverse, out);
+    else
+      hipLaunchKernelGGL((cumsum_col_tiles_kernel<T, false>), dim3(tile_grid(ntiles - 1)), dim3(tile_nt), 0, stream,
+                         x, rows, cols, ntiles, reverse, out);
+    // lines per chain workgroup: enough workgroups to spread the loads, the
+    // lanes of wave 0 chaining their lines side by side
+    int gl = 1;
+    while (gl < 64 && nlines / (gl * 2) >= 256) gl *= 2;
+    const int64_t cgrid = (nlines + gl - 1) / gl;
+    hipLaunchKernelGGL(cumsum_chain_kernel<T>, dim3((unsigned)cgrid), dim3(kChainNT), 0, stream, out, nlines,
+                       axis == 1 ? cols : (int64_t)1, axis == 1 ? (int64_t)1 : cols, ts, ntiles * ts, reverse,
+                       ntiles - 1, gl, axis == 1 ? 1 : 0);
+  }
+  if (axis == 1)
+    hipLaunchKernelGGL((cumsum_row_tiles_kernel<T, true>), dim3(tile_grid(ntiles)), dim3(tile_nt), 0, stream, x,
+                       rows, cols, ntiles, reverse, out);
+  else
+    hipLaunchKernelGGL((cumsum_col_tiles_kernel<T, true>), dim3(tile_grid(ntiles)), dim3(tile_nt), 0, stream, x,
+                       rows, cols, ntiles, reverse, out);
 }
 
 }  // namespace tx
@@ -313,22 +562,31 @@ int tallax_cumsum(const void* x, int dtype, int64_t rows, int64_t cols, int axis
   if (axis != 0 && axis != 1) { set_error("axis must be 0 or 1, got %d", axis); return kInvalidArgument; }
   if (rows < 0 || cols < 0) { set_error("negative extent"); return kInvalidArgument; }
   if (rows == 0 || cols == 0) return kOk;
+  {
+    const uintptr_t xb = (uintptr_t)x, ob = (uintptr_t)out, nb = (uintptr_t)(rows * cols) * 4u;
+    if (xb < ob + nb && ob < xb + nb) {
+      set_error("cumsum out must not overlap x (tile totals are staged in out)");
+      return kInvalidArgument;
+    }
+  }
   if (axis == 1) {
-    if (rows > 2147483647) { set_error("too many rows"); return kUnsupported; }
-    if (dtype == kF32)
-      hipLaunchKernelGGL(cumsum_rows_kernel<float>, dim3((unsigned)rows), dim3(kScanNT), 0, stream,
-                         (const float*)x, cols, reverse, (float*)out);
-    else
-      hipLaunchKernelGGL(cumsum_rows_kernel<int32_t>, dim3((unsigned)rows), dim3(kScanNT), 0, stream,
-                         (const int32_t*)x, cols, reverse, (int32_t*)out);
+    const int64_t ntiles = (cols + 127) / 128;
+    if (rows >= kRowKernelMinRows && ntiles >= kRowKernelMinTiles && rows <= 2147483647) {
+      if (dtype == kF32)
+        hipLaunchKernelGGL(cumsum_rows_kernel<float>, dim3((unsigned)rows), dim3(kScanNT), 0, stream,
+                           (const float*)x, cols, reverse, (float*)out);
+      else
+        hipLaunchKernelGGL(cumsum_rows_kernel<int32_t>, dim3((unsigned)rows), dim3(kScanNT), 0, stream,
+                           (const int32_t*)x, cols, reverse, (int32_t*)out);
+    } else if (dtype == kF32) {
+      cumsum_three_launch<float>((const float*)x, rows, cols, 1, reverse, (float*)out, stream);
+    } else {
+      cumsum_three_launch<int32_t>((const int32_t*)x, rows, cols, 1, reverse, (int32_t*)out, stream);
+    }
+  } else if (dtype == kF32) {
+    cumsum_three_launch<float>((const float*)x, rows, cols, 0, reverse, (float*)out, stream);
   } else {
-    const unsigned blocks = (unsigned)((cols + 255) / 256);
-    if (dtype == kF32)
-      hipLaunchKernelGGL(cumsum_cols_kernel<float>, dim3(blocks), dim3(256), 0, stream, (const float*)x, rows,
-                         cols, reverse, (float*)out);
-    else
-      hipLaunchKernelGGL(cumsum_cols_kernel<int32_t>, dim3(blocks), dim3(256), 0, stream, (const int32_t*)x,
-                         rows, cols, reverse, (int32_t*)out);
+    cumsum_three_launch<int32_t>((const int32_t*)x, rows, cols, 0, reverse, (int32_t*)out, stream);
   }
   return launch_status("tallax_cumsum");
 }

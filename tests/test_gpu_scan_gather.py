@@ -91,7 +91,36 @@ def test_cumsum_parity_f32(gpu, shape, axis, reverse):
     assert np.all(np.abs(g - r64) <= 1e-5 * scale)
 
 
-@pytest.mark.parametrize("shape", [(64, 5000), (300, 9), (4, 128)])
+# Each launch route of tallax_cumsum: one workgroup per row (>= 256 rows of
+# >= 64 tiles; 65 and 71 tiles leave a partial chunk of 64), and the three
+# launches (tile totals -> chain -> rescan) with one line per chain workgroup,
+# several lines per workgroup (gl 2 and 4, the last group partial), and
+# chains longer than one staged block of totals.
+ROUTES = [((256, 9000), 1), ((300, 8320), 1), ((255, 9000), 1), ((256, 1500), 1), ((1101, 1900), 1),
+          ((1, 2200000), 1), ((140000, 2), 0), ((66000, 513), 0), ((5, 7), 0), ((9, 1), 0)]
+
+
+@pytest.mark.parametrize("shape,axis", ROUTES)
+@pytest.mark.parametrize("reverse", [False, True])
+def test_cumsum_parity_routes(gpu, shape, axis, reverse):
+    from tallax_amd import tax
+    _log(f"cumsum route {shape} axis={axis} reverse={reverse}")
+    rng = np.random.default_rng(shape[0] * 7 + shape[1] + axis)
+    x = rng.standard_normal(shape).astype(np.float32)
+    x.flat[::89] = -0.0
+    got = tax.cumsum(torch.from_numpy(x).to(gpu), axis, reverse=reverse).cpu().numpy()
+    assert np.array_equal(bits(got), bits(O.cumsum(x, axis, reverse)))
+
+
+def test_cumsum_rejects_overlap(gpu):
+    from tallax_amd import _lib
+    x = torch.zeros((4, 300), device=gpu)
+    rc = _lib.LIB.tallax_cumsum(x.data_ptr(), _lib.F32, 4, 300, 1, 0, x.data_ptr() + 512,
+                                _lib.stream_of(x))
+    assert rc != 0 and b"overlap" in _lib.LIB.tallax_last_error()
+
+
+@pytest.mark.parametrize("shape", [(64, 5000), (300, 9), (4, 128), (256, 9000), (40000, 3)])
 @pytest.mark.parametrize("axis", [0, 1])
 @pytest.mark.parametrize("reverse", [False, True])
 def test_cumsum_int32_exact(gpu, shape, axis, reverse):
