@@ -34,6 +34,13 @@ namespace tx {
 // index loads (kGatherBatch blocks of each) before waiting for any of them.
 constexpr int kGatherNT = 256;
 constexpr int kGatherBatch = 4;
+// Value rows staged in LDS: up to 64 KiB, or 80 KiB (two workgroups per CU)
+// from 512 rows.  Longer rows gather in XCD-ordered chunks instead (measured,
+// f32: [64, 40960] 12.6 against 24.9 us staged, [256, 32768] 33.4 against
+// 38.7, [256, 40960] 42.4 against 48.6; [512, 20000] 29.9 staged against 40.9).
+constexpr int64_t kGatherLdsMax = 64 * 1024;
+constexpr int64_t kGatherLdsMaxMany = 80 * 1024;
+constexpr int64_t kGatherManyRows = 512;
 template <typename T>
 __global__ __launch_bounds__(kGatherNT) void gather_row_lds_kernel(const T* __restrict__ val, int64_t vcols,
                                                                    const int32_t* __restrict__ idx,
@@ -104,6 +111,45 @@ __global__ __launch_bounds__(kGatherNT) void gather_row_lds_kernel(const T* __re
   for (int64_t j = t; j < icols; j += kGatherNT) {
     const int32_t i = ir[j];
     orow[j] = (i >= 0 && (int64_t)i < vcols) ? row_vals[i] : (T)0;
+  }
+}
+
+// axis 1, rows longer than LDS: workgroup b runs on XCD b % 8 (dispatch
+// order), and the workgroups of one XCD take the chunks of rows xcd, xcd + 8,
+// ... one row after another, so the rows an XCD gathers from at a time stay
+// in its own L2 (about 64 chunks per row keep ~4 rows of 0.5 MiB in flight
+// per XCD).  Each thread issues kXcdBatch index loads, then the value loads
+// they address, then the stores.
+constexpr int kXcdBatch = 8;
+template <typename T>
+__global__ __launch_bounds__(256) void gather_row_xcd_kernel(const T* __restrict__ val, int64_t vcols,
+                                                             const int32_t* __restrict__ idx, int64_t icols,
+                                                             int64_t rows, int64_t chunks, T* __restrict__ out) {
+  const int64_t b = blockIdx.x;
+  const int64_t xcd = b % 8, i = b / 8;
+  const int64_t r = xcd + 8 * (i / chunks);
+  if (r >= rows) return;
+  const int64_t ch = i % chunks;
+  const int64_t per = (icols + chunks - 1) / chunks;
+  const int64_t c0 = ch * per, c1 = c0 + per < icols ? c0 + per : icols;
+  const T* vr = val + r * vcols;
+  const int32_t* ir = idx + r * icols;
+  T* orow = out + r * icols;
+  for (int64_t j0 = c0 + threadIdx.x; j0 < c1; j0 += (int64_t)256 * kXcdBatch) {
+    int32_t q[kXcdBatch];
+#pragma unroll
+    for (int u = 0; u < kXcdBatch; ++u) {
+      const int64_t j = j0 + (int64_t)u * 256;
+      q[u] = j < c1 ? ir[j] : -1;
+    }
+    T v[kXcdBatch];
+#pragma unroll
+    for (int u = 0; u < kXcdBatch; ++u) v[u] = (q[u] >= 0 && (int64_t)q[u] < vcols) ? vr[q[u]] : (T)0;
+#pragma unroll
+    for (int u = 0; u < kXcdBatch; ++u) {
+      const int64_t j = j0 + (int64_t)u * 256;
+      if (j < c1) orow[j] = v[u];
+    }
   }
 }
 
@@ -526,14 +572,33 @@ int tallax_take_along_axis(const void* values, int dtype, int64_t vrows, int64_t
                          total * es);
       return launch_status("tallax_take_along_axis");
     }
-    if (vcols * es <= 64 * 1024 && irows <= 2147483647) {
+    const int64_t lds_max = irows >= kGatherManyRows ? kGatherLdsMaxMany : kGatherLdsMax;
+    if (vcols * es <= lds_max && irows <= 2147483647) {
       const size_t lds = (size_t)vcols * es;
+      const void* kern = es == 2 ? (const void*)gather_row_lds_kernel<uint16_t> : (const void*)gather_row_lds_kernel<uint32_t>;
+      if (lds > 64 * 1024) {
+        const hipError_t attr = set_dynamic_lds_limit(kern, (int)lds, stream);
+        if (attr != hipSuccess) {
+          set_error("hipFuncSetAttribute: %s", hipGetErrorString(attr));
+          return kHipError;
+        }
+      }
       if (es == 2)
         hipLaunchKernelGGL(gather_row_lds_kernel<uint16_t>, dim3((unsigned)irows), dim3(kGatherNT), lds, stream,
                            (const uint16_t*)values, vcols, indices, icols, (uint16_t*)out);
       else
         hipLaunchKernelGGL(gather_row_lds_kernel<uint32_t>, dim3((unsigned)irows), dim3(kGatherNT), lds, stream,
                            (const uint32_t*)values, vcols, indices, icols, (uint32_t*)out);
+    } else if (irows * 64 <= 2147483647 / 8 && icols >= 64 * 256) {
+      // chunks of >= 256 outputs, ~64 per row
+      const int64_t chunks = 64;
+      const unsigned grid = (unsigned)(8 * ((irows + 7) / 8) * chunks);
+      if (es == 2)
+        hipLaunchKernelGGL(gather_row_xcd_kernel<uint16_t>, dim3(grid), dim3(256), 0, stream, (const uint16_t*)values,
+                           vcols, indices, icols, irows, chunks, (uint16_t*)out);
+      else
+        hipLaunchKernelGGL(gather_row_xcd_kernel<uint32_t>, dim3(grid), dim3(256), 0, stream, (const uint32_t*)values,
+                           vcols, indices, icols, irows, chunks, (uint32_t*)out);
     } else if (es == 2) {
       hipLaunchKernelGGL(gather_row_kernel<uint16_t>, dim3(grid_for(total)), dim3(256), 0, stream,
                          (const uint16_t*)values, vcols, indices, icols, total, (uint16_t*)out);

@@ -20,6 +20,10 @@ def _log(msg):
 @pytest.mark.parametrize("shape_v,shape_i,axis", [
     ((256, 4096), (256, 4096), 1),      # config 2's gather (values staged in LDS)
     ((16, 40000), (16, 300), 1),        # long rows: direct global gather
+    ((512, 20480), (512, 700), 1),      # f32 rows of exactly 80 KiB staged in LDS (>= 512 rows)
+    ((8, 40960), (8, 40960), 1),        # rows beyond LDS: XCD-ordered chunks
+    ((9, 70000), (9, 20000), 1),        # XCD-ordered chunks, 9 rows (two XCD rounds)
+    ((3, 100003), (3, 16384), 1),       # XCD chunks at the smallest index row it takes
     ((7, 130), (7, 50), 1),             # ragged
     ((1000, 33), (200, 33), 0),         # axis 0
     ((5, 1), (5, 9), 1),
