@@ -56,7 +56,7 @@ def _run_all(b):
     out["gather"] = tumpy.take_along_axis(b["sort_x"], out["sort_p"], 1)
     out["pf"] = prefill.softmax_topk_cumsum(b["pf_x"], k=256, p=0.9)
     out["cumsum"] = tax.cumsum(b["cs_x"], axis=1)
-    st, out["noalloc"] = _noalloc(b, b["na_x"])   # [64, 200000] bf16: segmented, uses the static scratch
+    st, out["noalloc"] = _noalloc(b, b["na_x"])   # [64, 200000] bf16: two whole-row parts per row, lists in the static scratch
     assert st == 0
     return out
 

@@ -99,9 +99,12 @@ def test_cumsum_parity_f32(gpu, shape, axis, reverse):
 # >= 64 tiles; 65 and 71 tiles leave a partial chunk of 64), and the three
 # launches (tile totals -> chain -> rescan) with one line per chain workgroup,
 # several lines per workgroup (gl 2 and 4, the last group partial), and
-# chains longer than one staged block of totals.
+# chains longer than one staged block of totals; and one thread per row for
+# rows of at most 16 elements (17 to 65 take a wave per tile).
 ROUTES = [((256, 9000), 1), ((300, 8320), 1), ((255, 9000), 1), ((256, 1500), 1), ((1101, 1900), 1),
-          ((1, 2200000), 1), ((140000, 2), 0), ((66000, 513), 0), ((5, 7), 0), ((9, 1), 0)]
+          ((1, 2200000), 1), ((140000, 2), 0), ((66000, 513), 0), ((5, 7), 0), ((9, 1), 0),
+          ((100000, 16), 1), ((70001, 5), 1), ((3, 17), 1), ((30000, 64), 1), ((20000, 50), 1),
+          ((5, 65), 1)]
 
 
 @pytest.mark.parametrize("shape,axis", ROUTES)
