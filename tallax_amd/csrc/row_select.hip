@@ -46,6 +46,7 @@
 #include <mutex>
 
 #include "tallax_hip.h"
+#include "tx_block_sort.h"
 #include "tx_common.h"
 #include "tx_host.h"
 #include "tx_math.h"
@@ -715,8 +716,8 @@ void seg_select_kernel(SelArgs a) {
   __shared__ uint4 stage[kStage * NT];  // staged vectors, slot-major
   const int tid = threadIdx.x;
   const int w = tid / kWave, l = lane_id();
-  const int seg = blockIdx.x;
-  const int64_t row = blockIdx.y;
+  const int64_t row = blockIdx.x / (unsigned)a.nseg;  // one-dimensional grid: rows beyond 65535
+  const int seg = (int)(blockIdx.x - row * a.nseg);
   const int k = a.k;
   const RowParams rp = load_row_params<SAMPLE>(a, row);
 
@@ -1775,8 +1776,8 @@ static size_t ws_bytes_for(int64_t rows, const Plan& p) {
 
 template <int DT, int MAXV, int NT, bool SAMPLE>
 static void launch_a(const SelArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((seg_select_kernel<DT, MAXV, NT, SAMPLE>), dim3((unsigned)a.nseg, (unsigned)a.rows),
-                     dim3(NT), 0, s, a);
+  hipLaunchKernelGGL((seg_select_kernel<DT, MAXV, NT, SAMPLE>), dim3((unsigned)(a.nseg * a.rows)), dim3(NT), 0, s,
+                     a);
 }
 
 template <int DT, bool SAMPLE>
@@ -1906,11 +1907,123 @@ int launch_segment_lists(const void* x, int dt, int64_t rows, int64_t cols, int 
   return launch_status("segment lists");
 }
 
+// ---------------------------------------------------------------------------
+// Short rows (at most 256 elements): every row sorted whole.  A 1024-thread
+// workgroup per row spends its setup on a handful of elements ([65536, 128]
+// f32, k = 8: 1444 us that way; a router-sized top-k).  Records order the
+// output ascending: (~select key) << 32 | column, the select key ordering
+// values as the reference's strict `>` admits them (top_k.py:64: -0 == +0,
+// NaN below -inf), ties by lowest column; padding records (all ones) go last.
+// Values at or below finfo(dtype).min, and NaNs, come out as finfo.min.
+//   * rows of at most 32: one thread per row, a register bitonic network;
+//   * rows of at most 256: one wave per row, block_bitonic_sort_c over P =
+//     64, 128 or 256 slots (E = P / 64 records per lane).
+// ---------------------------------------------------------------------------
+constexpr int kTopkShortCols = 256;
+
+__device__ __forceinline__ uint32_t topk_select_key(uint32_t b) {  // b: float32 bits
+  const uint32_t a = b & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return 1u;
+  if (a == 0u) return 0x80000000u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t topk_f32_bits(const void* x, int64_t i) {
+  return DT == kBF16 ? (uint32_t)((const uint16_t*)x)[i] << 16 : ((const uint32_t*)x)[i];
+}
+
+template <int DT>
+__device__ __forceinline__ void topk_short_out(uint64_t rec, const void* x, int64_t base, int64_t o, void* out_vals,
+                                               int32_t* out_idx) {
+  const uint32_t col = (uint32_t)rec;
+  uint32_t b = topk_f32_bits<DT>(x, base + col);
+  const uint32_t kmin = topk_select_key(DT == kBF16 ? 0xFF7F0000u : 0xFF7FFFFFu);
+  if (topk_select_key(b) <= kmin) b = DT == kBF16 ? 0xFF7F0000u : 0xFF7FFFFFu;
+  out_idx[o] = (int32_t)col;
+  if (DT == kBF16) ((uint16_t*)out_vals)[o] = (uint16_t)(b >> 16);
+  else ((uint32_t*)out_vals)[o] = b;
+}
+
+template <int DT, int NC>
+__global__ __launch_bounds__(256) void topk_short_thread_kernel(const void* __restrict__ x, int64_t rows, int cols,
+                                                                int k, void* out_vals, int32_t* out_idx) {
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const int64_t base = row * cols;
+  uint64_t v[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i)
+    v[i] = i < cols ? ((uint64_t)~topk_select_key(topk_f32_bits<DT>(x, base + i)) << 32) | (uint32_t)i : ~0ull;
+#pragma unroll
+  for (int kk = 2; kk <= NC; kk <<= 1) {
+#pragma unroll
+    for (int j = kk >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int o = i ^ j;
+        if (o > i) {
+          const uint64_t a = v[i], b = v[o];
+          const bool sw = (i & kk) == 0 ? a > b : a < b;
+          v[i] = sw ? b : a;
+          v[o] = sw ? a : b;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NC; ++i)
+    if (i < k) topk_short_out<DT>(v[i], x, base, row * k + i, out_vals, out_idx);
+}
+
+template <int DT, int P>
+__global__ __launch_bounds__(kWave) void topk_short_wave_kernel(const void* __restrict__ x, int cols, int k,
+                                                                void* out_vals, int32_t* out_idx) {
+  constexpr int E = P / kWave;
+  __shared__ uint64_t lds[P];
+  const int64_t row = blockIdx.x;
+  const int64_t base = row * cols;
+  const int t = threadIdx.x;
+  uint64_t v[E];
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int i = t * E + r;
+    v[r] = i < cols ? ((uint64_t)~topk_select_key(topk_f32_bits<DT>(x, base + i)) << 32) | (uint32_t)i : ~0ull;
+  }
+  block_bitonic_sort_c<uint64_t, E, P, false>(v, lds);
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const int i = t * E + r;
+    if (i < k) topk_short_out<DT>(v[r], x, base, row * k + i, out_vals, out_idx);
+  }
+}
+
+template <int DT>
+static int launch_topk_short(const void* x, int64_t rows, int64_t cols, int k, void* out_vals, int32_t* out_idx,
+                             hipStream_t s) {
+  const int c = (int)cols;
+  if (cols <= 32) {
+    const unsigned grid = (unsigned)((rows + 255) / 256);
+    if (cols <= 16)
+      hipLaunchKernelGGL((topk_short_thread_kernel<DT, 16>), dim3(grid), dim3(256), 0, s, x, rows, c, k, out_vals, out_idx);
+    else
+      hipLaunchKernelGGL((topk_short_thread_kernel<DT, 32>), dim3(grid), dim3(256), 0, s, x, rows, c, k, out_vals, out_idx);
+  } else if (cols <= 64) {
+    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 64>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, out_vals, out_idx);
+  } else if (cols <= 128) {
+    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 128>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, out_vals, out_idx);
+  } else {
+    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 256>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, out_vals, out_idx);
+  }
+  return launch_status("tallax_topk (short rows)");
+}
+
 static int check_common(const void* x, int dt, int64_t rows, int64_t cols) {
   if (!x) { set_error("null input pointer"); return kInvalidArgument; }
   if (dt != kF32 && dt != kBF16) { set_error("dtype %d not supported (f32=0, bf16=1)", dt); return kUnsupported; }
   if (rows < 0 || cols <= 0) { set_error("bad shape [%lld, %lld]", (long long)rows, (long long)cols); return kInvalidArgument; }
-  if (rows > 65535) { set_error("rows %lld exceeds grid limit 65535", (long long)rows); return kUnsupported; }
+  // workgroups per launch: rows x segments (at most 64) stay within the grid's 2^31 - 1
+  if (rows > ((int64_t)1 << 31) / 64 - 1) { set_error("rows %lld exceed the grid limit", (long long)rows); return kUnsupported; }
   if (cols >= (int64_t)1 << 31) { set_error("cols must fit int32 indices"); return kInvalidArgument; }
   return kOk;
 }
@@ -1993,6 +2106,9 @@ int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k,
   if (rows == 0) return kOk;
   if (dtype == kI32)
     return topk_i32(x, rows, cols, k, nullptr, 0.0, out_vals, out_idx, workspace, workspace_bytes, stream, "tallax_topk");
+  if (cols <= kTopkShortCols)
+    return dtype == kF32 ? launch_topk_short<kF32>(x, rows, cols, (int)k, out_vals, out_idx, stream)
+                         : launch_topk_short<kBF16>(x, rows, cols, (int)k, out_vals, out_idx, stream);
   Plan p;
   st = plan_rows(rows, cols, dtype, &p);
   if (st) return st;

@@ -14,8 +14,10 @@
 //     non-stable descending argsort orders ties by descending index (the
 //     packed key makes the order unique, utils.py:205-216).
 //
-// One workgroup sorts one row.  Three kernels, by row length:
-//   * rows of at most 512 elements: records (transformed key, tie value) are
+// Four kernels, by row length:
+//   * rows of at most 32 elements: one thread per row, a register bitonic
+//     network over the same records (sort_narrow_rows_kernel);
+//   * one workgroup per row from here on.  Rows of at most 512 elements: records (transformed key, tie value) are
 //     padded to P = 2^m >= cols with the largest record and sorted ascending
 //     by a bitonic network (sort_rows_kernel, P / 4 threads).  Each thread
 //     holds E consecutive records in registers; strides < E are exchanged
@@ -45,6 +47,7 @@
 namespace tx {
 
 constexpr int kSortMaxCols = 16384;
+constexpr int kSortNarrowCols = 32;  // rows sorted by one thread each
 
 template <typename R>
 struct RecT;
@@ -236,6 +239,83 @@ __global__ __launch_bounds__(kRadixNT) void radix_sort_rows_kernel(SortArgs a) {
   }
 }
 
+// Rows of at most NC (16 or 32) elements: one thread per row, the row's
+// records sorted in registers by a bitonic network (ascending records; the
+// padding records, all ones, go last), then the same outputs as
+// sort_rows_kernel.  A wave per row would spend 256 padded slots on 8
+// elements ([1000000, 8] f32 argsort: 1154 us that way).
+template <typename R, int NC>
+__global__ __launch_bounds__(256) void sort_narrow_rows_kernel(SortArgs a, int64_t rows) {
+  using RT = RecT<R>;
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  const int64_t base = row * a.cols;
+  const int cols = (int)a.cols;
+  const uint32_t tie_mask = RT::kTieBits == 32 ? 0x7FFFFFFFu : 0xFFFFu;
+  R v[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    if (i < cols) {
+      const int64_t src = a.perm_in ? (int64_t)a.perm_in[base + i] : (int64_t)i;
+      uint32_t k = sort_order_bits(a.key, a.key_dtype, base + src);
+      if (a.descending) k = ~k;
+      const uint32_t tie = a.ties_desc ? (tie_mask - (uint32_t)i) : (uint32_t)i;
+      v[i] = RT::make(k, tie);
+    } else {
+      v[i] = ~(R)0;
+    }
+  }
+#pragma unroll
+  for (int k = 2; k <= NC; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int o = i ^ j;
+        if (o > i) {
+          const R x = v[i], y = v[o];
+          const bool up = (i & k) == 0;  // this block ascends
+          const bool sw = up ? x > y : x < y;
+          v[i] = sw ? y : x;
+          v[o] = sw ? x : y;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    if (i >= cols) continue;
+    const uint32_t tie = RT::tie(v[i]);
+    const int pos = a.ties_desc ? (int)(tie_mask - tie) : (int)tie;
+    const int32_t src = a.perm_in ? a.perm_in[base + pos] : pos;
+    a.perm_out[base + i] = src;
+    if (a.key_out) {
+      uint32_t k = RT::key(v[i]);
+      if (a.descending) k = ~k;
+      if (sizeof(R) == 4) {  // rebuild the full order bits of a bf16 key from its high half
+        k &= 0xFFFF0000u;
+        if (k < 0x80000000u) k |= 0xFFFFu;
+        else if (k > 0xFF800000u) k = 0xFFFFFFFEu;
+      }
+      store_sorted(a.key_out, a.key_out_dtype, a.key_dtype, base + i, k);
+    }
+    if (a.aux_out) {
+      const uint32_t u = sort_order_bits(a.aux, a.aux_dtype, base + src);
+      store_sorted(a.aux_out, a.aux_out_dtype, a.aux_dtype, base + i, u);
+    }
+  }
+}
+
+template <typename R>
+static int launch_sort_narrow(const SortArgs& a, int64_t rows, hipStream_t s) {
+  const unsigned grid = (unsigned)((rows + 255) / 256);
+  if (a.cols <= 16)
+    hipLaunchKernelGGL((sort_narrow_rows_kernel<R, 16>), dim3(grid), dim3(256), 0, s, a, rows);
+  else
+    hipLaunchKernelGGL((sort_narrow_rows_kernel<R, 32>), dim3(grid), dim3(256), 0, s, a, rows);
+  return kOk;
+}
+
 static int launch_radix8(const SortArgs& a, int64_t rows, hipStream_t s) {
   hipLaunchKernelGGL((radix_sort_rows_kernel<8>), dim3((unsigned)rows), dim3(kRadixNT), 0, s, a);
   return kOk;
@@ -306,6 +386,8 @@ int tallax_sort_rows_ws(const void* key, int key_dtype, int64_t rows, int64_t co
   int st;
   if (narrow && rows <= 256 && cols > 2048 && cols <= 4 * kRadixNT)
     st = launch_radix8(a, rows, stream);
+  else if (cols <= kSortNarrowCols)
+    st = narrow ? launch_sort_narrow<uint32_t>(a, rows, stream) : launch_sort_narrow<uint64_t>(a, rows, stream);
   else if (cols <= 512)
     st = narrow ? launch_sort_p<uint32_t>(a, rows, stream) : launch_sort_p<uint64_t>(a, rows, stream);
   else

@@ -230,6 +230,44 @@ def test_topk_parity(gpu, rows, cols, k, dtype, kind):
     assert np.array_equal(bits(gv), bits(ov))
 
 
+@pytest.mark.parametrize("rows,cols,k", [(1000, 1, 1), (1000, 7, 3), (5000, 16, 16), (3000, 17, 2), (5000, 32, 8),
+                                         (3000, 33, 5), (2000, 64, 64), (2000, 100, 8), (700, 128, 128),
+                                         (700, 129, 1), (500, 256, 100), (66000, 64, 2)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_topk_short_rows(gpu, rows, cols, k, dtype):
+    """Rows of at most 256 elements (one thread or one wave per row): heavy
+    ties, signed zeros, NaNs, +-inf and finfo.min, against the oracle."""
+    from tallax_amd import tax
+    _log(f"top_k short rows={rows} cols={cols} k={k} {dtype}")
+    rng = np.random.default_rng(rows * 31 + cols + k)
+    x = np.round(rng.standard_normal((rows, cols)) * 2).astype(np.float32) / 2
+    fmin = np.float32(-3.3895314e38) if dtype == "bf16" else np.finfo(np.float32).min
+    special = np.array([np.nan, -0.0, 0.0, np.inf, -np.inf, fmin, -np.nan], np.float32)
+    mask = rng.random((rows, cols)) < 0.15
+    x[mask] = rng.choice(special, int(mask.sum()))
+    x[::11] = np.nan                      # rows with nothing admissible
+    xv = host_values(x, dtype)
+    vals, idx = tax.top_k(to_dev(x, dtype, gpu), k)
+    torch.cuda.synchronize()
+    ov, oi = O.top_k(xv, k, dtype)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(bits(from_dev_vals(vals)), bits(ov))
+
+
+@pytest.mark.parametrize("rows,cols,k", [(70000, 300, 8), (66000, 1024, 64)])
+def test_topk_more_rows_than_a_grid_dimension(gpu, rows, cols, k):
+    """More than 65535 rows: every launch is a one-dimensional grid."""
+    from tallax_amd import tax
+    _log(f"top_k rows={rows} cols={cols} k={k}")
+    rng = np.random.default_rng(rows + k)
+    x = np.round(rng.standard_normal((rows, cols)) * 16).astype(np.float32) / 16
+    vals, idx = tax.top_k(torch.from_numpy(x).to(gpu), k)
+    torch.cuda.synchronize()
+    ov, oi = O.top_k(x, k)
+    assert np.array_equal(idx.cpu().numpy(), oi)
+    assert np.array_equal(bits(vals.cpu().numpy()), bits(ov))
+
+
 def test_topk_config3_spikes(gpu):
     """Config 3: f32 [128, 151936], N(0, sigma=2) plus 32 spikes per row at
     exactly 8.0 (32-way ties inside the top-50), k=50."""

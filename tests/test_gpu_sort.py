@@ -74,7 +74,7 @@ def test_config2_argsort_then_gather(gpu):
     assert _same(from_dev_vals(sorted_keys), sk)
 
 
-@pytest.mark.parametrize("cols", [1, 7, 255, 256, 1000, 4096, 5000, 16384])
+@pytest.mark.parametrize("cols", [1, 7, 16, 17, 32, 255, 256, 1000, 4096, 5000, 16384])
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "i32"])
 @pytest.mark.parametrize("descending", [False, True])
 @pytest.mark.parametrize("stable,argsort", [(True, True), (False, True), (True, False), (False, False)])
@@ -104,11 +104,34 @@ def test_sort_one_key(gpu, cols, dtype, descending, stable, argsort):
         assert _same(_host(g), w)
 
 
+@pytest.mark.parametrize("shape,dtype,descending,stable", [((70001, 8), "f32", True, True),
+                                                           ((4099, 32), "bf16", True, False),
+                                                           ((1000, 13), "i32", False, True)])
+def test_sort_narrow_many_rows(gpu, shape, dtype, descending, stable):
+    """Rows of at most 32 elements, one thread per row, across many workgroups."""
+    from tallax_amd import tax
+    _log(f"narrow sort {shape} {dtype} desc={descending} stable={stable}")
+    rng = np.random.default_rng(shape[0])
+    if dtype == "i32":
+        x = rng.integers(-3, 3, shape).astype(np.int32)
+        xd, host = torch.from_numpy(x).to(gpu), x
+    else:
+        x = np.round(rng.standard_normal(shape) * 4).astype(np.float32) / 4
+        x[::97, ::3] = np.nan
+        xd, host = to_dev(x, dtype, gpu), O.round_to_dtype(x, dtype)
+    got = tax.sort(xd, num_keys=1, is_stable=stable, return_argsort=True, descending=descending)
+    torch.cuda.synchronize()
+    want, _ = O.sort([host], 1, is_stable=stable, return_argsort=True, descending=descending, dtypes=[dtype])
+    for g, w in zip(got, want):
+        assert _same(_host(g), w)
+
+
+@pytest.mark.parametrize("cols", [3000, 24])   # 24: one thread per row, with a permutation in
 @pytest.mark.parametrize("descending", [False, True])
-def test_sort_two_keys_with_payloads(gpu, descending):
+def test_sort_two_keys_with_payloads(gpu, descending, cols):
     from tallax_amd import tax
     rng = np.random.default_rng(9)
-    rows, cols = 6, 3000
+    rows = 6
     k0 = rng.integers(0, 4, (rows, cols)).astype(np.int32)
     k1 = np.round(rng.standard_normal((rows, cols)) * 2).astype(np.float32) / 2
     k1[0, ::13] = np.nan
