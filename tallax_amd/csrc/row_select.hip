@@ -1933,13 +1933,26 @@ __device__ __forceinline__ uint32_t topk_f32_bits(const void* x, int64_t i) {
   return DT == kBF16 ? (uint32_t)((const uint16_t*)x)[i] << 16 : ((const uint32_t*)x)[i];
 }
 
+// Output position i of a row: positions >= k_rows[row] (when k_rows is
+// given) keep the index and take the replacement value (float32 bits).
+struct TopkShortOut {
+  void* vals;
+  int32_t* idx;
+  const int32_t* k_rows;
+  uint32_t replace_bits;
+};
+
 template <int DT>
-__device__ __forceinline__ void topk_short_out(uint64_t rec, const void* x, int64_t base, int64_t o, void* out_vals,
-                                               int32_t* out_idx) {
+__device__ __forceinline__ void topk_short_out(uint64_t rec, const void* x, int64_t base, int64_t row, int i, int k,
+                                               const TopkShortOut& ot) {
+  const int64_t o = row * k + i;
+  void* out_vals = ot.vals;
+  int32_t* out_idx = ot.idx;
   const uint32_t col = (uint32_t)rec;
   uint32_t b = topk_f32_bits<DT>(x, base + col);
   const uint32_t kmin = topk_select_key(DT == kBF16 ? 0xFF7F0000u : 0xFF7FFFFFu);
   if (topk_select_key(b) <= kmin) b = DT == kBF16 ? 0xFF7F0000u : 0xFF7FFFFFu;
+  if (ot.k_rows && i >= ot.k_rows[row]) b = ot.replace_bits;
   out_idx[o] = (int32_t)col;
   if (DT == kBF16) ((uint16_t*)out_vals)[o] = (uint16_t)(b >> 16);
   else ((uint32_t*)out_vals)[o] = b;
@@ -1947,7 +1960,7 @@ __device__ __forceinline__ void topk_short_out(uint64_t rec, const void* x, int6
 
 template <int DT, int NC>
 __global__ __launch_bounds__(256) void topk_short_thread_kernel(const void* __restrict__ x, int64_t rows, int cols,
-                                                                int k, void* out_vals, int32_t* out_idx) {
+                                                                int k, TopkShortOut ot) {
   const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (row >= rows) return;
   const int64_t base = row * cols;
@@ -1973,12 +1986,12 @@ __global__ __launch_bounds__(256) void topk_short_thread_kernel(const void* __re
   }
 #pragma unroll
   for (int i = 0; i < NC; ++i)
-    if (i < k) topk_short_out<DT>(v[i], x, base, row * k + i, out_vals, out_idx);
+    if (i < k) topk_short_out<DT>(v[i], x, base, row, i, k, ot);
 }
 
 template <int DT, int P>
 __global__ __launch_bounds__(kWave) void topk_short_wave_kernel(const void* __restrict__ x, int cols, int k,
-                                                                void* out_vals, int32_t* out_idx) {
+                                                                TopkShortOut ot) {
   constexpr int E = P / kWave;
   __shared__ uint64_t lds[P];
   const int64_t row = blockIdx.x;
@@ -1994,28 +2007,28 @@ __global__ __launch_bounds__(kWave) void topk_short_wave_kernel(const void* __re
 #pragma unroll
   for (int r = 0; r < E; ++r) {
     const int i = t * E + r;
-    if (i < k) topk_short_out<DT>(v[r], x, base, row * k + i, out_vals, out_idx);
+    if (i < k) topk_short_out<DT>(v[r], x, base, row, i, k, ot);
   }
 }
 
 template <int DT>
-static int launch_topk_short(const void* x, int64_t rows, int64_t cols, int k, void* out_vals, int32_t* out_idx,
+static int launch_topk_short(const void* x, int64_t rows, int64_t cols, int k, const TopkShortOut& ot,
                              hipStream_t s) {
   const int c = (int)cols;
   if (cols <= 32) {
     const unsigned grid = (unsigned)((rows + 255) / 256);
     if (cols <= 16)
-      hipLaunchKernelGGL((topk_short_thread_kernel<DT, 16>), dim3(grid), dim3(256), 0, s, x, rows, c, k, out_vals, out_idx);
+      hipLaunchKernelGGL((topk_short_thread_kernel<DT, 16>), dim3(grid), dim3(256), 0, s, x, rows, c, k, ot);
     else
-      hipLaunchKernelGGL((topk_short_thread_kernel<DT, 32>), dim3(grid), dim3(256), 0, s, x, rows, c, k, out_vals, out_idx);
+      hipLaunchKernelGGL((topk_short_thread_kernel<DT, 32>), dim3(grid), dim3(256), 0, s, x, rows, c, k, ot);
   } else if (cols <= 64) {
-    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 64>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, out_vals, out_idx);
+    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 64>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, ot);
   } else if (cols <= 128) {
-    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 128>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, out_vals, out_idx);
+    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 128>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, ot);
   } else {
-    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 256>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, out_vals, out_idx);
+    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 256>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, ot);
   }
-  return launch_status("tallax_topk (short rows)");
+  return launch_status("top-k (short rows)");
 }
 
 static int check_common(const void* x, int dt, int64_t rows, int64_t cols) {
@@ -2106,9 +2119,11 @@ int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k,
   if (rows == 0) return kOk;
   if (dtype == kI32)
     return topk_i32(x, rows, cols, k, nullptr, 0.0, out_vals, out_idx, workspace, workspace_bytes, stream, "tallax_topk");
-  if (cols <= kTopkShortCols)
-    return dtype == kF32 ? launch_topk_short<kF32>(x, rows, cols, (int)k, out_vals, out_idx, stream)
-                         : launch_topk_short<kBF16>(x, rows, cols, (int)k, out_vals, out_idx, stream);
+  if (cols <= kTopkShortCols) {
+    const TopkShortOut ot = {out_vals, out_idx, nullptr, 0u};
+    return dtype == kF32 ? launch_topk_short<kF32>(x, rows, cols, (int)k, ot, stream)
+                         : launch_topk_short<kBF16>(x, rows, cols, (int)k, ot, stream);
+  }
   Plan p;
   st = plan_rows(rows, cols, dtype, &p);
   if (st) return st;
@@ -2138,6 +2153,15 @@ int tallax_topk_replace(const void* x, int dtype, int64_t rows, int64_t cols, in
   if (dtype == kI32)
     return topk_i32(x, rows, cols, k, k_rows, replace_val, out_vals, out_idx, workspace, workspace_bytes, stream,
                     "tallax_topk_replace");
+  if (cols <= kTopkShortCols) {
+    const float rf = (float)replace_val;
+    uint32_t rb;
+    const float rd = dtype == kBF16 ? round_to_bf16(rf) : rf;
+    memcpy(&rb, &rd, sizeof(rb));
+    const TopkShortOut ot = {out_vals, out_idx, k_rows, rb};
+    return dtype == kF32 ? launch_topk_short<kF32>(x, rows, cols, (int)k, ot, stream)
+                         : launch_topk_short<kBF16>(x, rows, cols, (int)k, ot, stream);
+  }
   Plan p;
   st = plan_rows(rows, cols, dtype, &p);
   if (st) return st;

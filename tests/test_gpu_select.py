@@ -284,7 +284,8 @@ def test_topk_config3_spikes(gpu):
 
 
 @pytest.mark.parametrize("rows,cols,k,dtype", [(256, 128256, 128, "bf16"), (128, 151936, 50, "f32"),
-                                               (16, 5003, 77, "bf16")])
+                                               (16, 5003, 77, "bf16"), (3000, 12, 5, "f32"), (2000, 40, 8, "bf16"),
+                                               (700, 256, 100, "f32")])   # short rows: one thread / wave per row
 def test_topk_replace_per_row_k(gpu, rows, cols, k, dtype):
     """tallax_topk_replace through the C ABI: the exact top-k whose positions
     >= k_rows[row] hold replace_val rounded to the input dtype
