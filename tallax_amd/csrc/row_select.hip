@@ -1908,18 +1908,29 @@ int launch_segment_lists(const void* x, int dt, int64_t rows, int64_t cols, int 
 }
 
 // ---------------------------------------------------------------------------
-// Short rows (at most 256 elements): every row sorted whole.  A 1024-thread
-// workgroup per row spends its setup on a handful of elements ([65536, 128]
-// f32, k = 8: 1444 us that way; a router-sized top-k).  Records order the
-// output ascending: (~select key) << 32 | column, the select key ordering
-// values as the reference's strict `>` admits them (top_k.py:64: -0 == +0,
-// NaN below -inf), ties by lowest column; padding records (all ones) go last.
-// Values at or below finfo(dtype).min, and NaNs, come out as finfo.min.
+// Short rows (at most 2048 elements): every row sorted whole.  A 1024-thread
+// select workgroup per row spends its fixed latency on a few hundred
+// elements (f32, k = 8: [65536, 128] 1444 us, [65536, 512] 1703 us,
+// [32768, 1024] 1051 us that way).  Records order the output ascending:
+// (~select key) << 32 | column, the select key ordering values as the
+// reference's strict `>` admits them (top_k.py:64: -0 == +0, NaN below -inf),
+// ties by lowest column; padding records (all ones) go last.  Values at or
+// below finfo(dtype).min, and NaNs, come out as finfo.min.
 //   * rows of at most 32: one thread per row, a register bitonic network;
-//   * rows of at most 256: one wave per row, block_bitonic_sort_c over P =
-//     64, 128 or 256 slots (E = P / 64 records per lane).
+//   * longer rows: block_bitonic_sort_c over P = 64 .. 2048 slots, E records
+//     per thread (one wave up to P = 512, then 128 and 256 threads).
 // ---------------------------------------------------------------------------
-constexpr int kTopkShortCols = 256;
+constexpr int kTopkShortCols = 2048;
+
+// Whole-row sorts pay off at any row count up to 256 elements; beyond that
+// only with many rows, where the select kernel's per-row latency adds up
+// (f32, k = 8, select -> sort: [65536, 512] 1711 -> 182 us, [32768, 1024]
+// 1056 -> 223, [16384, 2048] 332 -> 271, [4096, 2048] 81 -> 80; few rows
+// lose: [64, 1024] 10.3 -> 12.0, [256, 2048] 6.7 -> 14.8, [1024, 2048]
+// k = 64 20.9 -> 28.9).
+static bool topk_short_route(int64_t rows, int64_t cols) {
+  return cols <= 256 || (cols <= 1024 && rows >= 512) || (cols <= kTopkShortCols && rows >= 8192);
+}
 
 __device__ __forceinline__ uint32_t topk_select_key(uint32_t b) {  // b: float32 bits
   const uint32_t a = b & 0x7FFFFFFFu;
@@ -1989,10 +2000,9 @@ __global__ __launch_bounds__(256) void topk_short_thread_kernel(const void* __re
     if (i < k) topk_short_out<DT>(v[i], x, base, row, i, k, ot);
 }
 
-template <int DT, int P>
-__global__ __launch_bounds__(kWave) void topk_short_wave_kernel(const void* __restrict__ x, int cols, int k,
-                                                                TopkShortOut ot) {
-  constexpr int E = P / kWave;
+template <int DT, int P, int E>
+__global__ __launch_bounds__(P / E) void topk_short_block_kernel(const void* __restrict__ x, int cols, int k,
+                                                                 TopkShortOut ot) {
   __shared__ uint64_t lds[P];
   const int64_t row = blockIdx.x;
   const int64_t base = row * cols;
@@ -2022,11 +2032,17 @@ static int launch_topk_short(const void* x, int64_t rows, int64_t cols, int k, c
     else
       hipLaunchKernelGGL((topk_short_thread_kernel<DT, 32>), dim3(grid), dim3(256), 0, s, x, rows, c, k, ot);
   } else if (cols <= 64) {
-    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 64>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, ot);
+    hipLaunchKernelGGL((topk_short_block_kernel<DT, 64, 1>), dim3((unsigned)rows), dim3(64), 0, s, x, c, k, ot);
   } else if (cols <= 128) {
-    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 128>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, ot);
+    hipLaunchKernelGGL((topk_short_block_kernel<DT, 128, 2>), dim3((unsigned)rows), dim3(64), 0, s, x, c, k, ot);
+  } else if (cols <= 256) {
+    hipLaunchKernelGGL((topk_short_block_kernel<DT, 256, 4>), dim3((unsigned)rows), dim3(64), 0, s, x, c, k, ot);
+  } else if (cols <= 512) {
+    hipLaunchKernelGGL((topk_short_block_kernel<DT, 512, 8>), dim3((unsigned)rows), dim3(64), 0, s, x, c, k, ot);
+  } else if (cols <= 1024) {
+    hipLaunchKernelGGL((topk_short_block_kernel<DT, 1024, 8>), dim3((unsigned)rows), dim3(128), 0, s, x, c, k, ot);
   } else {
-    hipLaunchKernelGGL((topk_short_wave_kernel<DT, 256>), dim3((unsigned)rows), dim3(kWave), 0, s, x, c, k, ot);
+    hipLaunchKernelGGL((topk_short_block_kernel<DT, 2048, 8>), dim3((unsigned)rows), dim3(256), 0, s, x, c, k, ot);
   }
   return launch_status("top-k (short rows)");
 }
@@ -2119,7 +2135,7 @@ int tallax_topk(const void* x, int dtype, int64_t rows, int64_t cols, int64_t k,
   if (rows == 0) return kOk;
   if (dtype == kI32)
     return topk_i32(x, rows, cols, k, nullptr, 0.0, out_vals, out_idx, workspace, workspace_bytes, stream, "tallax_topk");
-  if (cols <= kTopkShortCols) {
+  if (topk_short_route(rows, cols)) {
     const TopkShortOut ot = {out_vals, out_idx, nullptr, 0u};
     return dtype == kF32 ? launch_topk_short<kF32>(x, rows, cols, (int)k, ot, stream)
                          : launch_topk_short<kBF16>(x, rows, cols, (int)k, ot, stream);
@@ -2153,7 +2169,7 @@ int tallax_topk_replace(const void* x, int dtype, int64_t rows, int64_t cols, in
   if (dtype == kI32)
     return topk_i32(x, rows, cols, k, k_rows, replace_val, out_vals, out_idx, workspace, workspace_bytes, stream,
                     "tallax_topk_replace");
-  if (cols <= kTopkShortCols) {
+  if (topk_short_route(rows, cols)) {
     const float rf = (float)replace_val;
     uint32_t rb;
     const float rd = dtype == kBF16 ? round_to_bf16(rf) : rf;

@@ -232,10 +232,12 @@ def test_topk_parity(gpu, rows, cols, k, dtype, kind):
 
 @pytest.mark.parametrize("rows,cols,k", [(1000, 1, 1), (1000, 7, 3), (5000, 16, 16), (3000, 17, 2), (5000, 32, 8),
                                          (3000, 33, 5), (2000, 64, 64), (2000, 100, 8), (700, 128, 128),
-                                         (700, 129, 1), (500, 256, 100), (66000, 64, 2)])
+                                         (700, 129, 1), (500, 256, 100), (66000, 64, 2), (3000, 257, 8),
+                                         (2000, 512, 128), (1000, 513, 50), (999, 1024, 64), (8192, 1500, 7),
+                                         (300, 2048, 128)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_topk_short_rows(gpu, rows, cols, k, dtype):
-    """Rows of at most 256 elements (one thread or one wave per row): heavy
+    """Short rows (one thread, one wave or one small block per row, by length and row count): heavy
     ties, signed zeros, NaNs, +-inf and finfo.min, against the oracle."""
     from tallax_amd import tax
     _log(f"top_k short rows={rows} cols={cols} k={k} {dtype}")
