@@ -10,6 +10,7 @@ maximum before exponentiating) and truncated at degree k.
 """
 from __future__ import annotations
 
+import functools
 import math
 
 import numpy as np
@@ -67,11 +68,18 @@ def calculate_depth_thresholds(k: int, num_bins: int, block_size: int = 8,
     return tuple(sorted(out))
 
 
+@functools.lru_cache(maxsize=256)
+def _auto_schedule(max_k: int, num_bins: int, block_token: int) -> tuple:
+    # computed once per shape, as the reference computes it once per trace
+    # (a few hundred microseconds of polynomial arithmetic on the host)
+    return tuple(t + 1 for t in calculate_depth_thresholds(max_k, num_bins, block_token,
+                                                           target_yields=(0.8, 0.98, 0.9999)))
+
+
 def topm_schedule(max_k: int, num_bins: int, block_token: int, schedule=None) -> tuple:
     """The depths top_dynamic_k evaluates (top_k.py:472-478), without the
     leading 0: the automatic one is the depth thresholds at yields
     (0.8, 0.98, 0.9999) plus one; user schedules are deduplicated and sorted."""
     if schedule is None:
-        schedule = tuple(t + 1 for t in calculate_depth_thresholds(max_k, num_bins, block_token,
-                                                                   target_yields=(0.8, 0.98, 0.9999)))
+        schedule = _auto_schedule(int(max_k), int(num_bins), int(block_token))
     return tuple(sorted(set(int(m) for m in schedule)))
