@@ -18,6 +18,10 @@ samples one token for each of the 256 rows.
                  take_along_axis of an f32 [256,4096] array
   prefill_c5     f32 [1024,201088] softmax -> top-2048 -> cumsum -> cutoff p=0.9
   sort_wide      tax.sort of f32 [1024,201088] probabilities, descending stable
+  topk_router    exact top-k k=8 of f32 [65536,128] (many short rows; not a
+                 BASELINE config)
+  cumsum_long    tax.cumsum of one f32 row of 4000000 (one long line; not a
+                 BASELINE config)
                  argsort with keys: the reference's own route for config 5's
                  sort (rows > 16384: chunk radix sorts + a splitter merge)
   copy           torch's device copy of 256 MiB (the counter calibration)
@@ -53,7 +57,7 @@ sys.path.insert(0, ROOT)
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E peak, GB/s
 COPY_BYTES = 256 << 20  # calibration copy: 256 MiB read + 256 MiB written per launch
 CONFIGS = ["sampler", "sampler_masked", "sampler_wide", "topk_c3", "topk_c3_approx", "topk_c1", "sort_c2", "prefill_c5",
-           "sort_wide", "copy", "read_calib"]
+           "sort_wide", "topk_router", "cumsum_long", "copy", "read_calib"]
 
 
 def _copy_rate(torch, dev, stream, steps, warmup):
@@ -133,6 +137,8 @@ TRAFFIC_KERNELS = {
     "sort_c2": ("tx::radix_sort_rows_kernel", "tx::gather_row_lds_kernel"),
     "prefill_c5": ("tx::softmax_topk_kernel",),
     "sort_wide": ("tx::sort_chunks_kernel", "tx::bucket_", "tx::merge_runs_kernel"),
+    "topk_router": ("tx::topk_short_block_kernel",),
+    "cumsum_long": ("tx::cumsum_",),
 }
 EXTRA_CONFIGS = ("topk_c3", "prefill_c5", "sort_c2")
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
@@ -488,6 +494,85 @@ def _sort_c2(torch, np, _lib, dev, s_handle, gen, nbuf):
     return w
 
 
+def _topk_router(torch, np, _lib, dev, s_handle, gen, nbuf):
+    """Many short rows: exact top-8 of f32 [65536, 128] (a router-sized
+    tax.top_k), one wave per row sorting the row whole."""
+    w = Workload()
+    rows, cols, k = 65536, 128, 8
+    nb = nbuf or 8
+    bufs = [torch.randn((rows, cols), generator=gen, device=dev) for _ in range(nb)]
+    vals = torch.empty((rows, k), dtype=torch.float32, device=dev)
+    idx = torch.empty((rows, k), dtype=torch.int32, device=dev)
+    w.metric = "rows/s + achieved HBM GB/s (% peak): topk_router"
+    w.rows, w.dtype, w.shape = rows, "f32", (rows, cols)
+    w.alg_bytes = rows * cols * 4 + rows * k * 8  # logits in, values and indices out
+    w.workload = "exact top-k (tax.top_k) k=8: f32 [65536,128] ~ N(0,1) (router-sized rows)"
+    w.kernel = "topk_short_block_kernel<0, 128, 2>"
+    w.cpu_batch = 4096
+
+    def launch(i):
+        x = bufs[i % nb]
+        _lib.check(_lib.LIB.tallax_topk(x.data_ptr(), _lib.F32, rows, cols, k, vals.data_ptr(), idx.data_ptr(), None,
+                                        0, s_handle), "top_k")
+
+    def host0(O):
+        if not hasattr(w, "h0"):
+            w.h0 = bufs[0].cpu().numpy()
+        return w.h0
+
+    def parity(O):
+        h = host0(O)
+        launch(0)
+        torch.cuda.synchronize()
+        ov, oi = O.top_k(h, k)
+        return bool(np.array_equal(idx.cpu().numpy(), oi) and
+                    np.array_equal(vals.cpu().numpy().view(np.uint32), ov.view(np.uint32)))
+
+    def cpu_job(O, r0, batch):
+        return ("top_k", (host0(O)[r0:r0 + batch], k), {})
+
+    w.launch, w.parity, w.cpu_job = launch, parity, cpu_job
+    return w
+
+
+def _cumsum_long(torch, np, _lib, dev, s_handle, gen, nbuf):
+    """One long line: tax.cumsum of f32 [1, 4000000] along axis 1 in the
+    reference's tile order (tile totals, the sequential chain, the rescan)."""
+    w = Workload()
+    rows, cols = 1, 4000000
+    nb = nbuf or 8
+    bufs = [torch.randn((rows, cols), generator=gen, device=dev) for _ in range(nb)]
+    out = torch.empty((rows, cols), dtype=torch.float32, device=dev)
+    w.metric = "rows/s + achieved HBM GB/s (% peak): cumsum_long"
+    w.rows, w.dtype, w.shape = rows, "f32", (rows, cols)
+    w.alg_bytes = rows * cols * 8  # read once, write once
+    w.workload = "tax.cumsum(axis=1) of f32 [1,4000000] ~ N(0,1), bit-exact to the (8,128)-tile order"
+    w.kernel = "cumsum_row_tiles_kernel + cumsum_chain_kernel + cumsum_row_tiles_kernel"
+    w.cpu_batch = 1
+
+    def launch(i):
+        x = bufs[i % nb]
+        _lib.check(_lib.LIB.tallax_cumsum(x.data_ptr(), _lib.F32, rows, cols, 1, 0, out.data_ptr(), s_handle),
+                   "cumsum")
+
+    def host0(O):
+        if not hasattr(w, "h0"):
+            w.h0 = bufs[0].cpu().numpy()
+        return w.h0
+
+    def parity(O):
+        h = host0(O)
+        launch(0)
+        torch.cuda.synchronize()
+        return bool(np.array_equal(out.cpu().numpy().view(np.uint32), O.cumsum(h, 1).view(np.uint32)))
+
+    def cpu_job(O, r0, batch):
+        return ("cumsum", (host0(O)[r0:r0 + batch], 1), {})
+
+    w.launch, w.parity, w.cpu_job = launch, parity, cpu_job
+    return w
+
+
 def _prefill_c5(torch, np, _lib, dev, s_handle, gen, nbuf):
     w = Workload()
     rows, cols, k, p = 1024, 201088, 2048, 0.9
@@ -750,12 +835,17 @@ def main() -> int:
         w = _sampler(torch, np, _lib, dev, s_handle, gen, args.nbuf, masked=True)
     elif args.config == "sampler_wide":
         w = _sampler(torch, np, _lib, dev, s_handle, gen, args.nbuf, max_k=1024)
+    elif args.config == "topk_router":
+        w = _topk_router(torch, np, _lib, dev, s_handle, gen, args.nbuf)
+    elif args.config == "cumsum_long":
+        w = _cumsum_long(torch, np, _lib, dev, s_handle, gen, args.nbuf)
     elif args.config.startswith("topk"):
         w = _topk(torch, np, _lib, dev, s_handle, gen, args.nbuf, args.config)
     elif args.config == "sort_c2":
         w = _sort_c2(torch, np, _lib, dev, s_handle, gen, args.nbuf)
     elif args.config == "sort_wide":
         w = _sort_wide(torch, np, _lib, dev, s_handle, gen, args.nbuf)
+
     else:
         w = _prefill_c5(torch, np, _lib, dev, s_handle, gen, args.nbuf)
     torch.cuda.synchronize()
